@@ -1,0 +1,203 @@
+#!/usr/bin/env python3
+"""Benchmark of the dsmoe DeepSeekMoE layer on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3]
+
+A step is one forward pass of the whole MoE layer (fused gate, permute,
+grouped SwiGLU GEMMs for routed and shared experts, combine) over one batch
+of synthetic tokens already resident in HBM.  The default workload is
+BASELINE config 3 (prefill): T=8192 tokens, dim 2048, 64 routed experts
+(inter 1408) top-6, 2 shared experts (inter 1408), bf16 activations and
+experts, fp32 gate.  ``value`` is routed tokens/s = T / step time.
+
+Printed as one JSON line, with
+* ``roofline`` for the dominant kernel (the routed gate/up SwiGLU grouped GEMM):
+  algorithmic FLOPs per launch (4*N*D*I, N = T*k slots) over its mean launch
+  time measured with HIP events recorded by the library on the launch stream;
+* ``cpu_baseline``: the CPU restatement of the reference stacked path
+  (oracle/moe_ref.py) timed on this host on a bounded token sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "deepseek-v3-lite_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "MoE-layer routed tokens/sec (fwd, fwd+bwd) at 1 GPU; % bf16 MFMA peak"
+PEAK_BF16_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+
+# name: (T, D, E, I, k, S, I_s, dtype, bias)
+CONFIGS = {
+    "c0": (1024, 64, 4, 128, 2, 1, 128, "float32", "zeros"),
+    "c1": (8192, 1024, 16, 512, 4, 1, 1024, "bfloat16", "normal"),
+    "c2": (8192, 1024, 16, 512, 4, 1, 1024, "bfloat16", "skew"),
+    "c3": (8192, 2048, 64, 1408, 6, 2, 1408, "bfloat16", "zeros"),
+    "c3_decode": (64, 2048, 64, 1408, 6, 2, 1408, "bfloat16", "zeros"),
+}
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def make_layer(cfg, device, seed: int = 0):
+    """Seeded synthetic inputs generated on the GPU: x ~ N(0,1), weights ~ N(0, 0.02)."""
+    import torch
+    T, D, E, I, k, S, I_s, dt, bias_kind = cfg
+    dtype = getattr(torch, dt)
+    g = torch.Generator(device=device).manual_seed(seed)
+    rn = lambda *s: torch.randn(*s, generator=g, device=device, dtype=torch.float32)
+    x = rn(T, D).to(dtype)
+    gate_w = rn(E, D) * 0.02
+    w1, w2, w3 = [], [], []
+    for _ in range(E):
+        w1.append((rn(I, D) * 0.02).to(dtype)); w3.append((rn(I, D) * 0.02).to(dtype))
+        w2.append((rn(D, I) * 0.02).to(dtype))
+    s1, s2, s3 = [], [], []
+    for _ in range(S):
+        s1.append((rn(I_s, D) * 0.02).to(dtype)); s3.append((rn(I_s, D) * 0.02).to(dtype))
+        s2.append((rn(D, I_s) * 0.02).to(dtype))
+    bias = torch.zeros(E, device=device)
+    if bias_kind == "normal":
+        bias = rn(E) * 0.01
+    elif bias_kind == "skew":
+        bias[:2] = 3.0
+    return x, gate_w, bias, (w1, w2, w3, s1, s2, s3)
+
+
+def cpu_baseline(cfg, x, gate_w, bias, weights, budget_s: float = 20.0):
+    """Times oracle/moe_ref.py's restatement of the reference stacked forward
+    (models/moe.py:74-179) on this host on a token sample sized to the budget."""
+    import torch
+    from oracle import moe_ref as R
+    T, D, E, I, k, S, I_s, dt, _ = cfg
+    cores = min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", "1024")))
+    torch.set_num_threads(cores)
+    w1, w2, w3, s1, s2, s3 = weights
+    cpu = lambda ts: [t.cpu() for t in ts]
+    p = R.MoEParams(gate_w.cpu(), bias.cpu(), cpu(w1), cpu(w2), cpu(w3), cpu(s1), cpu(s2), cpu(s3))
+    xs = x.cpu()
+    n = min(T, 256)
+    t0 = time.perf_counter()
+    R.moe_forward_ref(xs[:n], p, k)
+    dt1 = time.perf_counter() - t0
+    n = int(min(T, max(n, n * (budget_s / 4.0) / max(dt1, 1e-6))))
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        R.moe_forward_ref(xs[:n], p, k)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {"value": n / med, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"first {n} of {T} tokens, same weights; median of 3 forward passes "
+                      f"({med * 1e3:.1f} ms each) after 1 warm-up; torch {torch.__version__} "
+                      f"{torch.backends.cpu.get_cpu_capability()}"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
+              "the multi-GPU (expert-parallel) path is not built", file=sys.stderr)
+        return 2
+
+    import torch
+    import dsmoe._lib as L
+    from dsmoe import moe_layer
+
+    dev = torch.device("cuda:0")
+    cfg = CONFIGS[args.config]
+    T, D, E, I, k, S, I_s, dt, bias_kind = cfg
+    log(f"[bench] config {args.config}: T={T} D={D} E={E} I={I} k={k} S={S}x{I_s} {dt}")
+    x, gate_w, bias, weights = make_layer(cfg, dev)
+    w1, w2, w3, s1, s2, s3 = weights
+
+    def step():
+        return moe_layer(x, gate_w, bias, w1, w2, w3, s1, s2, s3, k=k, training=False)
+
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        log(f"[bench] warm-up done ({args.warmup} steps)")
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        ev0.record()
+        for _ in range(args.steps):
+            step()
+        ev1.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        ms = ev0.elapsed_time(ev1) / args.steps
+        log(f"[bench] timed {args.steps} steps: {ms:.3f} ms/step (host wall {wall * 1e3 / args.steps:.3f} ms/step)")
+
+        # per-stage HIP events recorded by the library on the launch stream
+        L.timing_enable(True)
+        for _ in range(args.steps):
+            step()
+        stages, ncalls = L.timing_read()
+        L.timing_enable(False)
+    stage_ms = {kname: v / max(ncalls, 1) for kname, v in stages.items()}
+    log(f"[bench] stages (ms/call): " + ", ".join(f"{a}={b:.4f}" for a, b in stage_ms.items()))
+
+    N = T * k
+    g1_flops = 4.0 * N * D * I
+    g1_ms = stage_ms.get("gemm1_routed", float("nan"))
+    achieved = g1_flops / (g1_ms * 1e-3) / 1e12
+    gemm_flops = 6.0 * N * D * I + 6.0 * T * D * S * I_s
+    gemm_ms = sum(stage_ms.get(s, 0.0) for s in ("gemm1_routed", "gemm1_shared", "gemm2_routed", "gemm2_shared"))
+    traffic = None
+    prof = ROOT / "profiles" / f"traffic_{args.config}.json"
+    if prof.exists():
+        traffic = json.loads(prof.read_text()).get("gemm1_routed_bytes")
+
+    result = {
+        "metric": METRIC,
+        "value": T / (ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if dt == "bfloat16" else "f32",
+        "data": "synthetic (seeded N(0,1) tokens, N(0,0.02) weights, generated on device)",
+        "config": {"workload": f"{args.config}: DeepSeekMoE layer forward, T={T} tokens, dim={D}, "
+                               f"{E} routed experts (inter {I}) top-{k}, {S} shared (inter {I_s}), {dt}, fp32 gate",
+                   "T": T, "D": D, "E": E, "I": I, "k": k, "S": S, "I_s": I_s},
+        "roofline": {"bound": "mfma", "kernel": "gemm1_routed (gate/up SwiGLU grouped GEMM)",
+                     "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / PEAK_BF16_TFLOPS, "traffic": traffic},
+        "slots_per_s": N / (ms * 1e-3),
+        "grouped_gemm_tflops": gemm_flops / (gemm_ms * 1e-3) / 1e12 if gemm_ms > 0 else None,
+        "grouped_gemm_frac": (gemm_flops / (gemm_ms * 1e-3) / 1e12) / PEAK_BF16_TFLOPS if gemm_ms > 0 else None,
+        "stage_ms": stage_ms,
+    }
+    if not args.no_cpu_baseline:
+        log("[bench] timing the CPU restatement of the reference path ...")
+        result["cpu_baseline"] = cpu_baseline(cfg, x, gate_w, bias, weights)
+        result["speedup_vs_cpu"] = result["value"] / result["cpu_baseline"]["value"]
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,461 @@
+// extern "C" entry points of libdsmoe.so (declared in include/dsmoe.h).
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "common.h"
+
+namespace dsmoe {
+
+// ---------------------------------------------------------------- errors
+static thread_local std::string g_last_error;
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(DSMOE_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+  return DSMOE_OK;
+}
+
+// ---------------------------------------------------------------- pointer tables
+struct PtrChunk {
+  const void* p[64];
+  int32_t n;
+  int32_t off;
+};
+
+__global__ void set_ptrs_kernel(PtrChunk c, const void** dst) {
+  const int i = threadIdx.x;
+  if (i < c.n) dst[c.off + i] = c.p[i];
+}
+
+// Copies `n` host-held device pointers into the device table at dst[off..].
+static int upload_ptrs(const void* const* host, int n, const void** dst, int off, hipStream_t st) {
+  for (int b = 0; b < n; b += 64) {
+    PtrChunk c;
+    c.n = n - b < 64 ? n - b : 64;
+    c.off = off + b;
+    for (int i = 0; i < c.n; ++i) c.p[i] = host[b + i];
+    hipLaunchKernelGGL(set_ptrs_kernel, dim3(1), dim3(64), 0, st, c, dst);
+  }
+  return check_launch("upload_ptrs");
+}
+
+static bool all_aligned16(const void* const* p, int n) {
+  for (int i = 0; i < n; ++i)
+    if (!p[i] || (reinterpret_cast<uintptr_t>(p[i]) & 15)) return false;
+  return true;
+}
+
+static int elem_size(int dtype) { return dtype == DSMOE_BF16 ? 2 : 4; }
+
+static int validate(const dsmoe_dims* d, bool need_experts) {
+  if (!d) return fail(DSMOE_ERR_INVALID, "dims is NULL");
+  if (d->dtype != DSMOE_F32 && d->dtype != DSMOE_BF16)
+    return fail(DSMOE_ERR_UNSUPPORTED, "dtype must be DSMOE_F32 or DSMOE_BF16");
+  if (d->T < 0 || d->D <= 0 || d->E <= 0) return fail(DSMOE_ERR_INVALID, "need T >= 0, D > 0, E > 0");
+  if (d->E > 256) return fail(DSMOE_ERR_UNSUPPORTED, "n_routed_experts > 256 is not supported");
+  if (d->k <= 0 || d->k > d->E) return fail(DSMOE_ERR_INVALID, "need 1 <= n_activated_experts <= n_routed_experts");
+  if (d->k > MAX_TOPK) return fail(DSMOE_ERR_UNSUPPORTED, "n_activated_experts > 16 is not supported");
+  if ((int64_t)d->T * d->k >= (int64_t(1) << 31)) return fail(DSMOE_ERR_UNSUPPORTED, "T * k must be < 2^31");
+  if (need_experts) {
+    if (d->I <= 0) return fail(DSMOE_ERR_INVALID, "moe_inter_dim must be > 0");
+    if (d->S < 0 || (d->S > 0 && d->I_s <= 0)) return fail(DSMOE_ERR_INVALID, "bad shared expert shape");
+  }
+  return DSMOE_OK;
+}
+
+// ---------------------------------------------------------------- layer workspace layout
+struct FwdLayout {
+  const void** ptrs;  // [w1 E][w3 E][w2 E][sw1 S][sw3 S][sw2 S]
+  int32_t* idx;
+  float* w;
+  float* sel;
+  int32_t* offsets;
+  int32_t* sorted_slot;
+  int32_t* sorted_token;
+  int32_t* slot_pos;
+  PermuteScratch ps;
+  void* h;
+  void* g;
+  void* u;
+  void* hs;
+  void* gs;
+  void* us;
+  void* o_slots;
+  void* shared_out;
+  size_t total;
+};
+
+static FwdLayout fwd_layout(const dsmoe_dims& d, int training, void* base) {
+  Carver c(base);
+  FwdLayout L;
+  const int64_t N = (int64_t)d.T * d.k;
+  const int es = elem_size(d.dtype);
+  L.ptrs = c.take<const void*>(3 * d.E + 3 * d.S);
+  L.idx = c.take<int32_t>(N);
+  L.w = c.take<float>(N);
+  L.sel = c.take<float>(N);
+  L.offsets = c.take<int32_t>(d.E + 1);
+  L.sorted_slot = c.take<int32_t>(N);
+  L.sorted_token = c.take<int32_t>(N);
+  L.slot_pos = c.take<int32_t>(N);
+  permute_scratch_carve(c, d, TILE_M, &L.ps);
+  L.h = c.take<char>((size_t)N * d.I * es);
+  L.g = training ? c.take<char>((size_t)N * d.I * es) : nullptr;
+  L.u = training ? c.take<char>((size_t)N * d.I * es) : nullptr;
+  const int64_t SIs = (int64_t)d.S * d.I_s;
+  L.hs = d.S ? c.take<char>((size_t)d.T * SIs * es) : nullptr;
+  L.gs = (d.S && training) ? c.take<char>((size_t)d.T * SIs * es) : nullptr;
+  L.us = (d.S && training) ? c.take<char>((size_t)d.T * SIs * es) : nullptr;
+  L.o_slots = c.take<char>((size_t)N * d.D * es);
+  L.shared_out = d.S ? c.take<char>((size_t)d.T * d.D * es) : nullptr;
+  L.total = c.used();
+  return L;
+}
+
+// ---------------------------------------------------------------- stage timing
+enum Stage : int {
+  ST_TABLES = 0, ST_GATE, ST_PERMUTE, ST_GEMM1, ST_GEMM1_SHARED, ST_GEMM2, ST_GEMM2_SHARED, ST_COMBINE,
+  ST_BWD_PREP, ST_BWD_DH, ST_BWD_DH_SHARED, ST_BWD_DX, ST_BWD_DX_SHARED, ST_BWD_DW13, ST_BWD_DW2,
+  ST_BWD_DW_SHARED, ST_BWD_GATE, ST_BWD_REDUCE, ST_COUNT
+};
+static const char* kStageNames[ST_COUNT] = {
+  "tables", "gate", "permute", "gemm1_routed", "gemm1_shared", "gemm2_routed", "gemm2_shared", "combine",
+  "bwd_prep", "bwd_dh_routed", "bwd_dh_shared", "bwd_dx_routed", "bwd_dx_shared", "bwd_dw13_routed",
+  "bwd_dw2_routed", "bwd_dw_shared", "bwd_gate", "bwd_reduce"};
+
+struct TimingState {
+  std::mutex mu;
+  bool on = false;
+  struct Rec { hipEvent_t a, b; int stage; };
+  std::vector<Rec> recs;
+  std::vector<int> calls;
+};
+static TimingState g_timing;
+
+// Records the boundary of `stage` on `st` when timing is enabled.
+class StageTimer {
+ public:
+  explicit StageTimer(hipStream_t st) : st_(st) {
+    std::lock_guard<std::mutex> lk(g_timing.mu);
+    on_ = g_timing.on;
+  }
+  void begin(int stage) {
+    if (!on_) return;
+    stage_ = stage;
+    (void)hipEventCreate(&a_);
+    (void)hipEventRecord(a_, st_);
+  }
+  void end() {
+    if (!on_ || stage_ < 0) return;
+    hipEvent_t b;
+    (void)hipEventCreate(&b);
+    (void)hipEventRecord(b, st_);
+    std::lock_guard<std::mutex> lk(g_timing.mu);
+    g_timing.recs.push_back({a_, b, stage_});
+    stage_ = -1;
+  }
+  void call_done(int kind) {
+    if (!on_) return;
+    std::lock_guard<std::mutex> lk(g_timing.mu);
+    g_timing.calls.push_back(kind);
+  }
+
+ private:
+  hipStream_t st_;
+  bool on_ = false;
+  int stage_ = -1;
+  hipEvent_t a_{};
+};
+
+static GemmDesc desc_zero() {
+  GemmDesc g;
+  std::memset(static_cast<void*>(&g), 0, sizeof(g));
+  g.nseg = 1;
+  return g;
+}
+
+}  // namespace dsmoe
+
+using namespace dsmoe;
+
+// =============================================================== C ABI
+extern "C" {
+
+const char* dsmoe_last_error(void) { return g_last_error.c_str(); }
+
+int dsmoe_version(void) { return 1; }
+
+int dsmoe_gate_fwd(const void* x, const float* gate_w, const float* gate_bias, const dsmoe_dims* dims, float* logits,
+                   int32_t* idx, int64_t* idx64, float* weights, void* weights_x, float* sel_scores, int32_t* counts,
+                   void* stream) {
+  int rc = validate(dims, false);
+  if (rc) return rc;
+  DSMOE_REQUIRE(x && gate_w && gate_bias && idx && weights, DSMOE_ERR_INVALID, "gate: NULL required pointer");
+  GateOut o{logits, idx, idx64, weights, weights_x, sel_scores, counts};
+  return launch_gate(x, nullptr, gate_w, gate_bias, *dims, o, static_cast<hipStream_t>(stream));
+}
+
+int dsmoe_route_from_logits(const float* logits, const float* gate_bias, const dsmoe_dims* dims, int32_t* idx,
+                            int64_t* idx64, float* weights, void* weights_x, float* sel_scores, int32_t* counts,
+                            void* stream) {
+  int rc = validate(dims, false);
+  if (rc) return rc;
+  DSMOE_REQUIRE(logits && gate_bias && idx && weights, DSMOE_ERR_INVALID, "route: NULL required pointer");
+  GateOut o{nullptr, idx, idx64, weights, weights_x, sel_scores, counts};
+  return launch_gate(nullptr, logits, nullptr, gate_bias, *dims, o, static_cast<hipStream_t>(stream));
+}
+
+size_t dsmoe_permute_workspace_size(const dsmoe_dims* dims) {
+  if (validate(dims, false)) return 0;
+  Carver c(nullptr);
+  return permute_scratch_carve(c, *dims, TILE_M, nullptr);
+}
+
+int dsmoe_permute(const int32_t* idx, const dsmoe_dims* dims, int32_t* offsets, int32_t* sorted_slot,
+                  int32_t* sorted_token, int32_t* slot_pos, int32_t* counts, const void* x, void* x_sorted,
+                  const float* weights, float* sorted_w, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = validate(dims, false);
+  if (rc) return rc;
+  DSMOE_REQUIRE(idx && offsets && sorted_slot && sorted_token && slot_pos, DSMOE_ERR_INVALID,
+                "permute: NULL required pointer");
+  DSMOE_REQUIRE((x == nullptr) == (x_sorted == nullptr), DSMOE_ERR_INVALID, "permute: x and x_sorted go together");
+  DSMOE_REQUIRE((weights == nullptr) == (sorted_w == nullptr), DSMOE_ERR_INVALID,
+                "permute: weights and sorted_w go together");
+  const size_t need = dsmoe_permute_workspace_size(dims);
+  DSMOE_REQUIRE(workspace && workspace_bytes >= need, DSMOE_ERR_WORKSPACE, "permute: workspace too small");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  Carver c(workspace);
+  PermuteScratch ps;
+  permute_scratch_carve(c, *dims, TILE_M, &ps);
+  rc = launch_permute(idx, *dims, TILE_M, ps, offsets, sorted_slot, sorted_token, slot_pos, counts, weights, sorted_w,
+                      st);
+  if (rc) return rc;
+  if (x) rc = launch_gather_rows(x, sorted_token, (int64_t)dims->T * dims->k, dims->D, elem_size(dims->dtype), x_sorted, st);
+  return rc;
+}
+
+static size_t grouped_ws(const dsmoe_dims& d, void* base, const void*** ptrs, int32_t** off32, MTile** sched,
+                         int32_t** cnt, void** h) {
+  Carver c(base);
+  const void** p = c.take<const void*>(3 * d.E);
+  int32_t* o = c.take<int32_t>(d.E + 1);
+  MTile* s = c.take<MTile>(sched_bound(d.T, d.E, TILE_M));
+  int32_t* n = c.take<int32_t>(1);
+  void* hh = c.take<char>((size_t)d.T * d.I * elem_size(d.dtype));
+  if (ptrs) {
+    *ptrs = p; *off32 = o; *sched = s; *cnt = n; *h = hh;
+  }
+  return c.used();
+}
+
+size_t dsmoe_grouped_swiglu_workspace_size(const dsmoe_dims* dims) {
+  if (!dims || dims->T < 0 || dims->E <= 0 || dims->D <= 0 || dims->I <= 0) return 0;
+  return grouped_ws(*dims, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr);
+}
+
+int dsmoe_grouped_swiglu_fwd(const void* x_sorted, const void* const* w1, const void* const* w2, const void* const* w3,
+                             const float* sorted_w, const int64_t* offsets, const dsmoe_dims* dims, void* y_sorted,
+                             void* workspace, size_t workspace_bytes, void* stream) {
+  DSMOE_REQUIRE(dims, DSMOE_ERR_INVALID, "dims is NULL");
+  const dsmoe_dims& d = *dims;
+  DSMOE_REQUIRE(d.dtype == DSMOE_F32 || d.dtype == DSMOE_BF16, DSMOE_ERR_UNSUPPORTED, "unsupported dtype");
+  DSMOE_REQUIRE(d.T >= 0 && d.E > 0 && d.D > 0 && d.I > 0, DSMOE_ERR_INVALID, "grouped: bad dims");
+  DSMOE_REQUIRE(x_sorted && w1 && w2 && w3 && offsets && y_sorted, DSMOE_ERR_INVALID, "grouped: NULL pointer");
+  const size_t need = dsmoe_grouped_swiglu_workspace_size(dims);
+  DSMOE_REQUIRE(workspace && workspace_bytes >= need, DSMOE_ERR_WORKSPACE, "grouped: workspace too small");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const void** ptrs;
+  int32_t* off32;
+  MTile* sched;
+  int32_t* cnt;
+  void* h;
+  grouped_ws(d, workspace, &ptrs, &off32, &sched, &cnt, &h);
+  int rc = upload_ptrs(w1, d.E, ptrs, 0, st);
+  if (!rc) rc = upload_ptrs(w3, d.E, ptrs, d.E, st);
+  if (!rc) rc = upload_ptrs(w2, d.E, ptrs, 2 * d.E, st);
+  if (!rc) rc = launch_sched_from_offsets(offsets, d.E, TILE_M, d.T, off32, sched, cnt, st);
+  if (rc) return rc;
+  const bool mf = all_aligned16(w1, d.E) && all_aligned16(w2, d.E) && all_aligned16(w3, d.E);
+  GemmDesc g = desc_zero();
+  g.sched = sched; g.sched_count = cnt; g.m_tiles_bound = (int32_t)sched_bound(d.T, d.E, TILE_M);
+  g.A = x_sorted; g.lda = d.D; g.B0 = ptrs; g.B1 = ptrs + d.E; g.ldb = d.D; g.kseg = d.D;
+  g.N = d.I; g.K = d.D; g.C = h; g.ldc = d.I;
+  rc = launch_grouped_gemm(g, EPI_SWIGLU, d.dtype, nullptr, mf, st);
+  if (rc) return rc;
+  GemmDesc g2 = desc_zero();
+  g2.sched = sched; g2.sched_count = cnt; g2.m_tiles_bound = g.m_tiles_bound;
+  g2.A = h; g2.lda = d.I; g2.B0 = ptrs + 2 * d.E; g2.ldb = d.I; g2.kseg = d.I;
+  g2.N = d.D; g2.K = d.I; g2.C = y_sorted; g2.ldc = d.D;
+  return launch_grouped_gemm(g2, EPI_STORE, d.dtype, sorted_w, mf, st);
+}
+
+int dsmoe_grouped_swiglu_bwd(const void*, const void* const*, const void* const*, const void* const*, const int64_t*,
+                             const void*, const dsmoe_dims*, void*, void* const*, void* const*, void* const*, void*,
+                             size_t, void*) {
+  return fail(DSMOE_ERR_UNSUPPORTED, "dsmoe_grouped_swiglu_bwd: not built yet");
+}
+
+int dsmoe_combine_fwd(const void* o_slots, const float* weights, const int32_t* idx, const void* shared,
+                      const dsmoe_dims* dims, void* y, void* stream) {
+  int rc = validate(dims, false);
+  if (rc) return rc;
+  DSMOE_REQUIRE(o_slots && weights && idx && y, DSMOE_ERR_INVALID, "combine: NULL required pointer");
+  return launch_combine(o_slots, weights, idx, shared, *dims, y, static_cast<hipStream_t>(stream));
+}
+
+size_t dsmoe_moe_fwd_workspace_size(const dsmoe_dims* dims, int training) {
+  if (validate(dims, true)) return 0;
+  return fwd_layout(*dims, training, nullptr).total;
+}
+
+int dsmoe_moe_fwd(const void* x, const float* gate_w, const float* gate_bias, const void* const* w1,
+                  const void* const* w2, const void* const* w3, const void* const* sw1, const void* const* sw2,
+                  const void* const* sw3, const dsmoe_dims* dims, int training, void* y, int64_t* idx64,
+                  void* weights_x, int32_t* counts, float* logits, void* workspace, size_t workspace_bytes,
+                  void* stream) {
+  int rc = validate(dims, true);
+  if (rc) return rc;
+  const dsmoe_dims& d = *dims;
+  DSMOE_REQUIRE(x && gate_w && gate_bias && w1 && w2 && w3 && y, DSMOE_ERR_INVALID, "moe_fwd: NULL required pointer");
+  DSMOE_REQUIRE(d.S == 0 || (sw1 && sw2 && sw3), DSMOE_ERR_INVALID, "moe_fwd: NULL shared expert pointers");
+  const size_t need = dsmoe_moe_fwd_workspace_size(dims, training);
+  DSMOE_REQUIRE(workspace && workspace_bytes >= need, DSMOE_ERR_WORKSPACE, "moe_fwd: workspace too small");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  FwdLayout L = fwd_layout(d, training, workspace);
+  const int64_t N = (int64_t)d.T * d.k;
+  StageTimer tm(st);
+
+  tm.begin(ST_TABLES);
+  rc = upload_ptrs(w1, d.E, L.ptrs, 0, st);
+  if (!rc) rc = upload_ptrs(w3, d.E, L.ptrs, d.E, st);
+  if (!rc) rc = upload_ptrs(w2, d.E, L.ptrs, 2 * d.E, st);
+  if (!rc && d.S) rc = upload_ptrs(sw1, d.S, L.ptrs, 3 * d.E, st);
+  if (!rc && d.S) rc = upload_ptrs(sw3, d.S, L.ptrs, 3 * d.E + d.S, st);
+  if (!rc && d.S) rc = upload_ptrs(sw2, d.S, L.ptrs, 3 * d.E + 2 * d.S, st);
+  if (rc) return rc;
+  const bool mf = all_aligned16(w1, d.E) && all_aligned16(w2, d.E) && all_aligned16(w3, d.E) &&
+                  (d.S == 0 || (all_aligned16(sw1, d.S) && all_aligned16(sw2, d.S) && all_aligned16(sw3, d.S)));
+
+  tm.end();
+  // (a) gate
+  GateOut go{logits, L.idx, idx64, L.w, weights_x, L.sel, nullptr};
+  tm.begin(ST_GATE);
+  rc = launch_gate(x, nullptr, gate_w, gate_bias, d, go, st);
+  tm.end();
+  if (rc) return rc;
+  // (b) permute (counts come from the scan: exact bincount, no atomics)
+  tm.begin(ST_PERMUTE);
+  rc = launch_permute(L.idx, d, TILE_M, L.ps, L.offsets, L.sorted_slot, L.sorted_token, L.slot_pos, counts, nullptr,
+                      nullptr, st);
+  tm.end();
+  if (rc) return rc;
+  const int32_t mbound = (int32_t)sched_bound(N, d.E, TILE_M);
+  // (c) routed gate/up + SwiGLU, rows gathered from x through sorted_token
+  GemmDesc g1 = desc_zero();
+  g1.sched = L.ps.sched; g1.sched_count = L.ps.sched_count; g1.m_tiles_bound = mbound;
+  g1.A = x; g1.lda = d.D; g1.a_map = L.sorted_token;
+  g1.B0 = L.ptrs; g1.B1 = L.ptrs + d.E; g1.ldb = d.D; g1.kseg = d.D;
+  g1.N = d.I; g1.K = d.D; g1.C = L.h; g1.ldc = d.I; g1.Gs = L.g; g1.Us = L.u;
+  tm.begin(ST_GEMM1);
+  rc = launch_grouped_gemm(g1, EPI_SWIGLU, d.dtype, nullptr, mf, st);
+  tm.end();
+  if (rc) return rc;
+  // shared experts: S dense groups over all tokens, h_shared = [h_0 | h_1 | ...]
+  if (d.S) {
+    GemmDesc s1 = desc_zero();
+    s1.dense_rows = d.T; s1.groups = d.S;
+    s1.A = x; s1.lda = d.D;
+    s1.B0 = L.ptrs + 3 * d.E; s1.B1 = L.ptrs + 3 * d.E + d.S; s1.ldb = d.D; s1.kseg = d.D;
+    s1.N = d.I_s; s1.K = d.D; s1.C = L.hs; s1.ldc = (int64_t)d.S * d.I_s; s1.c_group_col = d.I_s;
+    s1.Gs = L.gs; s1.Us = L.us;
+    tm.begin(ST_GEMM1_SHARED);
+    rc = launch_grouped_gemm(s1, EPI_SWIGLU, d.dtype, nullptr, mf, st);
+    tm.end();
+    if (rc) return rc;
+  }
+  // routed down projection, rows written back in slot order (t*k + j)
+  GemmDesc g2 = desc_zero();
+  g2.sched = L.ps.sched; g2.sched_count = L.ps.sched_count; g2.m_tiles_bound = mbound;
+  g2.A = L.h; g2.lda = d.I; g2.B0 = L.ptrs + 2 * d.E; g2.ldb = d.I; g2.kseg = d.I;
+  g2.N = d.D; g2.K = d.I; g2.C = L.o_slots; g2.ldc = d.D; g2.c_map = L.sorted_slot;
+  tm.begin(ST_GEMM2);
+  rc = launch_grouped_gemm(g2, EPI_STORE, d.dtype, nullptr, mf, st);
+  tm.end();
+  if (rc) return rc;
+  // shared down projection: one GEMM with K = S * I_s summing all shared experts
+  if (d.S) {
+    GemmDesc s2 = desc_zero();
+    s2.dense_rows = d.T; s2.groups = 1;
+    s2.A = L.hs; s2.lda = (int64_t)d.S * d.I_s;
+    s2.B0 = L.ptrs + 3 * d.E + 2 * d.S; s2.ldb = d.I_s; s2.kseg = d.I_s; s2.nseg = d.S;
+    s2.N = d.D; s2.K = d.S * d.I_s; s2.C = L.shared_out; s2.ldc = d.D;
+    tm.begin(ST_GEMM2_SHARED);
+    rc = launch_grouped_gemm(s2, EPI_STORE, d.dtype, nullptr, mf, st);
+    tm.end();
+    if (rc) return rc;
+  }
+  // (d) combine
+  tm.begin(ST_COMBINE);
+  rc = launch_combine(L.o_slots, L.w, L.idx, L.shared_out, d, y, st);
+  tm.end();
+  tm.call_done(0);
+  return rc;
+}
+
+size_t dsmoe_moe_bwd_workspace_size(const dsmoe_dims* dims) {
+  if (validate(dims, true)) return 0;
+  return 0;
+}
+
+int dsmoe_moe_bwd(const void*, const float*, const void* const*, const void* const*, const void* const*,
+                  const void* const*, const void* const*, const void* const*, const dsmoe_dims*, const void*,
+                  const void*, void*, float*, void* const*, void* const*, void* const*, void* const*, void* const*,
+                  void* const*, void*, size_t, void*) {
+  return fail(DSMOE_ERR_UNSUPPORTED, "dsmoe_moe_bwd: not built yet");
+}
+
+int dsmoe_update_bias(const int32_t* counts, float* gate_bias, int E, float speed, float upper, float lower,
+                      void* stream) {
+  DSMOE_REQUIRE(counts && gate_bias && E > 0, DSMOE_ERR_INVALID, "update_bias: bad arguments");
+  return launch_update_bias(counts, gate_bias, E, speed, upper, lower, static_cast<hipStream_t>(stream));
+}
+
+int dsmoe_timing_enable(int on) {
+  std::lock_guard<std::mutex> lk(g_timing.mu);
+  for (auto& r : g_timing.recs) {
+    (void)hipEventDestroy(r.a);
+    (void)hipEventDestroy(r.b);
+  }
+  g_timing.recs.clear();
+  g_timing.calls.clear();
+  g_timing.on = on != 0;
+  return DSMOE_OK;
+}
+
+int dsmoe_timing_read(double* stage_ms, int max_stages, int* n_calls) {
+  std::lock_guard<std::mutex> lk(g_timing.mu);
+  for (int i = 0; i < max_stages; ++i) stage_ms[i] = 0.0;
+  for (auto& r : g_timing.recs) {
+    if (hipEventSynchronize(r.b) != hipSuccess) return fail(DSMOE_ERR_HIP, "timing: event sync failed");
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, r.a, r.b) != hipSuccess) return fail(DSMOE_ERR_HIP, "timing: elapsed failed");
+    if (r.stage < max_stages) stage_ms[r.stage] += ms;
+  }
+  if (n_calls) *n_calls = (int)g_timing.calls.size();
+  return ST_COUNT;
+}
+
+const char* dsmoe_timing_stage_name(int stage) {
+  return (stage >= 0 && stage < ST_COUNT) ? kStageNames[stage] : "";
+}
+
+}  // extern "C"

@@ -1,0 +1,175 @@
+// (d) Weighted combine + shared add, and the f1 bias update.
+//
+// combine:  y[t] = sum_{j by ascending expert id} w[t,j] * o_slots[t*k+j] + shared[t]
+// restates the out-of-place index_add loop of models/moe.py:118-133 (the
+// reference adds expert outputs in ascending expert id) and the shared add of
+// models/moe.py:100-102.  Accumulation is fp32 with one final rounding; the k
+// rows of a token are contiguous (slot order), so every access is a coalesced
+// 16-byte vector.
+#include "common.h"
+
+namespace dsmoe {
+
+constexpr int CMB_MAX_K = 16;
+
+template <typename T, int VEC>
+struct Vec;
+template <>
+struct Vec<uint16_t, 8> {
+  using type = uint4;
+  static __device__ __forceinline__ void to_f(const uint4& v, float* f) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = bf2f((uint16_t)(w[i] & 0xffffu));
+      f[2 * i + 1] = bf2f((uint16_t)(w[i] >> 16));
+    }
+  }
+  static __device__ __forceinline__ uint4 from_f(const float* f) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = (uint32_t)f2bf(f[2 * i]) | ((uint32_t)f2bf(f[2 * i + 1]) << 16);
+    return make_uint4(w[0], w[1], w[2], w[3]);
+  }
+};
+template <>
+struct Vec<float, 4> {
+  using type = float4;
+  static __device__ __forceinline__ void to_f(const float4& v, float* f) {
+    f[0] = v.x; f[1] = v.y; f[2] = v.z; f[3] = v.w;
+  }
+  static __device__ __forceinline__ float4 from_f(const float* f) { return make_float4(f[0], f[1], f[2], f[3]); }
+};
+
+// Sort a token's k (expert, slot j) pairs by expert id (insertion sort, k <= 16).
+__device__ __forceinline__ void order_by_expert(const int32_t* idx_row, int k, int* ord) {
+  int ev[CMB_MAX_K];
+  for (int j = 0; j < k; ++j) {
+    const int e = idx_row[j];
+    int p = j;
+    while (p > 0 && ev[p - 1] > e) {
+      ev[p] = ev[p - 1];
+      ord[p] = ord[p - 1];
+      --p;
+    }
+    ev[p] = e;
+    ord[p] = j;
+  }
+}
+
+// One thread per (token, VEC-wide column chunk).
+template <typename T, int VEC>
+__global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ o_slots, const float* __restrict__ w,
+                                                      const int32_t* __restrict__ idx, const T* __restrict__ shared,
+                                                      int T_, int D, int k, T* __restrict__ y) {
+  using V = Vec<T, VEC>;
+  using VT = typename V::type;
+  const int cpr = D / VEC;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)T_ * cpr) return;
+  const int64_t t = i / cpr;
+  const int c = (int)(i - t * cpr);
+  int ord[CMB_MAX_K];
+  order_by_expert(idx + t * k, k, ord);
+  float acc[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
+  for (int q = 0; q < k; ++q) {
+    const int j = ord[q];
+    const float wj = w[t * k + j];
+    float f[VEC];
+    V::to_f(reinterpret_cast<const VT*>(o_slots + (t * k + j) * (int64_t)D)[c], f);
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) acc[v] = fmaf(wj, f[v], acc[v]);
+  }
+  if (shared) {
+    float f[VEC];
+    V::to_f(reinterpret_cast<const VT*>(shared + t * (int64_t)D)[c], f);
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) acc[v] += f[v];
+  }
+  reinterpret_cast<VT*>(y + t * (int64_t)D)[c] = V::from_f(acc);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void combine_scalar_kernel(const T* __restrict__ o_slots, const float* __restrict__ w,
+                                                             const int32_t* __restrict__ idx,
+                                                             const T* __restrict__ shared, int T_, int D, int k,
+                                                             T* __restrict__ y) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)T_ * D) return;
+  const int64_t t = i / D;
+  const int c = (int)(i - t * D);
+  int ord[CMB_MAX_K];
+  order_by_expert(idx + t * k, k, ord);
+  float acc = 0.0f;
+  for (int q = 0; q < k; ++q) {
+    const int j = ord[q];
+    acc = fmaf(w[t * k + j], to_f<T>(o_slots[(t * k + j) * (int64_t)D + c]), acc);
+  }
+  if (shared) acc += to_f<T>(shared[t * (int64_t)D + c]);
+  y[t * (int64_t)D + c] = from_f<T>(acc);
+}
+
+int launch_combine(const void* o_slots, const float* w, const int32_t* idx, const void* shared, const dsmoe_dims& d,
+                   void* y, hipStream_t st) {
+  if (d.T == 0) return DSMOE_OK;
+  const bool al = ((reinterpret_cast<uintptr_t>(o_slots) | reinterpret_cast<uintptr_t>(y) |
+                    reinterpret_cast<uintptr_t>(shared)) & 15) == 0;
+  if (d.dtype == DSMOE_BF16) {
+    if (d.D % 8 == 0 && al) {
+      const int64_t n = (int64_t)d.T * (d.D / 8);
+      hipLaunchKernelGGL((combine_kernel<uint16_t, 8>), dim3((unsigned)cdiv(n, 256)), dim3(256), 0, st,
+                         static_cast<const uint16_t*>(o_slots), w, idx, static_cast<const uint16_t*>(shared), d.T, d.D,
+                         d.k, static_cast<uint16_t*>(y));
+    } else {
+      const int64_t n = (int64_t)d.T * d.D;
+      hipLaunchKernelGGL(combine_scalar_kernel<uint16_t>, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, st,
+                         static_cast<const uint16_t*>(o_slots), w, idx, static_cast<const uint16_t*>(shared), d.T, d.D,
+                         d.k, static_cast<uint16_t*>(y));
+    }
+  } else {
+    if (d.D % 4 == 0 && al) {
+      const int64_t n = (int64_t)d.T * (d.D / 4);
+      hipLaunchKernelGGL((combine_kernel<float, 4>), dim3((unsigned)cdiv(n, 256)), dim3(256), 0, st,
+                         static_cast<const float*>(o_slots), w, idx, static_cast<const float*>(shared), d.T, d.D, d.k,
+                         static_cast<float*>(y));
+    } else {
+      const int64_t n = (int64_t)d.T * d.D;
+      hipLaunchKernelGGL(combine_scalar_kernel<float>, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, st,
+                         static_cast<const float*>(o_slots), w, idx, static_cast<const float*>(shared), d.T, d.D, d.k,
+                         static_cast<float*>(y));
+    }
+  }
+  return check_launch("combine");
+}
+
+// f1: models/moe.py:21-27 on device.  One block; counts int32 (E).
+__global__ void update_bias_kernel(const int32_t* __restrict__ counts, float* __restrict__ bias, int E, float speed,
+                                   float upper, float lower) {
+  __shared__ float s_avg;
+  if (threadIdx.x == 0) {
+    // mean of the fp32-cast counts in ascending order (the counts are exact
+    // integers far below 2^24, so every partial sum is exact)
+    float s = 0.0f;
+    for (int e = 0; e < E; ++e) s += (float)counts[e];
+    s_avg = s / (float)E;
+  }
+  __syncthreads();
+  const float avg = s_avg;
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    const float c = (float)counts[e];
+    float b = bias[e];
+    if (c > avg * (1.0f + upper)) b -= speed;
+    if (c < avg * (1.0f - lower)) b += speed;
+    bias[e] = b;
+  }
+}
+
+int launch_update_bias(const int32_t* counts, float* bias, int E, float speed, float upper, float lower,
+                       hipStream_t st) {
+  hipLaunchKernelGGL(update_bias_kernel, dim3(1), dim3(256), 0, st, counts, bias, E, speed, upper, lower);
+  return check_launch("update_bias");
+}
+
+}  // namespace dsmoe

@@ -1,0 +1,161 @@
+// Internal helpers shared by the dsmoe HIP sources (gfx950 / CDNA4 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "dsmoe.h"
+
+namespace dsmoe {
+
+using bf16_t = uint16_t;  // bf16 storage; arithmetic is done in fp32
+
+// ---------------------------------------------------------------- conversions
+__device__ __forceinline__ float bf2f(bf16_t v) { return __uint_as_float(static_cast<uint32_t>(v) << 16); }
+
+// fp32 -> bf16, round to nearest even (NaN kept quiet).
+__device__ __forceinline__ bf16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return static_cast<bf16_t>((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<bf16_t>(u >> 16);
+}
+
+template <typename T>
+__device__ __forceinline__ float to_f(T v);
+template <>
+__device__ __forceinline__ float to_f<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ float to_f<bf16_t>(bf16_t v) { return bf2f(v); }
+
+template <typename T>
+__device__ __forceinline__ T from_f(float v);
+template <>
+__device__ __forceinline__ float from_f<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ bf16_t from_f<bf16_t>(float v) { return f2bf(v); }
+
+// silu(g) = g * sigmoid(g), fp32.
+__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + __expf(-g)); }
+__device__ __forceinline__ float sigmoid_f(float g) { return 1.0f / (1.0f + __expf(-g)); }
+
+// Routing sigmoid: double evaluation, single rounding to fp32 (matches the oracle).
+__device__ __forceinline__ float route_sigmoid(float x) {
+  return static_cast<float>(1.0 / (1.0 + exp(-static_cast<double>(x))));
+}
+
+__host__ __device__ __forceinline__ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+__host__ __device__ __forceinline__ size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// ---------------------------------------------------------------- errors
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int check_launch(const char* what);
+
+#define DSMOE_REQUIRE(cond, code, msg)                         \
+  do {                                                         \
+    if (!(cond)) return ::dsmoe::fail((code), std::string(msg)); \
+  } while (0)
+
+// ---------------------------------------------------------------- workspace carving
+struct Carver {
+  char* base;
+  size_t off = 0;
+  explicit Carver(void* b) : base(static_cast<char*>(b)) {}
+  template <typename T>
+  T* take(size_t count) {
+    off = align_up(off, 256);
+    T* p = base ? reinterpret_cast<T*>(base + off) : nullptr;
+    off += count * sizeof(T);
+    return p;
+  }
+  size_t used() const { return align_up(off, 256); }
+};
+
+// ---------------------------------------------------------------- grouped GEMM description
+// One launch computes, for every group g and every row r of the group's row range:
+//   C[cmap(r)][c_col(g) + n] = epilogue( sum_k A[amap(r)][k] * B_g(n, k) )
+// where row ranges come from a device-side M-tile schedule (routed experts) or
+// are dense (every group covers rows [0, dense_rows)).
+enum Epi : int {
+  EPI_STORE = 0,        // C = acc (rounded to C dtype)
+  EPI_SWIGLU = 1,       // two B operands (W1, W3): C = silu(acc0) * acc1; optional G/U saves
+};
+
+struct MTile {  // one M tile of the routed schedule
+  int32_t group;
+  int32_t row0;   // first row (sorted position)
+  int32_t rows;   // valid rows in this tile (<= BM)
+  int32_t pad;
+};
+
+struct GemmDesc {
+  // schedule
+  const MTile* sched;         // routed schedule (device) or nullptr for dense
+  const int32_t* sched_count; // number of valid entries in sched (device)
+  int32_t dense_rows;         // dense: rows per group
+  int32_t groups;             // number of groups (dense)
+  int32_t m_tiles_bound;      // host upper bound of M tiles (grid sizing)
+  // A operand: rows of length K (K contiguous)
+  const void* A;
+  int64_t lda;
+  const int32_t* a_map;       // row -> A row, nullptr = identity
+  // B operand(s): per group and K segment: B0[g * nseg + s] points at an (N x kseg) row-major block
+  const void* const* B0;
+  const void* const* B1;
+  int64_t ldb;
+  int32_t kseg;
+  int32_t nseg;
+  int32_t N, K;
+  // outputs
+  void* C;
+  int64_t ldc;
+  const int32_t* c_map;       // row -> C row, nullptr = identity
+  int64_t c_group_col;        // column offset per group (dense shared GEMM1)
+  void* Gs;                   // SWIGLU: optional pre-activation saves (same indexing as C)
+  void* Us;
+};
+
+constexpr int TILE_M = 128;   // M tile of every grouped GEMM and of the permute schedule
+constexpr int MAX_TOPK = 16;
+
+struct GateOut {
+  float* logits;
+  int32_t* idx;
+  int64_t* idx64;
+  float* weights;
+  void* weights_x;  // x dtype
+  float* sel_scores;
+  int32_t* counts;
+};
+
+struct PermuteScratch {
+  int32_t* blockhist;
+  int32_t* blockbase;
+  int32_t* local_rank;
+  MTile* sched;
+  int32_t* sched_count;
+};
+
+// ---------------------------------------------------------------- launchers
+int launch_gate(const void* x, const float* logits_in, const float* gw, const float* bias, const dsmoe_dims& d,
+                const GateOut& out, hipStream_t st);
+void launch_fill_i32(int32_t* p, int n, int32_t v, hipStream_t st);
+int64_t sched_bound(int64_t rows, int groups, int bm);
+size_t permute_scratch_carve(Carver& c, const dsmoe_dims& d, int bm, PermuteScratch* out);
+int launch_permute(const int32_t* idx, const dsmoe_dims& d, int bm, const PermuteScratch& s, int32_t* offsets,
+                   int32_t* sorted_slot, int32_t* sorted_token, int32_t* slot_pos, int32_t* counts, const float* w,
+                   float* sorted_w, hipStream_t st);
+int launch_gather_rows(const void* x, const int32_t* rows, int64_t nrows, int D, int elem, void* dst, hipStream_t st);
+int launch_sched_from_offsets(const int64_t* offsets64, int E, int bm, int64_t rows, int32_t* offsets32, MTile* sched,
+                              int32_t* sched_count, hipStream_t st);
+int launch_grouped_gemm(const GemmDesc& g, int epi, int dtype, const float* row_scale, bool allow_mfma,
+                        hipStream_t st);
+int launch_combine(const void* o_slots, const float* w, const int32_t* idx, const void* shared, const dsmoe_dims& d,
+                   void* y, hipStream_t st);
+int launch_update_bias(const int32_t* counts, float* bias, int E, float speed, float upper, float lower,
+                       hipStream_t st);
+
+}  // namespace dsmoe

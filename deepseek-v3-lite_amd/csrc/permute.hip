@@ -1,0 +1,232 @@
+// (b) Permute / dispatch: stable (expert, token) order without a host sync.
+// Restates models/moe.py:107-117 (argsort, bincount, offsets) and the row
+// gather flat[sorted_token_ids] of models/moe.py:127,150.
+//
+//   rank_kernel     one wave per 64 tokens: for each expert a wave ballot gives
+//                   every slot its rank among the block's earlier tokens, and
+//                   the block histogram (no atomics, deterministic).
+//   scan_kernel     one block: per-expert exclusive scan over block histograms,
+//                   counts, offsets (E+1), and the M-tile schedule used by the
+//                   grouped GEMMs (tiles of PERM_BM rows inside each expert).
+//   scatter_kernel  pos = offsets[e] + blockbase[b][e] + rank; writes the
+//                   sorted order, its inverse and optional weight gather.
+//   gather_rows     x_sorted[p] = x[sorted_token[p]] with 16-byte accesses.
+#include "common.h"
+
+namespace dsmoe {
+
+constexpr int RANK_TOKENS = 64;  // one wave64 per block, one token per lane
+constexpr int MAX_K = 16;
+
+__global__ __launch_bounds__(64) void rank_kernel(const int32_t* __restrict__ idx, int T, int k, int E,
+                                                  int32_t* __restrict__ blockhist, int32_t* __restrict__ local_rank) {
+  const int lane = threadIdx.x;
+  const int t = blockIdx.x * RANK_TOKENS + lane;
+  int ex[MAX_K];
+#pragma unroll
+  for (int j = 0; j < MAX_K; ++j) ex[j] = -1;
+  if (t < T)
+    for (int j = 0; j < k; ++j) ex[j] = idx[(int64_t)t * k + j];
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int e = 0; e < E; ++e) {
+    int jsel = -1;
+#pragma unroll
+    for (int j = 0; j < MAX_K; ++j)
+      if (ex[j] == e) jsel = j;
+    const uint64_t mask = __ballot(jsel >= 0);
+    if (jsel >= 0) local_rank[(int64_t)t * k + jsel] = __popcll(mask & below);
+    if (lane == 0) blockhist[(int64_t)blockIdx.x * E + e] = __popcll(mask);
+  }
+}
+
+// Single block.  LDS: cnt[E], off[E+1], tiles[E+1].
+__global__ __launch_bounds__(256) void scan_kernel(const int32_t* __restrict__ blockhist, int nb, int E, int bm,
+                                                   int32_t* __restrict__ blockbase, int32_t* __restrict__ counts,
+                                                   int32_t* __restrict__ offsets, MTile* __restrict__ sched,
+                                                   int32_t* __restrict__ sched_count) {
+  extern __shared__ int32_t sh[];
+  int32_t* cnt = sh;
+  int32_t* off = sh + E;
+  int32_t* til = off + E + 1;
+  const int tid = threadIdx.x;
+  for (int e = tid; e < E; e += blockDim.x) {
+    int32_t run = 0;
+    int b = 0;
+    for (; b + 4 <= nb; b += 4) {
+      int32_t v0 = blockhist[(int64_t)(b + 0) * E + e], v1 = blockhist[(int64_t)(b + 1) * E + e];
+      int32_t v2 = blockhist[(int64_t)(b + 2) * E + e], v3 = blockhist[(int64_t)(b + 3) * E + e];
+      blockbase[(int64_t)(b + 0) * E + e] = run; run += v0;
+      blockbase[(int64_t)(b + 1) * E + e] = run; run += v1;
+      blockbase[(int64_t)(b + 2) * E + e] = run; run += v2;
+      blockbase[(int64_t)(b + 3) * E + e] = run; run += v3;
+    }
+    for (; b < nb; ++b) {
+      int32_t v = blockhist[(int64_t)b * E + e];
+      blockbase[(int64_t)b * E + e] = run;
+      run += v;
+    }
+    cnt[e] = run;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int32_t o = 0, tl = 0;
+    for (int e = 0; e < E; ++e) {
+      off[e] = o;
+      til[e] = tl;
+      o += cnt[e];
+      tl += (cnt[e] + bm - 1) / bm;
+    }
+    off[E] = o;
+    til[E] = tl;
+    *sched_count = tl;
+  }
+  __syncthreads();
+  for (int e = tid; e <= E; e += blockDim.x) {
+    offsets[e] = off[e];
+    if (e < E && counts) counts[e] = cnt[e];
+  }
+  for (int e = tid; e < E; e += blockDim.x) {
+    const int32_t c = cnt[e], base = til[e];
+    for (int i = 0; i * bm < c; ++i) {
+      MTile m;
+      m.group = e;
+      m.row0 = off[e] + i * bm;
+      m.rows = min(bm, c - i * bm);
+      m.pad = 0;
+      sched[base + i] = m;
+    }
+  }
+}
+
+__global__ void scatter_kernel(const int32_t* __restrict__ idx, const int32_t* __restrict__ local_rank,
+                               const int32_t* __restrict__ blockbase, const int32_t* __restrict__ offsets, int T, int k,
+                               int E, int32_t* __restrict__ sorted_slot, int32_t* __restrict__ sorted_token,
+                               int32_t* __restrict__ slot_pos, const float* __restrict__ w, float* __restrict__ sorted_w) {
+  const int64_t s = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (s >= (int64_t)T * k) return;
+  const int t = (int)(s / k);
+  const int e = idx[s];
+  if ((unsigned)e >= (unsigned)E) return;  // ids are validated upstream; never write out of bounds
+  const int b = t / RANK_TOKENS;
+  const int32_t pos = offsets[e] + blockbase[(int64_t)b * E + e] + local_rank[s];
+  sorted_slot[pos] = (int32_t)s;
+  sorted_token[pos] = t;
+  slot_pos[s] = pos;
+  if (sorted_w) sorted_w[pos] = w[s];
+}
+
+// Row gather with 16-byte vectors; row_bytes % 16 == 0.
+__global__ void gather_rows_kernel(const uint4* __restrict__ src, const int32_t* __restrict__ rows, int64_t nrows,
+                                   int vec_per_row, uint4* __restrict__ dst) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nrows * vec_per_row) return;
+  const int64_t r = i / vec_per_row;
+  const int c = (int)(i - r * vec_per_row);
+  dst[i] = src[(int64_t)rows[r] * vec_per_row + c];
+}
+
+template <typename T>
+__global__ void gather_rows_scalar_kernel(const T* __restrict__ src, const int32_t* __restrict__ rows, int64_t nrows,
+                                          int D, T* __restrict__ dst) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nrows * D) return;
+  const int64_t r = i / D;
+  const int c = (int)(i - r * D);
+  dst[i] = src[(int64_t)rows[r] * D + c];
+}
+
+// Schedule from caller-provided int64 offsets (E+1) (grouped operator seam).
+// Offsets that are not monotone, do not start at 0 or exceed `rows` yield an
+// empty schedule (nothing is computed) instead of out-of-bounds accesses.
+__global__ __launch_bounds__(256) void sched_from_offsets_kernel(const int64_t* __restrict__ offsets64, int E, int bm,
+                                                                 int64_t rows, int32_t* __restrict__ offsets32,
+                                                                 MTile* __restrict__ sched,
+                                                                 int32_t* __restrict__ sched_count) {
+  extern __shared__ int32_t til[];  // E+1, then one flag
+  const int tid = threadIdx.x;
+  if (tid == 0) {
+    int32_t tl = 0;
+    bool ok = offsets64[0] == 0 && offsets64[E] <= rows;
+    for (int e = 0; e < E; ++e) {
+      til[e] = tl;
+      const int64_t c = offsets64[e + 1] - offsets64[e];
+      if (c < 0) ok = false;
+      tl += (int32_t)((c + bm - 1) / bm);
+    }
+    til[E] = tl;
+    til[E + 1] = ok ? 1 : 0;
+    *sched_count = ok ? tl : 0;
+  }
+  __syncthreads();
+  if (!til[E + 1]) return;
+  for (int e = tid; e <= E; e += blockDim.x) offsets32[e] = (int32_t)offsets64[e];
+  for (int e = tid; e < E; e += blockDim.x) {
+    const int32_t o = (int32_t)offsets64[e];
+    const int32_t c = (int32_t)(offsets64[e + 1] - offsets64[e]);
+    for (int i = 0; i * bm < c; ++i) {
+      MTile m;
+      m.group = e;
+      m.row0 = o + i * bm;
+      m.rows = min(bm, c - i * bm);
+      m.pad = 0;
+      sched[til[e] + i] = m;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- host side
+int64_t sched_bound(int64_t rows, int groups, int bm) { return rows / bm + groups + 1; }
+
+size_t permute_scratch_carve(Carver& c, const dsmoe_dims& d, int bm, PermuteScratch* out) {
+  const int64_t nb = cdiv(d.T, RANK_TOKENS);
+  const int64_t N = (int64_t)d.T * d.k;
+  PermuteScratch s;
+  s.blockhist = c.take<int32_t>(nb * d.E);
+  s.blockbase = c.take<int32_t>(nb * d.E);
+  s.local_rank = c.take<int32_t>(N);
+  s.sched = c.take<MTile>(sched_bound(N, d.E, bm));
+  s.sched_count = c.take<int32_t>(1);
+  if (out) *out = s;
+  return c.used();
+}
+
+int launch_permute(const int32_t* idx, const dsmoe_dims& d, int bm, const PermuteScratch& s, int32_t* offsets,
+                   int32_t* sorted_slot, int32_t* sorted_token, int32_t* slot_pos, int32_t* counts, const float* w,
+                   float* sorted_w, hipStream_t st) {
+  const int nb = (int)cdiv(d.T, RANK_TOKENS);
+  const int64_t N = (int64_t)d.T * d.k;
+  if (nb > 0) hipLaunchKernelGGL(rank_kernel, dim3(nb), dim3(64), 0, st, idx, d.T, d.k, d.E, s.blockhist, s.local_rank);
+  const size_t lds = sizeof(int32_t) * (3 * d.E + 2);
+  hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(256), lds, st, s.blockhist, nb, d.E, bm, s.blockbase, counts, offsets,
+                     s.sched, s.sched_count);
+  if (N > 0)
+    hipLaunchKernelGGL(scatter_kernel, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, st, idx, s.local_rank, s.blockbase,
+                       offsets, d.T, d.k, d.E, sorted_slot, sorted_token, slot_pos, w, sorted_w);
+  return check_launch("permute");
+}
+
+int launch_gather_rows(const void* x, const int32_t* rows, int64_t nrows, int D, int elem, void* dst, hipStream_t st) {
+  if (nrows == 0) return DSMOE_OK;
+  const int64_t row_bytes = (int64_t)D * elem;
+  if (row_bytes % 16 == 0 && ((uintptr_t)x % 16 == 0) && ((uintptr_t)dst % 16 == 0)) {
+    const int vpr = (int)(row_bytes / 16);
+    hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)cdiv(nrows * vpr, 256)), dim3(256), 0, st,
+                       static_cast<const uint4*>(x), rows, nrows, vpr, static_cast<uint4*>(dst));
+  } else if (elem == 2) {
+    hipLaunchKernelGGL(gather_rows_scalar_kernel<uint16_t>, dim3((unsigned)cdiv(nrows * D, 256)), dim3(256), 0, st,
+                       static_cast<const uint16_t*>(x), rows, nrows, D, static_cast<uint16_t*>(dst));
+  } else {
+    hipLaunchKernelGGL(gather_rows_scalar_kernel<float>, dim3((unsigned)cdiv(nrows * D, 256)), dim3(256), 0, st,
+                       static_cast<const float*>(x), rows, nrows, D, static_cast<float*>(dst));
+  }
+  return check_launch("gather_rows");
+}
+
+int launch_sched_from_offsets(const int64_t* offsets64, int E, int bm, int64_t rows, int32_t* offsets32, MTile* sched,
+                              int32_t* sched_count, hipStream_t st) {
+  hipLaunchKernelGGL(sched_from_offsets_kernel, dim3(1), dim3(256), sizeof(int32_t) * (E + 2), st, offsets64, E, bm,
+                     rows, offsets32, sched, sched_count);
+  return check_launch("sched_from_offsets");
+}
+
+}  // namespace dsmoe

@@ -1,0 +1,64 @@
+"""Compile the HIP sources in ../csrc into dsmoe/libdsmoe.so for gfx950.
+
+Run as ``python -m dsmoe.build`` (from deepseek-v3-lite_amd/) or through
+``__graft_entry__.build()``.  hipcc cross-compiles without a GPU.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent                      # deepseek-v3-lite_amd/
+REPO = ROOT.parent
+CSRC = ROOT / "csrc"
+INCLUDE = REPO / "include"
+BUILD = ROOT / "_build"
+LIB = PKG / "libdsmoe.so"
+
+ARCH = "gfx950"
+HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
+CFLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",
+    # No packed-FP32 instructions in device code.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{INCLUDE}", f"-I{CSRC}",
+]
+SOURCES = ["api.hip", "gate.hip", "permute.hip", "gemm.hip", "combine.hip"]
+
+
+def _compile(src: Path) -> Path:
+    obj = BUILD / (src.stem + ".o")
+    cmd = [HIPCC, *CFLAGS, "-c", str(src), "-o", str(obj)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src.name}:\n{r.stdout}\n{r.stderr}")
+    warn = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l and l.strip())
+    if warn:
+        print(f"[dsmoe.build] {src.name}:\n{warn}", file=sys.stderr)
+    return obj
+
+
+def build(verbose: bool = True) -> Path:
+    """Compile every source and link libdsmoe.so (always rebuilds)."""
+    BUILD.mkdir(exist_ok=True)
+    srcs = [CSRC / s for s in SOURCES]
+    with ThreadPoolExecutor(max_workers=min(len(srcs), 8)) as ex:
+        objs = list(ex.map(_compile, srcs))
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
+    tmp.replace(LIB)
+    if verbose:
+        print(f"[dsmoe.build] built {LIB} ({LIB.stat().st_size} bytes)")
+    return LIB
+
+
+if __name__ == "__main__":
+    build()

@@ -1,0 +1,288 @@
+"""Torch-facing operators over the dsmoe C ABI (device tensors only).
+
+* ``moe_layer``            whole-layer autograd op (DeepSeekMoE.forward, models/moe.py:74-103)
+* ``grouped_moe_dispatch`` the operator seam of models/moe_triton.py:504-525
+* ``gate_forward``, ``route_from_logits``, ``permute``, ``combine``:
+  the individual stages, exposed for tests and for callers that compose them.
+
+Every function requires ROCm device tensors and the built HIP library; there
+is no CPU path.
+"""
+from __future__ import annotations
+
+from typing import List, Optional, Sequence, Tuple
+
+import torch
+
+from . import _lib as L
+
+
+def _require_gpu(*ts: torch.Tensor) -> torch.device:
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError("dsmoe: tensors must be on a ROCm GPU (the layer has no CPU implementation)")
+    return ts[0].device
+
+
+def _c(t: torch.Tensor) -> torch.Tensor:
+    return t if t.is_contiguous() else t.contiguous()
+
+
+def _ws(nbytes: int, device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+
+
+# ---------------------------------------------------------------------------- stages
+def gate_forward(x: torch.Tensor, gate_w: torch.Tensor, gate_bias: torch.Tensor, k: int, route_scale: float = 1.0,
+                 want_logits: bool = False):
+    """AuxLossFreeGate.forward (models/moe.py:29-37), fp32 logits.
+
+    Returns dict: idx (T,k) int32, idx64 int64, weights fp32, weights_x (x dtype),
+    sel_scores fp32, counts (E,) int32, logits (T,E) fp32 or None."""
+    dev = _require_gpu(x, gate_w, gate_bias)
+    x = _c(x)
+    T, D = x.shape
+    E = gate_w.shape[0]
+    d = L.make_dims(T, D, E, k, 1, 0, 0, x.dtype, route_scale)
+    out = {
+        "idx": torch.empty(T, k, dtype=torch.int32, device=dev),
+        "idx64": torch.empty(T, k, dtype=torch.int64, device=dev),
+        "weights": torch.empty(T, k, dtype=torch.float32, device=dev),
+        "weights_x": torch.empty(T, k, dtype=x.dtype, device=dev),
+        "sel_scores": torch.empty(T, k, dtype=torch.float32, device=dev),
+        "counts": torch.empty(E, dtype=torch.int32, device=dev),
+        "logits": torch.empty(T, E, dtype=torch.float32, device=dev) if want_logits else None,
+    }
+    gw, gb = _c(gate_w.float()), _c(gate_bias.float())
+    rc = L.load().dsmoe_gate_fwd(L.ptr(x), L.ptr(gw), L.ptr(gb), d, L.ptr(out["logits"]), L.ptr(out["idx"]),
+                                 L.ptr(out["idx64"]), L.ptr(out["weights"]), L.ptr(out["weights_x"]),
+                                 L.ptr(out["sel_scores"]), L.ptr(out["counts"]), L.stream_ptr(dev))
+    L.check(rc, "dsmoe_gate_fwd")
+    return out
+
+
+def route_from_logits(logits: torch.Tensor, gate_bias: torch.Tensor, k: int, route_scale: float = 1.0,
+                      x_dtype: torch.dtype = torch.float32):
+    """models/moe.py:32-36 after F.linear, from given fp32 logits (T,E)."""
+    dev = _require_gpu(logits, gate_bias)
+    logits = _c(logits.float())
+    T, E = logits.shape
+    d = L.make_dims(T, 1, E, k, 1, 0, 0, x_dtype, route_scale)
+    out = {
+        "idx": torch.empty(T, k, dtype=torch.int32, device=dev),
+        "idx64": torch.empty(T, k, dtype=torch.int64, device=dev),
+        "weights": torch.empty(T, k, dtype=torch.float32, device=dev),
+        "weights_x": torch.empty(T, k, dtype=x_dtype, device=dev),
+        "sel_scores": torch.empty(T, k, dtype=torch.float32, device=dev),
+        "counts": torch.empty(E, dtype=torch.int32, device=dev),
+    }
+    gb = _c(gate_bias.float())
+    rc = L.load().dsmoe_route_from_logits(L.ptr(logits), L.ptr(gb), d, L.ptr(out["idx"]), L.ptr(out["idx64"]),
+                                          L.ptr(out["weights"]), L.ptr(out["weights_x"]), L.ptr(out["sel_scores"]),
+                                          L.ptr(out["counts"]), L.stream_ptr(dev))
+    L.check(rc, "dsmoe_route_from_logits")
+    return out
+
+
+def permute(idx: torch.Tensor, E: int, x: Optional[torch.Tensor] = None, weights: Optional[torch.Tensor] = None):
+    """Routing prep of models/moe.py:107-117 (+ optional row gather of :150)."""
+    dev = _require_gpu(idx)
+    idx = _c(idx.to(torch.int32))
+    T, k = idx.shape
+    N = T * k
+    D = x.shape[1] if x is not None else 1
+    dt = x.dtype if x is not None else torch.float32
+    d = L.make_dims(T, D, E, k, 1, 0, 0, dt, 1.0)
+    lib = L.load()
+    ws = _ws(lib.dsmoe_permute_workspace_size(d), dev)
+    out = {
+        "offsets": torch.empty(E + 1, dtype=torch.int32, device=dev),
+        "sorted_slot": torch.empty(N, dtype=torch.int32, device=dev),
+        "sorted_token": torch.empty(N, dtype=torch.int32, device=dev),
+        "slot_pos": torch.empty(N, dtype=torch.int32, device=dev),
+        "counts": torch.empty(E, dtype=torch.int32, device=dev),
+        "x_sorted": torch.empty(N, D, dtype=dt, device=dev) if x is not None else None,
+        "sorted_w": torch.empty(N, dtype=torch.float32, device=dev) if weights is not None else None,
+    }
+    xc = _c(x) if x is not None else None
+    wc = _c(weights.float()) if weights is not None else None
+    rc = lib.dsmoe_permute(L.ptr(idx), d, L.ptr(out["offsets"]), L.ptr(out["sorted_slot"]), L.ptr(out["sorted_token"]),
+                           L.ptr(out["slot_pos"]), L.ptr(out["counts"]), L.ptr(xc), L.ptr(out["x_sorted"]), L.ptr(wc),
+                           L.ptr(out["sorted_w"]), L.ptr(ws), ws.numel(), L.stream_ptr(dev))
+    L.check(rc, "dsmoe_permute")
+    return out
+
+
+def combine(o_slots: torch.Tensor, weights: torch.Tensor, idx: torch.Tensor, shared: Optional[torch.Tensor] = None):
+    """Weighted combine of models/moe.py:132 plus the shared add of :100-102.
+    o_slots (T*k, D) in slot order, weights (T,k) fp32, idx (T,k)."""
+    dev = _require_gpu(o_slots, weights, idx)
+    T, k = idx.shape
+    D = o_slots.shape[1]
+    d = L.make_dims(T, D, k, k, 1, 0, 0, o_slots.dtype, 1.0)  # the combine does not read E
+    y = torch.empty(T, D, dtype=o_slots.dtype, device=dev)
+    oc, wc, ic = _c(o_slots), _c(weights.float()), _c(idx.to(torch.int32))
+    sc = _c(shared) if shared is not None else None
+    rc = L.load().dsmoe_combine_fwd(L.ptr(oc), L.ptr(wc), L.ptr(ic), L.ptr(sc), d, L.ptr(y), L.stream_ptr(dev))
+    L.check(rc, "dsmoe_combine_fwd")
+    return y
+
+
+def update_bias_(counts: torch.Tensor, bias: torch.Tensor, speed: float, upper: float, lower: float) -> None:
+    """In-place f1 bias update on device (models/moe.py:21-27), no host sync."""
+    dev = _require_gpu(counts, bias)
+    if bias.dtype != torch.float32 or not bias.is_contiguous():
+        raise ValueError("dsmoe: gate bias must be a contiguous float32 tensor")
+    c = _c(counts.to(torch.int32))
+    rc = L.load().dsmoe_update_bias(L.ptr(c), L.ptr(bias), bias.numel(), float(speed), float(upper), float(lower),
+                                    L.stream_ptr(dev))
+    L.check(rc, "dsmoe_update_bias")
+
+
+# ---------------------------------------------------------------------------- whole layer
+class _MoELayerFn(torch.autograd.Function):
+    """Forward = dsmoe_moe_fwd, backward = dsmoe_moe_bwd.  The forward
+    workspace (routing, sorted order, pre-activations, expert outputs) is kept
+    on ctx for the backward."""
+
+    @staticmethod
+    def forward(ctx, meta, x, gate_w, gate_bias, *weights):
+        E, S, k, I, I_s, rs, training = meta
+        dev = x.device
+        T, D = x.shape
+        d = L.make_dims(T, D, E, k, I, S, I_s, x.dtype, rs)
+        lib = L.load()
+        ws = _ws(lib.dsmoe_moe_fwd_workspace_size(d, int(training)), dev)
+        y = torch.empty_like(x)
+        idx64 = torch.empty(T, k, dtype=torch.int64, device=dev)
+        wx = torch.empty(T, k, dtype=x.dtype, device=dev)
+        counts = torch.empty(E, dtype=torch.int32, device=dev)
+        w1, w2, w3 = weights[:E], weights[E:2 * E], weights[2 * E:3 * E]
+        s1, s2, s3 = weights[3 * E:3 * E + S], weights[3 * E + S:3 * E + 2 * S], weights[3 * E + 2 * S:]
+        p1, k1 = L.ptr_array(w1); p2, k2 = L.ptr_array(w2); p3, k3 = L.ptr_array(w3)
+        q1, j1 = L.ptr_array(s1); q2, j2 = L.ptr_array(s2); q3, j3 = L.ptr_array(s3)
+        rc = lib.dsmoe_moe_fwd(L.ptr(x), L.ptr(gate_w), L.ptr(gate_bias), p1, p2, p3, q1, q2, q3, d, int(training),
+                               L.ptr(y), L.ptr(idx64), L.ptr(wx), L.ptr(counts), None, L.ptr(ws), ws.numel(),
+                               L.stream_ptr(dev))
+        L.check(rc, "dsmoe_moe_fwd")
+        ctx.meta = meta
+        ctx.ws = ws
+        ctx.save_for_backward(x, gate_w, *weights)
+        ctx.mark_non_differentiable(idx64, wx, counts)
+        return y, idx64, wx, counts
+
+    @staticmethod
+    def backward(ctx, dy, *_unused):
+        E, S, k, I, I_s, rs, training = ctx.meta
+        if not training:
+            raise RuntimeError("dsmoe: forward ran without saving activations for backward")
+        x, gate_w, *weights = ctx.saved_tensors
+        dev = x.device
+        T, D = x.shape
+        d = L.make_dims(T, D, E, k, I, S, I_s, x.dtype, rs)
+        lib = L.load()
+        bws = _ws(lib.dsmoe_moe_bwd_workspace_size(d), dev)
+        dy = _c(dy)
+        dx = torch.empty_like(x)
+        dgw = torch.empty(E, D, dtype=torch.float32, device=dev)
+        dws = [torch.empty_like(w) for w in weights]
+        w1, w2, w3 = weights[:E], weights[E:2 * E], weights[2 * E:3 * E]
+        s1, s2, s3 = weights[3 * E:3 * E + S], weights[3 * E + S:3 * E + 2 * S], weights[3 * E + 2 * S:]
+        g1, g2, g3 = dws[:E], dws[E:2 * E], dws[2 * E:3 * E]
+        h1, h2, h3 = dws[3 * E:3 * E + S], dws[3 * E + S:3 * E + 2 * S], dws[3 * E + 2 * S:]
+        arrs = [L.ptr_array(a) for a in (w1, w2, w3, s1, s2, s3, g1, g2, g3, h1, h2, h3)]
+        rc = lib.dsmoe_moe_bwd(L.ptr(x), L.ptr(gate_w), *[a[0] for a in arrs[:6]], d, L.ptr(dy), L.ptr(ctx.ws),
+                               L.ptr(dx), L.ptr(dgw), *[a[0] for a in arrs[6:]], L.ptr(bws), bws.numel(),
+                               L.stream_ptr(dev))
+        L.check(rc, "dsmoe_moe_bwd")
+        return (None, dx, dgw, None, *dws)
+
+
+def moe_layer(x: torch.Tensor, gate_w: torch.Tensor, gate_bias: torch.Tensor, w1: Sequence[torch.Tensor],
+              w2: Sequence[torch.Tensor], w3: Sequence[torch.Tensor], sw1: Sequence[torch.Tensor] = (),
+              sw2: Sequence[torch.Tensor] = (), sw3: Sequence[torch.Tensor] = (), *, k: int,
+              route_scale: float = 1.0, training: Optional[bool] = None):
+    """One DeepSeekMoE layer on (T, D) tokens.  Expert weights must be in
+    x.dtype; gate_w and gate_bias are fp32.  Returns (y, idx64, weights_x, counts)."""
+    _require_gpu(x, gate_w, gate_bias, *w1)
+    E, S = len(w1), len(sw1)
+    I = w1[0].shape[0]
+    I_s = sw1[0].shape[0] if S else 0
+    if training is None:
+        training = torch.is_grad_enabled() and (x.requires_grad or gate_w.requires_grad or
+                                                any(w.requires_grad for w in (*w1, *w2, *w3, *sw1, *sw2, *sw3)))
+    for w in (*w1, *w2, *w3, *sw1, *sw2, *sw3):
+        if w.dtype != x.dtype:
+            raise ValueError(f"dsmoe: expert weight dtype {w.dtype} differs from activation dtype {x.dtype}")
+    meta = (E, S, int(k), int(I), int(I_s), float(route_scale), bool(training))
+    ws = [_c(w) for w in (*w1, *w2, *w3, *sw1, *sw2, *sw3)]
+    return _MoELayerFn.apply(meta, _c(x), _c(gate_w), _c(gate_bias), *ws)
+
+
+# ---------------------------------------------------------------------------- operator seam
+class _GroupedSwiGLUFn(torch.autograd.Function):
+    """_TritonGroupedMoeFunction's contract (models/moe_triton.py:390-501):
+    unweighted y_sorted; backward gives dx and fp32-accumulated dW in the
+    weight dtype."""
+
+    @staticmethod
+    def forward(ctx, x_sorted, w1, w2, w3, expert_offsets, sorted_w=None):
+        dev = x_sorted.device
+        N, D = x_sorted.shape
+        E, I, _ = w1.shape
+        d = L.make_dims(N, D, E, 1, I, 0, 0, x_sorted.dtype, 1.0)
+        lib = L.load()
+        ws = _ws(lib.dsmoe_grouped_swiglu_workspace_size(d), dev)
+        y = torch.empty(N, D, dtype=x_sorted.dtype, device=dev)
+        p1, k1 = L.ptr_array(list(w1.unbind(0))); p2, k2 = L.ptr_array(list(w2.unbind(0)))
+        p3, k3 = L.ptr_array(list(w3.unbind(0)))
+        off = _c(expert_offsets.to(torch.int64))
+        rc = lib.dsmoe_grouped_swiglu_fwd(L.ptr(x_sorted), p1, p2, p3, L.ptr(sorted_w), L.ptr(off), d, L.ptr(y),
+                                          L.ptr(ws), ws.numel(), L.stream_ptr(dev))
+        L.check(rc, "dsmoe_grouped_swiglu_fwd")
+        ctx.save_for_backward(x_sorted, w1, w2, w3, off)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x_sorted, w1, w2, w3, off = ctx.saved_tensors
+        dev = x_sorted.device
+        N, D = x_sorted.shape
+        E, I, _ = w1.shape
+        d = L.make_dims(N, D, E, 1, I, 0, 0, x_sorted.dtype, 1.0)
+        lib = L.load()
+        ws = _ws(lib.dsmoe_grouped_swiglu_workspace_size(d) * 4, dev)
+        dx = torch.empty_like(x_sorted)
+        dw1, dw2, dw3 = torch.empty_like(w1), torch.empty_like(w2), torch.empty_like(w3)
+        arrs = [L.ptr_array(list(t.unbind(0))) for t in (w1, w2, w3, dw1, dw2, dw3)]
+        rc = lib.dsmoe_grouped_swiglu_bwd(L.ptr(x_sorted), arrs[0][0], arrs[1][0], arrs[2][0], L.ptr(off),
+                                          L.ptr(_c(dy)), d, L.ptr(dx), arrs[3][0], arrs[4][0], arrs[5][0], L.ptr(ws),
+                                          ws.numel(), L.stream_ptr(dev))
+        L.check(rc, "dsmoe_grouped_swiglu_bwd")
+        return dx, dw1, dw2, dw3, None, None
+
+
+def grouped_moe_dispatch(x_sorted: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, w3: torch.Tensor,
+                         sorted_weights: torch.Tensor, expert_offsets: torch.Tensor) -> torch.Tensor:
+    """Drop-in for triton_grouped_moe_dispatch (models/moe_triton.py:504-525):
+    x_sorted (N,D), w1/w3 (E,I,D), w2 (E,D,I), sorted_weights (N,), expert_offsets
+    (E+1,) int64.  The gate weight is applied outside the autograd Function so
+    routing receives gradients, as in the reference; without grad it is fused
+    into the down-projection epilogue."""
+    _require_gpu(x_sorted, w1, w2, w3, expert_offsets)
+    if w1.dim() != 3 or w2.dim() != 3 or w3.dim() != 3:
+        raise ValueError("dsmoe: w1/w3 must be (E, I, D) and w2 (E, D, I)")
+    if x_sorted.dtype != w1.dtype or w1.dtype != w2.dtype or w2.dtype != w3.dtype:
+        raise ValueError("dsmoe: x_sorted and expert weights must share one dtype")
+    xs, a, b, c = _c(x_sorted), _c(w1), _c(w2), _c(w3)
+    needs_grad = torch.is_grad_enabled() and any(t.requires_grad for t in (x_sorted, w1, w2, w3, sorted_weights))
+    if not needs_grad:
+        sw = _c(sorted_weights.float())
+        return _GroupedSwiGLUFn.forward(_NoCtx(), xs, a, b, c, expert_offsets, sw)
+    out = _GroupedSwiGLUFn.apply(xs, a, b, c, expert_offsets)
+    return out * sorted_weights.unsqueeze(-1).to(out.dtype)
+
+
+class _NoCtx:
+    def save_for_backward(self, *a):
+        pass

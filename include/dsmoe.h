@@ -1,0 +1,181 @@
+/* dsmoe — MI355X (gfx950) DeepSeekMoE layer hot path behind a C ABI.
+ *
+ * Every function takes raw device pointers, plain sizes and a HIP stream
+ * (passed as void*), returns an int status (0 = ok, negative = error, see
+ * DSMOE_ERR_*) and never throws.  dsmoe_last_error() gives a thread-local
+ * message for the last failing call on the calling thread.
+ *
+ * Ownership: the caller allocates every buffer, including the workspace whose
+ * size the *_workspace_size() functions report.  The library allocates and
+ * frees no device memory and keeps no pointer past a call.  All work is
+ * enqueued on the given stream; no function synchronises the host.
+ *
+ * Layouts (row-major, as nn.Linear stores them):
+ *   x, y            (T, D)      activations, dtype DSMOE_F32 or DSMOE_BF16
+ *   gate_w          (E, D)      fp32          gate.weight
+ *   gate_bias       (E)         fp32          gate.bias (buffer)
+ *   w1[e], w3[e]    (I, D)      activation dtype   experts.{e}.w1/w3.weight
+ *   w2[e]           (D, I)      activation dtype   experts.{e}.w2.weight
+ *   sw1/sw3[s]      (I_s, D), sw2[s] (D, I_s)      shared_experts.{s}.*
+ * Per-expert weights are passed as HOST arrays of device pointers, so the
+ * module's separate per-expert tensors are used in place (no re-stacking).
+ *
+ * Routing conventions (identical in the CPU oracle):
+ *   scores  s = sigmoid(logit), evaluated in double and rounded once to fp32;
+ *   top-k   descending (s + bias); equal values ordered by lower expert id;
+ *   weights s_sel / max(sum_j s_sel, 1e-10) * route_scale, sum over j in order;
+ *   sorted order = stable (expert, token); slot id = t*k + j.
+ */
+#ifndef DSMOE_H
+#define DSMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DSMOE_OK 0
+#define DSMOE_ERR_INVALID (-1)     /* bad argument / shape (Python: ValueError) */
+#define DSMOE_ERR_UNSUPPORTED (-2) /* dtype or shape not supported (ValueError) */
+#define DSMOE_ERR_WORKSPACE (-3)   /* workspace too small (ValueError)          */
+#define DSMOE_ERR_HIP (-4)         /* HIP launch/runtime error (RuntimeError)   */
+
+#define DSMOE_F32 0
+#define DSMOE_BF16 1
+
+/* Shape of one DeepSeekMoE layer call.  Mirrors the config keys read by
+ * models/moe.py:11-16,56-61 (dim, n_routed_experts, n_activated_experts,
+ * moe_inter_dim, n_shared_experts, route_scale) plus T = flattened tokens and
+ * I_s = shared expert inter width (extension; equals I in the reference). */
+typedef struct dsmoe_dims {
+  int32_t T;      /* tokens (x.view(-1, D).size(0))          */
+  int32_t D;      /* dim                                     */
+  int32_t E;      /* n_routed_experts                        */
+  int32_t k;      /* n_activated_experts                     */
+  int32_t I;      /* moe_inter_dim                           */
+  int32_t S;      /* n_shared_experts                        */
+  int32_t I_s;    /* shared expert inter dim                 */
+  int32_t dtype;  /* DSMOE_F32 | DSMOE_BF16 (x, y, experts)  */
+  float route_scale;
+} dsmoe_dims;
+
+const char* dsmoe_last_error(void);
+int dsmoe_version(void);
+
+/* ---------------------------------------------------------------------------
+ * (a) Gate.  Replaces AuxLossFreeGate.forward, models/moe.py:29-37, with the
+ * logits computed in fp32 from x (bf16 upcast exactly) and the fp32 weight.
+ *   logits      (T,E) fp32, may be NULL
+ *   idx         (T,k) int32 expert ids (descending biased score)
+ *   idx64       (T,k) int64 copy for _last_indices, may be NULL
+ *   weights     (T,k) fp32 renormalised weights
+ *   weights_x   (T,k) weights cast to x dtype (_last_weights), may be NULL
+ *   sel_scores  (T,k) fp32 unbiased scores of the selected experts, may be NULL
+ *   counts      (E)   int32 per-expert histogram (== bincount(idx)), may be NULL
+ */
+int dsmoe_gate_fwd(const void* x, const float* gate_w, const float* gate_bias, const dsmoe_dims* dims,
+                   float* logits, int32_t* idx, int64_t* idx64, float* weights, void* weights_x,
+                   float* sel_scores, int32_t* counts, void* stream);
+
+/* Route from given fp32 logits (T,E): the part of models/moe.py:32-36 after
+ * F.linear, plus the bincount of models/moe.py:114.  Same outputs as above. */
+int dsmoe_route_from_logits(const float* logits, const float* gate_bias, const dsmoe_dims* dims, int32_t* idx,
+                            int64_t* idx64, float* weights, void* weights_x, float* sel_scores, int32_t* counts,
+                            void* stream);
+
+/* ---------------------------------------------------------------------------
+ * (b) Permute.  Replaces the routing prep of models/moe.py:107-117 (and the
+ * row gather flat[sorted_token_ids] of :127 / :150) without a host sync.
+ *   idx          (T,k) int32
+ *   offsets      (E+1) int32 (the (E+1) form of models/moe_triton.py:33)
+ *   sorted_slot  (N) int32   slot id t*k+j at each sorted position
+ *   sorted_token (N) int32   token id at each sorted position
+ *   slot_pos     (N) int32   sorted position of each slot (inverse)
+ *   counts       (E) int32, may be NULL
+ *   x, x_sorted  optional row gather x_sorted[p] = x[sorted_token[p]] (both NULL to skip)
+ *   sorted_w     optional (N) fp32 gather of weights (T,k) (both NULL to skip)
+ *   workspace    dsmoe_permute_workspace_size() bytes
+ */
+size_t dsmoe_permute_workspace_size(const dsmoe_dims* dims);
+int dsmoe_permute(const int32_t* idx, const dsmoe_dims* dims, int32_t* offsets, int32_t* sorted_slot,
+                  int32_t* sorted_token, int32_t* slot_pos, int32_t* counts, const void* x, void* x_sorted,
+                  const float* weights, float* sorted_w, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * (c) Grouped SwiGLU experts on expert-sorted rows.  Replaces the operator
+ * seam triton_grouped_moe_dispatch / _TritonGroupedMoeFunction.forward,
+ * models/moe_triton.py:390-436,504-525, with no dimension cap:
+ *   y_sorted[r] = (silu(x_sorted[r] W1[e]^T) * (x_sorted[r] W3[e]^T)) W2[e]^T * sorted_w[r]
+ * for offsets[e] <= r < offsets[e+1].  sorted_w may be NULL (unweighted, the
+ * Function's own output).  offsets (E+1) int64 on device; rows = offsets[E].
+ * dims: D, E, I and dtype are used; T is the number of sorted rows.
+ */
+size_t dsmoe_grouped_swiglu_workspace_size(const dsmoe_dims* dims);
+int dsmoe_grouped_swiglu_fwd(const void* x_sorted, const void* const* w1, const void* const* w2,
+                             const void* const* w3, const float* sorted_w, const int64_t* offsets,
+                             const dsmoe_dims* dims, void* y_sorted, void* workspace, size_t workspace_bytes,
+                             void* stream);
+
+/* Backward of the seam (models/moe_triton.py:438-501): given dy_sorted of the
+ * UNWEIGHTED output, writes dx_sorted and dW1/dW2/dW3 (per-expert device
+ * pointers, weight dtype, fp32 accumulation in ascending row order). */
+int dsmoe_grouped_swiglu_bwd(const void* x_sorted, const void* const* w1, const void* const* w2,
+                             const void* const* w3, const int64_t* offsets, const void* dy_sorted,
+                             const dsmoe_dims* dims, void* dx_sorted, void* const* dw1, void* const* dw2,
+                             void* const* dw3, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * (d) Combine.  Replaces the weighted out-of-place index_add of
+ * models/moe.py:132 and the shared add of :100-102:
+ *   y[t] = sum_{j in ascending expert id} weights[t,j] * o_slots[t*k+j] + shared[t]
+ * accumulated in fp32, rounded once.  shared may be NULL. */
+int dsmoe_combine_fwd(const void* o_slots, const float* weights, const int32_t* idx, const void* shared,
+                      const dsmoe_dims* dims, void* y, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Whole layer.  Replaces DeepSeekMoE.forward (models/moe.py:74-103) and its
+ * autograd backward.  The forward workspace holds everything the backward
+ * needs when training != 0, so the caller keeps it alive until backward.
+ *   outputs: y (T,D); idx64/weights_x/counts/logits as in dsmoe_gate_fwd.
+ */
+size_t dsmoe_moe_fwd_workspace_size(const dsmoe_dims* dims, int training);
+int dsmoe_moe_fwd(const void* x, const float* gate_w, const float* gate_bias, const void* const* w1,
+                  const void* const* w2, const void* const* w3, const void* const* sw1, const void* const* sw2,
+                  const void* const* sw3, const dsmoe_dims* dims, int training, void* y, int64_t* idx64,
+                  void* weights_x, int32_t* counts, float* logits, void* workspace, size_t workspace_bytes,
+                  void* stream);
+
+/* Backward of dsmoe_moe_fwd (training != 0).  dy (T,D).  Writes dx (T,D),
+ * dgate_w (E,D) fp32, and per-expert weight gradients (device pointers, the
+ * weight dtype): dw1[e], dw2[e], dw3[e], dsw1[s], dsw2[s], dsw3[s].  Unrouted
+ * experts receive zeros.  fwd_workspace is the forward call's workspace. */
+size_t dsmoe_moe_bwd_workspace_size(const dsmoe_dims* dims);
+int dsmoe_moe_bwd(const void* x, const float* gate_w, const void* const* w1, const void* const* w2,
+                  const void* const* w3, const void* const* sw1, const void* const* sw2, const void* const* sw3,
+                  const dsmoe_dims* dims, const void* dy, const void* fwd_workspace, void* dx, float* dgate_w,
+                  void* const* dw1, void* const* dw2, void* const* dw3, void* const* dsw1, void* const* dsw2,
+                  void* const* dsw3, void* workspace, size_t workspace_bytes, void* stream);
+
+/* f1: aux-loss-free bias update on device (models/moe.py:21-27,194-201).
+ * counts (E) int32 -> bias (E) fp32 updated in place by the +/-speed band rule. */
+int dsmoe_update_bias(const int32_t* counts, float* gate_bias, int E, float speed, float upper, float lower,
+                      void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Stage timing for measurement tools (no counterpart in the reference, which
+ * has no timing hooks).  While enabled, dsmoe_moe_fwd / dsmoe_moe_bwd record
+ * HIP events on their own stream at every stage boundary;
+ * dsmoe_timing_read() waits for the recorded events and returns, per stage,
+ * the summed milliseconds over all calls since the last enable.  Stage ids and
+ * names: dsmoe_timing_stage_name(i) for i < dsmoe_timing_read's return value. */
+int dsmoe_timing_enable(int on);
+int dsmoe_timing_read(double* stage_ms, int max_stages, int* n_calls);
+const char* dsmoe_timing_stage_name(int stage);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSMOE_H */

@@ -1,0 +1,78 @@
+"""The C ABI library loads and exports every function include/dsmoe.h declares
+(CPU only: no call here reaches the GPU)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "dsmoe.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dsmoe_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    import dsmoe._lib as L
+    if not L.LIB_PATH.exists():
+        from dsmoe import build
+        build.build(verbose=False)
+    return L.load()
+
+
+def test_header_declares_the_boundary():
+    names = _declared()
+    for must in ("dsmoe_gate_fwd", "dsmoe_route_from_logits", "dsmoe_permute", "dsmoe_grouped_swiglu_fwd",
+                 "dsmoe_grouped_swiglu_bwd", "dsmoe_combine_fwd", "dsmoe_moe_fwd", "dsmoe_moe_bwd",
+                 "dsmoe_update_bias", "dsmoe_last_error"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    missing = [n for n in _declared() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_python_binding_covers_every_declared_symbol():
+    import dsmoe._lib as L
+    assert set(L.exported_symbols()) == set(_declared())
+
+
+def test_dims_struct_matches_header_layout():
+    import dsmoe._lib as L
+    assert ctypes.sizeof(L.Dims) == 9 * 4
+    assert [f[0] for f in L.Dims._fields_] == ["T", "D", "E", "k", "I", "S", "I_s", "dtype", "route_scale"]
+
+
+def test_validation_errors_without_launch(lib):
+    import dsmoe._lib as L
+    d = L.Dims(16, 64, 4, 5, 32, 1, 32, L.DSMOE_F32, 1.0)          # k > E
+    assert lib.dsmoe_moe_fwd_workspace_size(ctypes.byref(d), 0) == 0
+    rc = lib.dsmoe_gate_fwd(None, None, None, ctypes.byref(d), None, None, None, None, None, None, None, None)
+    assert rc == L.DSMOE_ERR_INVALID
+    assert b"n_activated_experts" in lib.dsmoe_last_error()
+    d = L.Dims(16, 64, 4, 2, 32, 1, 32, 7, 1.0)                      # bad dtype
+    rc = lib.dsmoe_gate_fwd(None, None, None, ctypes.byref(d), None, None, None, None, None, None, None, None)
+    assert rc == L.DSMOE_ERR_UNSUPPORTED
+    d = L.Dims(16, 64, 4, 2, 32, 1, 32, L.DSMOE_BF16, 1.0)
+    rc = lib.dsmoe_gate_fwd(None, None, None, ctypes.byref(d), None, None, None, None, None, None, None, None)
+    assert rc == L.DSMOE_ERR_INVALID and b"NULL" in lib.dsmoe_last_error()
+    with pytest.raises(ValueError, match="NULL"):
+        L.check(rc, "dsmoe_gate_fwd")
+
+
+def test_workspace_sizes_are_consistent(lib):
+    import dsmoe._lib as L
+    d = L.Dims(8192, 2048, 64, 6, 1408, 2, 1408, L.DSMOE_BF16, 1.0)
+    inf = lib.dsmoe_moe_fwd_workspace_size(ctypes.byref(d), 0)
+    trn = lib.dsmoe_moe_fwd_workspace_size(ctypes.byref(d), 1)
+    N = 8192 * 6
+    # at least h (N x I), o_slots (N x D), shared h and out; training adds g and u
+    assert inf >= 2 * (N * 1408 + N * 2048 + 8192 * 2816 + 8192 * 2048)
+    assert trn - inf >= 2 * 2 * (N * 1408 + 8192 * 2816)
+    assert lib.dsmoe_permute_workspace_size(ctypes.byref(d)) > 0
