@@ -111,6 +111,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-mb", type=int, default=0,
+                    help="instead of the layer, run --steps device copies of this many MiB (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -122,6 +124,15 @@ def main() -> int:
     from dsmoe import moe_layer
 
     dev = torch.device("cuda:0")
+    if args.copy_mb:
+        n = args.copy_mb * (1 << 20)
+        src = torch.ones(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_per_launch": n, "launches": args.steps}), flush=True)
+        return 0
     cfg = CONFIGS[args.config]
     T, D, E, I, k, S, I_s, dt, bias_kind = cfg
     log(f"[bench] config {args.config}: T={T} D={D} E={E} I={I} k={k} S={S}x{I_s} {dt}")

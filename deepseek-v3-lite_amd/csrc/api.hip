@@ -1,6 +1,8 @@
 // extern "C" entry points of libdsmoe.so (declared in include/dsmoe.h).
 #include <cstring>
+#include <initializer_list>
 #include <mutex>
+#include <utility>
 #include <string>
 #include <vector>
 
@@ -25,26 +27,38 @@ int check_launch(const char* what) {
 }
 
 // ---------------------------------------------------------------- pointer tables
+constexpr int PTR_CHUNK = 192;  // pointers per upload launch (kernel argument space)
+
 struct PtrChunk {
-  const void* p[64];
+  const void* p[PTR_CHUNK];
   int32_t n;
   int32_t off;
 };
 
 __global__ void set_ptrs_kernel(PtrChunk c, const void** dst) {
-  const int i = threadIdx.x;
-  if (i < c.n) dst[c.off + i] = c.p[i];
+  for (int i = threadIdx.x; i < c.n; i += blockDim.x) dst[c.off + i] = c.p[i];
 }
 
-// Copies `n` host-held device pointers into the device table at dst[off..].
-static int upload_ptrs(const void* const* host, int n, const void** dst, int off, hipStream_t st) {
-  for (int b = 0; b < n; b += 64) {
-    PtrChunk c;
-    c.n = n - b < 64 ? n - b : 64;
-    c.off = off + b;
-    for (int i = 0; i < c.n; ++i) c.p[i] = host[b + i];
-    hipLaunchKernelGGL(set_ptrs_kernel, dim3(1), dim3(64), 0, st, c, dst);
+// Copies the concatenation of `lists` (host arrays of device pointers) into
+// the device table dst[0..], in as few launches as the argument space allows.
+static int upload_ptr_lists(std::initializer_list<std::pair<const void* const*, int>> lists, const void** dst,
+                            hipStream_t st) {
+  PtrChunk c;
+  c.n = 0;
+  c.off = 0;
+  int pos = 0;
+  for (const auto& l : lists) {
+    for (int i = 0; i < l.second; ++i) {
+      c.p[c.n++] = l.first[i];
+      ++pos;
+      if (c.n == PTR_CHUNK) {
+        hipLaunchKernelGGL(set_ptrs_kernel, dim3(1), dim3(256), 0, st, c, dst);
+        c.off = pos;
+        c.n = 0;
+      }
+    }
   }
+  if (c.n) hipLaunchKernelGGL(set_ptrs_kernel, dim3(1), dim3(256), 0, st, c, dst);
   return check_launch("upload_ptrs");
 }
 
@@ -279,23 +293,26 @@ int dsmoe_grouped_swiglu_fwd(const void* x_sorted, const void* const* w1, const 
   int32_t* cnt;
   void* h;
   grouped_ws(d, workspace, &ptrs, &off32, &sched, &cnt, &h);
-  int rc = upload_ptrs(w1, d.E, ptrs, 0, st);
-  if (!rc) rc = upload_ptrs(w3, d.E, ptrs, d.E, st);
-  if (!rc) rc = upload_ptrs(w2, d.E, ptrs, 2 * d.E, st);
-  if (!rc) rc = launch_sched_from_offsets(offsets, d.E, TILE_M, d.T, off32, sched, cnt, st);
+  int rc = upload_ptr_lists({{w1, d.E}, {w3, d.E}, {w2, d.E}}, ptrs, st);
   if (rc) return rc;
   const bool mf = all_aligned16(w1, d.E) && all_aligned16(w2, d.E) && all_aligned16(w3, d.E);
   GemmDesc g = desc_zero();
-  g.sched = sched; g.sched_count = cnt; g.m_tiles_bound = (int32_t)sched_bound(d.T, d.E, TILE_M);
-  g.A = x_sorted; g.lda = d.D; g.B0 = ptrs; g.B1 = ptrs + d.E; g.ldb = d.D; g.kseg = d.D;
+  g.A = x_sorted; g.lda = d.D; g.a_rows = d.T; g.B0 = ptrs; g.B1 = ptrs + d.E; g.ldb = d.D; g.kseg = d.D;
   g.N = d.I; g.K = d.D; g.C = h; g.ldc = d.I;
-  rc = launch_grouped_gemm(g, EPI_SWIGLU, d.dtype, nullptr, mf, st);
-  if (rc) return rc;
   GemmDesc g2 = desc_zero();
-  g2.sched = sched; g2.sched_count = cnt; g2.m_tiles_bound = g.m_tiles_bound;
-  g2.A = h; g2.lda = d.I; g2.B0 = ptrs + 2 * d.E; g2.ldb = d.I; g2.kseg = d.I;
+  g2.A = h; g2.lda = d.I; g2.a_rows = d.T; g2.B0 = ptrs + 2 * d.E; g2.ldb = d.I; g2.kseg = d.I;
   g2.N = d.D; g2.K = d.I; g2.C = y_sorted; g2.ldc = d.D;
-  return launch_grouped_gemm(g2, EPI_STORE, d.dtype, sorted_w, mf, st);
+  const bool mfr = gemm_mfma_eligible(g, d.dtype, mf) && gemm_mfma_eligible(g2, d.dtype, mf);
+  const int bm = gemm_tile_m(mfr);
+  rc = launch_sched_from_offsets(offsets, d.E, bm, d.T, off32, sched, cnt, st);
+  if (rc) return rc;
+  g.sched = g2.sched = sched;
+  g.sched_count = g2.sched_count = cnt;
+  g.m_tiles_bound = g2.m_tiles_bound = (int32_t)sched_bound(d.T, d.E, bm);
+  g.bm = g2.bm = bm;
+  rc = launch_grouped_gemm(g, EPI_SWIGLU, d.dtype, nullptr, mfr, st);
+  if (rc) return rc;
+  return launch_grouped_gemm(g2, EPI_STORE, d.dtype, sorted_w, mfr, st);
 }
 
 int dsmoe_grouped_swiglu_bwd(const void*, const void* const*, const void* const*, const void* const*, const int64_t*,
@@ -335,12 +352,7 @@ int dsmoe_moe_fwd(const void* x, const float* gate_w, const float* gate_bias, co
   StageTimer tm(st);
 
   tm.begin(ST_TABLES);
-  rc = upload_ptrs(w1, d.E, L.ptrs, 0, st);
-  if (!rc) rc = upload_ptrs(w3, d.E, L.ptrs, d.E, st);
-  if (!rc) rc = upload_ptrs(w2, d.E, L.ptrs, 2 * d.E, st);
-  if (!rc && d.S) rc = upload_ptrs(sw1, d.S, L.ptrs, 3 * d.E, st);
-  if (!rc && d.S) rc = upload_ptrs(sw3, d.S, L.ptrs, 3 * d.E + d.S, st);
-  if (!rc && d.S) rc = upload_ptrs(sw2, d.S, L.ptrs, 3 * d.E + 2 * d.S, st);
+  rc = upload_ptr_lists({{w1, d.E}, {w3, d.E}, {w2, d.E}, {sw1, d.S}, {sw3, d.S}, {sw2, d.S}}, L.ptrs, st);
   if (rc) return rc;
   const bool mf = all_aligned16(w1, d.E) && all_aligned16(w2, d.E) && all_aligned16(w3, d.E) &&
                   (d.S == 0 || (all_aligned16(sw1, d.S) && all_aligned16(sw2, d.S) && all_aligned16(sw3, d.S)));
@@ -352,52 +364,58 @@ int dsmoe_moe_fwd(const void* x, const float* gate_w, const float* gate_bias, co
   rc = launch_gate(x, nullptr, gate_w, gate_bias, d, go, st);
   tm.end();
   if (rc) return rc;
+  // GEMM descriptors; the routed schedule height follows the kernel choice
+  GemmDesc g1 = desc_zero();
+  g1.A = x; g1.lda = d.D; g1.a_rows = d.T; g1.a_map = L.sorted_token;
+  g1.B0 = L.ptrs; g1.B1 = L.ptrs + d.E; g1.ldb = d.D; g1.kseg = d.D;
+  g1.N = d.I; g1.K = d.D; g1.C = L.h; g1.ldc = d.I; g1.Gs = L.g; g1.Us = L.u;
+  GemmDesc g2 = desc_zero();
+  g2.A = L.h; g2.lda = d.I; g2.a_rows = N; g2.B0 = L.ptrs + 2 * d.E; g2.ldb = d.I; g2.kseg = d.I;
+  g2.N = d.D; g2.K = d.I; g2.C = L.o_slots; g2.ldc = d.D; g2.c_map = L.sorted_slot;
+  const bool mfr = gemm_mfma_eligible(g1, d.dtype, mf) && gemm_mfma_eligible(g2, d.dtype, mf);
+  const int bm = gemm_tile_m(mfr);
   // (b) permute (counts come from the scan: exact bincount, no atomics)
   tm.begin(ST_PERMUTE);
-  rc = launch_permute(L.idx, d, TILE_M, L.ps, L.offsets, L.sorted_slot, L.sorted_token, L.slot_pos, counts, nullptr,
+  rc = launch_permute(L.idx, d, bm, L.ps, L.offsets, L.sorted_slot, L.sorted_token, L.slot_pos, counts, nullptr,
                       nullptr, st);
   tm.end();
   if (rc) return rc;
-  const int32_t mbound = (int32_t)sched_bound(N, d.E, TILE_M);
+  g1.sched = g2.sched = L.ps.sched;
+  g1.sched_count = g2.sched_count = L.ps.sched_count;
+  g1.m_tiles_bound = g2.m_tiles_bound = (int32_t)sched_bound(N, d.E, bm);
+  g1.bm = g2.bm = bm;
   // (c) routed gate/up + SwiGLU, rows gathered from x through sorted_token
-  GemmDesc g1 = desc_zero();
-  g1.sched = L.ps.sched; g1.sched_count = L.ps.sched_count; g1.m_tiles_bound = mbound;
-  g1.A = x; g1.lda = d.D; g1.a_map = L.sorted_token;
-  g1.B0 = L.ptrs; g1.B1 = L.ptrs + d.E; g1.ldb = d.D; g1.kseg = d.D;
-  g1.N = d.I; g1.K = d.D; g1.C = L.h; g1.ldc = d.I; g1.Gs = L.g; g1.Us = L.u;
   tm.begin(ST_GEMM1);
-  rc = launch_grouped_gemm(g1, EPI_SWIGLU, d.dtype, nullptr, mf, st);
+  rc = launch_grouped_gemm(g1, EPI_SWIGLU, d.dtype, nullptr, mfr, st);
   tm.end();
   if (rc) return rc;
   // shared experts: S dense groups over all tokens, h_shared = [h_0 | h_1 | ...]
   if (d.S) {
     GemmDesc s1 = desc_zero();
     s1.dense_rows = d.T; s1.groups = d.S;
-    s1.A = x; s1.lda = d.D;
+    s1.A = x; s1.lda = d.D; s1.a_rows = d.T;
     s1.B0 = L.ptrs + 3 * d.E; s1.B1 = L.ptrs + 3 * d.E + d.S; s1.ldb = d.D; s1.kseg = d.D;
     s1.N = d.I_s; s1.K = d.D; s1.C = L.hs; s1.ldc = (int64_t)d.S * d.I_s; s1.c_group_col = d.I_s;
     s1.Gs = L.gs; s1.Us = L.us;
+    s1.bm = gemm_tile_m(gemm_mfma_eligible(s1, d.dtype, mf));
     tm.begin(ST_GEMM1_SHARED);
     rc = launch_grouped_gemm(s1, EPI_SWIGLU, d.dtype, nullptr, mf, st);
     tm.end();
     if (rc) return rc;
   }
   // routed down projection, rows written back in slot order (t*k + j)
-  GemmDesc g2 = desc_zero();
-  g2.sched = L.ps.sched; g2.sched_count = L.ps.sched_count; g2.m_tiles_bound = mbound;
-  g2.A = L.h; g2.lda = d.I; g2.B0 = L.ptrs + 2 * d.E; g2.ldb = d.I; g2.kseg = d.I;
-  g2.N = d.D; g2.K = d.I; g2.C = L.o_slots; g2.ldc = d.D; g2.c_map = L.sorted_slot;
   tm.begin(ST_GEMM2);
-  rc = launch_grouped_gemm(g2, EPI_STORE, d.dtype, nullptr, mf, st);
+  rc = launch_grouped_gemm(g2, EPI_STORE, d.dtype, nullptr, mfr, st);
   tm.end();
   if (rc) return rc;
   // shared down projection: one GEMM with K = S * I_s summing all shared experts
   if (d.S) {
     GemmDesc s2 = desc_zero();
     s2.dense_rows = d.T; s2.groups = 1;
-    s2.A = L.hs; s2.lda = (int64_t)d.S * d.I_s;
+    s2.A = L.hs; s2.lda = (int64_t)d.S * d.I_s; s2.a_rows = d.T;
     s2.B0 = L.ptrs + 3 * d.E + 2 * d.S; s2.ldb = d.I_s; s2.kseg = d.I_s; s2.nseg = d.S;
     s2.N = d.D; s2.K = d.S * d.I_s; s2.C = L.shared_out; s2.ldc = d.D;
+    s2.bm = gemm_tile_m(gemm_mfma_eligible(s2, d.dtype, mf));
     tm.begin(ST_GEMM2_SHARED);
     rc = launch_grouped_gemm(s2, EPI_STORE, d.dtype, nullptr, mf, st);
     tm.end();

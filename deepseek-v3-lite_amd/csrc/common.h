@@ -98,9 +98,12 @@ struct GemmDesc {
   int32_t dense_rows;         // dense: rows per group
   int32_t groups;             // number of groups (dense)
   int32_t m_tiles_bound;      // host upper bound of M tiles (grid sizing)
+  int32_t bm;                 // rows per M tile (must equal the schedule's tile height)
+  int32_t raster;             // block -> tile order (0: XCD-chunked, 1: linear, 2: XCD-chunked N-major groups)
   // A operand: rows of length K (K contiguous)
   const void* A;
   int64_t lda;
+  int64_t a_rows;             // rows addressable through A (bounds the offset width)
   const int32_t* a_map;       // row -> A row, nullptr = identity
   // B operand(s): per group and K segment: B0[g * nseg + s] points at an (N x kseg) row-major block
   const void* const* B0;
@@ -118,7 +121,7 @@ struct GemmDesc {
   void* Us;
 };
 
-constexpr int TILE_M = 128;   // M tile of every grouped GEMM and of the permute schedule
+constexpr int TILE_M = 128;   // M tile of the SIMT fallback GEMM
 constexpr int MAX_TOPK = 16;
 
 struct GateOut {
@@ -151,6 +154,13 @@ int launch_permute(const int32_t* idx, const dsmoe_dims& d, int bm, const Permut
 int launch_gather_rows(const void* x, const int32_t* rows, int64_t nrows, int D, int elem, void* dst, hipStream_t st);
 int launch_sched_from_offsets(const int64_t* offsets64, int E, int bm, int64_t rows, int32_t* offsets32, MTile* sched,
                               int32_t* sched_count, hipStream_t st);
+// Whether launch_grouped_gemm will take the MFMA kernel for this descriptor,
+// and the M-tile height of that choice; the routed schedule (and desc.bm) must
+// be built with the same height.
+bool gemm_mfma_eligible(const GemmDesc& g, int dtype, bool allow_mfma);
+int gemm_tile_m(bool mfma);
+bool gemm_dl_ok(const GemmDesc& g, int64_t a_rows);
+int launch_gemm_dl(const GemmDesc& g, int epi, const float* row_scale, hipStream_t st);
 int launch_grouped_gemm(const GemmDesc& g, int epi, int dtype, const float* row_scale, bool allow_mfma,
                         hipStream_t st);
 int launch_combine(const void* o_slots, const float* w, const int32_t* idx, const void* shared, const dsmoe_dims& d,

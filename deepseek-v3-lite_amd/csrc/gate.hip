@@ -1,38 +1,262 @@
 // (a) Fused gate: fp32 logits = x . W_gate^T, sigmoid, +bias, top-k,
 // renormalisation, per-expert histogram.  Restates models/moe.py:29-37 and
 // the bincount of models/moe.py:114 (see dsmoe.h for the tie rule).
+//
+// Logits.  bf16 x: MFMA.  Each fp32 gate weight is split exactly into three
+// bf16 parts by truncation (w = hi + mid + lo: hi keeps the top 8 significand
+// bits, mid the next 8, lo the last 8), so x.w = x.hi + x.mid + x.lo with
+// every product exact; the MFMA accumulates in fp32.  A block takes 32 tokens
+// and all experts; its 4 waves split D in quarters and the four partial sums
+// are added in a fixed order, so the result is deterministic.  fp32 x: SIMT
+// FMA tiles.
+//
+// Routing.  One wave per token, one lane per expert (E <= 64; E <= 256 with
+// several experts per lane): sigmoid in double rounded once, + bias, then k
+// rounds of a wave-wide arg-max ordered by (value desc, expert id asc).
 #include "common.h"
 
 namespace dsmoe {
 
-constexpr int GATE_THREADS = 256;
-constexpr int GATE_KC = 32;   // K chunk staged through LDS
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 g_bf16x8_t;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float g_f32x16_t;
+typedef float g_f32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int g_u32x4_t __attribute__((ext_vector_type(4)));
 
-// Top-k over one token's row of scores held in LDS.  Ties -> lower expert id.
-__device__ __forceinline__ void topk_row(const float* sc, const float* bias_s, int E, int k, float* topv, int* topi) {
-  int n = 0;
-  for (int e = 0; e < E; ++e) {
-    float b = sc[e] + bias_s[e];
-    int pos = n;
-    while (pos > 0 && topv[pos - 1] < b) --pos;
-    if (pos >= k) continue;
-    int last = n < k ? n : k - 1;
-    for (int q = last; q > pos; --q) {
-      topv[q] = topv[q - 1];
-      topi[q] = topi[q - 1];
+constexpr int GATE_THREADS = 256;
+constexpr int GATE_KC = 32;        // SIMT: K chunk staged through LDS
+constexpr int GM_TOK = 32;         // MFMA: tokens per block
+constexpr int MAX_EPL = 4;         // experts per lane in routing (E <= 256)
+
+// ------------------------------------------------------------------ routing
+// Routes tokens [t0, t0 + ntok) whose fp32 logits sit in LDS rows lg[t*ldl].
+// Wave w takes tokens w, w+nw, ...; lane l holds expert l (E <= 64) or
+// experts l, l+64, ... (E <= 256).
+//
+// Selection by rank: every expert's biased score goes to a per-wave LDS row;
+// each lane counts the experts that beat its own under the order (value
+// desc, id asc).  Rank < k selects the expert and is its output slot j, so
+// the result equals k rounds of arg-max with that tie rule.  The renormalising
+// sum then runs over slots j = 0..k-1 in order, as in the oracle.
+// wscr: per-wave LDS scratch of 64 * MAX_EPL + MAX_TOPK floats.
+//
+// Lanes of one wave exchange values through LDS: a wave's LDS operations
+// complete in issue order, so waiting for this wave's LDS counter (and a
+// compiler barrier) is enough.  A memory fence would also wait for the
+// token's global output stores.
+__device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+template <int EPL>  // experts per lane: 1 for E <= 64, MAX_EPL otherwise
+__device__ __forceinline__ void route_tokens_t(const float* lg, int ldl, int ntok, int t0, const float* bias_s, int E,
+                                               int k, float route_scale, int xdtype, const GateOut& out, int* hist,
+                                               float* wscr_all) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nw = blockDim.x >> 6;
+  float* wb = wscr_all + wave * (64 * MAX_EPL + MAX_TOPK);   // biased scores [E]
+  float* ws = wb + 64 * MAX_EPL;                              // selected scores by slot [k]
+  const int e4 = (E + 3) & ~3;
+  for (int t = wave; t < ntok; t += nw) {
+    const float* row = lg + t * ldl;
+    float sv[EPL], bv[EPL];
+#pragma unroll
+    for (int q = 0; q < EPL; ++q) {
+      const int e = lane + 64 * q;
+      sv[q] = 0.0f;
+      bv[q] = -INFINITY;
+      if (e < E) {
+        sv[q] = route_sigmoid(row[e]);
+        bv[q] = sv[q] + bias_s[e];
+      }
+      if (e < e4) wb[e] = bv[q];
     }
-    topv[pos] = b;
-    topi[pos] = e;
-    if (n < k) ++n;
+    wave_lds_sync();
+    int rank[EPL];
+#pragma unroll
+    for (int q = 0; q < EPL; ++q) rank[q] = 0;
+    for (int c = 0; c < e4; c += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(wb + c);
+      const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int q = 0; q < EPL; ++q) {
+          const int e = lane + 64 * q;
+          // branch-free: (value desc, id asc) order
+          rank[q] += (int)(vv[i] > bv[q]) | ((int)(vv[i] == bv[q]) & (int)(c + i < e));
+        }
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < EPL; ++q) {
+      const int e = lane + 64 * q;
+      if (e < E && rank[q] < k) ws[rank[q]] = sv[q];
+    }
+    wave_lds_sync();
+    float ssum = 0.0f;
+    for (int j = 0; j < k; ++j) ssum += ws[j];
+    const float den = ssum < 1e-10f ? 1e-10f : ssum;
+    const int64_t o = (int64_t)(t0 + t) * k;
+#pragma unroll
+    for (int q = 0; q < EPL; ++q) {
+      const int e = lane + 64 * q;
+      if (e < E && rank[q] < k) {
+        const int j = rank[q];
+        const float w = sv[q] / den * route_scale;
+        out.idx[o + j] = e;
+        if (out.idx64) out.idx64[o + j] = e;
+        out.weights[o + j] = w;
+        if (out.weights_x) {
+          if (xdtype == DSMOE_BF16)
+            static_cast<bf16_t*>(out.weights_x)[o + j] = f2bf(w);
+          else
+            static_cast<float*>(out.weights_x)[o + j] = w;
+        }
+        if (out.sel_scores) out.sel_scores[o + j] = sv[q];
+        if (hist) atomicAdd(&hist[e], 1);
+      }
+    }
+    // the next token reuses wb/ws: make sure every lane finished reading them
+    wave_lds_sync();
   }
 }
 
-// LDS layout (floats): xs[KC][TB+4] | ws[KC][EC+4] | lg[TB][E+1] | bias[E] | hist[E] (int)
+__device__ __forceinline__ void route_tokens(const float* lg, int ldl, int ntok, int t0, const float* bias_s, int E,
+                                             int k, float route_scale, int xdtype, const GateOut& out, int* hist,
+                                             float* wscr_all) {
+  if (E <= 64)
+    route_tokens_t<1>(lg, ldl, ntok, t0, bias_s, E, k, route_scale, xdtype, out, hist, wscr_all);
+  else
+    route_tokens_t<MAX_EPL>(lg, ldl, ntok, t0, bias_s, E, k, route_scale, xdtype, out, hist, wscr_all);
+}
+
+__device__ __forceinline__ void flush_hist(const int* hist, int E, int32_t* counts) {
+  if (!counts) return;
+  for (int e = threadIdx.x; e < E; e += blockDim.x)
+    if (hist[e]) atomicAdd(&counts[e], hist[e]);
+}
+
+// ------------------------------------------------------------------ MFMA logits (bf16 x)
+// Splits 8 consecutive fp32 weights into three bf16x8 vectors whose sum is exact.
+__device__ __forceinline__ void split3(const g_f32x4_t& a, const g_f32x4_t& b, g_bf16x8_t& hi, g_bf16x8_t& mid,
+                                       g_bf16x8_t& lo) {
+  const float w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  unsigned short h[8], m[8], l[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t wb = __float_as_uint(w[i]);
+    const float fh = __uint_as_float(wb & 0xffff0000u);
+    const float r1 = w[i] - fh;                       // exact
+    const uint32_t rb = __float_as_uint(r1);
+    const float fm = __uint_as_float(rb & 0xffff0000u);
+    const float r2 = r1 - fm;                         // exact, <= 8 significant bits
+    h[i] = (unsigned short)(wb >> 16);
+    m[i] = (unsigned short)(rb >> 16);
+    l[i] = (unsigned short)(__float_as_uint(r2) >> 16);
+  }
+  __builtin_memcpy(&hi, h, 16);
+  __builtin_memcpy(&mid, m, 16);
+  __builtin_memcpy(&lo, l, 16);
+}
+
+constexpr int ROUTE_SCR = GATE_THREADS / 64 * (64 * MAX_EPL + MAX_TOPK);  // floats of routing scratch
+
+// LDS: part[4][GM_TOK][EP+1] fp32 partial logits (reused for the reduced
+// logits), bias[E], hist[E], routing scratch.
+template <int NT>
+__global__ __launch_bounds__(GATE_THREADS) void gate_mfma_kernel(const bf16_t* __restrict__ x,
+                                                                 const float* __restrict__ gw,
+                                                                 const float* __restrict__ bias, int T, int D, int E,
+                                                                 int k, float route_scale, GateOut out) {
+  constexpr int EP = NT * 32;
+  constexpr int LDP = EP + 1;
+  extern __shared__ float gsm[];
+  float* part = gsm;                                   // [4][GM_TOK][LDP]
+  float* bias_s = part + 4 * GM_TOK * LDP;
+  int* hist = reinterpret_cast<int*>(bias_s + E);
+  // 16-byte aligned offset from the LDS base (pointer arithmetic keeps the
+  // accesses in the LDS address space)
+  float* rscr = gsm + ((4 * GM_TOK * LDP + 2 * E + 3) & ~3);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int t0 = blockIdx.x * GM_TOK;
+  for (int e = tid; e < E; e += GATE_THREADS) {
+    bias_s[e] = bias[e];
+    hist[e] = 0;
+  }
+  const int kq = D / 4;
+  const int kbeg = wave * kq;
+  const int m = lane & 31;
+  const int row = min(t0 + m, T - 1);
+  const bf16_t* xr = x + (int64_t)row * D + (lane >> 5) * 8;
+  const float* wr[NT];
+#pragma unroll
+  for (int ni = 0; ni < NT; ++ni) wr[ni] = gw + (int64_t)min(ni * 32 + m, E - 1) * D + (lane >> 5) * 8;
+
+  g_f32x16_t acc[NT];
+#pragma unroll
+  for (int ni = 0; ni < NT; ++ni)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[ni][r] = 0.0f;
+
+  // K loop in chunks of PF steps: the loads of a whole chunk are issued before
+  // its MFMAs, so PF global round trips overlap (the loop is latency-bound
+  // otherwise: one block streams all of W_gate).
+  constexpr int PF = (NT <= 2) ? 8 : 2;
+  const int kend = kbeg + kq;
+  for (int k0 = kbeg; k0 < kend; k0 += 16 * PF) {
+    g_bf16x8_t a[PF];
+    g_f32x4_t w0[PF][NT], w1[PF][NT];
+#pragma unroll
+    for (int p = 0; p < PF; ++p) {
+      const int kk = min(k0 + 16 * p, kend - 16);
+      a[p] = *reinterpret_cast<const g_bf16x8_t*>(xr + kk);
+#pragma unroll
+      for (int ni = 0; ni < NT; ++ni) {
+        w0[p][ni] = *reinterpret_cast<const g_f32x4_t*>(wr[ni] + kk);
+        w1[p][ni] = *reinterpret_cast<const g_f32x4_t*>(wr[ni] + kk + 4);
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < PF; ++p) {
+      if (k0 + 16 * p >= kend) break;
+#pragma unroll
+      for (int ni = 0; ni < NT; ++ni) {
+        g_bf16x8_t hi, mid, lo;
+        split3(w0[p][ni], w1[p][ni], hi, mid, lo);
+        acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lo, a[p], acc[ni], 0, 0, 0);
+        acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mid, a[p], acc[ni], 0, 0, 0);
+        acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(hi, a[p], acc[ni], 0, 0, 0);
+      }
+    }
+  }
+  // lane holds token m, experts ni*32 + 8*(r/4) + 4*(lane/32) + r%4
+  float* pw = part + wave * GM_TOK * LDP + m * LDP;
+#pragma unroll
+  for (int ni = 0; ni < NT; ++ni)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) pw[ni * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)] = acc[ni][r];
+  __syncthreads();
+  const int ntok = min(GM_TOK, T - t0);
+  for (int i = tid; i < GM_TOK * E; i += GATE_THREADS) {
+    const int t = i / E, e = i - t * E;
+    const int o = t * LDP + e;
+    const float v = ((part[o] + part[GM_TOK * LDP + o]) + part[2 * GM_TOK * LDP + o]) + part[3 * GM_TOK * LDP + o];
+    part[o] = v;
+    if (out.logits && t < ntok) out.logits[(int64_t)(t0 + t) * E + e] = v;
+  }
+  __syncthreads();
+  route_tokens(part, LDP, ntok, t0, bias_s, E, k, route_scale, DSMOE_BF16, out, out.counts ? hist : nullptr, rscr);
+  __syncthreads();
+  flush_hist(hist, E, out.counts);
+}
+
+// ------------------------------------------------------------------ SIMT logits (fp32 x) / given logits
+// LDS layout (floats): xs[KC][TB+4] | ws[KC][EC+4] | lg[TB][E+1] | bias[E] | hist[E] (int) | routing scratch
 template <typename XT, int EC, bool FROM_LOGITS>
 __global__ __launch_bounds__(GATE_THREADS) void gate_kernel(const XT* __restrict__ x, const float* __restrict__ logits_in,
                                                             const float* __restrict__ gw, const float* __restrict__ bias,
-                                                            int T, int D, int E, int k, float route_scale, GateOut out) {
-  constexpr int TX = EC / 4;                // threads along experts
+                                                            int T, int D, int E, int k, float route_scale, int xdtype,
+                                                            GateOut out) {
+  constexpr int TX = EC / 4;                   // threads along experts
   constexpr int TB = (GATE_THREADS / TX) * 4;  // tokens per block
   extern __shared__ float smem[];
   float* xs = smem;                             // [KC][TB+4]
@@ -40,6 +264,7 @@ __global__ __launch_bounds__(GATE_THREADS) void gate_kernel(const XT* __restrict
   float* lg = ws + GATE_KC * (EC + 4);          // [TB][E+1]
   float* bias_s = lg + TB * (E + 1);            // [E]
   int* hist = reinterpret_cast<int*>(bias_s + E);  // [E]
+  float* rscr = smem + ((GATE_KC * (TB + 4) + GATE_KC * (EC + 4) + TB * (E + 1) + 2 * E + 3) & ~3);
 
   const int tid = threadIdx.x;
   const int t0 = blockIdx.x * TB;
@@ -76,11 +301,11 @@ __global__ __launch_bounds__(GATE_THREADS) void gate_kernel(const XT* __restrict
         for (int kk = 0; kk < GATE_KC; ++kk) {
           float4 a = *reinterpret_cast<const float4*>(&xs[kk * (TB + 4) + ty * 4]);
           float4 b = *reinterpret_cast<const float4*>(&ws[kk * (EC + 4) + tx * 4]);
-          float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+          float av[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
           for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
+            for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], bw[j], acc[i][j]);
         }
         __syncthreads();
       }
@@ -94,46 +319,16 @@ __global__ __launch_bounds__(GATE_THREADS) void gate_kernel(const XT* __restrict
     }
   }
   __syncthreads();
+  const int ntok = min(TB, T - t0);
   if (!FROM_LOGITS && out.logits) {
-    for (int i = tid; i < TB * E; i += GATE_THREADS) {
+    for (int i = tid; i < ntok * E; i += GATE_THREADS) {
       int t = i / E, e = i - t * E;
-      if (t0 + t < T) out.logits[(int64_t)(t0 + t) * E + e] = lg[t * ldl + e];
+      out.logits[(int64_t)(t0 + t) * E + e] = lg[t * ldl + e];
     }
   }
-  for (int i = tid; i < TB * E; i += GATE_THREADS) {
-    int t = i / E, e = i - t * E;
-    lg[t * ldl + e] = route_sigmoid(lg[t * ldl + e]);
-  }
+  route_tokens(lg, ldl, ntok, t0, bias_s, E, k, route_scale, xdtype, out, out.counts ? hist : nullptr, rscr);
   __syncthreads();
-  for (int t = tid; t < TB; t += GATE_THREADS) {
-    if (t0 + t >= T) break;
-    float topv[MAX_TOPK];
-    int topi[MAX_TOPK];
-    const float* row = lg + t * ldl;
-    topk_row(row, bias_s, E, k, topv, topi);
-    float sel[MAX_TOPK];
-    float ssum = 0.0f;
-    for (int j = 0; j < k; ++j) {
-      sel[j] = row[topi[j]];
-      ssum += sel[j];
-    }
-    const float den = ssum < 1e-10f ? 1e-10f : ssum;
-    const int64_t o = (int64_t)(t0 + t) * k;
-    for (int j = 0; j < k; ++j) {
-      float w = sel[j] / den * route_scale;
-      out.idx[o + j] = topi[j];
-      if (out.idx64) out.idx64[o + j] = topi[j];
-      out.weights[o + j] = w;
-      if (out.weights_x) static_cast<XT*>(out.weights_x)[o + j] = from_f<XT>(w);
-      if (out.sel_scores) out.sel_scores[o + j] = sel[j];
-      atomicAdd(&hist[topi[j]], 1);
-    }
-  }
-  __syncthreads();
-  if (out.counts) {
-    for (int e = tid; e < E; e += GATE_THREADS)
-      if (hist[e]) atomicAdd(&out.counts[e], hist[e]);
-  }
+  flush_hist(hist, E, out.counts);
 }
 
 __global__ void fill_i32_kernel(int32_t* p, int n, int32_t v) {
@@ -141,21 +336,40 @@ __global__ void fill_i32_kernel(int32_t* p, int n, int32_t v) {
   if (i < n) p[i] = v;
 }
 
+static int set_lds(const void* kern, size_t lds) {
+  if (lds > 64 * 1024 &&
+      hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+    return fail(DSMOE_ERR_HIP, "gate: cannot raise LDS limit");
+  return DSMOE_OK;
+}
+
 template <typename XT, int EC, bool FROM_LOGITS>
 static int launch_gate_t(const void* x, const float* logits_in, const float* gw, const float* bias, const dsmoe_dims& d,
                          const GateOut& out, hipStream_t st) {
   constexpr int TX = EC / 4;
   constexpr int TB = (GATE_THREADS / TX) * 4;
-  size_t lds = sizeof(float) * (GATE_KC * (TB + 4) + GATE_KC * (EC + 4) + TB * (d.E + 1) + d.E) + sizeof(int) * d.E;
+  const size_t lds = sizeof(float) * (GATE_KC * (TB + 4) + GATE_KC * (EC + 4) + TB * (d.E + 1) + d.E) +
+                     sizeof(int) * d.E + 16 + sizeof(float) * ROUTE_SCR;
   auto kern = gate_kernel<XT, EC, FROM_LOGITS>;
-  if (lds > 64 * 1024) {
-    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-      return fail(DSMOE_ERR_HIP, "gate: cannot raise LDS limit");
-  }
+  int rc = set_lds((const void*)kern, lds);
+  if (rc) return rc;
   int blocks = (int)cdiv(d.T, TB);
   hipLaunchKernelGGL(kern, dim3(blocks), dim3(GATE_THREADS), lds, st, static_cast<const XT*>(x), logits_in, gw, bias,
-                     d.T, d.D, d.E, d.k, d.route_scale, out);
+                     d.T, d.D, d.E, d.k, d.route_scale, d.dtype, out);
   return check_launch("gate");
+}
+
+template <int NT>
+static int launch_gate_mfma(const void* x, const float* gw, const float* bias, const dsmoe_dims& d, const GateOut& out,
+                            hipStream_t st) {
+  const size_t lds = sizeof(float) * (4 * GM_TOK * (NT * 32 + 1) + d.E) + sizeof(int) * ((d.E + 3) & ~3) +
+                     sizeof(float) * ROUTE_SCR;
+  auto kern = gate_mfma_kernel<NT>;
+  int rc = set_lds((const void*)kern, lds);
+  if (rc) return rc;
+  hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(d.T, GM_TOK)), dim3(GATE_THREADS), lds, st,
+                     static_cast<const bf16_t*>(x), gw, bias, d.T, d.D, d.E, d.k, d.route_scale, out);
+  return check_launch("gate_mfma");
 }
 
 int launch_gate(const void* x, const float* logits_in, const float* gw, const float* bias, const dsmoe_dims& d,
@@ -164,10 +378,18 @@ int launch_gate(const void* x, const float* logits_in, const float* gw, const fl
     hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)cdiv(d.E, 256)), dim3(256), 0, st, out.counts, d.E, 0);
   }
   if (d.T == 0) return check_launch("gate(fill)");
-  const bool fl = logits_in != nullptr;
-  if (fl) {
-    if (d.dtype == DSMOE_BF16) return launch_gate_t<bf16_t, 64, true>(nullptr, logits_in, gw, bias, d, out, st);
-    return launch_gate_t<float, 64, true>(nullptr, logits_in, gw, bias, d, out, st);
+  if (logits_in) return launch_gate_t<float, 64, true>(nullptr, logits_in, gw, bias, d, out, st);
+  const bool mfma = d.dtype == DSMOE_BF16 && d.D % 64 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+                    (reinterpret_cast<uintptr_t>(gw) & 15) == 0;
+  if (mfma) {
+    const int nt = (int)cdiv(d.E, 32);
+    switch (nt) {
+      case 1: return launch_gate_mfma<1>(x, gw, bias, d, out, st);
+      case 2: return launch_gate_mfma<2>(x, gw, bias, d, out, st);
+      case 3: return launch_gate_mfma<3>(x, gw, bias, d, out, st);
+      case 4: return launch_gate_mfma<4>(x, gw, bias, d, out, st);
+      default: return launch_gate_mfma<8>(x, gw, bias, d, out, st);
+    }
   }
   if (d.dtype == DSMOE_BF16) {
     if (d.E <= 16) return launch_gate_t<bf16_t, 16, false>(x, nullptr, gw, bias, d, out, st);

@@ -7,177 +7,177 @@
 //
 // Work split: a launch enumerates (M tile, N tile) pairs, N fastest.  M tiles
 // come from the device-side schedule the permute scan writes (one entry per
-// 128-row tile inside each expert, so skewed loads simply produce more tiles
+// BM-row tile inside each expert, so skewed loads simply produce more tiles
 // for the hot experts) or are dense (shared experts: every group covers all
 // rows).  Block b runs on XCD b % 8; each XCD takes one contiguous eighth of
 // the tile list so the weight tiles of an expert stay in that XCD's L2.  The
 // grid is sized from a host bound; blocks past the device count exit.
 //
 // Kernels:
-//   gemm_mfma_kernel  bf16, gfx950 v_mfma_f32_32x32x16_bf16, 128x128x64
-//                     block tile (x2 B operands for SwiGLU), 4 waves (2x2,
-//                     64x64 each), LDS double buffer with XOR-swizzled 16-byte
-//                     chunks, global prefetch of the next K slab in registers.
+//   gemm_mfma_kernel  bf16 on gfx950 v_mfma_f32_32x32x16_bf16.  Block =
+//                     WM x WN waves, each owning TM x TN 32x32 output tiles
+//                     (x2 for SwiGLU: the W1 and W3 tiles of the same columns
+//                     sit in the same lane, so silu(g)*u is a register op).
+//                     K slabs of 64 go global -> registers -> LDS (double
+//                     buffered, XOR-swizzled 16-byte chunks) one slab ahead.
+//                     Rows past a tile's end are clamped to a valid row: their
+//                     results are discarded, so no load is predicated.
 //   gemm_simt_kernel  fp32 FMA fallback for fp32 and for shapes the MFMA
 //                     kernel does not take (any N, K, strides).
-#include "common.h"
+#include <cstdlib>
+#include <cstring>
+
+#include "gemm_tile.h"
 
 namespace dsmoe {
-
-// ----------------------------------------------------------------- tile lookup
-__device__ __forceinline__ bool tile_for_block(const GemmDesc& g, int n_tiles, int& grp, int& row0, int& rows,
-                                               int& n_tile) {
-  int64_t m_total;
-  int tpg = 0;
-  if (g.sched) {
-    m_total = *g.sched_count;
-  } else {
-    tpg = (int)cdiv(g.dense_rows, TILE_M);
-    m_total = (int64_t)tpg * g.groups;
-  }
-  const int64_t total = m_total * n_tiles;
-  const int64_t per_xcd = cdiv(total, 8);
-  const int64_t j = blockIdx.x >> 3;
-  if (j >= per_xcd) return false;
-  const int64_t lin = (int64_t)(blockIdx.x & 7) * per_xcd + j;
-  if (lin >= total) return false;
-  const int64_t m_tile = lin / n_tiles;
-  n_tile = (int)(lin - m_tile * n_tiles);
-  if (g.sched) {
-    const MTile t = g.sched[m_tile];
-    grp = t.group;
-    row0 = t.row0;
-    rows = t.rows;
-  } else {
-    grp = (int)(m_tile / tpg);
-    const int mt = (int)(m_tile - (int64_t)grp * tpg);
-    row0 = mt * TILE_M;
-    rows = min(TILE_M, g.dense_rows - row0);
-  }
-  return true;
-}
 
 // =============================================================== MFMA kernel
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));  // native vector: stays in registers
 
-constexpr int MF_N = 128;
-constexpr int MF_K = 64;
-constexpr int MF_THREADS = 256;
+constexpr int MF_K = 64;  // K slab per pipeline stage (8 chunks of 16 bytes per row)
 
-__device__ __forceinline__ int swz(int row, int chunk) { return row * MF_K + ((chunk ^ (row & 7)) << 3); }
+// LDS row = 64 bf16 = 128 bytes = 8 chunks of 16 bytes.  gfx950 serves a
+// ds_read_b128 16 lanes (256 bytes, two rows) per cycle; chunk c of row r is
+// stored at c ^ ((r >> 1) & 7), so the 16 rows read at one logical chunk by
+// a fragment load land on 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int swz(int row, int chunk) { return row * MF_K + ((chunk ^ ((row >> 1) & 7)) << 3); }
 
-template <int EPI>
-__global__ __launch_bounds__(MF_THREADS) void gemm_mfma_kernel(const GemmDesc g, const float* __restrict__ row_scale) {
-  constexpr int NB = (EPI == EPI_SWIGLU) ? 2 : 1;
-  constexpr int A_EL = TILE_M * MF_K;
-  constexpr int B_EL = MF_N * MF_K;
-  constexpr int STAGE = A_EL + NB * B_EL;
+template <int EPI, int WM, int WN, int TM, int TN>
+struct MfCfg {
+  static constexpr int NB = (EPI == EPI_SWIGLU) ? 2 : 1;
+  static constexpr int THREADS = 64 * WM * WN;
+  static constexpr int BM = WM * TM * 32;
+  static constexpr int BN = WN * TN * 32;
+  static constexpr int A_EL = BM * MF_K;
+  static constexpr int B_EL = BN * MF_K;
+  static constexpr int STAGE = A_EL + NB * B_EL;
+  static constexpr int RSTEP = THREADS / 8;       // rows covered by one pass of the block
+  static constexpr int A_LD = BM / RSTEP;         // 16-byte chunks per thread per stage (A)
+  static constexpr int B_LD = BN / RSTEP;         // per B operand
+  static constexpr size_t LDS_BYTES = 2ull * STAGE * sizeof(bf16_t);
+  static_assert(BM % RSTEP == 0 && BN % RSTEP == 0, "tile rows must be a multiple of threads/8");
+};
+
+template <int N>
+__device__ __forceinline__ void load_rows(const bf16_t* __restrict__ base, const int64_t (&off)[N], int k0,
+                                          u32x4_t (&r)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) r[i] = *reinterpret_cast<const u32x4_t*>(base + off[i] + k0);
+}
+
+template <int N, int RSTEP>
+__device__ __forceinline__ void store_rows(bf16_t* __restrict__ s, int lr, int lc, const u32x4_t (&r)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) *reinterpret_cast<u32x4_t*>(s + swz(lr + i * RSTEP, lc)) = r[i];
+}
+
+template <int EPI, int WM, int WN, int TM, int TN>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_mfma_kernel(const GemmDesc g, const float* __restrict__ row_scale) {
+  using CF = MfCfg<EPI, WM, WN, TM, TN>;
+  constexpr int NB = CF::NB, BM = CF::BM, BN = CF::BN, RSTEP = CF::RSTEP;
+  constexpr int A_LD = CF::A_LD, B_LD = CF::B_LD;
   extern __shared__ __attribute__((aligned(16))) bf16_t smem_mf[];
 
-  const int n_tiles = (int)cdiv(g.N, MF_N);
+  const int n_tiles = (int)cdiv(g.N, BN);
   int grp, row0, rows, n_tile;
-  if (!tile_for_block(g, n_tiles, grp, row0, rows, n_tile)) return;
-  const int n0 = n_tile * MF_N;
+  if (!tile_for_block<BM>(g, n_tiles, grp, row0, rows, n_tile)) return;
+  const int n0 = n_tile * BN;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-
-  // ---- global -> register assignment: chunk lc (16 bytes) of rows lr + 32*i
+  const int wm = wave / WN, wn = wave % WN;
   const int lc = tid & 7;
   const int lr = tid >> 3;
-  const bf16_t* A = static_cast<const bf16_t*>(g.A);
-  const bf16_t* a_src[4];
-  bool a_ok[4];
+
+  // Source offsets of this thread's 16-byte chunks (row-clamped).
+  const bf16_t* __restrict__ A = static_cast<const bf16_t*>(g.A);
+  int64_t a_off[A_LD];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = lr + 32 * i;
-    a_ok[i] = r < rows;
-    int64_t arow = 0;
-    if (a_ok[i]) arow = g.a_map ? g.a_map[row0 + r] : (row0 + r);
-    a_src[i] = A + arow * g.lda + lc * 8;
+  for (int i = 0; i < A_LD; ++i) {
+    const int r = min(lr + i * RSTEP, rows - 1);
+    const int64_t arow = g.a_map ? (int64_t)g.a_map[row0 + r] : (int64_t)(row0 + r);
+    a_off[i] = arow * g.lda + lc * 8;
   }
-  bool b_ok[4];
+  int64_t b_off[B_LD];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) b_ok[i] = (n0 + lr + 32 * i) < g.N;
+  for (int i = 0; i < B_LD; ++i) b_off[i] = (int64_t)min(n0 + lr + i * RSTEP, g.N - 1) * g.ldb + lc * 8;
 
-  uint4 ra[4];
-  uint4 rb[NB][4];
-  const uint4 z4 = make_uint4(0, 0, 0, 0);
+  u32x4_t ra[A_LD];
+  u32x4_t rb0[B_LD];
+  u32x4_t rb1[B_LD];
 
-  auto gload = [&](int kb) {
-    const int k0 = kb * MF_K;
-    const int seg = k0 / g.kseg;
-    const int kin = k0 - seg * g.kseg;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) ra[i] = a_ok[i] ? *reinterpret_cast<const uint4*>(a_src[i] + k0) : z4;
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      const bf16_t* base = static_cast<const bf16_t*>((b == 0 ? g.B0 : g.B1)[grp * g.nseg + seg]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        rb[b][i] = b_ok[i] ? *reinterpret_cast<const uint4*>(base + (int64_t)(n0 + lr + 32 * i) * g.ldb + kin + lc * 8)
-                           : z4;
-    }
-  };
-  auto lstore = [&](int stage) {
-    bf16_t* sA = smem_mf + stage * STAGE;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(sA + swz(lr + 32 * i, lc)) = ra[i];
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      bf16_t* sB = sA + A_EL + b * B_EL;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(sB + swz(lr + 32 * i, lc)) = rb[b][i];
-    }
-  };
-
-  f32x16_t acc[NB][2][2];
+  f32x16_t acc[NB][TM][TN];
 #pragma unroll
   for (int b = 0; b < NB; ++b)
 #pragma unroll
-    for (int mi = 0; mi < 2; ++mi)
+    for (int mi = 0; mi < TM; ++mi)
 #pragma unroll
-      for (int ni = 0; ni < 2; ++ni)
+      for (int ni = 0; ni < TN; ++ni)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[b][mi][ni][r] = 0.0f;
 
   const int nk = g.K / MF_K;
-  gload(0);
-  lstore(0);
+  const void* const* __restrict__ tab0 = g.B0 + (int64_t)grp * g.nseg;
+  const void* const* __restrict__ tab1 = (NB == 2) ? g.B1 + (int64_t)grp * g.nseg : nullptr;
+
+  // ---- prologue: slab 0 -> LDS stage 0
+  {
+    load_rows(A, a_off, 0, ra);
+    load_rows(static_cast<const bf16_t*>(tab0[0]), b_off, 0, rb0);
+    if (NB == 2) load_rows(static_cast<const bf16_t*>(tab1[0]), b_off, 0, rb1);
+    bf16_t* s = smem_mf;
+    store_rows<A_LD, RSTEP>(s, lr, lc, ra);
+    store_rows<B_LD, RSTEP>(s + CF::A_EL, lr, lc, rb0);
+    if (NB == 2) store_rows<B_LD, RSTEP>(s + CF::A_EL + CF::B_EL, lr, lc, rb1);
+  }
   __syncthreads();
+
   for (int kb = 0; kb < nk; ++kb) {
     const int cur = kb & 1;
-    if (kb + 1 < nk) gload(kb + 1);
-    const bf16_t* sA = smem_mf + cur * STAGE;
+    const bool more = kb + 1 < nk;
+    if (more) {
+      const int k0 = (kb + 1) * MF_K;
+      const int seg = k0 / g.kseg;
+      const int kin = k0 - seg * g.kseg;
+      load_rows(A, a_off, k0, ra);
+      load_rows(static_cast<const bf16_t*>(tab0[seg]), b_off, kin, rb0);
+      if (NB == 2) load_rows(static_cast<const bf16_t*>(tab1[seg]), b_off, kin, rb1);
+    }
+    const bf16_t* sA = smem_mf + cur * CF::STAGE;
 #pragma unroll
     for (int kk = 0; kk < MF_K / 16; ++kk) {
       const int c = kk * 2 + (lane >> 5);
-      bf16x8_t af[2];
+      bf16x8_t af[TM];
 #pragma unroll
-      for (int mi = 0; mi < 2; ++mi) {
-        const int r = wm * 64 + mi * 32 + (lane & 31);
+      for (int mi = 0; mi < TM; ++mi) {
+        const int r = (wm * TM + mi) * 32 + (lane & 31);
         af[mi] = *reinterpret_cast<const bf16x8_t*>(sA + swz(r, c));
       }
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
-        const bf16_t* sB = sA + A_EL + b * B_EL;
-        bf16x8_t bfr[2];
+        const bf16_t* sB = sA + CF::A_EL + b * CF::B_EL;
+        bf16x8_t bfr[TN];
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni) {
-          const int n = wn * 64 + ni * 32 + (lane & 31);
+        for (int ni = 0; ni < TN; ++ni) {
+          const int n = (wn * TN + ni) * 32 + (lane & 31);
           bfr[ni] = *reinterpret_cast<const bf16x8_t*>(sB + swz(n, c));
         }
 #pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
+        for (int mi = 0; mi < TM; ++mi)
 #pragma unroll
-          for (int ni = 0; ni < 2; ++ni)
+          for (int ni = 0; ni < TN; ++ni)
             acc[b][mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[ni], af[mi], acc[b][mi][ni], 0, 0, 0);
       }
     }
-    if (kb + 1 < nk) lstore(cur ^ 1);
+    if (more) {
+      bf16_t* s = smem_mf + (cur ^ 1) * CF::STAGE;
+      store_rows<A_LD, RSTEP>(s, lr, lc, ra);
+      store_rows<B_LD, RSTEP>(s + CF::A_EL, lr, lc, rb0);
+      if (NB == 2) store_rows<B_LD, RSTEP>(s + CF::A_EL + CF::B_EL, lr, lc, rb1);
+    }
     __syncthreads();
   }
 
@@ -186,17 +186,17 @@ __global__ __launch_bounds__(MF_THREADS) void gemm_mfma_kernel(const GemmDesc g,
   bf16_t* C = static_cast<bf16_t*>(g.C);
   const int64_t ccol = (int64_t)grp * g.c_group_col;
 #pragma unroll
-  for (int mi = 0; mi < 2; ++mi) {
-    const int m = wm * 64 + mi * 32 + (lane & 31);
+  for (int mi = 0; mi < TM; ++mi) {
+    const int m = (wm * TM + mi) * 32 + (lane & 31);
     if (m >= rows) continue;
-    const int64_t crow = g.c_map ? g.c_map[row0 + m] : (row0 + m);
+    const int64_t crow = g.c_map ? (int64_t)g.c_map[row0 + m] : (int64_t)(row0 + m);
     float scale = 1.0f;
     if (EPI == EPI_STORE && row_scale) scale = row_scale[row0 + m];
 #pragma unroll
-    for (int ni = 0; ni < 2; ++ni) {
+    for (int ni = 0; ni < TN; ++ni) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int n = n0 + wn * 64 + ni * 32 + q * 8 + (lane >> 5) * 4;
+        const int n = n0 + (wn * TN + ni) * 32 + q * 8 + (lane >> 5) * 4;
         if (n >= g.N) continue;
         const int64_t o = crow * g.ldc + ccol + n;
         uint32_t packed[2];
@@ -236,7 +236,7 @@ __global__ __launch_bounds__(256) void gemm_simt_kernel(const GemmDesc g, const 
   __shared__ float Bs[NB][SM_K][SM_N + 4];
   const int n_tiles = (int)cdiv(g.N, SM_N);
   int grp, row0, rows, n_tile;
-  if (!tile_for_block(g, n_tiles, grp, row0, rows, n_tile)) return;
+  if (!tile_for_block<TILE_M>(g, n_tiles, grp, row0, rows, n_tile)) return;
   const int n0 = n_tile * SM_N;
   const int tid = threadIdx.x;
   const int ty = tid >> 4, tx = tid & 15;  // rows ty*8.., cols tx*4..
@@ -320,42 +320,89 @@ __global__ __launch_bounds__(256) void gemm_simt_kernel(const GemmDesc g, const 
 // =============================================================== host launch
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// MFMA tile configuration.  All configurations use 256-row M tiles (the
+// routed schedule height); DSMOE_GEMM_CFG selects among them for tuning.
+//   0: 4 waves (2x2), per wave 4x2 tiles (SwiGLU: x2) / 4x4 tiles (store)
+//   1: 8 waves (2x4), per wave 4x1 (SwiGLU x2) / 4x2 (store)
+//   2: 8 waves (4x2), per wave 2x2 (SwiGLU x2) / 2x4 (store)
+//   3: direct global->LDS kernel of gemm_dl.hip (4 waves, 4-deep LDS ring)
+constexpr int MF_BM = 256;
+
+static int gemm_cfg() {
+  static int cfg = [] {
+    const char* s = std::getenv("DSMOE_GEMM_CFG");
+    int v = s ? std::atoi(s) : 2;
+    return (v >= 0 && v <= 3) ? v : 2;
+  }();
+  return cfg;
+}
+
 // The MFMA kernel needs bf16, 16-byte aligned operands and strides, K and the
 // K segment multiples of 64, N a multiple of 4 and 8-byte aligned output rows.
 static bool mfma_ok(const GemmDesc& g) {
-  return g.K % MF_K == 0 && g.kseg % MF_K == 0 && g.N % 4 == 0 && g.lda % 8 == 0 && g.ldb % 8 == 0 &&
+  return g.K % MF_K == 0 && g.kseg % MF_K == 0 && g.lda % 8 == 0 && g.ldb % 8 == 0 && g.N % 4 == 0 &&
          g.ldc % 4 == 0 && g.c_group_col % 4 == 0 && aligned16(g.A) && ((reinterpret_cast<uintptr_t>(g.C) & 7) == 0);
 }
 
-static int64_t grid_for(const GemmDesc& g, int tile_n) {
-  const int64_t m_bound = g.sched ? g.m_tiles_bound : cdiv(g.dense_rows, TILE_M) * g.groups;
+bool gemm_mfma_eligible(const GemmDesc& g, int dtype, bool allow_mfma) {
+  return dtype == DSMOE_BF16 && allow_mfma && mfma_ok(g);
+}
+
+int gemm_tile_m(bool mfma) { return mfma ? MF_BM : TILE_M; }
+
+static int64_t grid_for(const GemmDesc& g, int bm, int tile_n) {
+  const int64_t m_bound = g.sched ? g.m_tiles_bound : cdiv(g.dense_rows, bm) * g.groups;
   const int64_t total = m_bound * cdiv(g.N, tile_n);
   return 8 * cdiv(total, 8);
 }
 
-int launch_grouped_gemm(const GemmDesc& g, int epi, int dtype, const float* row_scale, bool allow_mfma,
-                        hipStream_t st) {
-  if (g.N <= 0 || g.K <= 0) return DSMOE_OK;
-  if (dtype == DSMOE_BF16 && allow_mfma && mfma_ok(g)) {
-    const int64_t grid = grid_for(g, MF_N);
-    if (grid == 0) return DSMOE_OK;
-    if (epi == EPI_SWIGLU) {
-      const size_t lds = 2 * sizeof(bf16_t) * (TILE_M * MF_K + 2 * MF_N * MF_K);
-      static bool attr = false;
-      if (!attr) {
-        if (hipFuncSetAttribute((const void*)gemm_mfma_kernel<EPI_SWIGLU>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)lds) != hipSuccess)
-          return fail(DSMOE_ERR_HIP, "gemm: cannot raise LDS limit");
-        attr = true;
-      }
-      hipLaunchKernelGGL(gemm_mfma_kernel<EPI_SWIGLU>, dim3((unsigned)grid), dim3(MF_THREADS), lds, st, g, row_scale);
-    } else {
-      const size_t lds = 2 * sizeof(bf16_t) * (TILE_M * MF_K + MF_N * MF_K);
-      hipLaunchKernelGGL(gemm_mfma_kernel<EPI_STORE>, dim3((unsigned)grid), dim3(MF_THREADS), lds, st, g, row_scale);
-    }
-    return check_launch("gemm_mfma");
+template <int EPI, int WM, int WN, int TM, int TN>
+static int launch_mfma_t(const GemmDesc& g, const float* row_scale, hipStream_t st) {
+  using CF = MfCfg<EPI, WM, WN, TM, TN>;
+  static_assert(CF::BM == MF_BM, "schedule height");
+  const int64_t grid = grid_for(g, CF::BM, CF::BN);
+  if (grid == 0) return DSMOE_OK;
+  auto kern = gemm_mfma_kernel<EPI, WM, WN, TM, TN>;
+  static bool attr = false;
+  if (!attr) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)CF::LDS_BYTES) !=
+        hipSuccess)
+      return fail(DSMOE_ERR_HIP, "gemm: cannot raise LDS limit");
+    attr = true;
   }
-  const int64_t grid = grid_for(g, SM_N);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(CF::THREADS), CF::LDS_BYTES, st, g, row_scale);
+  return check_launch("gemm_mfma");
+}
+
+static int gemm_raster() {
+  static int r = [] {
+    const char* s = std::getenv("DSMOE_GEMM_RASTER");
+    const int v = s ? std::atoi(s) : 0;
+    return (v >= 0 && v <= 2) ? v : 0;
+  }();
+  return r;
+}
+
+int launch_grouped_gemm(const GemmDesc& g_in, int epi, int dtype, const float* row_scale, bool allow_mfma,
+                        hipStream_t st) {
+  GemmDesc g = g_in;
+  g.raster = gemm_raster();
+  if (g.N <= 0 || g.K <= 0) return DSMOE_OK;
+  if (gemm_mfma_eligible(g, dtype, allow_mfma)) {
+    if (g.bm != MF_BM) return fail(DSMOE_ERR_INVALID, "gemm: schedule tile height does not match the MFMA kernel");
+    const int cfg = gemm_cfg();
+    if (cfg == 3 && gemm_dl_ok(g, g.a_rows)) return launch_gemm_dl(g, epi, row_scale, st);
+    if (epi == EPI_SWIGLU) {
+      if (cfg == 1) return launch_mfma_t<EPI_SWIGLU, 2, 4, 4, 1>(g, row_scale, st);
+      if (cfg == 2) return launch_mfma_t<EPI_SWIGLU, 4, 2, 2, 2>(g, row_scale, st);
+      return launch_mfma_t<EPI_SWIGLU, 2, 2, 4, 2>(g, row_scale, st);
+    }
+    if (cfg == 1) return launch_mfma_t<EPI_STORE, 2, 4, 4, 2>(g, row_scale, st);
+    if (cfg == 2) return launch_mfma_t<EPI_STORE, 4, 2, 2, 4>(g, row_scale, st);
+    return launch_mfma_t<EPI_STORE, 2, 2, 4, 4>(g, row_scale, st);
+  }
+  if (g.bm != TILE_M) return fail(DSMOE_ERR_INVALID, "gemm: schedule tile height does not match the SIMT kernel");
+  const int64_t grid = grid_for(g, TILE_M, SM_N);
   if (grid == 0) return DSMOE_OK;
   if (dtype == DSMOE_BF16) {
     if (epi == EPI_SWIGLU)
