@@ -96,6 +96,7 @@ struct FwdLayout {
   int32_t* sorted_slot;
   int32_t* sorted_token;
   int32_t* slot_pos;
+  float* sorted_w;  // training: weights in sorted order
   PermuteScratch ps;
   void* h;
   void* g;
@@ -121,6 +122,7 @@ static FwdLayout fwd_layout(const dsmoe_dims& d, int training, void* base) {
   L.sorted_slot = c.take<int32_t>(N);
   L.sorted_token = c.take<int32_t>(N);
   L.slot_pos = c.take<int32_t>(N);
+  L.sorted_w = training ? c.take<float>(N) : nullptr;
   permute_scratch_carve(c, d, TILE_M, &L.ps);
   L.h = c.take<char>((size_t)N * d.I * es);
   L.g = training ? c.take<char>((size_t)N * d.I * es) : nullptr;
@@ -376,8 +378,8 @@ int dsmoe_moe_fwd(const void* x, const float* gate_w, const float* gate_bias, co
   const int bm = gemm_tile_m(mfr);
   // (b) permute (counts come from the scan: exact bincount, no atomics)
   tm.begin(ST_PERMUTE);
-  rc = launch_permute(L.idx, d, bm, L.ps, L.offsets, L.sorted_slot, L.sorted_token, L.slot_pos, counts, nullptr,
-                      nullptr, st);
+  rc = launch_permute(L.idx, d, bm, L.ps, L.offsets, L.sorted_slot, L.sorted_token, L.slot_pos, counts,
+                      training ? L.w : nullptr, L.sorted_w, st);
   tm.end();
   if (rc) return rc;
   g1.sched = g2.sched = L.ps.sched;
@@ -429,16 +431,222 @@ int dsmoe_moe_fwd(const void* x, const float* gate_w, const float* gate_bias, co
   return rc;
 }
 
-size_t dsmoe_moe_bwd_workspace_size(const dsmoe_dims* dims) {
-  if (validate(dims, true)) return 0;
-  return 0;
+// Backward workspace layout (device pointer tables, then buffers).
+struct BwdLayout {
+  const void** w1;
+  const void** w3;
+  const void** w2;
+  const void** w13;   // [w1_e, w3_e] per expert: the two K segments of dx
+  const void** sw1;
+  const void** sw3;
+  const void** sw2;
+  const void** sw13;  // [sw1_0, sw3_0, sw1_1, sw3_1, ...]: one group, 2S segments
+  void** dw1;
+  void** dw3;
+  void** dw2;
+  void** dsw1;
+  void** dsw3;
+  void** dsw2;
+  float* dw;          // (N) d weights, slot order
+  float* dlog;        // (N) d logits of the selected experts, slot order
+  MTile* sched;
+  int32_t* sched_count;
+  void* dgdu;         // (N, 2I)   [dg | du] in sorted order
+  void* dx_slots;     // (N, D)    slot order
+  void* dgdu_s;       // (T, 2 S I_s)
+  void* dx_shared;    // (T, D)
+  size_t total;
+};
+
+constexpr int BWD_BM = 64;  // schedule height used by the backward GEMMs
+
+static BwdLayout bwd_layout(const dsmoe_dims& d, void* base) {
+  Carver c(base);
+  BwdLayout B;
+  const int64_t N = (int64_t)d.T * d.k;
+  const int es = elem_size(d.dtype);
+  // pointer tables: each group is one contiguous block (uploaded in one call)
+  const void** rt = c.take<const void*>(5 * d.E);
+  B.w1 = rt;
+  B.w3 = rt + d.E;
+  B.w2 = rt + 2 * d.E;
+  B.w13 = rt + 3 * d.E;
+  const void** st = c.take<const void*>(5 * d.S + 1);
+  B.sw1 = st;
+  B.sw3 = st + d.S;
+  B.sw2 = st + 2 * d.S;
+  B.sw13 = st + 3 * d.S;
+  void** ro = c.take<void*>(3 * d.E);
+  B.dw1 = ro;
+  B.dw3 = ro + d.E;
+  B.dw2 = ro + 2 * d.E;
+  void** so = c.take<void*>(3 * d.S + 1);
+  B.dsw1 = so;
+  B.dsw3 = so + d.S;
+  B.dsw2 = so + 2 * d.S;
+  B.dw = c.take<float>(N);
+  B.dlog = c.take<float>(N);
+  B.sched = c.take<MTile>(sched_bound(N, d.E, BWD_BM));
+  B.sched_count = c.take<int32_t>(1);
+  B.dgdu = c.take<char>((size_t)N * 2 * d.I * es);
+  B.dx_slots = c.take<char>((size_t)N * d.D * es);
+  B.dgdu_s = d.S ? c.take<char>((size_t)d.T * 2 * d.S * d.I_s * es) : nullptr;
+  B.dx_shared = d.S ? c.take<char>((size_t)d.T * d.D * es) : nullptr;
+  B.total = c.used();
+  return B;
 }
 
-int dsmoe_moe_bwd(const void*, const float*, const void* const*, const void* const*, const void* const*,
-                  const void* const*, const void* const*, const void* const*, const dsmoe_dims*, const void*,
-                  const void*, void*, float*, void* const*, void* const*, void* const*, void* const*, void* const*,
-                  void* const*, void*, size_t, void*) {
-  return fail(DSMOE_ERR_UNSUPPORTED, "dsmoe_moe_bwd: not built yet");
+static XGemm xdesc_zero() {
+  XGemm g;
+  std::memset(static_cast<void*>(&g), 0, sizeof(g));
+  g.nseg = 1;
+  return g;
+}
+
+size_t dsmoe_moe_bwd_workspace_size(const dsmoe_dims* dims) {
+  if (validate(dims, true)) return 0;
+  return bwd_layout(*dims, nullptr).total;
+}
+
+int dsmoe_moe_bwd(const void* x, const float* gate_w, const void* const* w1, const void* const* w2,
+                  const void* const* w3, const void* const* sw1, const void* const* sw2, const void* const* sw3,
+                  const dsmoe_dims* dims, const void* dy, const void* fwd_workspace, void* dx, float* dgate_w,
+                  void* const* dw1, void* const* dw2, void* const* dw3, void* const* dsw1, void* const* dsw2,
+                  void* const* dsw3, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = validate(dims, true);
+  if (rc) return rc;
+  const dsmoe_dims& d = *dims;
+  DSMOE_REQUIRE(x && gate_w && w1 && w2 && w3 && dy && fwd_workspace && dx && dgate_w && dw1 && dw2 && dw3,
+                DSMOE_ERR_INVALID, "moe_bwd: NULL required pointer");
+  DSMOE_REQUIRE(d.S == 0 || (sw1 && sw2 && sw3 && dsw1 && dsw2 && dsw3), DSMOE_ERR_INVALID,
+                "moe_bwd: NULL shared expert pointers");
+  const size_t need = dsmoe_moe_bwd_workspace_size(dims);
+  DSMOE_REQUIRE(workspace && workspace_bytes >= need, DSMOE_ERR_WORKSPACE, "moe_bwd: workspace too small");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  // the forward layout of a training call (the caller passes that workspace)
+  const FwdLayout F = fwd_layout(d, 1, const_cast<void*>(fwd_workspace));
+  BwdLayout B = bwd_layout(d, workspace);
+  const int64_t N = (int64_t)d.T * d.k;
+  StageTimer tm(st);
+
+  std::vector<const void*> w13h(2 * d.E), sw13h(2 * d.S + 1);
+  for (int e = 0; e < d.E; ++e) {
+    w13h[2 * e] = w1[e];
+    w13h[2 * e + 1] = w3[e];
+  }
+  for (int s = 0; s < d.S; ++s) {
+    sw13h[2 * s] = sw1[s];
+    sw13h[2 * s + 1] = sw3[s];
+  }
+  tm.begin(ST_BWD_PREP);
+  // each table group is contiguous in the workspace, in this order
+  rc = upload_ptr_lists({{w1, d.E}, {w3, d.E}, {w2, d.E}, {w13h.data(), 2 * d.E}}, B.w1, st);
+  if (!rc && d.S) rc = upload_ptr_lists({{sw1, d.S}, {sw3, d.S}, {sw2, d.S}, {sw13h.data(), 2 * d.S}}, B.sw1, st);
+  if (!rc)
+    rc = upload_ptr_lists({{(const void* const*)dw1, d.E}, {(const void* const*)dw3, d.E}, {(const void* const*)dw2, d.E}},
+                          (const void**)B.dw1, st);
+  if (!rc && d.S)
+    rc = upload_ptr_lists({{(const void* const*)dsw1, d.S}, {(const void* const*)dsw3, d.S},
+                           {(const void* const*)dsw2, d.S}},
+                          (const void**)B.dsw1, st);
+  if (rc) return rc;
+  // gate gradient path: d weights -> d logits
+  rc = launch_dw_dot(dy, F.o_slots, N, d.k, d.D, d.dtype, B.dw, st);
+  if (!rc) rc = launch_gate_bwd(B.dw, F.sel, d.T, d.k, d.route_scale, B.dlog, st);
+  if (!rc) rc = launch_sched32(F.offsets, d.E, BWD_BM, B.sched, B.sched_count, st);
+  tm.end();
+  if (rc) return rc;
+  const int32_t mbound = (int32_t)sched_bound(N, d.E, BWD_BM);
+
+  // routed dh = w * (dy W2), SwiGLU backward -> [dg | du]
+  XGemm h = xdesc_zero();
+  h.sched_mode = XS_ROUTED; h.sched = B.sched; h.sched_count = B.sched_count; h.m_tiles_bound = mbound;
+  h.bm = BWD_BM; h.N = d.I; h.K = d.D;
+  h.a_mode = XA_ROWS; h.A = dy; h.lda = d.D; h.a_map = F.sorted_token;
+  h.b_mode = XB_W_NN; h.Btab = B.w2; h.ldb = d.I; h.kseg = d.D;
+  h.C = B.dgdu; h.ldc = 2 * (int64_t)d.I; h.du_off = d.I;
+  h.Gs = F.g; h.Us = F.u; h.ld_gu = d.I; h.row_w = F.sorted_w;
+  tm.begin(ST_BWD_DH);
+  rc = launch_xgemm(h, XE_SWIGLU_BWD, d.dtype, st);
+  tm.end();
+  if (rc) return rc;
+  // routed dx_slot = [dg | du] [W1; W3], rows back to slot order
+  XGemm xg = xdesc_zero();
+  xg.sched_mode = XS_ROUTED; xg.sched = B.sched; xg.sched_count = B.sched_count; xg.m_tiles_bound = mbound;
+  xg.bm = BWD_BM; xg.N = d.D; xg.K = 2 * d.I;
+  xg.a_mode = XA_ROWS; xg.A = B.dgdu; xg.lda = 2 * (int64_t)d.I;
+  xg.b_mode = XB_W_NN; xg.Btab = B.w13; xg.ldb = d.D; xg.kseg = d.I; xg.nseg = 2;
+  xg.C = B.dx_slots; xg.ldc = d.D; xg.c_map = F.sorted_slot;
+  tm.begin(ST_BWD_DX);
+  rc = launch_xgemm(xg, XE_STORE, d.dtype, st);
+  tm.end();
+  if (rc) return rc;
+  // routed dW1, dW3 = [dg | du]^T X_e ; dW2 = (w dY)^T H_e
+  XGemm w13 = xdesc_zero();
+  w13.sched_mode = XS_WGRAD; w13.groups = d.E; w13.k_off = F.offsets; w13.M = 2 * d.I; w13.N = d.D; w13.K = (int32_t)N;
+  w13.a_mode = XA_KMAJOR; w13.A = B.dgdu; w13.lda = 2 * (int64_t)d.I;
+  w13.b_mode = XB_ACT_KMAJOR; w13.Bact = x; w13.b_map = F.sorted_token; w13.ldb = d.D;
+  w13.Ctab0 = B.dw1; w13.Ctab1 = B.dw3; w13.msplit = d.I; w13.ldc = d.D;
+  tm.begin(ST_BWD_DW13);
+  rc = launch_xgemm(w13, XE_WGRAD, d.dtype, st);
+  tm.end();
+  if (rc) return rc;
+  XGemm w2g = xdesc_zero();
+  w2g.sched_mode = XS_WGRAD; w2g.groups = d.E; w2g.k_off = F.offsets; w2g.M = d.D; w2g.N = d.I; w2g.K = (int32_t)N;
+  w2g.a_mode = XA_KMAJOR; w2g.A = dy; w2g.lda = d.D; w2g.a_map = F.sorted_token; w2g.a_kscale = F.sorted_w;
+  w2g.b_mode = XB_ACT_KMAJOR; w2g.Bact = F.h; w2g.ldb = d.I;
+  w2g.Ctab0 = B.dw2; w2g.Ctab1 = B.dw2; w2g.msplit = d.D; w2g.ldc = d.I;
+  tm.begin(ST_BWD_DW2);
+  rc = launch_xgemm(w2g, XE_WGRAD, d.dtype, st);
+  tm.end();
+  if (rc) return rc;
+
+  if (d.S) {
+    const int64_t SIs = (int64_t)d.S * d.I_s;
+    XGemm sh = xdesc_zero();
+    sh.sched_mode = XS_DENSE; sh.dense_rows = d.T; sh.groups = d.S; sh.N = d.I_s; sh.K = d.D;
+    sh.a_mode = XA_ROWS; sh.A = dy; sh.lda = d.D;
+    sh.b_mode = XB_W_NN; sh.Btab = B.sw2; sh.ldb = d.I_s; sh.kseg = d.D;
+    sh.C = B.dgdu_s; sh.ldc = 2 * SIs; sh.c_group_col = 2 * (int64_t)d.I_s; sh.du_off = d.I_s;
+    sh.Gs = F.gs; sh.Us = F.us; sh.ld_gu = SIs; sh.gu_group_col = d.I_s;
+    tm.begin(ST_BWD_DH_SHARED);
+    rc = launch_xgemm(sh, XE_SWIGLU_BWD, d.dtype, st);
+    tm.end();
+    if (rc) return rc;
+    XGemm sx = xdesc_zero();
+    sx.sched_mode = XS_DENSE; sx.dense_rows = d.T; sx.groups = 1; sx.N = d.D; sx.K = (int32_t)(2 * SIs);
+    sx.a_mode = XA_ROWS; sx.A = B.dgdu_s; sx.lda = 2 * SIs;
+    sx.b_mode = XB_W_NN; sx.Btab = B.sw13; sx.ldb = d.D; sx.kseg = d.I_s; sx.nseg = 2 * d.S;
+    sx.C = B.dx_shared; sx.ldc = d.D;
+    tm.begin(ST_BWD_DX_SHARED);
+    rc = launch_xgemm(sx, XE_STORE, d.dtype, st);
+    tm.end();
+    if (rc) return rc;
+    XGemm s13 = xdesc_zero();
+    s13.sched_mode = XS_WGRAD; s13.groups = d.S; s13.M = 2 * d.I_s; s13.N = d.D; s13.K = d.T;
+    s13.a_mode = XA_KMAJOR; s13.A = B.dgdu_s; s13.lda = 2 * SIs; s13.a_col = 2 * (int64_t)d.I_s;
+    s13.b_mode = XB_ACT_KMAJOR; s13.Bact = x; s13.ldb = d.D;
+    s13.Ctab0 = B.dsw1; s13.Ctab1 = B.dsw3; s13.msplit = d.I_s; s13.ldc = d.D;
+    XGemm s2 = xdesc_zero();
+    s2.sched_mode = XS_WGRAD; s2.groups = d.S; s2.M = d.D; s2.N = d.I_s; s2.K = d.T;
+    s2.a_mode = XA_KMAJOR; s2.A = dy; s2.lda = d.D;
+    s2.b_mode = XB_ACT_KMAJOR; s2.Bact = F.hs; s2.ldb = SIs; s2.b_col = d.I_s;
+    s2.Ctab0 = B.dsw2; s2.Ctab1 = B.dsw2; s2.msplit = d.D; s2.ldc = d.I_s;
+    tm.begin(ST_BWD_DW_SHARED);
+    rc = launch_xgemm(s13, XE_WGRAD, d.dtype, st);
+    if (!rc) rc = launch_xgemm(s2, XE_WGRAD, d.dtype, st);
+    tm.end();
+    if (rc) return rc;
+  }
+  tm.begin(ST_BWD_GATE);
+  rc = launch_dwgate(x, B.dlog, F.sorted_slot, F.sorted_token, F.offsets, d.E, d.D, d.dtype, dgate_w, st);
+  tm.end();
+  if (rc) return rc;
+  tm.begin(ST_BWD_REDUCE);
+  rc = launch_dx_final(B.dx_slots, B.dx_shared, B.dlog, F.idx, gate_w, d.T, d.D, d.k, d.dtype, dx, st);
+  tm.end();
+  tm.call_done(1);
+  return rc;
 }
 
 int dsmoe_update_bias(const int32_t* counts, float* gate_bias, int E, float speed, float upper, float lower,

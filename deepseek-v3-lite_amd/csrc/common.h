@@ -168,4 +168,81 @@ int launch_combine(const void* o_slots, const float* w, const int32_t* idx, cons
 int launch_update_bias(const int32_t* counts, float* bias, int E, float speed, float upper, float lower,
                        hipStream_t st);
 
+
+// ---------------------------------------------------------------- backward GEMM description
+// C(m, n) = sum_k A(m, k) * B(n, k) with the operand layouts the backward
+// pass needs.  "rowspace" indices are sorted positions (routed) or token ids
+// (dense / shared).
+enum XAMode : int {
+  XA_ROWS = 0,   // A(m, k) = A[amap(r) * lda + k], r = rowspace row of output row m
+  XA_KMAJOR = 1, // A(m, k) = A[amap(p) * lda + a_col + m] * kscale(p), p = rowspace index k
+};
+enum XBMode : int {
+  XB_W_NT = 0,     // B(n, k) = Btab[g*nseg + seg][n * ldb + kin]      (weights, K contiguous)
+  XB_W_NN = 1,     // B(n, k) = Btab[g*nseg + seg][kin * ldb + n]      (weights, N contiguous)
+  XB_ACT_KMAJOR = 2, // B(n, k) = Bact[bmap(p) * ldb + b_col + n], p = rowspace index k
+};
+enum XSched : int {
+  XS_ROUTED = 0,  // M tiles from the routed schedule, full K
+  XS_DENSE = 1,   // groups x dense_rows, full K
+  XS_WGRAD = 2,   // groups x M x N output per group, K = rowspace range k_off[g] .. k_off[g+1] (or 0..K)
+};
+enum XEpi : int {
+  XE_STORE = 0,       // C[cmap(r) * ldc + g * c_group_col + n] = acc
+  XE_SWIGLU_BWD = 1,  // dh = row_w(r) * acc; with g, u saved: dg -> C[..+n], du -> C[..+du_off+n]
+  XE_WGRAD = 2,       // per-group output pointers, rows split at msplit into Ctab0 / Ctab1
+};
+
+struct XGemm {
+  int32_t sched_mode;
+  const MTile* sched;
+  const int32_t* sched_count;
+  int32_t m_tiles_bound;
+  int32_t bm;                  // schedule tile height (routed)
+  int32_t dense_rows;
+  int32_t groups;
+  const int32_t* k_off;        // XS_WGRAD: per-group K range (groups + 1 entries), null -> [0, K)
+  int32_t M, N, K;             // M: output rows per group (XS_WGRAD)
+  // A
+  int32_t a_mode;
+  const void* A;
+  int64_t lda;
+  int64_t a_col;               // XA_KMAJOR: column offset per group (times group index)
+  const int32_t* a_map;
+  const float* a_kscale;
+  // B
+  int32_t b_mode;
+  const void* const* Btab;
+  int64_t ldb;
+  int32_t kseg;
+  int32_t nseg;
+  const void* Bact;
+  const int32_t* b_map;
+  int64_t b_col;               // XB_ACT_KMAJOR: column offset per group (times group index)
+  // C
+  void* C;
+  int64_t ldc;
+  const int32_t* c_map;
+  int64_t c_group_col;
+  void* const* Ctab0;
+  void* const* Ctab1;
+  int32_t msplit;
+  // SwiGLU backward
+  const void* Gs;
+  const void* Us;
+  int64_t ld_gu;
+  int64_t gu_group_col;
+  const float* row_w;
+  int64_t du_off;
+};
+
+int launch_xgemm(const XGemm& g, int epi, int dtype, hipStream_t st);
+int launch_dw_dot(const void* dy, const void* o_slots, int64_t N, int k, int D, int dtype, float* dw, hipStream_t st);
+int launch_gate_bwd(const float* dw, const float* sel, int T, int k, float rs, float* dlog, hipStream_t st);
+int launch_dwgate(const void* x, const float* dlog, const int32_t* sorted_slot, const int32_t* sorted_token,
+                  const int32_t* offsets, int E, int D, int dtype, float* dgw, hipStream_t st);
+int launch_dx_final(const void* dx_slots, const void* dx_shared, const float* dlog, const int32_t* idx, const float* gw,
+                    int T, int D, int k, int dtype, void* dx, hipStream_t st);
+int launch_sched32(const int32_t* offsets, int E, int bm, MTile* sched, int32_t* sched_count, hipStream_t st);
+
 }  // namespace dsmoe
