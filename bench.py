@@ -15,7 +15,10 @@ Printed as one JSON line, with
   algorithmic FLOPs per launch (4*N*D*I, N = T*k slots) over its mean launch
   time measured with HIP events recorded by the library on the launch stream;
 * ``cpu_baseline``: the CPU restatement of the reference stacked path
-  (oracle/moe_ref.py) timed on this host on a bounded token sample.
+  (oracle/moe_ref.py) timed on this host on a bounded token sample;
+* ``fwd_bwd``: the training step of BASELINE config 4 (the config-3 layer at
+  T=16384: forward, then backward to dx, dW_gate and every expert's dW) with
+  its own per-stage times and CPU baseline (the oracle under autograd).
 """
 from __future__ import annotations
 
@@ -43,7 +46,9 @@ CONFIGS = {
     "c2": (8192, 1024, 16, 512, 4, 1, 1024, "bfloat16", "skew"),
     "c3": (8192, 2048, 64, 1408, 6, 2, 1408, "bfloat16", "zeros"),
     "c3_decode": (64, 2048, 64, 1408, 6, 2, 1408, "bfloat16", "zeros"),
+    "c4": (16384, 2048, 64, 1408, 6, 2, 1408, "bfloat16", "zeros"),
 }
+FWD_ONLY = ("c0", "c1", "c2", "c3", "c3_decode")
 
 
 def log(msg: str) -> None:
@@ -75,33 +80,121 @@ def make_layer(cfg, device, seed: int = 0):
     return x, gate_w, bias, (w1, w2, w3, s1, s2, s3)
 
 
-def cpu_baseline(cfg, x, gate_w, bias, weights, budget_s: float = 20.0):
+def cpu_baseline(cfg, x, gate_w, bias, weights, budget_s: float = 16.0, backward: bool = False):
     """Times oracle/moe_ref.py's restatement of the reference stacked forward
-    (models/moe.py:74-179) on this host on a token sample sized to the budget."""
+    (models/moe.py:74-179) on this host on a token sample sized to the budget;
+    with ``backward`` the autograd forward+backward of the same path."""
     import torch
     from oracle import moe_ref as R
     T, D, E, I, k, S, I_s, dt, _ = cfg
     cores = min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", "1024")))
     torch.set_num_threads(cores)
     w1, w2, w3, s1, s2, s3 = weights
-    cpu = lambda ts: [t.cpu() for t in ts]
-    p = R.MoEParams(gate_w.cpu(), bias.cpu(), cpu(w1), cpu(w2), cpu(w3), cpu(s1), cpu(s2), cpu(s3))
-    xs = x.cpu()
+    cpu = lambda ts: [t.detach().cpu() for t in ts]
+    p = R.MoEParams(gate_w.detach().cpu(), bias.cpu(), cpu(w1), cpu(w2), cpu(w3), cpu(s1), cpu(s2), cpu(s3))
+    xs = x.detach().cpu()
+    dys = torch.randn(xs.shape, generator=torch.Generator().manual_seed(2)).to(xs.dtype) if backward else None
+
+    def run(n):
+        if backward:
+            R.moe_forward_backward_ref(xs[:n], p, k, dys[:n])
+        else:
+            with torch.no_grad():
+                R.moe_forward_ref(xs[:n], p, k)
+
     n = min(T, 256)
     t0 = time.perf_counter()
-    R.moe_forward_ref(xs[:n], p, k)
+    run(n)
     dt1 = time.perf_counter() - t0
     n = int(min(T, max(n, n * (budget_s / 4.0) / max(dt1, 1e-6))))
     times = []
     for _ in range(3):
         t0 = time.perf_counter()
-        R.moe_forward_ref(xs[:n], p, k)
+        run(n)
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
+    what = "forward+backward (autograd) passes" if backward else "forward passes"
     return {"value": n / med, "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"first {n} of {T} tokens, same weights; median of 3 forward passes "
+            "sample": f"first {n} of {T} tokens, same weights; median of 3 {what} "
                       f"({med * 1e3:.1f} ms each) after 1 warm-up; torch {torch.__version__} "
                       f"{torch.backends.cpu.get_cpu_capability()}"}
+
+
+def time_steps(step, steps: int, warmup: int):
+    """-> (ms per step from events on the current stream, host wall ms per step)."""
+    import torch
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(steps):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    return ev0.elapsed_time(ev1) / steps, (time.perf_counter() - t0) * 1e3 / steps
+
+
+def stage_times(step, steps: int):
+    """Per-stage ms per step from the HIP events the library records on its
+    launch stream (a training step makes two library calls, forward and
+    backward, so totals are divided by steps, not by calls)."""
+    import dsmoe._lib as L
+    L.timing_enable(True)
+    try:
+        for _ in range(steps):
+            step()
+        torch_sync()
+        stages, _ncalls = L.timing_read()
+    finally:
+        L.timing_enable(False)
+    return {kname: v / steps for kname, v in stages.items()}
+
+
+def torch_sync():
+    import torch
+    torch.cuda.synchronize()
+
+
+def fwd_bwd_bench(name: str, dev, steps: int, warmup: int, with_cpu: bool):
+    """Training step of the layer (config 4): forward, then backward to dx,
+    dW_gate and every expert dW (torch.autograd.grad, no accumulation)."""
+    import torch
+    from dsmoe import moe_layer
+    cfg = CONFIGS[name]
+    T, D, E, I, k, S, I_s, dt, _ = cfg
+    log(f"[bench] fwd+bwd config {name}: T={T} D={D} E={E} I={I} k={k} S={S}x{I_s} {dt}")
+    x, gate_w, bias, weights = make_layer(cfg, dev)
+    w1, w2, w3, s1, s2, s3 = [[t.requires_grad_(True) for t in ws] for ws in weights]
+    x.requires_grad_(True)
+    gate_w.requires_grad_(True)
+    dy = torch.randn(x.shape, generator=torch.Generator(device=dev).manual_seed(2), device=dev).to(x.dtype)
+    leaves = [x, gate_w, *w1, *w2, *w3, *s1, *s2, *s3]
+
+    def step():
+        y = moe_layer(x, gate_w, bias, w1, w2, w3, s1, s2, s3, k=k, training=True)[0]
+        return torch.autograd.grad(y, leaves, dy)
+
+    ms, wall = time_steps(step, steps, warmup)
+    log(f"[bench] fwd+bwd timed {steps} steps: {ms:.3f} ms/step (host wall {wall:.3f} ms/step)")
+    stage_ms = stage_times(step, steps)
+    log(f"[bench] fwd+bwd stages (ms/call): " + ", ".join(f"{a}={b:.4f}" for a, b in stage_ms.items()))
+    N = T * k
+    flops = 3.0 * (6.0 * N * D * I + 6.0 * T * D * S * I_s)
+    gemm_ms = sum(v for s, v in stage_ms.items() if s.startswith(("gemm", "bwd_d")) and s != "bwd_dw_dot")
+    out = {"workload": f"{name}: DeepSeekMoE layer forward+backward (dx, dW_gate, every expert dW), T={T}, dim={D}, "
+                       f"{E} routed (inter {I}) top-{k}, {S} shared (inter {I_s}), {dt}, fp32 gate",
+           "value": T / (ms * 1e-3), "unit": "tokens/s", "ms_per_step": ms, "steps": steps, "warmup": warmup,
+           "gemm_tflops": flops / (gemm_ms * 1e-3) / 1e12 if gemm_ms > 0 else None,
+           "gemm_frac": flops / (gemm_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS if gemm_ms > 0 else None,
+           "stage_ms": stage_ms}
+    if with_cpu:
+        log("[bench] timing the CPU restatement of the reference path (fwd+bwd) ...")
+        out["cpu_baseline"] = cpu_baseline(cfg, x, gate_w, bias, (w1, w2, w3, s1, s2, s3), budget_s=12.0,
+                                           backward=True)
+        out["speedup_vs_cpu"] = out["value"] / out["cpu_baseline"]["value"]
+    return out
 
 
 def main() -> int:
@@ -109,7 +202,10 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="c3", choices=FWD_ONLY)
+    ap.add_argument("--fwd-bwd-config", default="c4", choices=sorted(CONFIGS),
+                    help="training-step workload reported under fwd_bwd")
+    ap.add_argument("--no-fwd-bwd", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="instead of the layer, run --steps device copies of this many MiB (counter calibration)")
@@ -120,7 +216,6 @@ def main() -> int:
         return 2
 
     import torch
-    import dsmoe._lib as L
     from dsmoe import moe_layer
 
     dev = torch.device("cuda:0")
@@ -143,28 +238,9 @@ def main() -> int:
         return moe_layer(x, gate_w, bias, w1, w2, w3, s1, s2, s3, k=k, training=False)
 
     with torch.no_grad():
-        for _ in range(args.warmup):
-            step()
-        torch.cuda.synchronize()
-        log(f"[bench] warm-up done ({args.warmup} steps)")
-        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        t0 = time.perf_counter()
-        ev0.record()
-        for _ in range(args.steps):
-            step()
-        ev1.record()
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-        ms = ev0.elapsed_time(ev1) / args.steps
-        log(f"[bench] timed {args.steps} steps: {ms:.3f} ms/step (host wall {wall * 1e3 / args.steps:.3f} ms/step)")
-
-        # per-stage HIP events recorded by the library on the launch stream
-        L.timing_enable(True)
-        for _ in range(args.steps):
-            step()
-        stages, ncalls = L.timing_read()
-        L.timing_enable(False)
-    stage_ms = {kname: v / max(ncalls, 1) for kname, v in stages.items()}
+        ms, wall = time_steps(step, args.steps, args.warmup)
+        log(f"[bench] timed {args.steps} steps: {ms:.3f} ms/step (host wall {wall:.3f} ms/step)")
+        stage_ms = stage_times(step, args.steps)
     log(f"[bench] stages (ms/call): " + ", ".join(f"{a}={b:.4f}" for a, b in stage_ms.items()))
 
     N = T * k
@@ -206,6 +282,10 @@ def main() -> int:
         log("[bench] timing the CPU restatement of the reference path ...")
         result["cpu_baseline"] = cpu_baseline(cfg, x, gate_w, bias, weights)
         result["speedup_vs_cpu"] = result["value"] / result["cpu_baseline"]["value"]
+    if not args.no_fwd_bwd:
+        del x, weights, w1, w2, w3, s1, s2, s3
+        result["fwd_bwd"] = fwd_bwd_bench(args.fwd_bwd_config, dev, max(3, args.steps // 4), max(1, args.warmup // 2),
+                                          not args.no_cpu_baseline)
     print(json.dumps(result), flush=True)
     return 0
 
