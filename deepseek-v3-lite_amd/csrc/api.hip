@@ -1,4 +1,5 @@
 // extern "C" entry points of libdsmoe.so (declared in include/dsmoe.h).
+#include <algorithm>
 #include <cstring>
 #include <initializer_list>
 #include <mutex>
@@ -455,10 +456,12 @@ struct BwdLayout {
   void* dx_slots;     // (N, D)    slot order
   void* dgdu_s;       // (T, 2 S I_s)
   void* dx_shared;    // (T, D)
+  int ks13, ks2;      // split-K of the shared-expert weight gradients (bf16 MFMA path)
+  float* part;        // fp32 split-K partials, max(ks13 * 2 I_s, ks2 * I_s) * S * D
   size_t total;
 };
 
-constexpr int BWD_BM = 64;  // schedule height used by the backward GEMMs
+constexpr int BWD_BM = 256;  // schedule height of the backward GEMMs (MFMA tile; the SIMT tiles split it)
 
 static BwdLayout bwd_layout(const dsmoe_dims& d, void* base) {
   Carver c(base);
@@ -492,6 +495,16 @@ static BwdLayout bwd_layout(const dsmoe_dims& d, void* base) {
   B.dx_slots = c.take<char>((size_t)N * d.D * es);
   B.dgdu_s = d.S ? c.take<char>((size_t)d.T * 2 * d.S * d.I_s * es) : nullptr;
   B.dx_shared = d.S ? c.take<char>((size_t)d.T * d.D * es) : nullptr;
+  B.ks13 = B.ks2 = 1;
+  B.part = nullptr;
+  if (d.S && d.dtype == DSMOE_BF16) {
+    B.ks13 = xgemm_pick_ksplit(xgemm_tiles(2 * (int64_t)d.I_s, d.D, d.S), d.T);
+    B.ks2 = xgemm_pick_ksplit(xgemm_tiles(d.D, d.I_s, d.S), d.T);
+    const int64_t n13 = B.ks13 > 1 ? (int64_t)B.ks13 * 2 * d.I_s : 0;
+    const int64_t n2 = B.ks2 > 1 ? (int64_t)B.ks2 * d.I_s : 0;
+    const int64_t nmax = std::max(n13, n2);
+    if (nmax) B.part = c.take<float>(nmax * d.S * d.D);
+  }
   B.total = c.used();
   return B;
 }
@@ -538,6 +551,14 @@ int dsmoe_moe_bwd(const void* x, const float* gate_w, const void* const* w1, con
     sw13h[2 * s] = sw1[s];
     sw13h[2 * s + 1] = sw3[s];
   }
+  // MFMA backward GEMMs need every weight and weight-gradient pointer 16-byte aligned
+  const bool mf = all_aligned16(w1, d.E) && all_aligned16(w2, d.E) && all_aligned16(w3, d.E) &&
+                  all_aligned16((const void* const*)dw1, d.E) && all_aligned16((const void* const*)dw2, d.E) &&
+                  all_aligned16((const void* const*)dw3, d.E) &&
+                  (d.S == 0 || (all_aligned16(sw1, d.S) && all_aligned16(sw2, d.S) && all_aligned16(sw3, d.S) &&
+                                all_aligned16((const void* const*)dsw1, d.S) &&
+                                all_aligned16((const void* const*)dsw2, d.S) &&
+                                all_aligned16((const void* const*)dsw3, d.S)));
   tm.begin(ST_BWD_PREP);
   // each table group is contiguous in the workspace, in this order
   rc = upload_ptr_lists({{w1, d.E}, {w3, d.E}, {w2, d.E}, {w13h.data(), 2 * d.E}}, B.w1, st);
@@ -567,7 +588,7 @@ int dsmoe_moe_bwd(const void* x, const float* gate_w, const void* const* w1, con
   h.C = B.dgdu; h.ldc = 2 * (int64_t)d.I; h.du_off = d.I;
   h.Gs = F.g; h.Us = F.u; h.ld_gu = d.I; h.row_w = F.sorted_w;
   tm.begin(ST_BWD_DH);
-  rc = launch_xgemm(h, XE_SWIGLU_BWD, d.dtype, st);
+  rc = launch_xgemm(h, XE_SWIGLU_BWD, d.dtype, mf, st);
   tm.end();
   if (rc) return rc;
   // routed dx_slot = [dg | du] [W1; W3], rows back to slot order
@@ -578,7 +599,7 @@ int dsmoe_moe_bwd(const void* x, const float* gate_w, const void* const* w1, con
   xg.b_mode = XB_W_NN; xg.Btab = B.w13; xg.ldb = d.D; xg.kseg = d.I; xg.nseg = 2;
   xg.C = B.dx_slots; xg.ldc = d.D; xg.c_map = F.sorted_slot;
   tm.begin(ST_BWD_DX);
-  rc = launch_xgemm(xg, XE_STORE, d.dtype, st);
+  rc = launch_xgemm(xg, XE_STORE, d.dtype, mf, st);
   tm.end();
   if (rc) return rc;
   // routed dW1, dW3 = [dg | du]^T X_e ; dW2 = (w dY)^T H_e
@@ -588,7 +609,7 @@ int dsmoe_moe_bwd(const void* x, const float* gate_w, const void* const* w1, con
   w13.b_mode = XB_ACT_KMAJOR; w13.Bact = x; w13.b_map = F.sorted_token; w13.ldb = d.D;
   w13.Ctab0 = B.dw1; w13.Ctab1 = B.dw3; w13.msplit = d.I; w13.ldc = d.D;
   tm.begin(ST_BWD_DW13);
-  rc = launch_xgemm(w13, XE_WGRAD, d.dtype, st);
+  rc = launch_xgemm(w13, XE_WGRAD, d.dtype, mf, st);
   tm.end();
   if (rc) return rc;
   XGemm w2g = xdesc_zero();
@@ -597,7 +618,7 @@ int dsmoe_moe_bwd(const void* x, const float* gate_w, const void* const* w1, con
   w2g.b_mode = XB_ACT_KMAJOR; w2g.Bact = F.h; w2g.ldb = d.I;
   w2g.Ctab0 = B.dw2; w2g.Ctab1 = B.dw2; w2g.msplit = d.D; w2g.ldc = d.I;
   tm.begin(ST_BWD_DW2);
-  rc = launch_xgemm(w2g, XE_WGRAD, d.dtype, st);
+  rc = launch_xgemm(w2g, XE_WGRAD, d.dtype, mf, st);
   tm.end();
   if (rc) return rc;
 
@@ -610,7 +631,7 @@ int dsmoe_moe_bwd(const void* x, const float* gate_w, const void* const* w1, con
     sh.C = B.dgdu_s; sh.ldc = 2 * SIs; sh.c_group_col = 2 * (int64_t)d.I_s; sh.du_off = d.I_s;
     sh.Gs = F.gs; sh.Us = F.us; sh.ld_gu = SIs; sh.gu_group_col = d.I_s;
     tm.begin(ST_BWD_DH_SHARED);
-    rc = launch_xgemm(sh, XE_SWIGLU_BWD, d.dtype, st);
+    rc = launch_xgemm(sh, XE_SWIGLU_BWD, d.dtype, mf, st);
     tm.end();
     if (rc) return rc;
     XGemm sx = xdesc_zero();
@@ -619,7 +640,7 @@ int dsmoe_moe_bwd(const void* x, const float* gate_w, const void* const* w1, con
     sx.b_mode = XB_W_NN; sx.Btab = B.sw13; sx.ldb = d.D; sx.kseg = d.I_s; sx.nseg = 2 * d.S;
     sx.C = B.dx_shared; sx.ldc = d.D;
     tm.begin(ST_BWD_DX_SHARED);
-    rc = launch_xgemm(sx, XE_STORE, d.dtype, st);
+    rc = launch_xgemm(sx, XE_STORE, d.dtype, mf, st);
     tm.end();
     if (rc) return rc;
     XGemm s13 = xdesc_zero();
@@ -627,14 +648,16 @@ int dsmoe_moe_bwd(const void* x, const float* gate_w, const void* const* w1, con
     s13.a_mode = XA_KMAJOR; s13.A = B.dgdu_s; s13.lda = 2 * SIs; s13.a_col = 2 * (int64_t)d.I_s;
     s13.b_mode = XB_ACT_KMAJOR; s13.Bact = x; s13.ldb = d.D;
     s13.Ctab0 = B.dsw1; s13.Ctab1 = B.dsw3; s13.msplit = d.I_s; s13.ldc = d.D;
+    s13.ksplit = B.ks13; s13.part = B.part;
     XGemm s2 = xdesc_zero();
     s2.sched_mode = XS_WGRAD; s2.groups = d.S; s2.M = d.D; s2.N = d.I_s; s2.K = d.T;
     s2.a_mode = XA_KMAJOR; s2.A = dy; s2.lda = d.D;
     s2.b_mode = XB_ACT_KMAJOR; s2.Bact = F.hs; s2.ldb = SIs; s2.b_col = d.I_s;
     s2.Ctab0 = B.dsw2; s2.Ctab1 = B.dsw2; s2.msplit = d.D; s2.ldc = d.I_s;
+    s2.ksplit = B.ks2; s2.part = B.part;
     tm.begin(ST_BWD_DW_SHARED);
-    rc = launch_xgemm(s13, XE_WGRAD, d.dtype, st);
-    if (!rc) rc = launch_xgemm(s2, XE_WGRAD, d.dtype, st);
+    rc = launch_xgemm(s13, XE_WGRAD, d.dtype, mf, st);
+    if (!rc) rc = launch_xgemm(s2, XE_WGRAD, d.dtype, mf, st);
     tm.end();
     if (rc) return rc;
   }

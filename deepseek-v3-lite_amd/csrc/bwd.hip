@@ -11,6 +11,8 @@
 //                    reduction over the sorted order.
 //   dx_final_kernel  dx[t] = sum_j (ascending expert id) dx_slot[t*k+j]
 //                    + dx_shared[t] + sum_j dlogit[t,j] W_gate[e_j], fp32, one rounding.
+#include <algorithm>
+
 #include "common.h"
 
 namespace dsmoe {
@@ -91,6 +93,138 @@ __global__ __launch_bounds__(256) void dx_final_kernel(const T* __restrict__ dx_
   dx[t * (int64_t)D + d] = from_f<T>(acc);
 }
 
+// Vectorised forms (VEC consecutive columns per thread, 16-byte loads).
+template <typename T>
+struct Vec16;
+template <>
+struct Vec16<bf16_t> {
+  static constexpr int N = 8;
+  __device__ static void load(const bf16_t* p, float (&v)[8]) {
+    const uint4 u = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+  __device__ static void store(bf16_t* p, const float (&v)[8]) {
+    uint4 u;
+    u.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
+    u.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
+    u.z = (uint32_t)f2bf(v[4]) | ((uint32_t)f2bf(v[5]) << 16);
+    u.w = (uint32_t)f2bf(v[6]) | ((uint32_t)f2bf(v[7]) << 16);
+    *reinterpret_cast<uint4*>(p) = u;
+  }
+};
+template <>
+struct Vec16<float> {
+  static constexpr int N = 4;
+  __device__ static void load(const float* p, float (&v)[4]) {
+    const float4 u = *reinterpret_cast<const float4*>(p);
+    v[0] = u.x; v[1] = u.y; v[2] = u.z; v[3] = u.w;
+  }
+  __device__ static void store(float* p, const float (&v)[4]) {
+    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  }
+};
+
+// dx[t] per token (one block): same order and rounding as dx_final_kernel.
+template <typename T>
+__global__ __launch_bounds__(256) void dx_final_vec_kernel(const T* __restrict__ dx_slots, const T* __restrict__ dx_shared,
+                                                           const float* __restrict__ dlog, const int32_t* __restrict__ idx,
+                                                           const float* __restrict__ gw, int D, int k,
+                                                           T* __restrict__ dx) {
+  constexpr int V = Vec16<T>::N;
+  const int64_t t = blockIdx.x;
+  int ord[MAX_TOPK], ev[MAX_TOPK];
+  for (int j = 0; j < k; ++j) {  // ascending expert id (insertion sort, k <= 16)
+    const int e = idx[t * k + j];
+    int p = j;
+    while (p > 0 && ev[p - 1] > e) {
+      ev[p] = ev[p - 1];
+      ord[p] = ord[p - 1];
+      --p;
+    }
+    ev[p] = e;
+    ord[p] = j;
+  }
+  for (int c = threadIdx.x; c * V < D; c += blockDim.x) {
+    const int d = c * V;
+    float acc[V], v[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+    for (int q = 0; q < k; ++q) {
+      Vec16<T>::load(dx_slots + (t * k + ord[q]) * (int64_t)D + d, v);
+#pragma unroll
+      for (int i = 0; i < V; ++i) acc[i] += v[i];
+    }
+    if (dx_shared) {
+      Vec16<T>::load(dx_shared + t * (int64_t)D + d, v);
+#pragma unroll
+      for (int i = 0; i < V; ++i) acc[i] += v[i];
+    }
+    for (int q = 0; q < k; ++q) {
+      const float dl = dlog[t * k + ord[q]];
+      const float* grow = gw + (int64_t)ev[q] * D + d;
+#pragma unroll
+      for (int i = 0; i < V; i += 4) {
+        const float4 w4 = *reinterpret_cast<const float4*>(grow + i);
+        acc[i] = fmaf(dl, w4.x, acc[i]);
+        acc[i + 1] = fmaf(dl, w4.y, acc[i + 1]);
+        acc[i + 2] = fmaf(dl, w4.z, acc[i + 2]);
+        acc[i + 3] = fmaf(dl, w4.w, acc[i + 3]);
+      }
+    }
+    Vec16<T>::store(dx + t * (int64_t)D + d, acc);
+  }
+}
+
+// dW_gate[e, cols] for one expert and 64 * VEC columns: 4 row groups of 64
+// threads take rows p0 + g, p0 + g + 4, ... of the expert's sorted rows; the
+// 4 partial sums are then added in group order (deterministic).
+template <typename T>
+__global__ __launch_bounds__(256) void dwgate_vec_kernel(const T* __restrict__ x, const float* __restrict__ dlog,
+                                                         const int32_t* __restrict__ sorted_slot,
+                                                         const int32_t* __restrict__ sorted_token,
+                                                         const int32_t* __restrict__ offsets, int D,
+                                                         float* __restrict__ dgw) {
+  constexpr int V = Vec16<T>::N;
+  __shared__ float red[3][64 * V];
+  const int e = blockIdx.y;
+  const int grp = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const int d = (blockIdx.x * 64 + l) * V;
+  const bool live = d < D;
+  const int p0 = offsets[e], p1 = offsets[e + 1];
+  float acc[V], v[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+  if (live) {
+    for (int p = p0 + grp; p < p1; p += 4) {
+      const float w = dlog[sorted_slot[p]];
+      Vec16<T>::load(x + (int64_t)sorted_token[p] * D + d, v);
+#pragma unroll
+      for (int i = 0; i < V; ++i) acc[i] = fmaf(w, v[i], acc[i]);
+    }
+  }
+  if (grp > 0) {
+#pragma unroll
+    for (int i = 0; i < V; ++i) red[grp - 1][l * V + i] = acc[i];
+  }
+  __syncthreads();
+  if (grp == 0 && live) {
+#pragma unroll
+    for (int gi = 0; gi < 3; ++gi)
+#pragma unroll
+      for (int i = 0; i < V; ++i) acc[i] += red[gi][l * V + i];
+    float* o = dgw + (int64_t)e * D + d;
+#pragma unroll
+    for (int i = 0; i < V; i += 4) *reinterpret_cast<float4*>(o + i) = make_float4(acc[i], acc[i + 1], acc[i + 2], acc[i + 3]);
+  }
+}
+
+static bool al16p(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 // ---------------------------------------------------------------- launchers
 int launch_dw_dot(const void* dy, const void* o_slots, int64_t N, int k, int D, int dtype, float* dw,
                   hipStream_t st) {
@@ -113,6 +247,17 @@ int launch_gate_bwd(const float* dw, const float* sel, int T, int k, float rs, f
 
 int launch_dwgate(const void* x, const float* dlog, const int32_t* sorted_slot, const int32_t* sorted_token,
                   const int32_t* offsets, int E, int D, int dtype, float* dgw, hipStream_t st) {
+  const int V = dtype == DSMOE_BF16 ? 8 : 4;
+  if (D % V == 0 && al16p(x) && al16p(dgw)) {
+    const dim3 gv((unsigned)cdiv(D, 64 * V), (unsigned)E);
+    if (dtype == DSMOE_BF16)
+      hipLaunchKernelGGL(dwgate_vec_kernel<bf16_t>, gv, dim3(256), 0, st, static_cast<const bf16_t*>(x), dlog,
+                         sorted_slot, sorted_token, offsets, D, dgw);
+    else
+      hipLaunchKernelGGL(dwgate_vec_kernel<float>, gv, dim3(256), 0, st, static_cast<const float*>(x), dlog,
+                         sorted_slot, sorted_token, offsets, D, dgw);
+    return check_launch("dwgate_vec");
+  }
   const dim3 grid((unsigned)cdiv(D, 256), (unsigned)E);
   if (dtype == DSMOE_BF16)
     hipLaunchKernelGGL(dwgate_kernel<bf16_t>, grid, dim3(256), 0, st, static_cast<const bf16_t*>(x), dlog, sorted_slot,
@@ -126,6 +271,19 @@ int launch_dwgate(const void* x, const float* dlog, const int32_t* sorted_slot, 
 int launch_dx_final(const void* dx_slots, const void* dx_shared, const float* dlog, const int32_t* idx, const float* gw,
                     int T, int D, int k, int dtype, void* dx, hipStream_t st) {
   if (T == 0) return DSMOE_OK;
+  const int V = dtype == DSMOE_BF16 ? 8 : 4;
+  if (D % V == 0 && al16p(dx_slots) && al16p(dx) && al16p(gw) && (!dx_shared || al16p(dx_shared))) {
+    const unsigned threads = (unsigned)std::min<int64_t>(256, cdiv(cdiv(D, V), 64) * 64);
+    if (dtype == DSMOE_BF16)
+      hipLaunchKernelGGL(dx_final_vec_kernel<bf16_t>, dim3((unsigned)T), dim3(threads), 0, st,
+                         static_cast<const bf16_t*>(dx_slots), static_cast<const bf16_t*>(dx_shared), dlog, idx, gw, D,
+                         k, static_cast<bf16_t*>(dx));
+    else
+      hipLaunchKernelGGL(dx_final_vec_kernel<float>, dim3((unsigned)T), dim3(threads), 0, st,
+                         static_cast<const float*>(dx_slots), static_cast<const float*>(dx_shared), dlog, idx, gw, D, k,
+                         static_cast<float*>(dx));
+    return check_launch("dx_final_vec");
+  }
   const unsigned grid = (unsigned)cdiv((int64_t)T * D, 256);
   if (dtype == DSMOE_BF16)
     hipLaunchKernelGGL(dx_final_kernel<bf16_t>, dim3(grid), dim3(256), 0, st, static_cast<const bf16_t*>(dx_slots),

@@ -234,9 +234,22 @@ struct XGemm {
   int64_t gu_group_col;
   const float* row_w;
   int64_t du_off;
+  // XS_WGRAD split-K (MFMA path only): each group's K range is cut into
+  // ksplit slab-aligned parts; part i writes fp32 partial sums to
+  // part[((i * groups + grp) * M + m) * N + n] and a second kernel adds the
+  // parts in ascending i and rounds once.  ksplit <= 1: direct store.
+  int32_t ksplit;
+  float* part;
 };
 
-int launch_xgemm(const XGemm& g, int epi, int dtype, hipStream_t st);
+// Backward grouped GEMM: MFMA kernel when dtype is bf16, allow_mfma is set
+// (the caller checked the alignment of every pointer-table entry) and the
+// shapes fit (xgemm_mfma_ok); fp32-FMA tiles otherwise.
+int launch_xgemm(const XGemm& g, int epi, int dtype, bool allow_mfma, hipStream_t st);
+bool xgemm_mfma_ok(const XGemm& g, int epi);
+int launch_xgemm_mfma(const XGemm& g, int epi, hipStream_t st);
+int xgemm_pick_ksplit(int64_t tiles, int64_t k_len);
+int64_t xgemm_tiles(int64_t M, int64_t N, int groups);
 int launch_dw_dot(const void* dy, const void* o_slots, int64_t N, int k, int D, int dtype, float* dw, hipStream_t st);
 int launch_gate_bwd(const float* dw, const float* sel, int T, int k, float rs, float* dlog, hipStream_t st);
 int launch_dwgate(const void* x, const float* dlog, const int32_t* sorted_slot, const int32_t* sorted_token,

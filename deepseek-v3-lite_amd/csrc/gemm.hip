@@ -28,22 +28,11 @@
 #include <cstring>
 
 #include "gemm_tile.h"
+#include "mfma.h"
 
 namespace dsmoe {
 
 // =============================================================== MFMA kernel
-typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
-typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));  // native vector: stays in registers
-
-constexpr int MF_K = 64;  // K slab per pipeline stage (8 chunks of 16 bytes per row)
-
-// LDS row = 64 bf16 = 128 bytes = 8 chunks of 16 bytes.  gfx950 serves a
-// ds_read_b128 16 lanes (256 bytes, two rows) per cycle; chunk c of row r is
-// stored at c ^ ((r >> 1) & 7), so the 16 rows read at one logical chunk by
-// a fragment load land on 16 distinct 16-byte bank groups.
-__device__ __forceinline__ int swz(int row, int chunk) { return row * MF_K + ((chunk ^ ((row >> 1) & 7)) << 3); }
-
 template <int EPI, int WM, int WN, int TM, int TN>
 struct MfCfg {
   static constexpr int NB = (EPI == EPI_SWIGLU) ? 2 : 1;

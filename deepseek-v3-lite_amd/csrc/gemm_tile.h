@@ -56,4 +56,67 @@ __device__ __forceinline__ bool tile_for_block(const GemmDesc& g, int n_tiles, i
   return true;
 }
 
+// Backward GEMM tile lookup for the three XGemm schedules (same XCD-chunked
+// enumeration as tile_for_block).  Returns false for surplus blocks.
+//   XS_ROUTED  schedule entries of height bm, split into bm / BMK sub-tiles;
+//   XS_DENSE   every group covers rows [0, dense_rows);
+//   XS_WGRAD   M = weight rows per group; K range = k_off[grp] .. k_off[grp+1],
+//              cut into ksplit parts of whole 64-row slabs (part index -> split).
+template <int BMK, int BNK>
+__device__ __forceinline__ bool xtile(const XGemm& g, int& grp, int& row0, int& rows, int& n_tile, int& kbeg, int& kend,
+                                      int& split) {
+  const int n_tiles = (int)cdiv(g.N, BNK);
+  int64_t m_total;
+  int sub = 1, tpg = 0;
+  if (g.sched_mode == XS_ROUTED) {
+    sub = g.bm / BMK;
+    m_total = (int64_t)(*g.sched_count) * sub;
+  } else if (g.sched_mode == XS_DENSE) {
+    tpg = (int)cdiv(g.dense_rows, BMK);
+    m_total = (int64_t)tpg * g.groups;
+  } else {
+    tpg = (int)cdiv(g.M, BMK);
+    m_total = (int64_t)tpg * g.groups * max(g.ksplit, 1);
+  }
+  const int64_t total = m_total * n_tiles;
+  const int64_t per_xcd = cdiv(total, 8);
+  const int64_t j = blockIdx.x >> 3;
+  if (j >= per_xcd) return false;
+  const int64_t lin = (int64_t)(blockIdx.x & 7) * per_xcd + j;
+  if (lin >= total) return false;
+  const int64_t mt = lin / n_tiles;
+  n_tile = (int)(lin - mt * n_tiles);
+  kbeg = 0;
+  kend = g.K;
+  split = 0;
+  if (g.sched_mode == XS_ROUTED) {
+    const MTile t = g.sched[mt / sub];
+    const int s = (int)(mt % sub);
+    grp = t.group;
+    row0 = t.row0 + s * BMK;
+    rows = min(BMK, t.rows - s * BMK);
+    if (rows <= 0) return false;
+  } else {
+    const int ks = (g.sched_mode == XS_WGRAD) ? max(g.ksplit, 1) : 1;
+    const int gs = (int)(mt / tpg);  // (group, split) in group-major order
+    grp = gs / ks;
+    split = gs - grp * ks;
+    const int m = (int)(mt - (int64_t)gs * tpg);
+    row0 = m * BMK;
+    rows = min(BMK, (g.sched_mode == XS_DENSE ? g.dense_rows : g.M) - row0);
+    if (g.sched_mode == XS_WGRAD && g.k_off) {
+      kbeg = g.k_off[grp];
+      kend = g.k_off[grp + 1];
+    }
+    if (ks > 1) {
+      const int len = kend - kbeg;
+      const int chunk = (int)cdiv(cdiv(len, ks), 64) * 64;
+      const int b = kbeg + split * chunk;
+      kend = min(kend, b + chunk);
+      kbeg = min(b, kend);
+    }
+  }
+  return true;
+}
+
 }  // namespace dsmoe

@@ -13,60 +13,13 @@
 // ascending order, so dW accumulation is deterministic with no atomics.
 //
 // xgemm_simt_kernel: fp32 FMA tiles for every mode (fp32 path and fallback).
-#include "common.h"
+#include "gemm_tile.h"
 
 namespace dsmoe {
 
 constexpr int XS_BM = 64;
 constexpr int XS_BN = 64;
 constexpr int XS_BK = 16;
-
-// Tile lookup for the three schedules.  Returns false for surplus blocks.
-// XS_ROUTED: schedule entries of height bm are split into bm / bm_k sub-tiles.
-template <int BMK, int BNK>
-__device__ __forceinline__ bool xtile(const XGemm& g, int& grp, int& row0, int& rows, int& n_tile, int& kbeg, int& kend) {
-  const int n_tiles = (int)cdiv(g.N, BNK);
-  int64_t m_total;
-  int sub = 1, tpg = 0;
-  if (g.sched_mode == XS_ROUTED) {
-    sub = g.bm / BMK;
-    m_total = (int64_t)(*g.sched_count) * sub;
-  } else if (g.sched_mode == XS_DENSE) {
-    tpg = (int)cdiv(g.dense_rows, BMK);
-    m_total = (int64_t)tpg * g.groups;
-  } else {
-    tpg = (int)cdiv(g.M, BMK);
-    m_total = (int64_t)tpg * g.groups;
-  }
-  const int64_t total = m_total * n_tiles;
-  const int64_t per_xcd = cdiv(total, 8);
-  const int64_t j = blockIdx.x >> 3;
-  if (j >= per_xcd) return false;
-  const int64_t lin = (int64_t)(blockIdx.x & 7) * per_xcd + j;
-  if (lin >= total) return false;
-  const int64_t mt = lin / n_tiles;
-  n_tile = (int)(lin - mt * n_tiles);
-  kbeg = 0;
-  kend = g.K;
-  if (g.sched_mode == XS_ROUTED) {
-    const MTile t = g.sched[mt / sub];
-    const int s = (int)(mt % sub);
-    grp = t.group;
-    row0 = t.row0 + s * BMK;
-    rows = min(BMK, t.rows - s * BMK);
-    if (rows <= 0) return false;
-  } else {
-    grp = (int)(mt / tpg);
-    const int m = (int)(mt - (int64_t)grp * tpg);
-    row0 = m * BMK;
-    rows = min(BMK, (g.sched_mode == XS_DENSE ? g.dense_rows : g.M) - row0);
-    if (g.sched_mode == XS_WGRAD && g.k_off) {
-      kbeg = g.k_off[grp];
-      kend = g.k_off[grp + 1];
-    }
-  }
-  return true;
-}
 
 template <typename T>
 __device__ __forceinline__ float xa_load(const XGemm& g, int grp, int row0, int m, int k) {
@@ -126,8 +79,8 @@ template <typename T, int EPI>
 __global__ __launch_bounds__(256) void xgemm_simt_kernel(const XGemm g) {
   __shared__ float As[XS_BK][XS_BM + 4];
   __shared__ float Bs[XS_BK][XS_BN + 4];
-  int grp, row0, rows, n_tile, kbeg, kend;
-  if (!xtile<XS_BM, XS_BN>(g, grp, row0, rows, n_tile, kbeg, kend)) return;
+  int grp, row0, rows, n_tile, kbeg, kend, split;
+  if (!xtile<XS_BM, XS_BN>(g, grp, row0, rows, n_tile, kbeg, kend, split)) return;
   const int n0 = n_tile * XS_BN;
   const int tid = threadIdx.x;
   const int ty = tid >> 4, tx = tid & 15;
@@ -211,8 +164,14 @@ static int launch_xsimt(const XGemm& g, int epi, hipStream_t st) {
   return check_launch("xgemm_simt");
 }
 
-int launch_xgemm(const XGemm& g, int epi, int dtype, hipStream_t st) {
+int launch_xgemm(const XGemm& g, int epi, int dtype, bool allow_mfma, hipStream_t st) {
   if (g.N <= 0 || (g.sched_mode == XS_WGRAD ? g.M <= 0 : false)) return DSMOE_OK;
+  if (dtype == DSMOE_BF16 && allow_mfma && xgemm_mfma_ok(g, epi)) return launch_xgemm_mfma(g, epi, st);
+  if (g.ksplit > 1) {  // the FMA tiles store directly
+    XGemm g1 = g;
+    g1.ksplit = 1;
+    return launch_xgemm(g1, epi, dtype, false, st);
+  }
   if (g.sched_mode == XS_ROUTED && g.bm % XS_BM != 0)
     return fail(DSMOE_ERR_INVALID, "xgemm: schedule height must be a multiple of 64");
   if (dtype == DSMOE_BF16) return launch_xsimt<bf16_t>(g, epi, st);

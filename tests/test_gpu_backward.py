@@ -88,7 +88,9 @@ def _oracle_case(case, seed=0):
 
 
 @pytest.mark.parametrize("case", [CS.C1.with_tokens(512), CS.C3.with_tokens(384),
-                                  CS.Case("bf16_small", 300, 128, 8, 64, 3, 1, 96, torch.bfloat16, "normal", 1.5)],
+                                  CS.Case("bf16_small", 300, 128, 8, 64, 3, 1, 96, torch.bfloat16, "normal", 1.5),
+                                  # +3 bias on experts 0 and 1 with k=2: experts 2..7 get no rows
+                                  CS.Case("bf16_skew_empty", 320, 256, 8, 128, 2, 1, 128, torch.bfloat16, "skew")],
                          ids=lambda c: c.name)
 def test_backward_bf16_vs_oracle(case):
     ref, f32, out = _oracle_case(case)
@@ -107,6 +109,11 @@ def test_backward_bf16_vs_oracle(case):
     for nm, a, b, truth in pairs:
         ours, theirs = _relerr(a, truth), _relerr(b, truth)
         assert ours <= max(2.0 * theirs, 1e-3), f"{nm}: rel L2 err vs fp32 {ours:.3e}, bf16 reference {theirs:.3e}"
+    # experts that received no rows get exactly zero weight gradients
+    counts = torch.bincount(out["idx"].flatten(), minlength=case.E)
+    for e in torch.nonzero(counts == 0).flatten().tolist():
+        for nm in ("dw1", "dw2", "dw3"):
+            assert not out[nm][e].any(), f"{nm}[{e}] of an expert with no rows is not zero"
 
 
 def test_backward_is_deterministic():
