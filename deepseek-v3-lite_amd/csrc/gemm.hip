@@ -53,7 +53,7 @@ template <int N>
 __device__ __forceinline__ void load_rows(const bf16_t* __restrict__ base, const int64_t (&off)[N], int k0,
                                           u32x4_t (&r)[N]) {
 #pragma unroll
-  for (int i = 0; i < N; ++i) r[i] = *reinterpret_cast<const u32x4_t*>(base + off[i] + k0);
+  for (int i = 0; i < N; ++i) r[i] = ldg16(base + off[i] + k0);
 }
 
 template <int N, int RSTEP>

@@ -49,8 +49,6 @@ __device__ __forceinline__ int xswz(int row, int chunk) {
   return row * MF_K + ((chunk ^ (((row >> 1) ^ ((row >> 2) & 4)) & 7)) << 3);
 }
 
-__device__ __forceinline__ u32x4_t ldg16(const bf16_t* p) { return *reinterpret_cast<const u32x4_t*>(p); }
-
 // Scales the 8 bf16 of v by s (fp32 product, rounded to nearest even once).
 __device__ __forceinline__ u32x4_t scale8(u32x4_t v, float s) {
   u32x4_t o;
@@ -75,9 +73,14 @@ __device__ __forceinline__ void km_store(bf16_t* __restrict__ s, int cc, int odd
     o[2 * d + 1].y = (v[2][d] >> 16) | (v[3][d] & 0xffff0000u);
   }
   const int c = q >> 1, half = q & 1;
+  const uint32_t msk = 0u - (uint32_t)odd;  // all ones for odd column chunks
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const u32x2_t val = odd ? o[i ^ 1] : o[i];
+    // odd lanes write column i ^ 1 at this step (a lane-dependent register
+    // choice written as a bit blend, so no dynamic register indexing)
+    u32x2_t val;
+    val.x = (o[i].x & ~msk) | (o[i ^ 1].x & msk);
+    val.y = (o[i].y & ~msk) | (o[i ^ 1].y & msk);
     *reinterpret_cast<u32x2_t*>(s + xswz(8 * cc + (i ^ odd), c) + 4 * half) = val;
   }
 }
@@ -142,6 +145,22 @@ __global__ __launch_bounds__(XM_THREADS) void xgemm_mfma_kernel(const XGemm g) {
   }
 
   u32x4_t ra[4], rb[4];
+  // Mapped K-major rows: the row indices (and scales) of a slab are fetched
+  // one slab ahead of its data, so the data loads never wait for them.
+  int32_t a_rows[4] = {0, 0, 0, 0}, b_rows[4] = {0, 0, 0, 0};
+  float a_sc[4] = {1.0f, 1.0f, 1.0f, 1.0f};     // fetched for the next slab to load
+  float a_sc_ld[4] = {1.0f, 1.0f, 1.0f, 1.0f};  // of the slab whose data is in flight
+  auto fetch_rows = [&](int k0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int kk = min(k0 + 4 * q + j, kend - 1);
+      if (AMODE == XA_KMAJOR) {
+        a_rows[j] = as.map ? as.map[kk] : kk;
+        if (as.kscale) a_sc[j] = as.kscale[kk];
+      }
+      if (BMODE == XB_ACT_KMAJOR) b_rows[j] = bs.map ? bs.map[kk] : kk;
+    }
+  };
   auto load_slab = [&](int k0) {
     // A
     if (AMODE == XA_ROWS) {
@@ -151,26 +170,14 @@ __global__ __launch_bounds__(XM_THREADS) void xgemm_mfma_kernel(const XGemm g) {
     } else {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int k = k0 + 4 * q + j;
-        const int kk = min(k, kend - 1);
-        const int64_t row = as.map ? (int64_t)as.map[kk] : (int64_t)kk;
-        u32x4_t v = ldg16(as.base + row * as.ld + a_col);
-        if (as.kscale) v = scale8(v, as.kscale[kk]);
-        if (k >= kend) v = u32x4_t{0u, 0u, 0u, 0u};
-        ra[j] = v;
+        ra[j] = ldg16(as.base + (int64_t)a_rows[j] * as.ld + a_col);
+        a_sc_ld[j] = a_sc[j];
       }
     }
     // B
     if (BMODE == XB_ACT_KMAJOR) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int k = k0 + 4 * q + j;
-        const int kk = min(k, kend - 1);
-        const int64_t row = bs.map ? (int64_t)bs.map[kk] : (int64_t)kk;
-        u32x4_t v = ldg16(bs.base + row * bs.ld + b_col);
-        if (k >= kend) v = u32x4_t{0u, 0u, 0u, 0u};
-        rb[j] = v;
-      }
+      for (int j = 0; j < 4; ++j) rb[j] = ldg16(bs.base + (int64_t)b_rows[j] * bs.ld + b_col);
     } else {
       // weights: the 64-row slab lies inside one K segment (kseg % 64 == 0)
       const int seg = k0 / g.kseg;
@@ -178,6 +185,22 @@ __global__ __launch_bounds__(XM_THREADS) void xgemm_mfma_kernel(const XGemm g) {
       const int kin = k0 - seg * g.kseg + 4 * q;
 #pragma unroll
       for (int j = 0; j < 4; ++j) rb[j] = ldg16(W + (int64_t)(kin + j) * g.ldb + b_col);
+    }
+  };
+  // Rows past the K range read a clamped valid row; zero them (and apply the
+  // per-row scale) once the data has arrived, right before the LDS store.
+  auto fix_rows = [&](int k0) {
+    if (AMODE == XA_KMAJOR) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (as.kscale) ra[j] = scale8(ra[j], a_sc_ld[j]);
+        if (k0 + 4 * q + j >= kend) ra[j] = u32x4_t{0u, 0u, 0u, 0u};
+      }
+    }
+    if (BMODE == XB_ACT_KMAJOR) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (k0 + 4 * q + j >= kend) rb[j] = u32x4_t{0u, 0u, 0u, 0u};
     }
   };
   auto store_slab = [&](bf16_t* s) {
@@ -200,14 +223,20 @@ __global__ __launch_bounds__(XM_THREADS) void xgemm_mfma_kernel(const XGemm g) {
 
   const int nk = (kend > kbeg) ? (int)cdiv(kend - kbeg, MF_K) : 0;
   if (nk > 0) {
+    fetch_rows(kbeg);
     load_slab(kbeg);
+    if (nk > 1) fetch_rows(kbeg + MF_K);
+    fix_rows(kbeg);
     store_slab(smem_x);
   }
   __syncthreads();
   for (int kb = 0; kb < nk; ++kb) {
     const int cur = kb & 1;
     const bool more = kb + 1 < nk;
-    if (more) load_slab(kbeg + (kb + 1) * MF_K);
+    if (more) {
+      load_slab(kbeg + (kb + 1) * MF_K);
+      if (kb + 2 < nk) fetch_rows(kbeg + (kb + 2) * MF_K);
+    }
     const bf16_t* sA = smem_x + cur * XM_STAGE;
     const bf16_t* sB = sA + XM_A_EL;
 #pragma unroll
@@ -226,7 +255,10 @@ __global__ __launch_bounds__(XM_THREADS) void xgemm_mfma_kernel(const XGemm g) {
         for (int ni = 0; ni < XM_TN; ++ni)
           acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[ni], af[mi], acc[mi][ni], 0, 0, 0);
     }
-    if (more) store_slab(smem_x + (cur ^ 1) * XM_STAGE);
+    if (more) {
+      fix_rows(kbeg + (kb + 1) * MF_K);
+      store_slab(smem_x + (cur ^ 1) * XM_STAGE);
+    }
     __syncthreads();
   }
 
