@@ -159,8 +159,8 @@ int launch_sched_from_offsets(const int64_t* offsets64, int E, int bm, int64_t r
 // be built with the same height.
 bool gemm_mfma_eligible(const GemmDesc& g, int dtype, bool allow_mfma);
 int gemm_tile_m(bool mfma);
-bool gemm_dl_ok(const GemmDesc& g, int64_t a_rows);
-int launch_gemm_dl(const GemmDesc& g, int epi, const float* row_scale, hipStream_t st);
+bool gemm_qw_ok(const GemmDesc& g);
+int launch_gemm_qw(const GemmDesc& g, int epi, const float* row_scale, hipStream_t st);
 int launch_grouped_gemm(const GemmDesc& g, int epi, int dtype, const float* row_scale, bool allow_mfma,
                         hipStream_t st);
 int launch_combine(const void* o_slots, const float* w, const int32_t* idx, const void* shared, const dsmoe_dims& d,

@@ -13,7 +13,9 @@
 // the tile list so the weight tiles of an expert stay in that XCD's L2.  The
 // grid is sized from a host bound; blocks past the device count exit.
 //
-// Kernels:
+// Kernels (the default bf16 path is gemm_qw_kernel in gemm_qw.hip; this file
+// holds the register-staged MFMA kernel for the shapes that one does not
+// take, the fp32 fallback and the dispatcher):
 //   gemm_mfma_kernel  bf16 on gfx950 v_mfma_f32_32x32x16_bf16.  Block =
 //                     WM x WN waves, each owning TM x TN 32x32 output tiles
 //                     (x2 for SwiGLU: the W1 and W3 tiles of the same columns
@@ -314,14 +316,15 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 //   0: 4 waves (2x2), per wave 4x2 tiles (SwiGLU: x2) / 4x4 tiles (store)
 //   1: 8 waves (2x4), per wave 4x1 (SwiGLU x2) / 4x2 (store)
 //   2: 8 waves (4x2), per wave 2x2 (SwiGLU x2) / 2x4 (store)
-//   3: direct global->LDS kernel of gemm_dl.hip (4 waves, 4-deep LDS ring)
+//   3: quad-wave kernel of gemm_qw.hip (4 waves of 128 x 128, K slabs of 64
+//      streamed by direct loads; the default where its constraints hold)
 constexpr int MF_BM = 256;
 
 static int gemm_cfg() {
   static int cfg = [] {
     const char* s = std::getenv("DSMOE_GEMM_CFG");
-    int v = s ? std::atoi(s) : 2;
-    return (v >= 0 && v <= 3) ? v : 2;
+    int v = s ? std::atoi(s) : 3;
+    return (v >= 0 && v <= 3) ? v : 3;
   }();
   return cfg;
 }
@@ -379,8 +382,9 @@ int launch_grouped_gemm(const GemmDesc& g_in, int epi, int dtype, const float* r
   if (g.N <= 0 || g.K <= 0) return DSMOE_OK;
   if (gemm_mfma_eligible(g, dtype, allow_mfma)) {
     if (g.bm != MF_BM) return fail(DSMOE_ERR_INVALID, "gemm: schedule tile height does not match the MFMA kernel");
-    const int cfg = gemm_cfg();
-    if (cfg == 3 && gemm_dl_ok(g, g.a_rows)) return launch_gemm_dl(g, epi, row_scale, st);
+    const int want = gemm_cfg();
+    if (want == 3 && gemm_qw_ok(g)) return launch_gemm_qw(g, epi, row_scale, st);
+    const int cfg = want == 3 ? 2 : want;  // shapes the quad-wave kernel does not take
     if (epi == EPI_SWIGLU) {
       if (cfg == 1) return launch_mfma_t<EPI_SWIGLU, 2, 4, 4, 1>(g, row_scale, st);
       if (cfg == 2) return launch_mfma_t<EPI_SWIGLU, 4, 2, 2, 2>(g, row_scale, st);

@@ -1,0 +1,422 @@
+// (c) Grouped NT GEMM for gfx950: four waves, one per SIMD, each owning a
+// 128 x 128 block of the 256 x 256 output tile, fed from LDS slabs that
+// stream in with direct global->LDS loads.
+//
+// Same contract and tile enumeration as gemm_mfma_kernel (gemm.hip).  The
+// shape follows from three gfx950 limits measured on MI355X:
+//  * L2 -> LDS direct loads are request-bound: a 64-byte row piece moves half
+//    the bytes per request of a 128-byte piece.  K therefore advances in slabs
+//    of 64 bf16 (one 128-byte cache line per row and operand).
+//  * LDS bandwidth (about 128 B/clk/CU): a 128 x 128 wave tile reads 8
+//    fragments per 16 MFMAs, against 12 for the 64 x 128 tiles of an 8-wave
+//    layout; with the direct-load writes this keeps LDS near 70 % busy at
+//    full MFMA rate.
+//  * 160 KB of LDS: two 64 KB slabs (A: 256 rows, B: 256 rows, 128 bytes
+//    each) double-buffer the K loop.
+//
+// Per slab kb a wave runs four 16-wide K steps.  Fragments for step s + 1 are
+// read into one register set while the 16 MFMAs of step s use the other, so
+// LDS latency hides behind MFMAs.  After the MFMAs of step 2 each wave waits
+// for its LDS reads of slab kb and its own direct loads of slab kb + 1, then
+// the workgroup barrier makes slab kb + 1 visible and frees slab kb's buffer,
+// into which the loads of slab kb + 2 are issued at once: every load has a
+// full slab of MFMAs to land.  Loads past the last slab re-read the last slab
+// into the free buffer (never read), so the loop body has no branches and the
+// compiler's wait counters stay exact; they are drained before the epilogue.
+//
+// Ragged tiles: the wave in row group wm owns the 32-row sub-tiles wm,
+// wm + 2, wm + 4 and wm + 6 of the block, so the valid rows of a partly
+// filled tile are spread over all four SIMDs; a wave skips the MFMAs and A
+// fragment reads of its sub-tiles past the valid rows (the main loop is
+// instantiated for 0..4 active sub-tiles to stay branch-free).
+//
+// LDS rows are 128 bytes (8 chunks of 16 bytes); chunk c of row r is stored
+// at chunk c ^ ((r >> 1) & 7), so the 16 rows read at one logical chunk by a
+// fragment load (16 lanes per LDS cycle) land on 16 distinct bank groups.  A
+// direct load writes 64 consecutive 16-byte chunks (lane i to chunk i) = 8
+// rows, so each lane fetches the global chunk that belongs at its position.
+#include "gemm_tile.h"
+#include "mfma.h"
+
+namespace dsmoe {
+
+constexpr int QW_BM = 256;
+constexpr int QW_BK = 64;                             // K per slab
+constexpr int QW_ROWB = QW_BK * 2;                    // bytes per LDS row (one cache line)
+constexpr int QW_REG = 256 * QW_ROWB;                 // one operand of a slab (32 KB)
+constexpr int QW_ASLOTS = 2;                          // A ring (activations: L2 / MALL hits)
+constexpr int QW_BSLOTS = 3;                          // B ring (weights: streamed from HBM)
+constexpr int QW_BOFF = QW_ASLOTS * QW_REG;           // B ring after the A ring
+constexpr size_t QW_LDS = (size_t)(QW_ASLOTS + QW_BSLOTS) * QW_REG;  // 160 KB (the epilogue reuses it)
+constexpr int QW_LD = QW_REG / 1024 / 4;              // direct loads per wave, operand and slab (8)
+constexpr int QW_MAX_SEG = 2;                         // K segments of B (shared experts summed in one GEMM)
+
+__device__ __forceinline__ int qw_swz(int r, int c) { return r * QW_ROWB + ((c ^ ((r >> 1) & 7)) << 4); }
+
+template <int EPI>
+struct QWCfg {
+  static constexpr int NB = (EPI == EPI_SWIGLU) ? 2 : 1;      // B operands
+  static constexpr int TN = (EPI == EPI_SWIGLU) ? 2 : 4;      // 32-column tiles per wave and B operand
+  static constexpr int BN = (EPI == EPI_SWIGLU) ? 128 : 256;  // output columns per block
+};
+
+// Direct-load sources of one wave (wave-uniform bases, per-lane offsets).
+// Wave w fills rows 64 w .. 64 w + 63 of both operand regions of a slab.
+struct QWLoad {
+  const bf16_t* a;         // A
+  const bf16_t* b0;        // this wave's B table entry, K segment 0
+  const bf16_t* b1;        // last K segment
+  uint32_t offa[QW_LD];    // per-lane element offsets of the 8 A loads
+  uint32_t offb[QW_LD];    // and of the 8 B loads
+  int kseg;                // K at which b1 takes over (0x7fffffff: one segment)
+  int lds_off;             // byte offset of this wave's 8 KB inside an operand region
+  int nk;                  // number of slabs
+};
+
+// Direct loads I0 .. I1-1 of this wave for A of slab ka (ring slot ka % 2),
+// and for B of slab kb (slot kb % 3).  Past the last slab the last slab is
+// reloaded into the (free) slot instead.
+template <int I0, int I1>
+__device__ __forceinline__ void qw_issue_a(const QWLoad& L, int ka) {
+  extern __shared__ __attribute__((aligned(16))) char qw_smem[];
+  const uint32_t da = lds_addr(qw_smem) + L.lds_off + (ka & 1) * QW_REG;
+  const int k0 = min(ka, L.nk - 1) * QW_BK;
+#pragma unroll
+  for (int i = I0; i < I1; ++i) dma16(L.a + L.offa[i] + k0, da + i * 1024);
+}
+
+template <int I0, int I1>
+__device__ __forceinline__ void qw_issue_b(const QWLoad& L, int kb) {
+  extern __shared__ __attribute__((aligned(16))) char qw_smem[];
+  const uint32_t db = lds_addr(qw_smem) + L.lds_off + QW_BOFF + (kb % QW_BSLOTS) * QW_REG;
+  const int k0 = min(kb, L.nk - 1) * QW_BK;
+  const bool hi = k0 >= L.kseg;
+  const bf16_t* src = hi ? L.b1 : L.b0;
+  const int kin = hi ? k0 - L.kseg : k0;
+#pragma unroll
+  for (int i = I0; i < I1; ++i) dma16(src + L.offb[i] + kin, db + i * 1024);
+}
+
+// Fragments of K step s (0..3) of slab kb: A sub-tiles j < NMI (rows
+// (2j + wm) * 32 ..), B tiles of this wave's columns.
+template <int EPI, int NMI>
+__device__ __forceinline__ void qw_read(int kb, int s, int wm, int wn, int lane, bf16x8_t (&fa)[4],
+                                        bf16x8_t (&fb)[QWCfg<EPI>::NB][QWCfg<EPI>::TN]) {
+  using CF = QWCfg<EPI>;
+  extern __shared__ __attribute__((aligned(16))) char qw_smem[];
+  const char* sA = qw_smem + (kb & 1) * QW_REG;
+  const char* sB = qw_smem + QW_BOFF + (kb % QW_BSLOTS) * QW_REG;
+  const int c = s * 2 + (lane >> 5);
+#pragma unroll
+  for (int j = 0; j < NMI; ++j)
+    fa[j] = *reinterpret_cast<const bf16x8_t*>(sA + qw_swz((2 * j + wm) * 32 + (lane & 31), c));
+  if (NMI > 0) {
+#pragma unroll
+    for (int b = 0; b < CF::NB; ++b)
+#pragma unroll
+      for (int ni = 0; ni < CF::TN; ++ni) {
+        const int r = (CF::NB == 2 ? b * 128 + wn * 64 : wn * 128) + ni * 32 + (lane & 31);
+        fb[b][ni] = *reinterpret_cast<const bf16x8_t*>(sB + qw_swz(r, c));
+      }
+  }
+}
+
+// MFMAs T0 .. T1-1 of one K step, in the order t = (j * NB + b) * TN + ni.
+template <int EPI, int NMI, int T0 = 0, int T1 = NMI * QWCfg<EPI>::NB * QWCfg<EPI>::TN>
+__device__ __forceinline__ void qw_mma(const bf16x8_t (&fa)[4], const bf16x8_t (&fb)[QWCfg<EPI>::NB][QWCfg<EPI>::TN],
+                                       f32x16_t (&acc)[QWCfg<EPI>::NB][4][QWCfg<EPI>::TN]) {
+  using CF = QWCfg<EPI>;
+#pragma unroll
+  for (int t = T0; t < T1; ++t) {
+    const int j = t / (CF::NB * CF::TN), b = (t / CF::TN) % CF::NB, ni = t % CF::TN;
+    acc[b][j][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[b][ni], fa[j], acc[b][j][ni], 0, 0, 0);
+  }
+}
+
+__device__ __forceinline__ void qw_sync() {
+  __builtin_amdgcn_sched_barrier(0);
+  lds_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Main loop for a wave with NMI active row sub-tiles.  On entry slab 0 is
+// visible to every wave, and A of slab 1 and B of slabs 1 and 2 are in
+// flight, in that order.
+//
+// Fragment reads run two K steps ahead of their MFMAs through three register
+// sets (step t of the kernel uses set t % 3; the four steps of a slab rotate
+// through the sets, so the roles shift by one set per slab and the loop body
+// covers three slabs).  The workgroup barrier of slab kb sits after its step
+// 1: by then the reads of steps 2 and 3 of slab kb are in flight and can be
+// waited for, and the reads of slab kb + 1 may start.
+template <int EPI, int NMI>
+struct QWPipe {
+  using CF = QWCfg<EPI>;
+  bf16x8_t fa[3][4];
+  bf16x8_t fb[3][CF::NB][CF::TN];
+};
+
+template <int EPI, int NMI, int SET>
+__device__ __forceinline__ void qw_read_set(QWPipe<EPI, NMI>& P, int kb, int s, int wm, int wn, int lane) {
+  qw_read<EPI, NMI>(kb, s, wm, wn, lane, P.fa[SET], P.fb[SET]);
+}
+
+// One slab whose step 0 uses register set S0 (steps use S0, S0+1, S0+2, S0 mod 3).
+template <int EPI, int NMI, int S0>
+__device__ __forceinline__ void qw_slab(QWPipe<EPI, NMI>& P, const QWLoad& L, int kb, int wm, int wn, int lane,
+                                        f32x16_t (&acc)[QWCfg<EPI>::NB][4][QWCfg<EPI>::TN]) {
+  using CF = QWCfg<EPI>;
+  constexpr int MMAS = NMI * CF::NB * CF::TN;   // MFMAs per K step
+  constexpr int A0 = S0 % 3, A1 = (S0 + 1) % 3, A2 = (S0 + 2) % 3;
+  // step 0: read step 2
+  __builtin_amdgcn_sched_barrier(0);
+  qw_read_set<EPI, NMI, A2>(P, kb, 2, wm, wn, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  qw_mma<EPI, NMI>(P.fa[A0], P.fb[A0], acc);
+  // step 1: read step 3 (into the set step 0 just used)
+  __builtin_amdgcn_sched_barrier(0);
+  qw_read_set<EPI, NMI, A0>(P, kb, 3, wm, wn, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  qw_mma<EPI, NMI>(P.fa[A1], P.fb[A1], acc);
+  __builtin_amdgcn_sched_barrier(0);
+  // Every read of slab kb has been issued; wait for them, and for this
+  // wave's loads of A and B of slab kb + 1: each slab issues A(kb + 2) before
+  // B(kb + 3), so only the 8 loads of B(kb + 2) may be younger and still in
+  // flight.  After the barrier slab kb + 1 is visible and the slots of slab
+  // kb are free for A of kb + 2 and B of kb + 3.
+  wait_lgkm0();
+  wait_vm<QW_LD>();
+  qw_sync();
+  // step 2: its first MFMAs interleave with the direct loads; then step 0 of
+  // slab kb + 1 is read (into the set step 1 used)
+  if (MMAS >= 4) {
+    qw_mma<EPI, NMI, 0, 1>(P.fa[A2], P.fb[A2], acc);
+    __builtin_amdgcn_sched_barrier(0);
+    qw_issue_a<0, 4>(L, kb + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    qw_mma<EPI, NMI, 1, 2>(P.fa[A2], P.fb[A2], acc);
+    __builtin_amdgcn_sched_barrier(0);
+    qw_issue_a<4, QW_LD>(L, kb + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    qw_mma<EPI, NMI, 2, 3>(P.fa[A2], P.fb[A2], acc);
+    __builtin_amdgcn_sched_barrier(0);
+    qw_issue_b<0, 4>(L, kb + 3);
+    __builtin_amdgcn_sched_barrier(0);
+    qw_mma<EPI, NMI, 3, 4>(P.fa[A2], P.fb[A2], acc);
+    __builtin_amdgcn_sched_barrier(0);
+    qw_issue_b<4, QW_LD>(L, kb + 3);
+    __builtin_amdgcn_sched_barrier(0);
+    qw_read_set<EPI, NMI, A1>(P, kb + 1, 0, wm, wn, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    qw_mma<EPI, NMI, 4, MMAS>(P.fa[A2], P.fb[A2], acc);
+  } else {
+    qw_issue_a<0, QW_LD>(L, kb + 2);
+    qw_issue_b<0, QW_LD>(L, kb + 3);
+    qw_read_set<EPI, NMI, A1>(P, kb + 1, 0, wm, wn, lane);
+  }
+  // step 3: read step 1 of slab kb + 1 (into the set step 2 used)
+  __builtin_amdgcn_sched_barrier(0);
+  qw_read_set<EPI, NMI, A2>(P, kb + 1, 1, wm, wn, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  qw_mma<EPI, NMI>(P.fa[A0], P.fb[A0], acc);
+}
+
+template <int EPI, int NMI>
+__device__ __forceinline__ void qw_loop(const QWLoad& L, int wm, int wn, int lane,
+                                        f32x16_t (&acc)[QWCfg<EPI>::NB][4][QWCfg<EPI>::TN]) {
+  // Slab kb's step 0 uses set (4 kb) % 3 = kb % 3.  No scalar load may be in
+  // flight at the loop head: scalar loads return out of order, and a pending
+  // one would turn every LDS wait in the loop into a full drain.
+  QWPipe<EPI, NMI> P;
+  qw_read_set<EPI, NMI, 0>(P, 0, 0, wm, wn, lane);
+  qw_read_set<EPI, NMI, 1>(P, 0, 1, wm, wn, lane);
+  wait_lgkm0();
+  int kb = 0;
+  for (; kb + 3 <= L.nk; kb += 3) {
+    qw_slab<EPI, NMI, 0>(P, L, kb, wm, wn, lane, acc);
+    qw_slab<EPI, NMI, 1>(P, L, kb + 1, wm, wn, lane, acc);
+    qw_slab<EPI, NMI, 2>(P, L, kb + 2, wm, wn, lane, acc);
+  }
+  if (kb < L.nk) qw_slab<EPI, NMI, 0>(P, L, kb, wm, wn, lane, acc);
+  if (kb + 1 < L.nk) qw_slab<EPI, NMI, 1>(P, L, kb + 1, wm, wn, lane, acc);
+  __builtin_amdgcn_sched_barrier(0);
+  wait_vm<0>();
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_qw_kernel(const GemmDesc g, const float* __restrict__ row_scale) {
+  using CF = QWCfg<EPI>;
+  constexpr int NB = CF::NB, TN = CF::TN, BN = CF::BN;
+
+  const int n_tiles = (int)cdiv(g.N, BN);
+  int grp, row0, rows, n_tile;
+  if (!tile_for_block<QW_BM>(g, n_tiles, grp, row0, rows, n_tile)) return;
+  grp = __builtin_amdgcn_readfirstlane(grp);
+  row0 = __builtin_amdgcn_readfirstlane(row0);
+  rows = __builtin_amdgcn_readfirstlane(rows);
+  n_tile = __builtin_amdgcn_readfirstlane(n_tile);
+  const int n0 = n_tile * BN;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // ---- direct-load sources.  Load i of wave w fills 1 KB block 8 w + i of
+  // an operand region, rows r = 8 (8 w + i) + (l >> 3); lane l writes
+  // physical chunk l & 7, i.e. logical chunk (l & 7) ^ ((r >> 1) & 7).
+  // SwiGLU: B rows 0..127 are W1 rows n0.., rows 128..255 the same W3 rows
+  // (waves 0-1 load the first half, waves 2-3 the second).
+  QWLoad L;
+  L.nk = g.K / QW_BK;
+  L.lds_off = wave * QW_LD * 1024;
+  L.a = static_cast<const bf16_t*>(g.A);
+  {
+    const void* const* tab = ((NB == 2 && wave >= 2) ? g.B1 : g.B0) + (int64_t)grp * g.nseg;
+    L.b0 = static_cast<const bf16_t*>(tab[0]);
+    L.b1 = static_cast<const bf16_t*>(tab[g.nseg - 1]);
+    L.kseg = g.nseg > 1 ? g.kseg : 0x7fffffff;
+  }
+#pragma unroll
+  for (int i = 0; i < QW_LD; ++i) {
+    const int r = (wave * QW_LD + i) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    const int ra = min(r, rows - 1);
+    const int64_t arow = g.a_map ? (int64_t)g.a_map[row0 + ra] : (int64_t)(row0 + ra);
+    L.offa[i] = (uint32_t)(arow * g.lda + c * 8);
+    const int bn = (NB == 2) ? n0 + (r & 127) : n0 + r;
+    L.offb[i] = (uint32_t)((int64_t)min(bn, g.N - 1) * g.ldb + c * 8);
+  }
+
+  f32x16_t acc[NB][4][TN];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int ni = 0; ni < TN; ++ni)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[b][j][ni][r] = 0.0f;
+
+  // ---- prologue: slab 0 visible to all waves; then A(1), B(1), B(2) in
+  // flight, in that order
+  qw_issue_a<0, QW_LD>(L, 0);
+  qw_issue_b<0, QW_LD>(L, 0);
+  wait_vm<0>();
+  qw_sync();
+  qw_issue_a<0, QW_LD>(L, 1);
+  qw_issue_b<0, QW_LD>(L, 1);
+  qw_issue_b<0, QW_LD>(L, 2);
+
+  // active sub-tiles of this wave: j with (2j + wm) * 32 < rows
+  const int nsub = (int)cdiv(rows, 32);
+  const int nmi = max(0, min(4, (nsub - wm + 1) >> 1));
+  switch (nmi) {
+    case 4: qw_loop<EPI, 4>(L, wm, wn, lane, acc); break;
+    case 3: qw_loop<EPI, 3>(L, wm, wn, lane, acc); break;
+    case 2: qw_loop<EPI, 2>(L, wm, wn, lane, acc); break;
+    case 1: qw_loop<EPI, 1>(L, wm, wn, lane, acc); break;
+    default: qw_loop<EPI, 0>(L, wm, wn, lane, acc); break;
+  }
+
+  // ---- epilogue.  Lane holds row m = (2j + wm) * 32 + (lane & 31) and, per
+  // q, columns .. + 8q + 4 (lane >> 5) + {0..3} (registers 4q..4q+3).  Each
+  // output (h, then g and u when saved; or the down projection) is rounded to
+  // bf16, staged in LDS as the block's row-major 256 x BN tile and written
+  // back one 16-byte chunk per lane, so every row leaves as whole cache lines
+  // (direct 8-byte stores from the MFMA layout would split each line over
+  // eight store instructions).  Staging: 8-byte unit u of row m sits at unit
+  // u ^ (m & 31), which keeps both the 32-row register writes and the 16-lane
+  // row reads free of bank conflicts.
+  __builtin_amdgcn_sched_barrier(0);
+  wait_lgkm0();
+  qw_sync();  // every wave is done with the slab buffers
+  extern __shared__ __attribute__((aligned(16))) char qw_smem[];
+  constexpr int ROWB = BN * 2;       // staged row bytes
+  constexpr int LPR = ROWB / 16;     // lanes per row in the write-back
+  constexpr int RPP = 256 / LPR;     // rows per write-back pass
+  const int npass = (EPI == EPI_SWIGLU) ? 1 + (g.Gs ? 1 : 0) + (g.Us ? 1 : 0) : 1;
+  const int64_t ccol = (int64_t)grp * g.c_group_col;
+  const int rr = tid / LPR, cc = tid % LPR;
+  for (int pass = 0; pass < npass; ++pass) {
+    // registers -> LDS
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int m = (2 * j + wm) * 32 + (lane & 31);
+      float scale = 1.0f;
+      if (EPI == EPI_STORE && row_scale) scale = (m < rows) ? row_scale[row0 + m] : 0.0f;
+#pragma unroll
+      for (int ni = 0; ni < TN; ++ni)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int u = (wn * (BN / 2) + ni * 32 + q * 8 + (lane >> 5) * 4) >> 2;
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float a0 = acc[0][j][ni][q * 4 + e];
+            if (EPI == EPI_SWIGLU) {
+              const float a1 = acc[NB - 1][j][ni][q * 4 + e];
+              v[e] = pass == 0 ? a0 * __builtin_amdgcn_rcpf(1.0f + __expf(-a0)) * a1
+                               : ((pass == 1 && g.Gs) ? a0 : a1);
+            } else {
+              v[e] = a0 * scale;
+            }
+          }
+          uint2 w;
+          w.x = pack_bf16x2(v[0], v[1]);
+          w.y = pack_bf16x2(v[2], v[3]);
+          *reinterpret_cast<uint2*>(qw_smem + m * ROWB + ((u ^ (m & 31)) << 3)) = w;
+        }
+    }
+    qw_sync();
+    // LDS -> global: lane cc of a row group stores 16-byte chunk cc of its row
+    bf16_t* C = static_cast<bf16_t*>(pass == 0 ? g.C : ((pass == 1 && g.Gs) ? g.Gs : g.Us));
+    const int n = n0 + cc * 8;
+    for (int r = rr; r < rows; r += RPP) {
+      const int pu = (2 * cc) ^ (r & 31);
+      u32x4_t v = *reinterpret_cast<const u32x4_t*>(qw_smem + r * ROWB + ((pu >> 1) << 4));
+      if (r & 1) v = u32x4_t{v.z, v.w, v.x, v.y};
+      if (n < g.N) {
+        const int64_t crow = g.c_map ? (int64_t)g.c_map[row0 + r] : (int64_t)(row0 + r);
+        *reinterpret_cast<u32x4_t*>(C + crow * g.ldc + ccol + n) = v;
+      }
+    }
+    if (pass + 1 < npass) qw_sync();
+  }
+}
+
+// Requirements beyond mfma_ok (gemm.hip): at most QW_MAX_SEG K segments, K
+// and the segment length multiples of 64, and 32-bit element offsets into A
+// and into every B block.
+bool gemm_qw_ok(const GemmDesc& g) {
+  const int64_t lim = int64_t(1) << 31;
+  const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  return g.nseg >= 1 && g.nseg <= QW_MAX_SEG && g.K % QW_BK == 0 && g.kseg % QW_BK == 0 && g.a_rows * g.lda < lim &&
+         (int64_t)g.N * g.ldb < lim && g.bm == QW_BM && g.N % 8 == 0 && g.ldc % 8 == 0 && g.c_group_col % 8 == 0 &&
+         a16(g.C) && a16(g.Gs) && a16(g.Us);
+}
+
+int launch_gemm_qw(const GemmDesc& g, int epi, const float* row_scale, hipStream_t st) {
+  const int bn = (epi == EPI_SWIGLU) ? QWCfg<EPI_SWIGLU>::BN : QWCfg<EPI_STORE>::BN;
+  const int64_t m_bound = g.sched ? g.m_tiles_bound : cdiv(g.dense_rows, QW_BM) * g.groups;
+  const int64_t grid = 8 * cdiv(m_bound * cdiv(g.N, bn), 8);
+  if (grid == 0) return DSMOE_OK;
+  if (epi == EPI_SWIGLU) {
+    static bool a = false;
+    if (!a && hipFuncSetAttribute((const void*)gemm_qw_kernel<EPI_SWIGLU>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)QW_LDS) != hipSuccess)
+      return fail(DSMOE_ERR_HIP, "gemm_qw: cannot raise LDS limit");
+    a = true;
+    hipLaunchKernelGGL(gemm_qw_kernel<EPI_SWIGLU>, dim3((unsigned)grid), dim3(256), QW_LDS, st, g, row_scale);
+  } else {
+    static bool a = false;
+    if (!a && hipFuncSetAttribute((const void*)gemm_qw_kernel<EPI_STORE>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)QW_LDS) != hipSuccess)
+      return fail(DSMOE_ERR_HIP, "gemm_qw: cannot raise LDS limit");
+    a = true;
+    hipLaunchKernelGGL(gemm_qw_kernel<EPI_STORE>, dim3((unsigned)grid), dim3(256), QW_LDS, st, g, row_scale);
+  }
+  return check_launch("gemm_qw");
+}
+
+}  // namespace dsmoe
