@@ -318,12 +318,6 @@ int dsmoe_grouped_swiglu_fwd(const void* x_sorted, const void* const* w1, const 
   return launch_grouped_gemm(g2, EPI_STORE, d.dtype, sorted_w, mfr, st);
 }
 
-int dsmoe_grouped_swiglu_bwd(const void*, const void* const*, const void* const*, const void* const*, const int64_t*,
-                             const void*, const dsmoe_dims*, void*, void* const*, void* const*, void* const*, void*,
-                             size_t, void*) {
-  return fail(DSMOE_ERR_UNSUPPORTED, "dsmoe_grouped_swiglu_bwd: not built yet");
-}
-
 int dsmoe_combine_fwd(const void* o_slots, const float* weights, const int32_t* idx, const void* shared,
                       const dsmoe_dims* dims, void* y, void* stream) {
   int rc = validate(dims, false);
@@ -670,6 +664,141 @@ int dsmoe_moe_bwd(const void* x, const float* gate_w, const void* const* w1, con
   tm.end();
   tm.call_done(1);
   return rc;
+}
+
+// Backward of the operator seam (models/moe_triton.py:438-501).  The forward
+// gate/up GEMM is recomputed (g, u, h), then the same grouped GEMMs as the
+// layer backward run with identity row maps: dh -> [dg | du] (SwiGLU
+// backward epilogue), dx = [dg | du] [W1; W3], dW1 | dW3 = [dg | du]^T X_e and
+// dW2 = dY_e^T H_e per expert, fp32 accumulation in ascending row order.
+struct GroupedBwdLayout {
+  const void** w1;   // [w1 E][w3 E][w2 E][w13 2E]
+  const void** w3;
+  const void** w2;
+  const void** w13;
+  void** dw1;        // [dw1 E][dw3 E][dw2 E]
+  void** dw3;
+  void** dw2;
+  int32_t* off32;
+  MTile* sched_f;    // forward recompute schedule (MFMA or SIMT tile height)
+  int32_t* cnt_f;
+  MTile* sched_b;    // backward schedule (BWD_BM)
+  int32_t* cnt_b;
+  void* g;
+  void* u;
+  void* h;
+  void* dgdu;
+  size_t total;
+};
+
+// bm_f: tile height the forward schedule is sized for (the smallest one a
+// launch may use, so one layout serves both kernel choices).
+static GroupedBwdLayout grouped_bwd_layout(const dsmoe_dims& d, int bm_f, void* base) {
+  Carver c(base);
+  GroupedBwdLayout B;
+  const int64_t N = d.T;
+  const int es = elem_size(d.dtype);
+  const void** t = c.take<const void*>(5 * d.E);
+  B.w1 = t; B.w3 = t + d.E; B.w2 = t + 2 * d.E; B.w13 = t + 3 * d.E;
+  void** o = c.take<void*>(3 * d.E);
+  B.dw1 = o; B.dw3 = o + d.E; B.dw2 = o + 2 * d.E;
+  B.off32 = c.take<int32_t>(d.E + 1);
+  B.sched_f = c.take<MTile>(sched_bound(N, d.E, bm_f));
+  B.cnt_f = c.take<int32_t>(1);
+  B.sched_b = c.take<MTile>(sched_bound(N, d.E, BWD_BM));
+  B.cnt_b = c.take<int32_t>(1);
+  B.g = c.take<char>((size_t)N * d.I * es);
+  B.u = c.take<char>((size_t)N * d.I * es);
+  B.h = c.take<char>((size_t)N * d.I * es);
+  B.dgdu = c.take<char>((size_t)N * 2 * d.I * es);
+  B.total = c.used();
+  return B;
+}
+
+static bool grouped_dims_ok(const dsmoe_dims* dims) {
+  return dims && (dims->dtype == DSMOE_F32 || dims->dtype == DSMOE_BF16) && dims->T >= 0 && dims->E > 0 &&
+         dims->D > 0 && dims->I > 0;
+}
+
+size_t dsmoe_grouped_swiglu_bwd_workspace_size(const dsmoe_dims* dims) {
+  if (!grouped_dims_ok(dims)) return 0;
+  return grouped_bwd_layout(*dims, TILE_M, nullptr).total;
+}
+
+int dsmoe_grouped_swiglu_bwd(const void* x_sorted, const void* const* w1, const void* const* w2, const void* const* w3,
+                             const int64_t* offsets, const void* dy_sorted, const dsmoe_dims* dims, void* dx_sorted,
+                             void* const* dw1, void* const* dw2, void* const* dw3, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  DSMOE_REQUIRE(grouped_dims_ok(dims), DSMOE_ERR_INVALID, "grouped_bwd: bad dims");
+  const dsmoe_dims& d = *dims;
+  DSMOE_REQUIRE(x_sorted && w1 && w2 && w3 && offsets && dy_sorted && dx_sorted && dw1 && dw2 && dw3,
+                DSMOE_ERR_INVALID, "grouped_bwd: NULL pointer");
+  const size_t need = dsmoe_grouped_swiglu_bwd_workspace_size(dims);
+  DSMOE_REQUIRE(workspace && workspace_bytes >= need, DSMOE_ERR_WORKSPACE, "grouped_bwd: workspace too small");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t N = d.T;
+  const bool mf = all_aligned16(w1, d.E) && all_aligned16(w2, d.E) && all_aligned16(w3, d.E) &&
+                  all_aligned16((const void* const*)dw1, d.E) && all_aligned16((const void* const*)dw2, d.E) &&
+                  all_aligned16((const void* const*)dw3, d.E);
+  // forward recompute descriptor (its tile height decides the forward schedule)
+  GemmDesc g1 = desc_zero();
+  g1.A = x_sorted; g1.lda = d.D; g1.a_rows = N; g1.ldb = d.D; g1.kseg = d.D;
+  g1.N = d.I; g1.K = d.D; g1.ldc = d.I;
+  const bool mfr = gemm_mfma_eligible(g1, d.dtype, mf);
+  const int bm_f = gemm_tile_m(mfr);
+  GroupedBwdLayout B = grouped_bwd_layout(d, TILE_M, workspace);
+  std::vector<const void*> w13h(2 * d.E);
+  for (int e = 0; e < d.E; ++e) {
+    w13h[2 * e] = w1[e];
+    w13h[2 * e + 1] = w3[e];
+  }
+  int rc = upload_ptr_lists({{w1, d.E}, {w3, d.E}, {w2, d.E}, {w13h.data(), 2 * d.E}}, B.w1, st);
+  if (!rc)
+    rc = upload_ptr_lists({{(const void* const*)dw1, d.E}, {(const void* const*)dw3, d.E},
+                           {(const void* const*)dw2, d.E}},
+                          (const void**)B.dw1, st);
+  if (!rc) rc = launch_sched_from_offsets(offsets, d.E, bm_f, N, B.off32, B.sched_f, B.cnt_f, st);
+  if (!rc) rc = launch_sched32(B.off32, d.E, BWD_BM, B.sched_b, B.cnt_b, st);
+  if (rc) return rc;
+  // recompute g = X W1^T, u = X W3^T, h = silu(g) * u
+  g1.B0 = B.w1; g1.B1 = B.w3; g1.C = B.h; g1.Gs = B.g; g1.Us = B.u;
+  g1.sched = B.sched_f; g1.sched_count = B.cnt_f; g1.m_tiles_bound = (int32_t)sched_bound(N, d.E, bm_f); g1.bm = bm_f;
+  rc = launch_grouped_gemm(g1, EPI_SWIGLU, d.dtype, nullptr, mfr, st);
+  if (rc) return rc;
+  const int32_t mbound = (int32_t)sched_bound(N, d.E, BWD_BM);
+  // dh = dY W2, SwiGLU backward -> [dg | du]
+  XGemm h = xdesc_zero();
+  h.sched_mode = XS_ROUTED; h.sched = B.sched_b; h.sched_count = B.cnt_b; h.m_tiles_bound = mbound;
+  h.bm = BWD_BM; h.N = d.I; h.K = d.D;
+  h.a_mode = XA_ROWS; h.A = dy_sorted; h.lda = d.D;
+  h.b_mode = XB_W_NN; h.Btab = B.w2; h.ldb = d.I; h.kseg = d.D;
+  h.C = B.dgdu; h.ldc = 2 * (int64_t)d.I; h.du_off = d.I;
+  h.Gs = B.g; h.Us = B.u; h.ld_gu = d.I;
+  rc = launch_xgemm(h, XE_SWIGLU_BWD, d.dtype, mf, st);
+  if (rc) return rc;
+  // dx = [dg | du] [W1; W3]
+  XGemm xg = xdesc_zero();
+  xg.sched_mode = XS_ROUTED; xg.sched = B.sched_b; xg.sched_count = B.cnt_b; xg.m_tiles_bound = mbound;
+  xg.bm = BWD_BM; xg.N = d.D; xg.K = 2 * d.I;
+  xg.a_mode = XA_ROWS; xg.A = B.dgdu; xg.lda = 2 * (int64_t)d.I;
+  xg.b_mode = XB_W_NN; xg.Btab = B.w13; xg.ldb = d.D; xg.kseg = d.I; xg.nseg = 2;
+  xg.C = dx_sorted; xg.ldc = d.D;
+  rc = launch_xgemm(xg, XE_STORE, d.dtype, mf, st);
+  if (rc) return rc;
+  // dW1 | dW3 = [dg | du]^T X_e ; dW2 = dY_e^T H_e
+  XGemm w13 = xdesc_zero();
+  w13.sched_mode = XS_WGRAD; w13.groups = d.E; w13.k_off = B.off32; w13.M = 2 * d.I; w13.N = d.D; w13.K = (int32_t)N;
+  w13.a_mode = XA_KMAJOR; w13.A = B.dgdu; w13.lda = 2 * (int64_t)d.I;
+  w13.b_mode = XB_ACT_KMAJOR; w13.Bact = x_sorted; w13.ldb = d.D;
+  w13.Ctab0 = B.dw1; w13.Ctab1 = B.dw3; w13.msplit = d.I; w13.ldc = d.D;
+  rc = launch_xgemm(w13, XE_WGRAD, d.dtype, mf, st);
+  if (rc) return rc;
+  XGemm w2g = xdesc_zero();
+  w2g.sched_mode = XS_WGRAD; w2g.groups = d.E; w2g.k_off = B.off32; w2g.M = d.D; w2g.N = d.I; w2g.K = (int32_t)N;
+  w2g.a_mode = XA_KMAJOR; w2g.A = dy_sorted; w2g.lda = d.D;
+  w2g.b_mode = XB_ACT_KMAJOR; w2g.Bact = B.h; w2g.ldb = d.I;
+  w2g.Ctab0 = B.dw2; w2g.Ctab1 = B.dw2; w2g.msplit = d.D; w2g.ldc = d.I;
+  return launch_xgemm(w2g, XE_WGRAD, d.dtype, mf, st);
 }
 
 int dsmoe_update_bias(const int32_t* counts, float* gate_bias, int E, float speed, float upper, float lower,

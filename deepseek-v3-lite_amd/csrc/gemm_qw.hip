@@ -338,6 +338,11 @@ __global__ __launch_bounds__(256) void gemm_qw_kernel(const GemmDesc g, const fl
   const int npass = (EPI == EPI_SWIGLU) ? 1 + (g.Gs ? 1 : 0) + (g.Us ? 1 : 0) : 1;
   const int64_t ccol = (int64_t)grp * g.c_group_col;
   const int rr = tid / LPR, cc = tid % LPR;
+  // Output rows of the tile: the c_map entries are fetched once, ahead of the
+  // staging writes, and kept in LDS past the staged tile (a map lookup per
+  // write-back pass would wait on global memory every pass).
+  int32_t* crow_tab = reinterpret_cast<int32_t*>(qw_smem + 256 * ROWB);
+  const int32_t my_crow = (g.c_map && tid < rows) ? g.c_map[row0 + tid] : row0 + tid;
   for (int pass = 0; pass < npass; ++pass) {
     // registers -> LDS
 #pragma unroll
@@ -368,6 +373,7 @@ __global__ __launch_bounds__(256) void gemm_qw_kernel(const GemmDesc g, const fl
           *reinterpret_cast<uint2*>(qw_smem + m * ROWB + ((u ^ (m & 31)) << 3)) = w;
         }
     }
+    if (pass == 0) crow_tab[tid] = my_crow;
     qw_sync();
     // LDS -> global: lane cc of a row group stores 16-byte chunk cc of its row
     bf16_t* C = static_cast<bf16_t*>(pass == 0 ? g.C : ((pass == 1 && g.Gs) ? g.Gs : g.Us));
@@ -377,8 +383,7 @@ __global__ __launch_bounds__(256) void gemm_qw_kernel(const GemmDesc g, const fl
       u32x4_t v = *reinterpret_cast<const u32x4_t*>(qw_smem + r * ROWB + ((pu >> 1) << 4));
       if (r & 1) v = u32x4_t{v.z, v.w, v.x, v.y};
       if (n < g.N) {
-        const int64_t crow = g.c_map ? (int64_t)g.c_map[row0 + r] : (int64_t)(row0 + r);
-        *reinterpret_cast<u32x4_t*>(C + crow * g.ldc + ccol + n) = v;
+        *reinterpret_cast<u32x4_t*>(C + (int64_t)crow_tab[r] * g.ldc + ccol + n) = v;
       }
     }
     if (pass + 1 < npass) qw_sync();

@@ -158,7 +158,11 @@ __global__ __launch_bounds__(256) void sched_from_offsets_kernel(const int64_t* 
     *sched_count = ok ? tl : 0;
   }
   __syncthreads();
-  if (!til[E + 1]) return;
+  if (!til[E + 1]) {
+    // invalid offsets: every group is empty for the consumers of offsets32
+    for (int e = tid; e <= E; e += blockDim.x) offsets32[e] = 0;
+    return;
+  }
   for (int e = tid; e <= E; e += blockDim.x) offsets32[e] = (int32_t)offsets64[e];
   for (int e = tid; e < E; e += blockDim.x) {
     const int32_t o = (int32_t)offsets64[e];

@@ -47,6 +47,7 @@ _SIGNATURES = {
     "dsmoe_permute": ([P, DIMS, P, P, P, P, P, P, P, P, P, P, SZ, P], I32),
     "dsmoe_grouped_swiglu_workspace_size": ([DIMS], SZ),
     "dsmoe_grouped_swiglu_fwd": ([P, PP, PP, PP, P, P, DIMS, P, P, SZ, P], I32),
+    "dsmoe_grouped_swiglu_bwd_workspace_size": ([DIMS], SZ),
     "dsmoe_grouped_swiglu_bwd": ([P, PP, PP, PP, P, P, DIMS, P, PP, PP, PP, P, SZ, P], I32),
     "dsmoe_combine_fwd": ([P, P, P, P, DIMS, P, P], I32),
     "dsmoe_moe_fwd_workspace_size": ([DIMS, I32], SZ),

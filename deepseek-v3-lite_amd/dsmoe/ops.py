@@ -222,8 +222,10 @@ def moe_layer(x: torch.Tensor, gate_w: torch.Tensor, gate_bias: torch.Tensor, w1
 # ---------------------------------------------------------------------------- operator seam
 class _GroupedSwiGLUFn(torch.autograd.Function):
     """_TritonGroupedMoeFunction's contract (models/moe_triton.py:390-501):
-    unweighted y_sorted; backward gives dx and fp32-accumulated dW in the
-    weight dtype."""
+    unweighted y_sorted; backward (dsmoe_grouped_swiglu_bwd) recomputes the
+    gate/up GEMM and gives dx and fp32-accumulated dW in the weight dtype,
+    returning (dx, dw1, dw2, dw3, None, None) like the reference's
+    (dx, dw1, dw2, dw3, None)."""
 
     @staticmethod
     def forward(ctx, x_sorted, w1, w2, w3, expert_offsets, sorted_w=None):
@@ -251,7 +253,7 @@ class _GroupedSwiGLUFn(torch.autograd.Function):
         E, I, _ = w1.shape
         d = L.make_dims(N, D, E, 1, I, 0, 0, x_sorted.dtype, 1.0)
         lib = L.load()
-        ws = _ws(lib.dsmoe_grouped_swiglu_workspace_size(d) * 4, dev)
+        ws = _ws(lib.dsmoe_grouped_swiglu_bwd_workspace_size(d), dev)
         dx = torch.empty_like(x_sorted)
         dw1, dw2, dw3 = torch.empty_like(w1), torch.empty_like(w2), torch.empty_like(w3)
         arrs = [L.ptr_array(list(t.unbind(0))) for t in (w1, w2, w3, dw1, dw2, dw3)]

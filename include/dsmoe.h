@@ -118,9 +118,14 @@ int dsmoe_grouped_swiglu_fwd(const void* x_sorted, const void* const* w1, const 
                              const dsmoe_dims* dims, void* y_sorted, void* workspace, size_t workspace_bytes,
                              void* stream);
 
-/* Backward of the seam (models/moe_triton.py:438-501): given dy_sorted of the
- * UNWEIGHTED output, writes dx_sorted and dW1/dW2/dW3 (per-expert device
- * pointers, weight dtype, fp32 accumulation in ascending row order). */
+/* Backward of the seam (_TritonGroupedMoeFunction.backward,
+ * models/moe_triton.py:438-501): given dy_sorted (rows, D) of the UNWEIGHTED
+ * output, writes dx_sorted (rows, D) and dW1/dW2/dW3 (per-expert device
+ * pointers, weight dtype; fp32 accumulation over each expert's rows in
+ * ascending order, one rounding; experts without rows get zeros).  The
+ * forward gate/up GEMM is recomputed.  Workspace:
+ * dsmoe_grouped_swiglu_bwd_workspace_size(). */
+size_t dsmoe_grouped_swiglu_bwd_workspace_size(const dsmoe_dims* dims);
 int dsmoe_grouped_swiglu_bwd(const void* x_sorted, const void* const* w1, const void* const* w2,
                              const void* const* w3, const int64_t* offsets, const void* dy_sorted,
                              const dsmoe_dims* dims, void* dx_sorted, void* const* dw1, void* const* dw2,

@@ -104,3 +104,17 @@ def load_module(case: Case, p: R.MoEParams, device, module_cls):
     m.gate.float()
     m.load_state_dict(sd)
     return m
+
+
+def grouped_case(T, D, E, I, counts, dtype, seed, scale=0.1):
+    """Inputs of the grouped operator seam (models/moe_triton.py:504-525):
+    x_sorted (T,D), w1/w3 (E,I,D), w2 (E,D,I), (E+1,) int64 offsets from
+    per-expert row counts, sorted gate weights (T,)."""
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(T, D, generator=g) * scale).to(dtype)
+    w1 = (torch.randn(E, I, D, generator=g) * scale).to(dtype)
+    w2 = (torch.randn(E, D, I, generator=g) * scale).to(dtype)
+    w3 = (torch.randn(E, I, D, generator=g) * scale).to(dtype)
+    off = torch.cat([torch.zeros(1, dtype=torch.int64), torch.tensor(counts).cumsum(0)])
+    gw = (torch.rand(T, generator=g) * 0.1).to(dtype)
+    return x, w1, w2, w3, off, gw

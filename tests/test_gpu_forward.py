@@ -97,17 +97,6 @@ def test_permute_bit_exact(T, E, k):
 
 
 # --------------------------------------------------------------------- grouped operator seam
-def _grouped_case(T, D, E, I, counts, dtype, seed, scale=0.1):
-    g = torch.Generator().manual_seed(seed)
-    x = (torch.randn(T, D, generator=g) * scale).to(dtype)
-    w1 = (torch.randn(E, I, D, generator=g) * scale).to(dtype)
-    w2 = (torch.randn(E, D, I, generator=g) * scale).to(dtype)
-    w3 = (torch.randn(E, I, D, generator=g) * scale).to(dtype)
-    off = torch.cat([torch.zeros(1, dtype=torch.int64), torch.tensor(counts).cumsum(0)])
-    gw = (torch.rand(T, generator=g) * 0.1).to(dtype)
-    return x, w1, w2, w3, off, gw
-
-
 @pytest.mark.parametrize("T,D,E,I,counts,dtype,tol", [
     (32, 32, 4, 16, [8, 6, 10, 8], torch.float32, 1e-5),        # tests/test_moe_triton.py:194-209 shape
     (64, 48, 4, 24, [16, 14, 18, 16], torch.bfloat16, 2e-2),    # :211-226 shape
@@ -117,7 +106,7 @@ def _grouped_case(T, D, E, I, counts, dtype, seed, scale=0.1):
     (520, 256, 3, 192, [257, 256, 7], torch.bfloat16, 2e-2),    # MFMA path, N tail (192 = 128 + 64)
 ])
 def test_grouped_operator_vs_oracle(T, D, E, I, counts, dtype, tol):
-    x, w1, w2, w3, off, gw = _grouped_case(T, D, E, I, counts, dtype, seed=T + D)
+    x, w1, w2, w3, off, gw = CS.grouped_case(T, D, E, I, counts, dtype, seed=T + D)
     from dsmoe import grouped_moe_dispatch
     with torch.no_grad():
         y = grouped_moe_dispatch(x.to(DEV), w1.to(DEV), w2.to(DEV), w3.to(DEV), gw.to(DEV), off.to(DEV)).cpu()

@@ -240,3 +240,19 @@ def test_grouped_ref_matches_naive_loop_reference_shape():
         s, t = off[e].item(), off[e + 1].item()
         ref = _expert(x[s:t].double(), w1[e].double(), w2[e].double(), w3[e].double()) * gw[s:t, None].double()
         torch.testing.assert_close(y[s:t].double(), ref, rtol=1e-5, atol=1e-6)
+
+
+def test_grouped_ref_gradients_pass_gradcheck():
+    """Pins the oracle's seam gradients (the expected values of the grouped
+    backward test): autograd of grouped_moe_ref against central finite
+    differences in fp64, with an empty expert, at a tiny shape."""
+    torch.manual_seed(0)
+    T, D, E, I = 7, 5, 3, 4
+    x = torch.randn(T, D, dtype=torch.float64, requires_grad=True)
+    w1 = (torch.randn(E, I, D, dtype=torch.float64) * 0.5).requires_grad_(True)
+    w2 = (torch.randn(E, D, I, dtype=torch.float64) * 0.5).requires_grad_(True)
+    w3 = (torch.randn(E, I, D, dtype=torch.float64) * 0.5).requires_grad_(True)
+    gw = torch.rand(T, dtype=torch.float64, requires_grad=True)
+    off = torch.tensor([0, 4, 4, 7])
+    assert torch.autograd.gradcheck(lambda a, b, c, d, w: R.grouped_moe_ref(a, b, c, d, off, w),
+                                    (x, w1, w2, w3, gw), eps=1e-6, atol=1e-7)
