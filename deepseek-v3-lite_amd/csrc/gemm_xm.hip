@@ -42,7 +42,8 @@ constexpr int XM_BN = XM_WN * XM_TN * 32;       // 256
 constexpr int XM_A_EL = XM_BM * MF_K;
 constexpr int XM_B_EL = XM_BN * MF_K;
 constexpr int XM_STAGE = XM_A_EL + XM_B_EL;
-constexpr size_t XM_LDS_BYTES = 2ull * XM_STAGE * sizeof(bf16_t);  // 128 KiB
+constexpr size_t XM_LDS_BYTES = 2ull * XM_STAGE * sizeof(bf16_t);  // 128 KiB of K slabs (then the staged tile)
+constexpr size_t XM_LDS_ALLOC = XM_LDS_BYTES + 256 * sizeof(int64_t); // + the epilogue's output row pointers
 static_assert(XM_BM == 256 && XM_BN == 256, "loader mappings assume 256 x 256 tiles and 512 threads");
 
 __device__ __forceinline__ int xswz(int row, int chunk) {
@@ -262,18 +263,15 @@ __global__ __launch_bounds__(XM_THREADS) void xgemm_mfma_kernel(const XGemm g) {
     __syncthreads();
   }
 
-  // ---- epilogue.  Lane holds tile row m = .. + (lane & 31) and, per q,
-  // columns n = .. + 8 qq + 4 (lane >> 5) + {0..3} (acc registers 4 qq ..).
+  // ---- epilogue.  Lane holds tile row m = (wm * 2 + mi) * 32 + (lane & 31)
+  // and, per qq, columns n = (wn * 4 + ni) * 32 + 8 qq + 4 (lane >> 5) + {0..3}
+  // (acc registers 4 qq ..).  Split-K partials go straight out as fp32.
+  if (EPI == XE_WGRAD && g.ksplit > 1) {
 #pragma unroll
-  for (int mi = 0; mi < XM_TM; ++mi) {
-    const int m = (wm * XM_TM + mi) * 32 + (lane & 31);
-    if (m >= rows) continue;
-    const int r = row0 + m;
-    bf16_t* out;
-    int64_t orow;
-    float rw = 1.0f;
-    if (EPI == XE_WGRAD && g.ksplit > 1) {
-      float* prow = g.part + (((int64_t)split * g.groups + grp) * g.M + r) * g.N;
+    for (int mi = 0; mi < XM_TM; ++mi) {
+      const int m = (wm * XM_TM + mi) * 32 + (lane & 31);
+      if (m >= rows) continue;
+      float* prow = g.part + (((int64_t)split * g.groups + grp) * g.M + row0 + m) * g.N;
 #pragma unroll
       for (int ni = 0; ni < XM_TN; ++ni)
 #pragma unroll
@@ -283,54 +281,100 @@ __global__ __launch_bounds__(XM_THREADS) void xgemm_mfma_kernel(const XGemm g) {
             *reinterpret_cast<float4*>(prow + n) = make_float4(acc[mi][ni][qq * 4], acc[mi][ni][qq * 4 + 1],
                                                                acc[mi][ni][qq * 4 + 2], acc[mi][ni][qq * 4 + 3]);
         }
-      continue;
     }
+    return;
+  }
+  // Otherwise the tile goes through LDS and leaves as whole rows (direct
+  // stores from the MFMA layout would split every cache line over several
+  // store instructions).  Output row pointers are resolved once per row.
+  char* sm = reinterpret_cast<char*>(smem_x);
+  int64_t* rowp = reinterpret_cast<int64_t*>(sm + XM_LDS_BYTES);  // past the staged tile
+  if (tid < 256) {
+    const int r = row0 + min(tid, rows - 1);
+    int64_t o;
     if (EPI == XE_WGRAD) {
-      out = static_cast<bf16_t*>(r < g.msplit ? g.Ctab0[grp] : g.Ctab1[grp]);
-      orow = (int64_t)(r < g.msplit ? r : r - g.msplit) * g.ldc;
+      o = reinterpret_cast<int64_t>(static_cast<bf16_t*>(r < g.msplit ? g.Ctab0[grp] : g.Ctab1[grp]) +
+                                    (int64_t)(r < g.msplit ? r : r - g.msplit) * g.ldc);
     } else {
-      out = static_cast<bf16_t*>(g.C) + (int64_t)grp * g.c_group_col;
-      orow = (g.c_map ? (int64_t)g.c_map[r] : (int64_t)r) * g.ldc;
-      if (EPI == XE_SWIGLU_BWD && g.row_w) rw = g.row_w[r];
+      o = reinterpret_cast<int64_t>(static_cast<bf16_t*>(g.C) + (int64_t)grp * g.c_group_col +
+                                    (g.c_map ? (int64_t)g.c_map[r] : (int64_t)r) * g.ldc);
     }
+    rowp[tid] = o;
+  }
+  if (EPI != XE_SWIGLU_BWD) {
+    // bf16 tile, 256 rows x 512 bytes; 8-byte unit u of row m at unit u ^ (m & 31)
 #pragma unroll
-    for (int ni = 0; ni < XM_TN; ++ni) {
+    for (int mi = 0; mi < XM_TM; ++mi) {
+      const int m = (wm * XM_TM + mi) * 32 + (lane & 31);
 #pragma unroll
-      for (int qq = 0; qq < 4; ++qq) {
-        const int n = n0 + (wn * XM_TN + ni) * 32 + qq * 8 + (lane >> 5) * 4;
-        if (n >= g.N) continue;
-        float a4[4];
+      for (int ni = 0; ni < XM_TN; ++ni)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) a4[e] = acc[mi][ni][qq * 4 + e];
-        if (EPI == XE_SWIGLU_BWD) {
-          const int64_t ogu = (int64_t)r * g.ld_gu + (int64_t)grp * g.gu_group_col + n;
-          const u32x2_t gp = *reinterpret_cast<const u32x2_t*>(static_cast<const bf16_t*>(g.Gs) + ogu);
-          const u32x2_t up = *reinterpret_cast<const u32x2_t*>(static_cast<const bf16_t*>(g.Us) + ogu);
-          uint32_t pg[2], pu[2];
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            float dg[2], du[2];
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-              const uint32_t gw = h ? gp.y : gp.x, uw = h ? up.y : up.x;
-              const float gv = __uint_as_float(e ? (gw & 0xffff0000u) : (gw << 16));
-              const float uv = __uint_as_float(e ? (uw & 0xffff0000u) : (uw << 16));
-              const float dh = rw * a4[2 * h + e];
-              const float sg = sigmoid_f(gv);
-              dg[e] = dh * uv * sg * (1.0f + gv * (1.0f - sg));
-              du[e] = dh * gv * sg;
-            }
-            pg[h] = (uint32_t)f2bf(dg[0]) | ((uint32_t)f2bf(dg[1]) << 16);
-            pu[h] = (uint32_t)f2bf(du[0]) | ((uint32_t)f2bf(du[1]) << 16);
-          }
-          *reinterpret_cast<u32x2_t*>(out + orow + n) = u32x2_t{pg[0], pg[1]};
-          *reinterpret_cast<u32x2_t*>(out + orow + g.du_off + n) = u32x2_t{pu[0], pu[1]};
-        } else {
-          const uint32_t p0 = (uint32_t)f2bf(a4[0]) | ((uint32_t)f2bf(a4[1]) << 16);
-          const uint32_t p1 = (uint32_t)f2bf(a4[2]) | ((uint32_t)f2bf(a4[3]) << 16);
-          *reinterpret_cast<u32x2_t*>(out + orow + n) = u32x2_t{p0, p1};
+        for (int qq = 0; qq < 4; ++qq) {
+          const int u = ((wn * XM_TN + ni) * 32 + qq * 8 + (lane >> 5) * 4) >> 2;
+          u32x2_t w;
+          w.x = pack_bf16x2(acc[mi][ni][qq * 4], acc[mi][ni][qq * 4 + 1]);
+          w.y = pack_bf16x2(acc[mi][ni][qq * 4 + 2], acc[mi][ni][qq * 4 + 3]);
+          *reinterpret_cast<u32x2_t*>(sm + m * 512 + ((u ^ (m & 31)) << 3)) = w;
         }
+    }
+    __syncthreads();
+    // 32 lanes per row, 16 bytes each; 16 rows per pass
+    const int cc = tid & 31, n = n0 + cc * 8;
+    for (int r = tid >> 5; r < rows; r += 16) {
+      const int pu = (2 * cc) ^ (r & 31);
+      u32x4_t v = *reinterpret_cast<const u32x4_t*>(sm + r * 512 + ((pu >> 1) << 4));
+      if (r & 1) v = u32x4_t{v.z, v.w, v.x, v.y};
+      if (n < g.N) *reinterpret_cast<u32x4_t*>(reinterpret_cast<bf16_t*>(rowp[r]) + n) = v;
+    }
+    return;
+  }
+  // SwiGLU backward: dh stays fp32 until dg and du are formed, so each column
+  // half of the tile (128 columns, owned by the waves with wn == half) is
+  // staged as fp32 in turn; 16-byte unit u (4 columns) of row m sits at unit
+  // u ^ (m & 31).  The write-back reads g and u row pieces coalesced.
+  const bf16_t* Gs = static_cast<const bf16_t*>(g.Gs);
+  const bf16_t* Us = static_cast<const bf16_t*>(g.Us);
+  for (int half = 0; half < 2; ++half) {
+    if (half) __syncthreads();  // the first half's reads are done
+    if (wn == half) {
+#pragma unroll
+      for (int mi = 0; mi < XM_TM; ++mi) {
+        const int m = (wm * XM_TM + mi) * 32 + (lane & 31);
+#pragma unroll
+        for (int ni = 0; ni < XM_TN; ++ni)
+#pragma unroll
+          for (int qq = 0; qq < 4; ++qq) {
+            const int u = (ni * 32 + qq * 8 + (lane >> 5) * 4) >> 2;
+            *reinterpret_cast<float4*>(sm + m * 512 + ((u ^ (m & 31)) << 4)) =
+                make_float4(acc[mi][ni][qq * 4], acc[mi][ni][qq * 4 + 1], acc[mi][ni][qq * 4 + 2],
+                            acc[mi][ni][qq * 4 + 3]);
+          }
       }
+    }
+    __syncthreads();
+    const int cc = tid & 31, n = n0 + half * 128 + cc * 4;
+    for (int r = tid >> 5; r < rows; r += 16) {
+      const float4 dh4 = *reinterpret_cast<const float4*>(sm + r * 512 + ((cc ^ (r & 31)) << 4));
+      if (n >= g.N) continue;
+      const float rw = g.row_w ? g.row_w[row0 + r] : 1.0f;
+      const int64_t ogu = (int64_t)(row0 + r) * g.ld_gu + (int64_t)grp * g.gu_group_col + n;
+      const u32x2_t gp = *reinterpret_cast<const u32x2_t*>(Gs + ogu);
+      const u32x2_t up = *reinterpret_cast<const u32x2_t*>(Us + ogu);
+      const float dhv[4] = {dh4.x, dh4.y, dh4.z, dh4.w};
+      float dg[4], du[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t gw = (e < 2) ? gp.x : gp.y, uw = (e < 2) ? up.x : up.y;
+        const float gv = __uint_as_float((e & 1) ? (gw & 0xffff0000u) : (gw << 16));
+        const float uv = __uint_as_float((e & 1) ? (uw & 0xffff0000u) : (uw << 16));
+        const float dh = rw * dhv[e];
+        const float sg = sigmoid_f(gv);
+        dg[e] = dh * uv * sg * (1.0f + gv * (1.0f - sg));
+        du[e] = dh * gv * sg;
+      }
+      bf16_t* out = reinterpret_cast<bf16_t*>(rowp[r]);
+      *reinterpret_cast<u32x2_t*>(out + n) = u32x2_t{pack_bf16x2(dg[0], dg[1]), pack_bf16x2(dg[2], dg[3])};
+      *reinterpret_cast<u32x2_t*>(out + g.du_off + n) = u32x2_t{pack_bf16x2(du[0], du[1]), pack_bf16x2(du[2], du[3])};
     }
   }
 }
@@ -383,13 +427,14 @@ bool xgemm_mfma_ok(const XGemm& g, int epi) {
     return false;
   }
   if (g.sched_mode == XS_ROUTED && g.bm % XM_BM) return false;
+  // the staged epilogue writes 16-byte row pieces (XE_SWIGLU_BWD: 8-byte)
   if (epi == XE_WGRAD)
-    return g.ldc % 4 == 0 && g.msplit % 4 == 0 && g.sched_mode == XS_WGRAD &&
+    return g.ldc % 8 == 0 && g.msplit % 4 == 0 && g.sched_mode == XS_WGRAD &&
            (g.ksplit <= 1 || (g.part && al16(g.part)));
-  if (g.ldc % 4 || g.c_group_col % 4 || !al8(g.C)) return false;
   if (epi == XE_SWIGLU_BWD)
-    return g.du_off % 4 == 0 && g.ld_gu % 4 == 0 && g.gu_group_col % 4 == 0 && al8(g.Gs) && al8(g.Us);
-  return true;
+    return g.ldc % 4 == 0 && g.c_group_col % 4 == 0 && al8(g.C) && g.du_off % 4 == 0 && g.ld_gu % 4 == 0 &&
+           g.gu_group_col % 4 == 0 && al8(g.Gs) && al8(g.Us);
+  return g.ldc % 8 == 0 && g.c_group_col % 8 == 0 && al16(g.C);
 }
 
 template <int EPI, int AMODE, int BMODE>
@@ -397,12 +442,12 @@ static int launch_xm_t(const XGemm& g, int64_t grid, hipStream_t st) {
   auto kern = xgemm_mfma_kernel<EPI, AMODE, BMODE>;
   static bool attr = false;
   if (!attr) {
-    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)XM_LDS_BYTES) !=
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)XM_LDS_ALLOC) !=
         hipSuccess)
       return fail(DSMOE_ERR_HIP, "xgemm: cannot raise LDS limit");
     attr = true;
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(XM_THREADS), XM_LDS_BYTES, st, g);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(XM_THREADS), XM_LDS_ALLOC, st, g);
   return check_launch("xgemm_mfma");
 }
 
