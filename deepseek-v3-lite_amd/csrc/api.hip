@@ -107,6 +107,7 @@ struct FwdLayout {
   void* us;
   void* o_slots;
   void* shared_out;
+  void* x_sorted;   // training: routed rows of x in sorted order (the backward's K-major operand)
   size_t total;
 };
 
@@ -134,6 +135,7 @@ static FwdLayout fwd_layout(const dsmoe_dims& d, int training, void* base) {
   L.us = (d.S && training) ? c.take<char>((size_t)d.T * SIs * es) : nullptr;
   L.o_slots = c.take<char>((size_t)N * d.D * es);
   L.shared_out = d.S ? c.take<char>((size_t)d.T * d.D * es) : nullptr;
+  L.x_sorted = training ? c.take<char>((size_t)N * d.D * es) : nullptr;
   L.total = c.used();
   return L;
 }
@@ -375,6 +377,12 @@ int dsmoe_moe_fwd(const void* x, const float* gate_w, const float* gate_bias, co
   tm.begin(ST_PERMUTE);
   rc = launch_permute(L.idx, d, bm, L.ps, L.offsets, L.sorted_slot, L.sorted_token, L.slot_pos, counts,
                       training ? L.w : nullptr, L.sorted_w, st);
+  if (!rc && training) {
+    // the routed rows of x in sorted order, for the backward's weight
+    // gradient (a K-major operand read without a row gather); gemm1 keeps
+    // gathering from x, which stays cache-resident
+    rc = launch_gather_rows(x, L.sorted_token, N, d.D, elem_size(d.dtype), L.x_sorted, st);
+  }
   tm.end();
   if (rc) return rc;
   g1.sched = g2.sched = L.ps.sched;
@@ -450,6 +458,7 @@ struct BwdLayout {
   void* dx_slots;     // (N, D)    slot order
   void* dgdu_s;       // (T, 2 S I_s)
   void* dx_shared;    // (T, D)
+  void* dy_w;         // bf16: (N, D) w * dY in sorted order (K-major operand of dW2)
   int ks13, ks2;      // split-K of the shared-expert weight gradients (bf16 MFMA path)
   float* part;        // fp32 split-K partials, max(ks13 * 2 I_s, ks2 * I_s) * S * D
   size_t total;
@@ -489,6 +498,7 @@ static BwdLayout bwd_layout(const dsmoe_dims& d, void* base) {
   B.dx_slots = c.take<char>((size_t)N * d.D * es);
   B.dgdu_s = d.S ? c.take<char>((size_t)d.T * 2 * d.S * d.I_s * es) : nullptr;
   B.dx_shared = d.S ? c.take<char>((size_t)d.T * d.D * es) : nullptr;
+  B.dy_w = d.dtype == DSMOE_BF16 ? c.take<char>((size_t)N * d.D * es) : nullptr;
   B.ks13 = B.ks2 = 1;
   B.part = nullptr;
   if (d.S && d.dtype == DSMOE_BF16) {
@@ -567,6 +577,7 @@ int dsmoe_moe_bwd(const void* x, const float* gate_w, const void* const* w1, con
   if (rc) return rc;
   // gate gradient path: d weights -> d logits
   rc = launch_dw_dot(dy, F.o_slots, N, d.k, d.D, d.dtype, B.dw, st);
+  if (!rc && B.dy_w) rc = launch_scale_gather_rows(dy, F.sorted_token, F.sorted_w, N, d.D, B.dy_w, st);
   if (!rc) rc = launch_gate_bwd(B.dw, F.sel, d.T, d.k, d.route_scale, B.dlog, st);
   if (!rc) rc = launch_sched32(F.offsets, d.E, BWD_BM, B.sched, B.sched_count, st);
   tm.end();
@@ -600,7 +611,7 @@ int dsmoe_moe_bwd(const void* x, const float* gate_w, const void* const* w1, con
   XGemm w13 = xdesc_zero();
   w13.sched_mode = XS_WGRAD; w13.groups = d.E; w13.k_off = F.offsets; w13.M = 2 * d.I; w13.N = d.D; w13.K = (int32_t)N;
   w13.a_mode = XA_KMAJOR; w13.A = B.dgdu; w13.lda = 2 * (int64_t)d.I;
-  w13.b_mode = XB_ACT_KMAJOR; w13.Bact = x; w13.b_map = F.sorted_token; w13.ldb = d.D;
+  w13.b_mode = XB_ACT_KMAJOR; w13.Bact = F.x_sorted; w13.ldb = d.D;
   w13.Ctab0 = B.dw1; w13.Ctab1 = B.dw3; w13.msplit = d.I; w13.ldc = d.D;
   tm.begin(ST_BWD_DW13);
   rc = launch_xgemm(w13, XE_WGRAD, d.dtype, mf, st);
@@ -608,7 +619,12 @@ int dsmoe_moe_bwd(const void* x, const float* gate_w, const void* const* w1, con
   if (rc) return rc;
   XGemm w2g = xdesc_zero();
   w2g.sched_mode = XS_WGRAD; w2g.groups = d.E; w2g.k_off = F.offsets; w2g.M = d.D; w2g.N = d.I; w2g.K = (int32_t)N;
-  w2g.a_mode = XA_KMAJOR; w2g.A = dy; w2g.lda = d.D; w2g.a_map = F.sorted_token; w2g.a_kscale = F.sorted_w;
+  w2g.a_mode = XA_KMAJOR; w2g.lda = d.D;
+  if (B.dy_w) {
+    w2g.A = B.dy_w;  // w * dY already gathered and rounded once
+  } else {
+    w2g.A = dy; w2g.a_map = F.sorted_token; w2g.a_kscale = F.sorted_w;
+  }
   w2g.b_mode = XB_ACT_KMAJOR; w2g.Bact = F.h; w2g.ldb = d.I;
   w2g.Ctab0 = B.dw2; w2g.Ctab1 = B.dw2; w2g.msplit = d.D; w2g.ldc = d.I;
   tm.begin(ST_BWD_DW2);

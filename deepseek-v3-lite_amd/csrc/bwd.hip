@@ -226,6 +226,39 @@ __global__ __launch_bounds__(256) void dwgate_vec_kernel(const T* __restrict__ x
 static bool al16p(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 // ---------------------------------------------------------------- launchers
+// dst[p] = bf16(w[p] * src[rows[p]]), 8 columns per thread: one fp32 product
+// per element rounded once, as the backward of the routed combine's
+// out * weight (models/moe.py:132) rounds it.
+__global__ __launch_bounds__(256) void scale_gather_kernel(const bf16_t* __restrict__ src, const int32_t* __restrict__ rows,
+                                                           const float* __restrict__ w, int64_t n, int vpr,
+                                                           bf16_t* __restrict__ dst) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n * vpr) return;
+  const int64_t p = i / vpr;
+  const int c = (int)(i - p * vpr);
+  const float s = w[p];
+  const uint4 v = reinterpret_cast<const uint4*>(src + (int64_t)rows[p] * vpr * 8)[c];
+  uint4 o;
+  const uint32_t in[4] = {v.x, v.y, v.z, v.w};
+  uint32_t out[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d)
+    out[d] = (uint32_t)f2bf(__uint_as_float(in[d] << 16) * s) |
+             ((uint32_t)f2bf(__uint_as_float(in[d] & 0xffff0000u) * s) << 16);
+  o.x = out[0]; o.y = out[1]; o.z = out[2]; o.w = out[3];
+  reinterpret_cast<uint4*>(dst + p * vpr * 8)[c] = o;
+}
+
+int launch_scale_gather_rows(const void* src, const int32_t* rows, const float* w, int64_t n, int D, void* dst,
+                             hipStream_t st) {
+  if (n == 0) return DSMOE_OK;
+  if (D % 8) return fail(DSMOE_ERR_UNSUPPORTED, "scale_gather: D must be a multiple of 8");
+  const int vpr = D / 8;
+  hipLaunchKernelGGL(scale_gather_kernel, dim3((unsigned)cdiv(n * vpr, 256)), dim3(256), 0, st,
+                     static_cast<const bf16_t*>(src), rows, w, n, vpr, static_cast<bf16_t*>(dst));
+  return check_launch("scale_gather");
+}
+
 int launch_dw_dot(const void* dy, const void* o_slots, int64_t N, int k, int D, int dtype, float* dw,
                   hipStream_t st) {
   if (N == 0) return DSMOE_OK;

@@ -248,6 +248,12 @@ struct XGemm {
 int launch_xgemm(const XGemm& g, int epi, int dtype, bool allow_mfma, hipStream_t st);
 bool xgemm_mfma_ok(const XGemm& g, int epi);
 int launch_xgemm_mfma(const XGemm& g, int epi, hipStream_t st);
+bool xgemm_q_ok(const XGemm& g, int epi);
+int launch_wgrad_reduce(const XGemm& g, hipStream_t st);
+int launch_xgemm_q(const XGemm& g, int epi, hipStream_t st);
+// dst[p] = bf16(w[p] * src[rows[p]]) for p < n, rows of D bf16 (w * dY in sorted order)
+int launch_scale_gather_rows(const void* src, const int32_t* rows, const float* w, int64_t n, int D, void* dst,
+                             hipStream_t st);
 int xgemm_pick_ksplit(int64_t tiles, int64_t k_len);
 int64_t xgemm_tiles(int64_t M, int64_t N, int groups);
 int launch_dw_dot(const void* dy, const void* o_slots, int64_t N, int k, int D, int dtype, float* dw, hipStream_t st);

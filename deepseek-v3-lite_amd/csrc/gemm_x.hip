@@ -166,6 +166,7 @@ static int launch_xsimt(const XGemm& g, int epi, hipStream_t st) {
 
 int launch_xgemm(const XGemm& g, int epi, int dtype, bool allow_mfma, hipStream_t st) {
   if (g.N <= 0 || (g.sched_mode == XS_WGRAD ? g.M <= 0 : false)) return DSMOE_OK;
+  if (dtype == DSMOE_BF16 && allow_mfma && xgemm_q_ok(g, epi)) return launch_xgemm_q(g, epi, st);
   if (dtype == DSMOE_BF16 && allow_mfma && xgemm_mfma_ok(g, epi)) return launch_xgemm_mfma(g, epi, st);
   if (g.ksplit > 1) {  // the FMA tiles store directly
     XGemm g1 = g;

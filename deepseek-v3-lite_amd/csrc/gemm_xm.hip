@@ -368,7 +368,7 @@ __global__ __launch_bounds__(XM_THREADS) void xgemm_mfma_kernel(const XGemm g) {
         const float gv = __uint_as_float((e & 1) ? (gw & 0xffff0000u) : (gw << 16));
         const float uv = __uint_as_float((e & 1) ? (uw & 0xffff0000u) : (uw << 16));
         const float dh = rw * dhv[e];
-        const float sg = sigmoid_f(gv);
+        const float sg = __builtin_amdgcn_rcpf(1.0f + __expf(-gv));  // 1 ulp; dg, du are rounded to bf16
         dg[e] = dh * uv * sg * (1.0f + gv * (1.0f - sg));
         du[e] = dh * gv * sg;
       }
@@ -466,7 +466,12 @@ int launch_xgemm_mfma(const XGemm& g, int epi, hipStream_t st) {
   if (epi == XE_STORE) return launch_xm_t<XE_STORE, XA_ROWS, XB_W_NN>(g, grid, st);
   int rc = launch_xm_t<XE_WGRAD, XA_KMAJOR, XB_ACT_KMAJOR>(g, grid, st);
   if (rc || g.ksplit <= 1) return rc;
+  return launch_wgrad_reduce(g, st);
+}
+
+int launch_wgrad_reduce(const XGemm& g, hipStream_t st) {
   const int64_t n4 = (int64_t)g.groups * g.M * (g.N / 4);
+  if (n4 == 0) return DSMOE_OK;
   hipLaunchKernelGGL(wgrad_reduce_kernel, dim3((unsigned)cdiv(n4, 256)), dim3(256), 0, st, g);
   return check_launch("wgrad_reduce");
 }

@@ -1,0 +1,534 @@
+// Backward grouped GEMMs on gfx950: the quad-wave design of gemm_qw.hip
+// (four waves, one per SIMD, each owning 128 x 128 of a 256 x 256 tile; K
+// slabs of 64 streamed into separate A and B LDS rings by direct
+// global -> LDS loads; fragment reads two K steps ahead of the MFMAs;
+// LDS-staged, whole-row epilogues) extended to operands whose reduction
+// index K is the ROW index of the stored matrix ("K-major", KM):
+//   dh   = dY W2            A = dY rows (K contiguous)     B(n=i, k=d) = W2[d][i]
+//   dx   = [dg|du][W1;W3]   A = [dg|du] rows               B(n=d, k=i) = W1[i][d] / W3[i][d]
+//   dW13 = [dg|du]^T X      A(m=i, k=r) = dgdu[r][i]       B(n=d, k=r) = Xs[r][d]
+//   dW2  = (w dY)^T H       A(m=d, k=r) = dYw[r][d]        B(n=i, k=r) = H[r][i]
+// (models/moe.py:127-131 under autograd; models/moe_triton.py:142-374.)
+// Every KM operand is read with identity rows: the layer materialises the
+// routed rows of X in sorted order (forward) and w * dY in sorted order
+// (backward preparation), so a KM slab is 64 consecutive rows of 512 bytes.
+//
+// KM slabs are stored untransposed, [64 k][256 columns], 512-byte rows, and
+// gfx950's transposing LDS read (ds_read_b64_tr_b16) builds the MFMA
+// fragment: within each 16-lane group, lane s supplies the 8-byte address of
+// row k0 + (s >> 2), columns c0 + 4 (s & 3) .. +3, and lane i receives the
+// column c0 + i of the four rows.  Two such reads (k0 and k0 + 4) give a
+// lane its 8 consecutive k of one column, the v_mfma_f32_32x32x16_bf16
+// operand layout.  8-byte unit u of k row r is stored at unit u ^ 8 (r & 3):
+// the 32 lanes of a half-wave read 4 rows x 8 units that land on 32
+// distinct bank pairs, and the 16-byte chunks a direct load writes stay
+// contiguous (the XOR leaves unit bits 0-2 alone).
+//
+// Weight-gradient K ranges (an expert's rows) are ragged: A rows past the
+// range are read from a zero block instead, so their products vanish.
+//
+// Determinism: one block owns each output tile and walks its K range in
+// ascending order (fp32 accumulation, one rounding); split-K partials of the
+// shared-expert weight gradients are added in ascending part order by
+// wgrad_reduce_kernel.
+#include <algorithm>
+
+#include "gemm_tile.h"
+#include "mfma.h"
+
+namespace dsmoe {
+
+constexpr int XQ_BM = 256, XQ_BN = 256;
+constexpr int XQ_BK = 64;                             // K per slab
+constexpr int XQ_REG = 32 * 1024;                     // one operand of a slab
+constexpr int XQ_ASLOTS = 2, XQ_BSLOTS = 3;
+constexpr int XQ_BOFF = XQ_ASLOTS * XQ_REG;
+constexpr size_t XQ_LDS = (size_t)(XQ_ASLOTS + XQ_BSLOTS) * XQ_REG;  // 160 KB (the epilogue reuses it)
+constexpr int XQ_LD = XQ_REG / 1024 / 4;              // direct loads per wave, operand and slab (8)
+
+// A block of zeros: the source of weight-gradient A rows past the K range.
+__device__ __attribute__((aligned(16))) uint4 g_xq_zero[4];
+
+typedef short xq_v4s __attribute__((ext_vector_type(4)));
+
+// K-contiguous ("NT") slab: [256 rows][64 k], 128-byte rows, 16-byte chunk c
+// of row r at chunk c ^ ((r >> 1) & 7).
+__device__ __forceinline__ int xq_nt(int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
+// K-major slab: [64 k][256 columns], 512-byte rows; 8-byte unit u of row k at
+// unit u ^ 8 (k & 3).  Byte offset of the 8 bytes holding columns 4u .. 4u+3.
+__device__ __forceinline__ int xq_km(int k, int u) { return k * 512 + ((u ^ ((k & 3) << 3)) << 3); }
+
+__device__ __forceinline__ xq_v4s xq_tr(const char* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) xq_v4s*)p);
+}
+
+// MFMA fragment of a KM slab region: 32 columns c0 .. c0+31 (lane l: column
+// c0 + (l & 31)) at k0 + 8 (l >> 5) .. +7.
+__device__ __forceinline__ bf16x8_t xq_km_frag(const char* reg, int k0, int c0, int lane) {
+  const int gq = lane >> 4, s = lane & 15;
+  const int k = k0 + 8 * (gq >> 1) + (s >> 2);
+  const int u = (c0 >> 2) + 4 * (gq & 1) + (s & 3);
+  const xq_v4s lo = xq_tr(reg + xq_km(k, u));
+  const xq_v4s hi = xq_tr(reg + xq_km(k + 4, u));
+  typedef short v8s __attribute__((ext_vector_type(8)));
+  const v8s v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+
+// Direct-load sources of one wave.  Wave w fills rows 64 w .. 64 w + 63 of an
+// NT region, or k rows 16 w .. 16 w + 15 of a KM region (load i: rows
+// 16 w + 2 i + (l >> 5)).
+struct XQLoad {
+  const bf16_t* a;        // A base (KM: + group column offset)
+  int64_t a_ld;           // KM: elements per k row
+  const bf16_t* b0;       // B, K segment 0 (weights) or matrix base (+ group column offset)
+  const bf16_t* b1;       // B, last K segment
+  int64_t b_ld;
+  uint32_t offa[XQ_LD];   // NT: row * lda + chunk (KM: unused)
+  uint32_t kma[2];        // KM A: offset of load i = kma[i & 1] + 2 i lda  (= k_i * lda + column)
+  uint32_t kmb[2];        // B: offset of load i = kmb[i & 1] + 2 i ldb  (= k_i * ldb + column)
+  int kseg;               // K at which b1 takes over (0x7fffffff: one segment)
+  int kbeg, kend, nk;
+  int lds_off;            // byte offset of this wave's 8 KB inside an operand region
+  int krow0;              // KM: first k row of this wave's loads (16 w)
+};
+
+template <int AMODE, int I0, int I1>
+__device__ __forceinline__ void xq_issue_a(const XQLoad& L, int ka, int lane) {
+  extern __shared__ __attribute__((aligned(16))) char xq_smem[];
+  const uint32_t da = lds_addr(xq_smem) + L.lds_off + (ka & 1) * XQ_REG;
+  const int k0 = L.kbeg + min(ka, L.nk - 1) * XQ_BK;
+#pragma unroll
+  for (int i = I0; i < I1; ++i) {
+    const bf16_t* src;
+    if (AMODE == XA_ROWS) {
+      src = L.a + L.offa[i] + k0;
+    } else {
+      // rows past the K range read zeros (weight-gradient tails)
+      const int kr = k0 + L.krow0 + 2 * i + (lane >> 5);
+      const uint32_t off = L.kma[i & 1] + (uint32_t)(2 * i) * (uint32_t)L.a_ld;
+      src = kr < L.kend ? L.a + (int64_t)k0 * L.a_ld + off : reinterpret_cast<const bf16_t*>(g_xq_zero);
+    }
+    dma16(src, da + i * 1024);
+  }
+}
+
+template <int BMODE, int I0, int I1>
+__device__ __forceinline__ void xq_issue_b(const XQLoad& L, int kb, int lane) {
+  extern __shared__ __attribute__((aligned(16))) char xq_smem[];
+  const uint32_t db = lds_addr(xq_smem) + L.lds_off + XQ_BOFF + (kb % XQ_BSLOTS) * XQ_REG;
+  const int k0 = L.kbeg + min(kb, L.nk - 1) * XQ_BK;
+  const bool hi = k0 >= L.kseg;
+  const bf16_t* src = (hi ? L.b1 : L.b0) + (int64_t)(hi ? k0 - L.kseg : k0) * L.b_ld;
+#pragma unroll
+  for (int i = I0; i < I1; ++i) {
+    const bf16_t* p = src + (L.kmb[i & 1] + (uint32_t)(2 * i) * (uint32_t)L.b_ld);
+    if (BMODE == XB_ACT_KMAJOR) {
+      // activation rows past the K range (the last one may be the matrix's
+      // last row) are not read: zeros instead
+      const int kr = k0 + L.krow0 + 2 * i + (lane >> 5);
+      if (kr >= L.kend) p = reinterpret_cast<const bf16_t*>(g_xq_zero);
+    }
+    dma16(p, db + i * 1024);
+  }
+}
+
+// Fragments of K step s (0..3) of slab kb: A sub-tiles j < NMI (rows
+// (2j + wm) * 32 ..), B tiles ni (columns wn * 128 + 32 ni ..).
+template <int AMODE, int NMI>
+__device__ __forceinline__ void xq_read(int kb, int s, int wm, int wn, int lane, bf16x8_t (&fa)[4],
+                                        bf16x8_t (&fb)[4]) {
+  extern __shared__ __attribute__((aligned(16))) char xq_smem[];
+  if (NMI == 0) return;
+  const char* sA = xq_smem + (kb & 1) * XQ_REG;
+  const char* sB = xq_smem + XQ_BOFF + (kb % XQ_BSLOTS) * XQ_REG;
+#pragma unroll
+  for (int j = 0; j < NMI; ++j) {
+    if (AMODE == XA_ROWS)
+      fa[j] = *reinterpret_cast<const bf16x8_t*>(sA + xq_nt((2 * j + wm) * 32 + (lane & 31), s * 2 + (lane >> 5)));
+    else
+      fa[j] = xq_km_frag(sA, s * 16, (2 * j + wm) * 32, lane);
+  }
+#pragma unroll
+  for (int ni = 0; ni < 4; ++ni) fb[ni] = xq_km_frag(sB, s * 16, wn * 128 + ni * 32, lane);
+}
+
+// MFMAs T0 .. T1-1 of one K step, t = j * 4 + ni.
+template <int NMI, int T0 = 0, int T1 = NMI * 4>
+__device__ __forceinline__ void xq_mma(const bf16x8_t (&fa)[4], const bf16x8_t (&fb)[4], f32x16_t (&acc)[4][4]) {
+#pragma unroll
+  for (int t = T0; t < T1; ++t)
+    acc[t / 4][t % 4] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[t % 4], fa[t / 4], acc[t / 4][t % 4], 0, 0, 0);
+}
+
+__device__ __forceinline__ void xq_sync() {
+  __builtin_amdgcn_sched_barrier(0);
+  lds_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+struct XQPipe {
+  bf16x8_t fa[3][4];
+  bf16x8_t fb[3][4];
+};
+
+// One slab whose step 0 uses register set S0 (see qw_slab in gemm_qw.hip:
+// reads run two steps ahead; the barrier follows step 1; step 2 issues the
+// loads of A(kb + 2) and B(kb + 3) into the slots slab kb frees).
+template <int AMODE, int NMI, int S0>
+__device__ __forceinline__ void xq_slab(XQPipe& P, const XQLoad& L, int kb, int wm, int wn, int lane,
+                                        f32x16_t (&acc)[4][4]) {
+  constexpr int MMAS = NMI * 4;
+  constexpr int A0 = S0 % 3, A1 = (S0 + 1) % 3, A2 = (S0 + 2) % 3;
+  __builtin_amdgcn_sched_barrier(0);
+  xq_read<AMODE, NMI>(kb, 2, wm, wn, lane, P.fa[A2], P.fb[A2]);
+  __builtin_amdgcn_sched_barrier(0);
+  xq_mma<NMI>(P.fa[A0], P.fb[A0], acc);
+  __builtin_amdgcn_sched_barrier(0);
+  xq_read<AMODE, NMI>(kb, 3, wm, wn, lane, P.fa[A0], P.fb[A0]);
+  __builtin_amdgcn_sched_barrier(0);
+  xq_mma<NMI>(P.fa[A1], P.fb[A1], acc);
+  __builtin_amdgcn_sched_barrier(0);
+  // all reads of slab kb issued: wait for them and for this wave's loads of
+  // A(kb + 1) and B(kb + 1) (only B(kb + 2), issued after A(kb + 1), may be
+  // younger); then slab kb + 1 is visible and slab kb's slots are free
+  wait_lgkm0();
+  wait_vm<XQ_LD>();
+  xq_sync();
+  if (MMAS >= 4) {
+    xq_mma<NMI, 0, 1>(P.fa[A2], P.fb[A2], acc);
+    __builtin_amdgcn_sched_barrier(0);
+    xq_issue_a<AMODE, 0, 4>(L, kb + 2, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    xq_mma<NMI, 1, 2>(P.fa[A2], P.fb[A2], acc);
+    __builtin_amdgcn_sched_barrier(0);
+    xq_issue_a<AMODE, 4, XQ_LD>(L, kb + 2, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    xq_mma<NMI, 2, 3>(P.fa[A2], P.fb[A2], acc);
+    __builtin_amdgcn_sched_barrier(0);
+    xq_issue_b<AMODE == XA_ROWS ? XB_W_NN : XB_ACT_KMAJOR, 0, 4>(L, kb + 3, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    xq_mma<NMI, 3, 4>(P.fa[A2], P.fb[A2], acc);
+    __builtin_amdgcn_sched_barrier(0);
+    xq_issue_b<AMODE == XA_ROWS ? XB_W_NN : XB_ACT_KMAJOR, 4, XQ_LD>(L, kb + 3, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    xq_read<AMODE, NMI>(kb + 1, 0, wm, wn, lane, P.fa[A1], P.fb[A1]);
+    __builtin_amdgcn_sched_barrier(0);
+    xq_mma<NMI, 4, MMAS>(P.fa[A2], P.fb[A2], acc);
+  } else {
+    xq_issue_a<AMODE, 0, XQ_LD>(L, kb + 2, lane);
+    xq_issue_b<AMODE == XA_ROWS ? XB_W_NN : XB_ACT_KMAJOR, 0, XQ_LD>(L, kb + 3, lane);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  xq_read<AMODE, NMI>(kb + 1, 1, wm, wn, lane, P.fa[A2], P.fb[A2]);
+  __builtin_amdgcn_sched_barrier(0);
+  xq_mma<NMI>(P.fa[A0], P.fb[A0], acc);
+}
+
+template <int AMODE, int NMI>
+__device__ __forceinline__ void xq_loop(const XQLoad& L, int wm, int wn, int lane, f32x16_t (&acc)[4][4]) {
+  XQPipe P;
+  xq_read<AMODE, NMI>(0, 0, wm, wn, lane, P.fa[0], P.fb[0]);
+  xq_read<AMODE, NMI>(0, 1, wm, wn, lane, P.fa[1], P.fb[1]);
+  wait_lgkm0();  // no scalar load in flight at the loop head (see qw_loop)
+  int kb = 0;
+  for (; kb + 3 <= L.nk; kb += 3) {
+    xq_slab<AMODE, NMI, 0>(P, L, kb, wm, wn, lane, acc);
+    xq_slab<AMODE, NMI, 1>(P, L, kb + 1, wm, wn, lane, acc);
+    xq_slab<AMODE, NMI, 2>(P, L, kb + 2, wm, wn, lane, acc);
+  }
+  if (kb < L.nk) xq_slab<AMODE, NMI, 0>(P, L, kb, wm, wn, lane, acc);
+  if (kb + 1 < L.nk) xq_slab<AMODE, NMI, 1>(P, L, kb + 1, wm, wn, lane, acc);
+  __builtin_amdgcn_sched_barrier(0);
+  wait_vm<0>();
+}
+
+template <int EPI, int AMODE>
+__global__ __launch_bounds__(256) void xgemm_q_kernel(const XGemm g) {
+  extern __shared__ __attribute__((aligned(16))) char xq_smem[];
+  int grp, row0, rows, n_tile, kbeg, kend, split;
+  if (!xtile<XQ_BM, XQ_BN>(g, grp, row0, rows, n_tile, kbeg, kend, split)) return;
+  grp = __builtin_amdgcn_readfirstlane(grp);
+  row0 = __builtin_amdgcn_readfirstlane(row0);
+  rows = __builtin_amdgcn_readfirstlane(rows);
+  n_tile = __builtin_amdgcn_readfirstlane(n_tile);
+  kbeg = __builtin_amdgcn_readfirstlane(kbeg);
+  kend = __builtin_amdgcn_readfirstlane(kend);
+  split = __builtin_amdgcn_readfirstlane(split);
+  const int n0 = n_tile * XQ_BN;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  XQLoad L;
+  L.kbeg = kbeg;
+  L.kend = kend;
+  L.nk = (kend > kbeg) ? (int)cdiv(kend - kbeg, XQ_BK) : 0;
+  L.lds_off = wave * XQ_LD * 1024;
+  L.krow0 = wave * 16;
+  constexpr int BM = AMODE == XA_ROWS ? XB_W_NN : XB_ACT_KMAJOR;  // B mode paired with the A mode
+  // ---- A sources
+  if (AMODE == XA_ROWS) {
+    // wave w: rows 64 w + 8 i + (l >> 3), chunk (l & 7) of 128-byte rows
+    L.a = static_cast<const bf16_t*>(g.A);
+    L.a_ld = g.lda;
+#pragma unroll
+    for (int i = 0; i < XQ_LD; ++i) {
+      const int r = (wave * XQ_LD + i) * 8 + (lane >> 3);
+      const int c = (lane & 7) ^ ((r >> 1) & 7);
+      const int ra = min(r, rows - 1);
+      const int64_t arow = g.a_map ? (int64_t)g.a_map[row0 + ra] : (int64_t)(row0 + ra);
+      L.offa[i] = (uint32_t)(arow * g.lda + c * 8);
+    }
+  } else {
+    // KM: k rows 16 w + 2 i + (l >> 5), 16-byte chunk (l & 31) of 512-byte
+    // rows; the chunk swizzle depends on k & 3, i.e. on the parity of i
+    L.a = static_cast<const bf16_t*>(g.A) + (int64_t)grp * g.a_col;
+    L.a_ld = g.lda;
+#pragma unroll
+    for (int par = 0; par < 2; ++par) {
+      // load i reads k row k_i = 16 w + 2 i + (l >> 5), whose swizzle depends
+      // on k_i & 3, i.e. on par = i & 1; the 2 i rows go into the per-load term
+      const int kr = wave * 16 + (lane >> 5);
+      const int c = (lane & 31) ^ (((kr + 2 * par) & 3) << 2);
+      const int m = min(row0 + 8 * c, g.M - 8);  // output rows are columns of the stored A
+      L.kma[par] = (uint32_t)((int64_t)kr * g.lda + m);
+    }
+  }
+  // ---- B sources (always KM)
+  if (BM == XB_W_NN) {
+    const void* const* tab = g.Btab + (int64_t)grp * g.nseg;
+    L.b0 = static_cast<const bf16_t*>(tab[0]);
+    L.b1 = static_cast<const bf16_t*>(tab[g.nseg - 1]);
+    L.kseg = g.nseg > 1 ? g.kseg : 0x7fffffff;
+  } else {
+    L.b0 = L.b1 = static_cast<const bf16_t*>(g.Bact) + (int64_t)grp * g.b_col;
+    L.kseg = 0x7fffffff;
+  }
+  L.b_ld = g.ldb;
+#pragma unroll
+  for (int par = 0; par < 2; ++par) {
+    const int kr = wave * 16 + (lane >> 5);
+    const int c = (lane & 31) ^ (((kr + 2 * par) & 3) << 2);
+    const int n = min(n0 + 8 * c, g.N - 8);
+    L.kmb[par] = (uint32_t)((int64_t)kr * g.ldb + n);
+  }
+
+  f32x16_t acc[4][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[j][ni][r] = 0.0f;
+
+  if (L.nk > 0) {
+    // ---- prologue: slab 0 visible to all waves; then A(1), B(1), B(2) in flight
+    xq_issue_a<AMODE, 0, XQ_LD>(L, 0, lane);
+    xq_issue_b<BM, 0, XQ_LD>(L, 0, lane);
+    wait_vm<0>();
+    xq_sync();
+    xq_issue_a<AMODE, 0, XQ_LD>(L, 1, lane);
+    xq_issue_b<BM, 0, XQ_LD>(L, 1, lane);
+    xq_issue_b<BM, 0, XQ_LD>(L, 2, lane);
+    // active row sub-tiles of this wave; none when its 128 columns all lie
+    // past N (the last column tile of N = 1408, for instance)
+    const int nsub = (int)cdiv(rows, 32);
+    const int nmi = (n0 + wn * 128 >= g.N) ? 0 : max(0, min(4, (nsub - wm + 1) >> 1));
+    switch (nmi) {
+      case 4: xq_loop<AMODE, 4>(L, wm, wn, lane, acc); break;
+      case 3: xq_loop<AMODE, 3>(L, wm, wn, lane, acc); break;
+      case 2: xq_loop<AMODE, 2>(L, wm, wn, lane, acc); break;
+      case 1: xq_loop<AMODE, 1>(L, wm, wn, lane, acc); break;
+      default: xq_loop<AMODE, 0>(L, wm, wn, lane, acc); break;
+    }
+  }
+
+  // ---- epilogue.  Lane holds tile row m = (2j + wm) * 32 + (lane & 31) and,
+  // per q, columns n = wn * 128 + 32 ni + 8 q + 4 (lane >> 5) + {0..3}
+  // (registers 4q .. 4q+3).  Split-K partials go straight out as fp32.
+  if (EPI == XE_WGRAD && g.ksplit > 1) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int m = (2 * j + wm) * 32 + (lane & 31);
+      if (m >= rows) continue;
+      float* prow = g.part + (((int64_t)split * g.groups + grp) * g.M + row0 + m) * g.N;
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int n = n0 + wn * 128 + ni * 32 + q * 8 + (lane >> 5) * 4;
+          if (n < g.N)
+            *reinterpret_cast<float4*>(prow + n) =
+                make_float4(acc[j][ni][q * 4], acc[j][ni][q * 4 + 1], acc[j][ni][q * 4 + 2], acc[j][ni][q * 4 + 3]);
+        }
+    }
+    return;
+  }
+  // Otherwise the tile goes through LDS and leaves as whole rows; output row
+  // pointers are resolved once per row.
+  __builtin_amdgcn_sched_barrier(0);
+  wait_lgkm0();
+  xq_sync();  // every wave is done with the slab buffers
+  char* sm = xq_smem;
+  int64_t* rowp = reinterpret_cast<int64_t*>(sm + 128 * 1024);  // past the staged tile (<= 128 KB)
+  int64_t my_rowp;
+  {
+    const int r = row0 + min(tid, rows - 1);
+    if (EPI == XE_WGRAD)
+      my_rowp = reinterpret_cast<int64_t>(static_cast<bf16_t*>(r < g.msplit ? g.Ctab0[grp] : g.Ctab1[grp]) +
+                                          (int64_t)(r < g.msplit ? r : r - g.msplit) * g.ldc);
+    else
+      my_rowp = reinterpret_cast<int64_t>(static_cast<bf16_t*>(g.C) + (int64_t)grp * g.c_group_col +
+                                          (g.c_map ? (int64_t)g.c_map[r] : (int64_t)r) * g.ldc);
+  }
+  if (EPI != XE_SWIGLU_BWD) {
+    // bf16 tile, 256 rows x 512 bytes; 8-byte unit u of row m at unit u ^ (m & 31)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int m = (2 * j + wm) * 32 + (lane & 31);
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int u = (wn * 128 + ni * 32 + q * 8 + (lane >> 5) * 4) >> 2;
+          u32x2_t w;
+          w.x = pack_bf16x2(acc[j][ni][q * 4], acc[j][ni][q * 4 + 1]);
+          w.y = pack_bf16x2(acc[j][ni][q * 4 + 2], acc[j][ni][q * 4 + 3]);
+          *reinterpret_cast<u32x2_t*>(sm + m * 512 + ((u ^ (m & 31)) << 3)) = w;
+        }
+    }
+    rowp[tid] = my_rowp;
+    xq_sync();
+    // 32 lanes per row, 16 bytes each; 8 rows per pass
+    const int cc = tid & 31, n = n0 + cc * 8;
+    for (int r = tid >> 5; r < rows; r += 8) {
+      const int pu = (2 * cc) ^ (r & 31);
+      u32x4_t v = *reinterpret_cast<const u32x4_t*>(sm + r * 512 + ((pu >> 1) << 4));
+      if (r & 1) v = u32x4_t{v.z, v.w, v.x, v.y};
+      if (n < g.N) *reinterpret_cast<u32x4_t*>(reinterpret_cast<bf16_t*>(rowp[r]) + n) = v;
+    }
+    return;
+  }
+  // SwiGLU backward: dh stays fp32 until dg and du are formed, so each column
+  // half (128 columns, owned by the waves with wn == half) is staged as fp32
+  // in turn; 16-byte unit u of row m at unit u ^ (m & 31).
+  const bf16_t* Gs = static_cast<const bf16_t*>(g.Gs);
+  const bf16_t* Us = static_cast<const bf16_t*>(g.Us);
+  rowp[tid] = my_rowp;
+  for (int half = 0; half < 2; ++half) {
+    if (half) xq_sync();  // the first half's reads are done
+    if (wn == half) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int m = (2 * j + wm) * 32 + (lane & 31);
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int u = (ni * 32 + q * 8 + (lane >> 5) * 4) >> 2;
+            *reinterpret_cast<float4*>(sm + m * 512 + ((u ^ (m & 31)) << 4)) =
+                make_float4(acc[j][ni][q * 4], acc[j][ni][q * 4 + 1], acc[j][ni][q * 4 + 2], acc[j][ni][q * 4 + 3]);
+          }
+      }
+    }
+    xq_sync();
+    const int cc = tid & 31, n = n0 + half * 128 + cc * 4;
+    for (int r = tid >> 5; r < rows; r += 8) {
+      const float4 dh4 = *reinterpret_cast<const float4*>(sm + r * 512 + ((cc ^ (r & 31)) << 4));
+      if (n >= g.N) continue;
+      const float rw = g.row_w ? g.row_w[row0 + r] : 1.0f;
+      const int64_t ogu = (int64_t)(row0 + r) * g.ld_gu + (int64_t)grp * g.gu_group_col + n;
+      const u32x2_t gp = *reinterpret_cast<const u32x2_t*>(Gs + ogu);
+      const u32x2_t up = *reinterpret_cast<const u32x2_t*>(Us + ogu);
+      const float dhv[4] = {dh4.x, dh4.y, dh4.z, dh4.w};
+      float dg[4], du[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t gw = (e < 2) ? gp.x : gp.y, uw = (e < 2) ? up.x : up.y;
+        const float gv = __uint_as_float((e & 1) ? (gw & 0xffff0000u) : (gw << 16));
+        const float uv = __uint_as_float((e & 1) ? (uw & 0xffff0000u) : (uw << 16));
+        const float dh = rw * dhv[e];
+        const float sg = __builtin_amdgcn_rcpf(1.0f + __expf(-gv));  // 1 ulp; dg, du are rounded to bf16
+        dg[e] = dh * uv * sg * (1.0f + gv * (1.0f - sg));
+        du[e] = dh * gv * sg;
+      }
+      bf16_t* out = reinterpret_cast<bf16_t*>(rowp[r]);
+      *reinterpret_cast<u32x2_t*>(out + n) = u32x2_t{pack_bf16x2(dg[0], dg[1]), pack_bf16x2(dg[2], dg[3])};
+      *reinterpret_cast<u32x2_t*>(out + g.du_off + n) = u32x2_t{pack_bf16x2(du[0], du[1]), pack_bf16x2(du[2], du[3])};
+    }
+  }
+}
+
+// ---------------------------------------------------------------- host side
+static bool xq_al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Shapes this kernel takes: identity KM rows (no K-side row map or scale),
+// 16-byte aligned operands and strides, K slabs of 64 inside one weight
+// segment, at most two weight segments, 32-bit operand offsets.
+bool xgemm_q_ok(const XGemm& g, int epi) {
+  const int64_t lim = int64_t(1) << 31;
+  if (g.N % 8 || g.N < 8) return false;
+  if (g.a_mode == XA_ROWS) {
+    if (g.lda % 8 || !xq_al16(g.A) || g.K % XQ_BK) return false;
+  } else {
+    if (g.a_map || g.a_kscale || g.lda % 8 || g.a_col % 8 || g.M % 8 || g.M < 8 || !xq_al16(g.A)) return false;
+    if ((int64_t)(XQ_BK + 1) * g.lda >= lim) return false;
+  }
+  if (g.b_mode == XB_W_NN) {
+    if (g.a_mode != XA_ROWS || g.kseg % XQ_BK || g.ldb % 8 || g.nseg < 1 || g.nseg > 2) return false;
+  } else if (g.b_mode == XB_ACT_KMAJOR) {
+    if (g.a_mode != XA_KMAJOR || g.b_map || g.ldb % 8 || g.b_col % 8 || !xq_al16(g.Bact)) return false;
+  } else {
+    return false;
+  }
+  if ((int64_t)XQ_BK * g.ldb >= lim) return false;
+  if (g.a_mode == XA_ROWS && g.sched_mode == XS_ROUTED && g.bm % XQ_BM) return false;
+  if (g.a_mode == XA_ROWS) {
+    const int64_t arows = g.sched_mode == XS_DENSE ? g.dense_rows : (int64_t)g.m_tiles_bound * g.bm;
+    if (arows * g.lda >= lim && !g.a_map) return false;
+  }
+  if (epi == XE_WGRAD)
+    return g.ldc % 8 == 0 && g.msplit % 4 == 0 && g.sched_mode == XS_WGRAD &&
+           (g.ksplit <= 1 || (g.part && xq_al16(g.part)));
+  if (epi == XE_SWIGLU_BWD)
+    return g.ldc % 4 == 0 && g.c_group_col % 4 == 0 && (reinterpret_cast<uintptr_t>(g.C) & 7) == 0 &&
+           g.du_off % 4 == 0 && g.ld_gu % 4 == 0 && g.gu_group_col % 4 == 0 &&
+           (reinterpret_cast<uintptr_t>(g.Gs) & 7) == 0 && (reinterpret_cast<uintptr_t>(g.Us) & 7) == 0;
+  return g.ldc % 8 == 0 && g.c_group_col % 8 == 0 && xq_al16(g.C);
+}
+
+template <int EPI, int AMODE>
+static int launch_xq_t(const XGemm& g, int64_t grid, hipStream_t st) {
+  auto kern = xgemm_q_kernel<EPI, AMODE>;
+  static bool attr = false;
+  if (!attr) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)XQ_LDS) != hipSuccess)
+      return fail(DSMOE_ERR_HIP, "xgemm_q: cannot raise LDS limit");
+    attr = true;
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(256), XQ_LDS, st, g);
+  return check_launch("xgemm_q");
+}
+
+int launch_xgemm_q(const XGemm& g, int epi, hipStream_t st) {
+  int64_t m_bound;
+  if (g.sched_mode == XS_ROUTED)
+    m_bound = (int64_t)g.m_tiles_bound * (g.bm / XQ_BM);
+  else if (g.sched_mode == XS_DENSE)
+    m_bound = cdiv(g.dense_rows, XQ_BM) * g.groups;
+  else
+    m_bound = cdiv(g.M, XQ_BM) * g.groups * std::max(g.ksplit, 1);
+  const int64_t grid = 8 * cdiv(m_bound * cdiv(g.N, XQ_BN), 8);
+  if (grid == 0) return DSMOE_OK;
+  if (grid > 0x7fffffff) return fail(DSMOE_ERR_UNSUPPORTED, "xgemm_q: grid too large");
+  if (epi == XE_SWIGLU_BWD) return launch_xq_t<XE_SWIGLU_BWD, XA_ROWS>(g, grid, st);
+  if (epi == XE_STORE) return launch_xq_t<XE_STORE, XA_ROWS>(g, grid, st);
+  const int rc = launch_xq_t<XE_WGRAD, XA_KMAJOR>(g, grid, st);
+  if (rc || g.ksplit <= 1) return rc;
+  return launch_wgrad_reduce(g, st);  // add the split-K partials in ascending part order
+}
+
+}  // namespace dsmoe
