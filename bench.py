@@ -152,6 +152,63 @@ def stage_times(step, steps: int):
     return {kname: v / steps for kname, v in stages.items()}
 
 
+def stage_rooflines(cfg, stage_ms):
+    """Per-stage rates against the stage's roof.  Algorithmic bytes / flops
+    per forward (bf16 activations and expert weights, fp32 gate):
+      gate     2TD (x) + 4ED (W_gate) + 8N (weights, indices) + 4E (counts)
+      permute  4N (indices read) + 12N (sorted_slot, sorted_token, slot_pos) + 8E
+      combine  2ND (slot rows) + 2TD (shared) + 4N (weights) + 4N (indices) + 2TD (y)
+      GEMMs    routed 6 N D I, shared 6 T D S I_s flops (bf16 MFMA)"""
+    T, D, E, I, k, S, I_s, dt, _ = cfg
+    es = 2 if dt == "bfloat16" else 4
+    N = T * k
+    out = {}
+    hbm = {"gate": es * T * D + 4 * E * D + 8 * N + 4 * E,
+           "permute": 16 * N + 8 * E,
+           "combine": es * N * D + 2 * es * T * D + 8 * N}
+    for name, nbytes in hbm.items():
+        ms = stage_ms.get(name)
+        if ms:
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            out[name] = {"ms": ms, "bytes": nbytes, "GB/s": gbs, "frac_hbm": gbs / PEAK_HBM_GBS}
+    flops = {"gemm1_routed": 4.0 * N * D * I, "gemm2_routed": 2.0 * N * D * I,
+             "gemm1_shared": 4.0 * T * D * S * I_s, "gemm2_shared": 2.0 * T * D * S * I_s}
+    for name, f in flops.items():
+        ms = stage_ms.get(name)
+        if ms:
+            tf = f / (ms * 1e-3) / 1e12
+            out[name] = {"ms": ms, "flop": f, "TFLOP/s": tf, "frac_mfma": tf / PEAK_BF16_TFLOPS}
+    return out
+
+
+def decode_bench(dev, steps: int, warmup: int):
+    """Config 3 decode (T=64): the forward streams the weights of every expert
+    that receives a token; reported as HBM GB/s of those weights against
+    8 TB/s.  Weight bytes = sum over routed experts with rows of 3 D I (bf16)
+    + the shared experts + the fp32 gate weight."""
+    import torch
+    from dsmoe import moe_layer
+    cfg = CONFIGS["c3_decode"]
+    T, D, E, I, k, S, I_s, dt, _ = cfg
+    log(f"[bench] decode config c3_decode: T={T}")
+    x, gate_w, bias, (w1, w2, w3, s1, s2, s3) = make_layer(cfg, dev)
+
+    def step():
+        return moe_layer(x, gate_w, bias, w1, w2, w3, s1, s2, s3, k=k, training=False)
+
+    with torch.no_grad():
+        counts = step()[3]
+        ms, wall = time_steps(step, steps, warmup)
+        stage_ms = stage_times(step, steps)
+    touched = int((counts > 0).sum().item())
+    nbytes = touched * 3 * D * I * 2 + S * 3 * D * I_s * 2 + E * D * 4
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    log(f"[bench] decode: {ms:.4f} ms/step, {touched} experts touched, {gbs:.0f} GB/s")
+    return {"workload": f"c3_decode: T={T} tokens, dim={D}, {E} routed (inter {I}) top-{k}, {S} shared, bf16",
+            "ms_per_step": ms, "tokens_per_s": T / (ms * 1e-3), "experts_touched": touched,
+            "weight_bytes": nbytes, "GB/s": gbs, "frac_hbm": gbs / PEAK_HBM_GBS, "stage_ms": stage_ms}
+
+
 def torch_sync():
     import torch
     torch.cuda.synchronize()
@@ -207,6 +264,7 @@ def main() -> int:
                     help="training-step workload reported under fwd_bwd")
     ap.add_argument("--no-fwd-bwd", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode", action="store_true", help="skip the config-3 decode (T=64) measurement")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="instead of the layer, run --steps device copies of this many MiB (counter calibration)")
     args = ap.parse_args()
@@ -244,6 +302,7 @@ def main() -> int:
     log(f"[bench] stages (ms/call): " + ", ".join(f"{a}={b:.4f}" for a, b in stage_ms.items()))
 
     N = T * k
+    stages = stage_rooflines(cfg, stage_ms)
     g1_flops = 4.0 * N * D * I
     g1_ms = stage_ms.get("gemm1_routed", float("nan"))
     achieved = g1_flops / (g1_ms * 1e-3) / 1e12
@@ -277,7 +336,10 @@ def main() -> int:
         "grouped_gemm_tflops": gemm_flops / (gemm_ms * 1e-3) / 1e12 if gemm_ms > 0 else None,
         "grouped_gemm_frac": (gemm_flops / (gemm_ms * 1e-3) / 1e12) / PEAK_BF16_TFLOPS if gemm_ms > 0 else None,
         "stage_ms": stage_ms,
+        "stages": stages,
     }
+    if not args.no_decode and args.config == "c3":
+        result["decode"] = decode_bench(dev, max(10, args.steps), max(3, args.warmup))
     if not args.no_cpu_baseline:
         log("[bench] timing the CPU restatement of the reference path ...")
         result["cpu_baseline"] = cpu_baseline(cfg, x, gate_w, bias, weights)
