@@ -11,18 +11,20 @@
 //    fragments per 16 MFMAs, against 12 for the 64 x 128 tiles of an 8-wave
 //    layout; with the direct-load writes this keeps LDS near 70 % busy at
 //    full MFMA rate.
-//  * 160 KB of LDS: two 64 KB slabs (A: 256 rows, B: 256 rows, 128 bytes
-//    each) double-buffer the K loop.
+//  * 160 KB of LDS: a slab is 32 KB per operand (256 rows of 128 bytes).  A
+//    (activation rows, mostly L2 / MALL hits) cycles through a ring of two
+//    slots, B (weights, streamed from HBM) through a ring of three, so B
+//    loads are issued a slab earlier than A loads.
 //
-// Per slab kb a wave runs four 16-wide K steps.  Fragments for step s + 1 are
-// read into one register set while the 16 MFMAs of step s use the other, so
-// LDS latency hides behind MFMAs.  After the MFMAs of step 2 each wave waits
-// for its LDS reads of slab kb and its own direct loads of slab kb + 1, then
-// the workgroup barrier makes slab kb + 1 visible and frees slab kb's buffer,
-// into which the loads of slab kb + 2 are issued at once: every load has a
-// full slab of MFMAs to land.  Loads past the last slab re-read the last slab
-// into the free buffer (never read), so the loop body has no branches and the
-// compiler's wait counters stay exact; they are drained before the epilogue.
+// Per slab kb a wave runs four 16-wide K steps.  Fragments are read two steps
+// ahead of their MFMAs through three register sets, so LDS latency hides
+// behind MFMAs.  After the MFMAs of step 1 each wave waits for its LDS reads
+// of slab kb and its own direct loads of slab kb + 1; the workgroup barrier
+// then makes slab kb + 1 visible and frees slab kb's slots, into which A of
+// slab kb + 2 and B of slab kb + 3 are issued between the first MFMAs of
+// step 2.  Loads past the last slab re-read the last slab into the free slot
+// (never read), so the loop body has no branches and the wait counts stay
+// exact; they are drained before the epilogue.
 //
 // Ragged tiles: the wave in row group wm owns the 32-row sub-tiles wm,
 // wm + 2, wm + 4 and wm + 6 of the block, so the valid rows of a partly
