@@ -21,8 +21,8 @@
 // behind MFMAs.  After the MFMAs of step 1 each wave waits for its LDS reads
 // of slab kb and its own direct loads of slab kb + 1; the workgroup barrier
 // then makes slab kb + 1 visible and frees slab kb's slots, into which A of
-// slab kb + 2 and B of slab kb + 3 are issued between the first MFMAs of
-// step 2.  Loads past the last slab re-read the last slab into the free slot
+// slab kb + 2 and B of slab kb + 3 are loaded, one direct load after every
+// second MFMA of steps 2 and 3.  Loads past the last slab re-read the last slab into the free slot
 // (never read), so the loop body has no branches and the wait counts stay
 // exact; they are drained before the epilogue.
 //
@@ -135,6 +135,50 @@ __device__ __forceinline__ void qw_mma(const bf16x8_t (&fa)[4], const bf16x8_t (
   }
 }
 
+// Refill load i (0 .. 2 QW_LD - 1) of slab kb's freed slots: A(kb + 2) for
+// i < QW_LD, then B(kb + 3).
+__device__ __forceinline__ void qw_issue_one(const QWLoad& L, int kb, int i) {
+  extern __shared__ __attribute__((aligned(16))) char qw_smem[];
+  if (i < QW_LD) {
+    const uint32_t da = lds_addr(qw_smem) + L.lds_off + (kb & 1) * QW_REG;
+    const int k0 = min(kb + 2, L.nk - 1) * QW_BK;
+    dma16(L.a + L.offa[i] + k0, da + i * 1024);
+  } else {
+    const uint32_t db = lds_addr(qw_smem) + L.lds_off + QW_BOFF + ((kb + 3) % QW_BSLOTS) * QW_REG;
+    const int k0 = min(kb + 3, L.nk - 1) * QW_BK;
+    const bool hi = k0 >= L.kseg;
+    const bf16_t* src = hi ? L.b1 : L.b0;
+    const int kin = hi ? k0 - L.kseg : k0;
+    dma16(src + L.offb[i - QW_LD] + kin, db + (i - QW_LD) * 1024);
+  }
+}
+
+// MFMAs T0 .. T1-1 of one K step of steps 2-3 (BASE: index of the step's
+// first MFMA within steps 2-3), each followed by its share of the refill
+// loads: MFMA g of the 2 MMAS is followed by loads [g n / 2 MMAS, (g + 1) n /
+// 2 MMAS), n = 2 QW_LD.
+template <int EPI, int NMI, int BASE, int T0, int T1>
+__device__ __forceinline__ void qw_mma_refill(const bf16x8_t (&fa)[4], const bf16x8_t (&fb)[QWCfg<EPI>::NB][QWCfg<EPI>::TN],
+                                              f32x16_t (&acc)[QWCfg<EPI>::NB][4][QWCfg<EPI>::TN], const QWLoad& L,
+                                              int kb) {
+  using CF = QWCfg<EPI>;
+  constexpr int MMAS = NMI * CF::NB * CF::TN;
+  constexpr int NL = 2 * QW_LD;
+#pragma unroll
+  for (int t = T0; t < T1; ++t) {
+    const int j = t / (CF::NB * CF::TN), b = (t / CF::TN) % CF::NB, ni = t % CF::TN;
+    acc[b][j][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[b][ni], fa[j], acc[b][j][ni], 0, 0, 0);
+    const int g = BASE + t;
+    const int l0 = g * NL / (2 * MMAS), l1 = (g + 1) * NL / (2 * MMAS);
+    if (l1 > l0) {
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = l0; i < l1; ++i) qw_issue_one(L, kb, i);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+}
+
 __device__ __forceinline__ void qw_sync() {
   __builtin_amdgcn_sched_barrier(0);
   lds_barrier();
@@ -189,38 +233,27 @@ __device__ __forceinline__ void qw_slab(QWPipe<EPI, NMI>& P, const QWLoad& L, in
   wait_lgkm0();
   wait_vm<QW_LD>();
   qw_sync();
-  // step 2: its first MFMAs interleave with the direct loads; then step 0 of
-  // slab kb + 1 is read (into the set step 1 used)
-  if (MMAS >= 4) {
-    qw_mma<EPI, NMI, 0, 1>(P.fa[A2], P.fb[A2], acc);
-    __builtin_amdgcn_sched_barrier(0);
-    qw_issue_a<0, 4>(L, kb + 2);
-    __builtin_amdgcn_sched_barrier(0);
-    qw_mma<EPI, NMI, 1, 2>(P.fa[A2], P.fb[A2], acc);
-    __builtin_amdgcn_sched_barrier(0);
-    qw_issue_a<4, QW_LD>(L, kb + 2);
-    __builtin_amdgcn_sched_barrier(0);
-    qw_mma<EPI, NMI, 2, 3>(P.fa[A2], P.fb[A2], acc);
-    __builtin_amdgcn_sched_barrier(0);
-    qw_issue_b<0, 4>(L, kb + 3);
-    __builtin_amdgcn_sched_barrier(0);
-    qw_mma<EPI, NMI, 3, 4>(P.fa[A2], P.fb[A2], acc);
-    __builtin_amdgcn_sched_barrier(0);
-    qw_issue_b<4, QW_LD>(L, kb + 3);
+  // Steps 2 and 3 refill the freed slots, A(kb + 2) first, then B(kb + 3),
+  // with the 16 direct loads spread evenly over their MFMAs (bursts of loads
+  // stall the wave at issue while the L2 -> LDS path drains, and with one
+  // wave per SIMD a stalled wave idles its MFMA pipe).  Step 0 of slab kb + 1
+  // is read after the first four MFMAs of step 2 (into the set step 1 used),
+  // step 1 of kb + 1 before step 3 (into the set step 2 used).
+  if constexpr (MMAS > 0) {
+    constexpr int H = MMAS < 4 ? MMAS : 4;
+    qw_mma_refill<EPI, NMI, 0, 0, H>(P.fa[A2], P.fb[A2], acc, L, kb);
     __builtin_amdgcn_sched_barrier(0);
     qw_read_set<EPI, NMI, A1>(P, kb + 1, 0, wm, wn, lane);
     __builtin_amdgcn_sched_barrier(0);
-    qw_mma<EPI, NMI, 4, MMAS>(P.fa[A2], P.fb[A2], acc);
+    qw_mma_refill<EPI, NMI, 0, H, MMAS>(P.fa[A2], P.fb[A2], acc, L, kb);
+    __builtin_amdgcn_sched_barrier(0);
+    qw_read_set<EPI, NMI, A2>(P, kb + 1, 1, wm, wn, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    qw_mma_refill<EPI, NMI, MMAS, 0, MMAS>(P.fa[A0], P.fb[A0], acc, L, kb);
   } else {
     qw_issue_a<0, QW_LD>(L, kb + 2);
     qw_issue_b<0, QW_LD>(L, kb + 3);
-    qw_read_set<EPI, NMI, A1>(P, kb + 1, 0, wm, wn, lane);
   }
-  // step 3: read step 1 of slab kb + 1 (into the set step 2 used)
-  __builtin_amdgcn_sched_barrier(0);
-  qw_read_set<EPI, NMI, A2>(P, kb + 1, 1, wm, wn, lane);
-  __builtin_amdgcn_sched_barrier(0);
-  qw_mma<EPI, NMI>(P.fa[A0], P.fb[A0], acc);
 }
 
 template <int EPI, int NMI>

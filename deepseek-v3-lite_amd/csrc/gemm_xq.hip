@@ -133,6 +133,38 @@ __device__ __forceinline__ void xq_issue_b(const XQLoad& L, int kb, int lane) {
   }
 }
 
+
+template <int AMODE>
+__device__ __forceinline__ void xq_issue_a_one(const XQLoad& L, int ka, int lane, int i) {
+  extern __shared__ __attribute__((aligned(16))) char xq_smem[];
+  const uint32_t da = lds_addr(xq_smem) + L.lds_off + (ka & 1) * XQ_REG;
+  const int k0 = L.kbeg + min(ka, L.nk - 1) * XQ_BK;
+  const bf16_t* src;
+  if (AMODE == XA_ROWS) {
+    src = L.a + L.offa[i] + k0;
+  } else {
+    const int kr = k0 + L.krow0 + 2 * i + (lane >> 5);
+    const uint32_t off = L.kma[i & 1] + (uint32_t)(2 * i) * (uint32_t)L.a_ld;
+    src = kr < L.kend ? L.a + (int64_t)k0 * L.a_ld + off : reinterpret_cast<const bf16_t*>(g_xq_zero);
+  }
+  dma16(src, da + i * 1024);
+}
+
+template <int BMODE>
+__device__ __forceinline__ void xq_issue_b_one(const XQLoad& L, int kb, int lane, int i) {
+  extern __shared__ __attribute__((aligned(16))) char xq_smem[];
+  const uint32_t db = lds_addr(xq_smem) + L.lds_off + XQ_BOFF + (kb % XQ_BSLOTS) * XQ_REG;
+  const int k0 = L.kbeg + min(kb, L.nk - 1) * XQ_BK;
+  const bool hi = k0 >= L.kseg;
+  const bf16_t* p = (hi ? L.b1 : L.b0) + (int64_t)(hi ? k0 - L.kseg : k0) * L.b_ld +
+                    (L.kmb[i & 1] + (uint32_t)(2 * i) * (uint32_t)L.b_ld);
+  if (BMODE == XB_ACT_KMAJOR) {
+    const int kr = k0 + L.krow0 + 2 * i + (lane >> 5);
+    if (kr >= L.kend) p = reinterpret_cast<const bf16_t*>(g_xq_zero);
+  }
+  dma16(p, db + i * 1024);
+}
+
 // Fragments of K step s (0..3) of slab kb: A sub-tiles j < NMI (rows
 // (2j + wm) * 32 ..), B tiles ni (columns wn * 128 + 32 ni ..).
 template <int AMODE, int NMI>
@@ -161,6 +193,36 @@ __device__ __forceinline__ void xq_mma(const bf16x8_t (&fa)[4], const bf16x8_t (
     acc[t / 4][t % 4] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[t % 4], fa[t / 4], acc[t / 4][t % 4], 0, 0, 0);
 }
 
+// MFMAs T0 .. T1-1 of one K step of steps 2-3 (BASE: index of the step's
+// first MFMA within steps 2-3), each followed by its share of the refill
+// loads A(kb + 2) (loads 0 .. XQ_LD-1) and B(kb + 3): MFMA g of the 2 MMAS is
+// followed by loads [g n / 2 MMAS, (g + 1) n / 2 MMAS), n = 2 XQ_LD.
+template <int AMODE, int NMI, int BASE, int T0, int T1>
+__device__ __forceinline__ void xq_mma_refill(const bf16x8_t (&fa)[4], const bf16x8_t (&fb)[4], f32x16_t (&acc)[4][4],
+                                              const XQLoad& L, int kb, int lane) {
+  constexpr int MMAS = NMI * 4;
+  constexpr int NL = 2 * XQ_LD;
+  constexpr int BM = AMODE == XA_ROWS ? XB_W_NN : XB_ACT_KMAJOR;
+#pragma unroll
+  for (int t = T0; t < T1; ++t) {
+    acc[t / 4][t % 4] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[t % 4], fa[t / 4], acc[t / 4][t % 4], 0, 0, 0);
+    const int g = BASE + t;
+    const int l0 = g * NL / (2 * MMAS), l1 = (g + 1) * NL / (2 * MMAS);
+    if (l1 > l0) {
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = l0; i < l1; ++i) {
+        if (i < XQ_LD) {
+          xq_issue_a_one<AMODE>(L, kb + 2, lane, i);
+        } else {
+          xq_issue_b_one<BM>(L, kb + 3, lane, i - XQ_LD);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+}
+
 __device__ __forceinline__ void xq_sync() {
   __builtin_amdgcn_sched_barrier(0);
   lds_barrier();
@@ -173,8 +235,8 @@ struct XQPipe {
 };
 
 // One slab whose step 0 uses register set S0 (see qw_slab in gemm_qw.hip:
-// reads run two steps ahead; the barrier follows step 1; step 2 issues the
-// loads of A(kb + 2) and B(kb + 3) into the slots slab kb frees).
+// reads run two steps ahead; the barrier follows step 1; steps 2 and 3 load
+// A(kb + 2) and B(kb + 3) into the slots slab kb frees).
 template <int AMODE, int NMI, int S0>
 __device__ __forceinline__ void xq_slab(XQPipe& P, const XQLoad& L, int kb, int wm, int wn, int lane,
                                         f32x16_t (&acc)[4][4]) {
@@ -195,34 +257,22 @@ __device__ __forceinline__ void xq_slab(XQPipe& P, const XQLoad& L, int kb, int 
   wait_lgkm0();
   wait_vm<XQ_LD>();
   xq_sync();
-  if (MMAS >= 4) {
-    xq_mma<NMI, 0, 1>(P.fa[A2], P.fb[A2], acc);
-    __builtin_amdgcn_sched_barrier(0);
-    xq_issue_a<AMODE, 0, 4>(L, kb + 2, lane);
-    __builtin_amdgcn_sched_barrier(0);
-    xq_mma<NMI, 1, 2>(P.fa[A2], P.fb[A2], acc);
-    __builtin_amdgcn_sched_barrier(0);
-    xq_issue_a<AMODE, 4, XQ_LD>(L, kb + 2, lane);
-    __builtin_amdgcn_sched_barrier(0);
-    xq_mma<NMI, 2, 3>(P.fa[A2], P.fb[A2], acc);
-    __builtin_amdgcn_sched_barrier(0);
-    xq_issue_b<AMODE == XA_ROWS ? XB_W_NN : XB_ACT_KMAJOR, 0, 4>(L, kb + 3, lane);
-    __builtin_amdgcn_sched_barrier(0);
-    xq_mma<NMI, 3, 4>(P.fa[A2], P.fb[A2], acc);
-    __builtin_amdgcn_sched_barrier(0);
-    xq_issue_b<AMODE == XA_ROWS ? XB_W_NN : XB_ACT_KMAJOR, 4, XQ_LD>(L, kb + 3, lane);
+  // refill loads spread evenly over the MFMAs of steps 2 and 3 (see qw_slab)
+  if constexpr (MMAS > 0) {
+    constexpr int H = MMAS < 4 ? MMAS : 4;
+    xq_mma_refill<AMODE, NMI, 0, 0, H>(P.fa[A2], P.fb[A2], acc, L, kb, lane);
     __builtin_amdgcn_sched_barrier(0);
     xq_read<AMODE, NMI>(kb + 1, 0, wm, wn, lane, P.fa[A1], P.fb[A1]);
     __builtin_amdgcn_sched_barrier(0);
-    xq_mma<NMI, 4, MMAS>(P.fa[A2], P.fb[A2], acc);
+    xq_mma_refill<AMODE, NMI, 0, H, MMAS>(P.fa[A2], P.fb[A2], acc, L, kb, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    xq_read<AMODE, NMI>(kb + 1, 1, wm, wn, lane, P.fa[A2], P.fb[A2]);
+    __builtin_amdgcn_sched_barrier(0);
+    xq_mma_refill<AMODE, NMI, MMAS, 0, MMAS>(P.fa[A0], P.fb[A0], acc, L, kb, lane);
   } else {
     xq_issue_a<AMODE, 0, XQ_LD>(L, kb + 2, lane);
     xq_issue_b<AMODE == XA_ROWS ? XB_W_NN : XB_ACT_KMAJOR, 0, XQ_LD>(L, kb + 3, lane);
   }
-  __builtin_amdgcn_sched_barrier(0);
-  xq_read<AMODE, NMI>(kb + 1, 1, wm, wn, lane, P.fa[A2], P.fb[A2]);
-  __builtin_amdgcn_sched_barrier(0);
-  xq_mma<NMI>(P.fa[A0], P.fb[A0], acc);
 }
 
 template <int AMODE, int NMI>
