@@ -11,9 +11,11 @@ BASELINE config 3 (prefill): T=8192 tokens, dim 2048, 64 routed experts
 experts, fp32 gate.  ``value`` is routed tokens/s = T / step time.
 
 Printed as one JSON line, with
-* ``roofline`` for the dominant kernel (the routed gate/up SwiGLU grouped GEMM):
-  algorithmic FLOPs per launch (4*N*D*I, N = T*k slots) over its mean launch
-  time measured with HIP events recorded by the library on the launch stream;
+* ``roofline`` for the dominant kernel, the gate/up SwiGLU grouped GEMM (one
+  launch covering the routed experts and the shared experts): algorithmic
+  FLOPs per launch (4*N*D*I + 4*T*D*S*I_s, N = T*k slots) over its mean
+  launch time measured with HIP events recorded by the library on the launch
+  stream;
 * ``cpu_baseline``: the CPU restatement of the reference stacked path
   (oracle/moe_ref.py) timed on this host on a bounded token sample;
 * ``fwd_bwd``: the training step of BASELINE config 4 (the config-3 layer at
@@ -158,7 +160,8 @@ def stage_rooflines(cfg, stage_ms):
       gate     2TD (x) + 4ED (W_gate) + 8N (weights, indices) + 4E (counts)
       permute  4N (indices read) + 12N (sorted_slot, sorted_token, slot_pos) + 8E
       combine  2ND (slot rows) + 2TD (shared) + 4N (weights) + 4N (indices) + 2TD (y)
-      GEMMs    routed 6 N D I, shared 6 T D S I_s flops (bf16 MFMA)"""
+      GEMMs    gemm1 (routed + shared gate/up) 4 N D I + 4 T D S I_s, gemm2
+               (down projections) 2 N D I + 2 T D S I_s flops (bf16 MFMA)"""
     T, D, E, I, k, S, I_s, dt, _ = cfg
     es = 2 if dt == "bfloat16" else 4
     N = T * k
@@ -171,8 +174,7 @@ def stage_rooflines(cfg, stage_ms):
         if ms:
             gbs = nbytes / (ms * 1e-3) / 1e9
             out[name] = {"ms": ms, "bytes": nbytes, "GB/s": gbs, "frac_hbm": gbs / PEAK_HBM_GBS}
-    flops = {"gemm1_routed": 4.0 * N * D * I, "gemm2_routed": 2.0 * N * D * I,
-             "gemm1_shared": 4.0 * T * D * S * I_s, "gemm2_shared": 2.0 * T * D * S * I_s}
+    flops = {"gemm1": 4.0 * N * D * I + 4.0 * T * D * S * I_s, "gemm2": 2.0 * N * D * I + 2.0 * T * D * S * I_s}
     for name, f in flops.items():
         ms = stage_ms.get(name)
         if ms:
@@ -303,15 +305,15 @@ def main() -> int:
 
     N = T * k
     stages = stage_rooflines(cfg, stage_ms)
-    g1_flops = 4.0 * N * D * I
-    g1_ms = stage_ms.get("gemm1_routed", float("nan"))
+    g1_flops = 4.0 * N * D * I + 4.0 * T * D * S * I_s
+    g1_ms = stage_ms.get("gemm1", float("nan"))
     achieved = g1_flops / (g1_ms * 1e-3) / 1e12
     gemm_flops = 6.0 * N * D * I + 6.0 * T * D * S * I_s
-    gemm_ms = sum(stage_ms.get(s, 0.0) for s in ("gemm1_routed", "gemm1_shared", "gemm2_routed", "gemm2_shared"))
+    gemm_ms = sum(stage_ms.get(s, 0.0) for s in ("gemm1", "gemm2"))
     traffic = None
     prof = ROOT / "profiles" / f"traffic_{args.config}.json"
     if prof.exists():
-        traffic = json.loads(prof.read_text()).get("gemm1_routed_bytes")
+        traffic = json.loads(prof.read_text()).get("gemm1_bytes")
 
     result = {
         "metric": METRIC,
@@ -329,7 +331,7 @@ def main() -> int:
         "config": {"workload": f"{args.config}: DeepSeekMoE layer forward, T={T} tokens, dim={D}, "
                                f"{E} routed experts (inter {I}) top-{k}, {S} shared (inter {I_s}), {dt}, fp32 gate",
                    "T": T, "D": D, "E": E, "I": I, "k": k, "S": S, "I_s": I_s},
-        "roofline": {"bound": "mfma", "kernel": "gemm1_routed (gate/up SwiGLU grouped GEMM)",
+        "roofline": {"bound": "mfma", "kernel": "gemm1 (gate/up SwiGLU grouped GEMM, routed + shared experts)",
                      "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / PEAK_BF16_TFLOPS, "traffic": traffic},
         "slots_per_s": N / (ms * 1e-3),

@@ -142,12 +142,12 @@ static FwdLayout fwd_layout(const dsmoe_dims& d, int training, void* base) {
 
 // ---------------------------------------------------------------- stage timing
 enum Stage : int {
-  ST_TABLES = 0, ST_GATE, ST_PERMUTE, ST_GEMM1, ST_GEMM1_SHARED, ST_GEMM2, ST_GEMM2_SHARED, ST_COMBINE,
+  ST_TABLES = 0, ST_GATE, ST_PERMUTE, ST_GEMM1, ST_GEMM2, ST_COMBINE,
   ST_BWD_PREP, ST_BWD_DH, ST_BWD_DH_SHARED, ST_BWD_DX, ST_BWD_DX_SHARED, ST_BWD_DW13, ST_BWD_DW2,
   ST_BWD_DW_SHARED, ST_BWD_GATE, ST_BWD_REDUCE, ST_COUNT
 };
 static const char* kStageNames[ST_COUNT] = {
-  "tables", "gate", "permute", "gemm1_routed", "gemm1_shared", "gemm2_routed", "gemm2_shared", "combine",
+  "tables", "gate", "permute", "gemm1", "gemm2", "combine",
   "bwd_prep", "bwd_dh_routed", "bwd_dh_shared", "bwd_dx_routed", "bwd_dx_shared", "bwd_dw13_routed",
   "bwd_dw2_routed", "bwd_dw_shared", "bwd_gate", "bwd_reduce"};
 
@@ -389,43 +389,35 @@ int dsmoe_moe_fwd(const void* x, const float* gate_w, const float* gate_bias, co
   g1.sched_count = g2.sched_count = L.ps.sched_count;
   g1.m_tiles_bound = g2.m_tiles_bound = (int32_t)sched_bound(N, d.E, bm);
   g1.bm = g2.bm = bm;
-  // (c) routed gate/up + SwiGLU, rows gathered from x through sorted_token
-  tm.begin(ST_GEMM1);
-  rc = launch_grouped_gemm(g1, EPI_SWIGLU, d.dtype, nullptr, mfr, st);
-  tm.end();
-  if (rc) return rc;
-  // shared experts: S dense groups over all tokens, h_shared = [h_0 | h_1 | ...]
+  // (c) gate/up + SwiGLU: routed rows gathered from x through sorted_token,
+  // and the shared experts as S dense groups over all tokens (h_shared =
+  // [h_0 | h_1 | ...]), in one launch when the quad-wave kernel takes both
+  GemmDesc s1 = desc_zero(), s2 = desc_zero();
   if (d.S) {
-    GemmDesc s1 = desc_zero();
     s1.dense_rows = d.T; s1.groups = d.S;
     s1.A = x; s1.lda = d.D; s1.a_rows = d.T;
     s1.B0 = L.ptrs + 3 * d.E; s1.B1 = L.ptrs + 3 * d.E + d.S; s1.ldb = d.D; s1.kseg = d.D;
     s1.N = d.I_s; s1.K = d.D; s1.C = L.hs; s1.ldc = (int64_t)d.S * d.I_s; s1.c_group_col = d.I_s;
     s1.Gs = L.gs; s1.Us = L.us;
     s1.bm = gemm_tile_m(gemm_mfma_eligible(s1, d.dtype, mf));
-    tm.begin(ST_GEMM1_SHARED);
-    rc = launch_grouped_gemm(s1, EPI_SWIGLU, d.dtype, nullptr, mf, st);
-    tm.end();
-    if (rc) return rc;
-  }
-  // routed down projection, rows written back in slot order (t*k + j)
-  tm.begin(ST_GEMM2);
-  rc = launch_grouped_gemm(g2, EPI_STORE, d.dtype, nullptr, mfr, st);
-  tm.end();
-  if (rc) return rc;
-  // shared down projection: one GEMM with K = S * I_s summing all shared experts
-  if (d.S) {
-    GemmDesc s2 = desc_zero();
+    // shared down projection: one GEMM with K = S * I_s summing all shared experts
     s2.dense_rows = d.T; s2.groups = 1;
     s2.A = L.hs; s2.lda = (int64_t)d.S * d.I_s; s2.a_rows = d.T;
     s2.B0 = L.ptrs + 3 * d.E + 2 * d.S; s2.ldb = d.I_s; s2.kseg = d.I_s; s2.nseg = d.S;
     s2.N = d.D; s2.K = d.S * d.I_s; s2.C = L.shared_out; s2.ldc = d.D;
     s2.bm = gemm_tile_m(gemm_mfma_eligible(s2, d.dtype, mf));
-    tm.begin(ST_GEMM2_SHARED);
-    rc = launch_grouped_gemm(s2, EPI_STORE, d.dtype, nullptr, mf, st);
-    tm.end();
-    if (rc) return rc;
   }
+  tm.begin(ST_GEMM1);
+  rc = d.S ? launch_grouped_gemm_pair(g1, s1, EPI_SWIGLU, d.dtype, nullptr, mfr, mf, st)
+           : launch_grouped_gemm(g1, EPI_SWIGLU, d.dtype, nullptr, mfr, st);
+  tm.end();
+  if (rc) return rc;
+  // down projections: routed rows written back in slot order (t*k + j)
+  tm.begin(ST_GEMM2);
+  rc = d.S ? launch_grouped_gemm_pair(g2, s2, EPI_STORE, d.dtype, nullptr, mfr, mf, st)
+           : launch_grouped_gemm(g2, EPI_STORE, d.dtype, nullptr, mfr, st);
+  tm.end();
+  if (rc) return rc;
   // (d) combine
   tm.begin(ST_COMBINE);
   rc = launch_combine(L.o_slots, L.w, L.idx, L.shared_out, d, y, st);

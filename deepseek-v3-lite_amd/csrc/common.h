@@ -161,8 +161,13 @@ bool gemm_mfma_eligible(const GemmDesc& g, int dtype, bool allow_mfma);
 int gemm_tile_m(bool mfma);
 bool gemm_qw_ok(const GemmDesc& g);
 int launch_gemm_qw(const GemmDesc& g, int epi, const float* row_scale, hipStream_t st);
+int launch_gemm_qw_pair(const GemmDesc& gr, const GemmDesc& gd, int epi, const float* row_scale, hipStream_t st);
 int launch_grouped_gemm(const GemmDesc& g, int epi, int dtype, const float* row_scale, bool allow_mfma,
                         hipStream_t st);
+// gr (routed or dense) then the dense gd (same epilogue): one quad-wave launch
+// when that kernel takes both, else two launches.  row_scale applies to gr.
+int launch_grouped_gemm_pair(const GemmDesc& gr, const GemmDesc& gd, int epi, int dtype, const float* row_scale,
+                             bool allow_mfma_r, bool allow_mfma_d, hipStream_t st);
 int launch_combine(const void* o_slots, const float* w, const int32_t* idx, const void* shared, const dsmoe_dims& d,
                    void* y, hipStream_t st);
 int launch_update_bias(const int32_t* counts, float* bias, int E, float speed, float upper, float lower,

@@ -411,4 +411,26 @@ int launch_grouped_gemm(const GemmDesc& g_in, int epi, int dtype, const float* r
   return check_launch("gemm_simt");
 }
 
+// DSMOE_GEMM_PAIR=0 launches the two problems separately.
+static bool gemm_pair() {
+  static bool on = [] {
+    const char* s = std::getenv("DSMOE_GEMM_PAIR");
+    return !(s && std::atoi(s) == 0);
+  }();
+  return on;
+}
+
+int launch_grouped_gemm_pair(const GemmDesc& gr_in, const GemmDesc& gd_in, int epi, int dtype, const float* row_scale,
+                             bool allow_mfma_r, bool allow_mfma_d, hipStream_t st) {
+  GemmDesc gr = gr_in, gd = gd_in;
+  gr.raster = gd.raster = gemm_raster();
+  const bool one = gemm_pair() && gr.raster == 0 && gemm_cfg() == 3 && gd.sched == nullptr && gr.N > 0 && gr.K > 0 && gd.N > 0 &&
+                   gd.K > 0 && gemm_mfma_eligible(gr, dtype, allow_mfma_r) && gemm_mfma_eligible(gd, dtype, allow_mfma_d) &&
+                   gemm_qw_ok(gr) && gemm_qw_ok(gd);
+  if (one) return launch_gemm_qw_pair(gr, gd, epi, row_scale, st);
+  const int rc = launch_grouped_gemm(gr_in, epi, dtype, row_scale, allow_mfma_r, st);
+  if (rc) return rc;
+  return launch_grouped_gemm(gd_in, epi, dtype, nullptr, allow_mfma_d, st);
+}
+
 }  // namespace dsmoe

@@ -278,14 +278,24 @@ __device__ __forceinline__ void qw_loop(const QWLoad& L, int wm, int wn, int lan
   wait_vm<0>();
 }
 
+// One launch computes g0 alone (pair = 0), or g0 and the dense problem g1
+// side by side (pair = 1, tiles enumerated by tile_for_block_pair); row_scale
+// applies to g0's rows only.
 template <int EPI>
-__global__ __launch_bounds__(256) void gemm_qw_kernel(const GemmDesc g, const float* __restrict__ row_scale) {
+__global__ __launch_bounds__(256) void gemm_qw_kernel(const GemmDesc g0, const GemmDesc g1, const int pair,
+                                                      const float* __restrict__ row_scale_0) {
   using CF = QWCfg<EPI>;
   constexpr int NB = CF::NB, TN = CF::TN, BN = CF::BN;
 
-  const int n_tiles = (int)cdiv(g.N, BN);
-  int grp, row0, rows, n_tile;
-  if (!tile_for_block<QW_BM>(g, n_tiles, grp, row0, rows, n_tile)) return;
+  int which = 0, grp, row0, rows, n_tile;
+  if (pair) {
+    if (!tile_for_block_pair<QW_BM>(g0, g1, BN, which, grp, row0, rows, n_tile)) return;
+  } else {
+    if (!tile_for_block<QW_BM>(g0, (int)cdiv(g0.N, BN), grp, row0, rows, n_tile)) return;
+  }
+  which = __builtin_amdgcn_readfirstlane(which);
+  const GemmDesc& g = which ? g1 : g0;
+  const float* row_scale = which ? nullptr : row_scale_0;
   grp = __builtin_amdgcn_readfirstlane(grp);
   row0 = __builtin_amdgcn_readfirstlane(row0);
   rows = __builtin_amdgcn_readfirstlane(rows);
@@ -436,27 +446,36 @@ bool gemm_qw_ok(const GemmDesc& g) {
          a16(g.C) && a16(g.Gs) && a16(g.Us);
 }
 
+template <int EPI>
+static int qw_launch(const GemmDesc& g0, const GemmDesc& g1, int pair, const float* row_scale, int64_t grid,
+                     hipStream_t st) {
+  if (grid == 0) return DSMOE_OK;
+  static bool raised = false;
+  if (!raised && hipFuncSetAttribute((const void*)gemm_qw_kernel<EPI>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     (int)QW_LDS) != hipSuccess)
+    return fail(DSMOE_ERR_HIP, "gemm_qw: cannot raise LDS limit");
+  raised = true;
+  hipLaunchKernelGGL(gemm_qw_kernel<EPI>, dim3((unsigned)grid), dim3(256), QW_LDS, st, g0, g1, pair, row_scale);
+  return check_launch("gemm_qw");
+}
+
 int launch_gemm_qw(const GemmDesc& g, int epi, const float* row_scale, hipStream_t st) {
   const int bn = (epi == EPI_SWIGLU) ? QWCfg<EPI_SWIGLU>::BN : QWCfg<EPI_STORE>::BN;
   const int64_t m_bound = g.sched ? g.m_tiles_bound : cdiv(g.dense_rows, QW_BM) * g.groups;
   const int64_t grid = 8 * cdiv(m_bound * cdiv(g.N, bn), 8);
-  if (grid == 0) return DSMOE_OK;
-  if (epi == EPI_SWIGLU) {
-    static bool a = false;
-    if (!a && hipFuncSetAttribute((const void*)gemm_qw_kernel<EPI_SWIGLU>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)QW_LDS) != hipSuccess)
-      return fail(DSMOE_ERR_HIP, "gemm_qw: cannot raise LDS limit");
-    a = true;
-    hipLaunchKernelGGL(gemm_qw_kernel<EPI_SWIGLU>, dim3((unsigned)grid), dim3(256), QW_LDS, st, g, row_scale);
-  } else {
-    static bool a = false;
-    if (!a && hipFuncSetAttribute((const void*)gemm_qw_kernel<EPI_STORE>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)QW_LDS) != hipSuccess)
-      return fail(DSMOE_ERR_HIP, "gemm_qw: cannot raise LDS limit");
-    a = true;
-    hipLaunchKernelGGL(gemm_qw_kernel<EPI_STORE>, dim3((unsigned)grid), dim3(256), QW_LDS, st, g, row_scale);
-  }
-  return check_launch("gemm_qw");
+  return epi == EPI_SWIGLU ? qw_launch<EPI_SWIGLU>(g, g, 0, row_scale, grid, st)
+                           : qw_launch<EPI_STORE>(g, g, 0, row_scale, grid, st);
+}
+
+// gr (routed schedule or dense) and the dense gd in one launch; the grid
+// covers gd's tiles exactly and gr's up to its host bound (tile_for_block_pair).
+int launch_gemm_qw_pair(const GemmDesc& gr, const GemmDesc& gd, int epi, const float* row_scale, hipStream_t st) {
+  const int bn = (epi == EPI_SWIGLU) ? QWCfg<EPI_SWIGLU>::BN : QWCfg<EPI_STORE>::BN;
+  const int64_t mr = gr.sched ? gr.m_tiles_bound : cdiv(gr.dense_rows, QW_BM) * gr.groups;
+  const int64_t md = cdiv(gd.dense_rows, QW_BM) * gd.groups;
+  const int64_t grid = 8 * (cdiv(md * cdiv(gd.N, bn), 8) + cdiv(mr * cdiv(gr.N, bn), 8));
+  return epi == EPI_SWIGLU ? qw_launch<EPI_SWIGLU>(gr, gd, 1, row_scale, grid, st)
+                           : qw_launch<EPI_STORE>(gr, gd, 1, row_scale, grid, st);
 }
 
 }  // namespace dsmoe

@@ -56,6 +56,60 @@ __device__ __forceinline__ bool tile_for_block(const GemmDesc& g, int n_tiles, i
   return true;
 }
 
+// Tile lookup for two problems in one launch: gr (routed schedule or dense)
+// and gd (dense, e.g. the shared experts over all tokens), both with output
+// tiles BN wide.  Each XCD takes the x-th eighth of gd's tiles first, then the
+// x-th eighth of gr's, so both problems are spread evenly over the XCDs and
+// the dense tiles (the longer ones when gd has the larger K) start first.
+// Surplus blocks return false.  which = 1 selects gd.
+template <int BM>
+__device__ __forceinline__ bool tile_for_block_pair(const GemmDesc& gr, const GemmDesc& gd, int bn, int& which,
+                                                    int& grp, int& row0, int& rows, int& n_tile) {
+  const int ntr = (int)cdiv(gr.N, bn), ntd = (int)cdiv(gd.N, bn);
+  const int tpg_d = (int)cdiv(gd.dense_rows, BM);
+  const int64_t td = (int64_t)tpg_d * gd.groups * ntd;
+  int tpg_r = 0;
+  int64_t mr;
+  if (gr.sched) {
+    mr = *gr.sched_count;
+  } else {
+    tpg_r = (int)cdiv(gr.dense_rows, BM);
+    mr = (int64_t)tpg_r * gr.groups;
+  }
+  const int64_t tr = mr * ntr;
+  const int64_t per_d = cdiv(td, 8), per_r = cdiv(tr, 8);
+  const int64_t j = blockIdx.x >> 3, x = blockIdx.x & 7;
+  int64_t lin;
+  if (j < per_d) {
+    which = 1;
+    lin = x * per_d + j;
+    if (lin >= td) return false;
+    const int64_t m_tile = lin / ntd;
+    n_tile = (int)(lin - m_tile * ntd);
+    grp = (int)(m_tile / tpg_d);
+    row0 = (int)(m_tile - (int64_t)grp * tpg_d) * BM;
+    rows = min(BM, gd.dense_rows - row0);
+    return true;
+  }
+  which = 0;
+  if (j - per_d >= per_r) return false;
+  lin = x * per_r + (j - per_d);
+  if (lin >= tr) return false;
+  const int64_t m_tile = lin / ntr;
+  n_tile = (int)(lin - m_tile * ntr);
+  if (gr.sched) {
+    const MTile t = gr.sched[m_tile];
+    grp = t.group;
+    row0 = t.row0;
+    rows = t.rows;
+  } else {
+    grp = (int)(m_tile / tpg_r);
+    row0 = (int)(m_tile - (int64_t)grp * tpg_r) * BM;
+    rows = min(BM, gr.dense_rows - row0);
+  }
+  return true;
+}
+
 // Backward GEMM tile lookup for the three XGemm schedules (same XCD-chunked
 // enumeration as tile_for_block).  Returns false for surplus blocks.
 //   XS_ROUTED  schedule entries of height bm, split into bm / BMK sub-tiles;
