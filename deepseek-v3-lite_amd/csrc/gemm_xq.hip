@@ -78,6 +78,8 @@ __device__ __forceinline__ bf16x8_t xq_km_frag(const char* reg, int k0, int c0, 
 // Direct-load sources of one wave.  Wave w fills rows 64 w .. 64 w + 63 of an
 // NT region, or k rows 16 w .. 16 w + 15 of a KM region (load i: rows
 // 16 w + 2 i + (l >> 5)).
+constexpr int XQ_EPI_U = 8;  // rows per thread whose g, u loads are in flight together (SwiGLU backward epilogue)
+
 struct XQLoad {
   const bf16_t* a;        // A base (KM: + group column offset)
   int64_t a_ld;           // KM: elements per k row
@@ -485,29 +487,46 @@ __global__ __launch_bounds__(256) void xgemm_q_kernel(const XGemm g) {
       }
     }
     xq_sync();
+    // rows r = (tid >> 5) + 8 i in batches of XQ_EPI_U: the batch's g, u and
+    // row weights are loaded first, so their latencies overlap
     const int cc = tid & 31, n = n0 + half * 128 + cc * 4;
-    for (int r = tid >> 5; r < rows; r += 8) {
-      const float4 dh4 = *reinterpret_cast<const float4*>(sm + r * 512 + ((cc ^ (r & 31)) << 4));
-      if (n >= g.N) continue;
-      const float rw = g.row_w ? g.row_w[row0 + r] : 1.0f;
-      const int64_t ogu = (int64_t)(row0 + r) * g.ld_gu + (int64_t)grp * g.gu_group_col + n;
-      const u32x2_t gp = *reinterpret_cast<const u32x2_t*>(Gs + ogu);
-      const u32x2_t up = *reinterpret_cast<const u32x2_t*>(Us + ogu);
-      const float dhv[4] = {dh4.x, dh4.y, dh4.z, dh4.w};
-      float dg[4], du[4];
+    const bool col_ok = n < g.N;
+    for (int rb = tid >> 5; rb < rows; rb += 8 * XQ_EPI_U) {
+      u32x2_t gp[XQ_EPI_U], up[XQ_EPI_U];
+      float rwv[XQ_EPI_U];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t gw = (e < 2) ? gp.x : gp.y, uw = (e < 2) ? up.x : up.y;
-        const float gv = __uint_as_float((e & 1) ? (gw & 0xffff0000u) : (gw << 16));
-        const float uv = __uint_as_float((e & 1) ? (uw & 0xffff0000u) : (uw << 16));
-        const float dh = rw * dhv[e];
-        const float sg = __builtin_amdgcn_rcpf(1.0f + __expf(-gv));  // 1 ulp; dg, du are rounded to bf16
-        dg[e] = dh * uv * sg * (1.0f + gv * (1.0f - sg));
-        du[e] = dh * gv * sg;
+      for (int i = 0; i < XQ_EPI_U; ++i) {
+        const int r = rb + 8 * i;
+        gp[i] = up[i] = u32x2_t{0u, 0u};
+        rwv[i] = 0.0f;
+        if (r < rows && col_ok) {
+          const int64_t ogu = (int64_t)(row0 + r) * g.ld_gu + (int64_t)grp * g.gu_group_col + n;
+          gp[i] = *reinterpret_cast<const u32x2_t*>(Gs + ogu);
+          up[i] = *reinterpret_cast<const u32x2_t*>(Us + ogu);
+          rwv[i] = g.row_w ? g.row_w[row0 + r] : 1.0f;
+        }
       }
-      bf16_t* out = reinterpret_cast<bf16_t*>(rowp[r]);
-      *reinterpret_cast<u32x2_t*>(out + n) = u32x2_t{pack_bf16x2(dg[0], dg[1]), pack_bf16x2(dg[2], dg[3])};
-      *reinterpret_cast<u32x2_t*>(out + g.du_off + n) = u32x2_t{pack_bf16x2(du[0], du[1]), pack_bf16x2(du[2], du[3])};
+#pragma unroll
+      for (int i = 0; i < XQ_EPI_U; ++i) {
+        const int r = rb + 8 * i;
+        if (r >= rows || !col_ok) continue;
+        const float4 dh4 = *reinterpret_cast<const float4*>(sm + r * 512 + ((cc ^ (r & 31)) << 4));
+        const float dhv[4] = {dh4.x, dh4.y, dh4.z, dh4.w};
+        float dg[4], du[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t gw = (e < 2) ? gp[i].x : gp[i].y, uw = (e < 2) ? up[i].x : up[i].y;
+          const float gv = __uint_as_float((e & 1) ? (gw & 0xffff0000u) : (gw << 16));
+          const float uv = __uint_as_float((e & 1) ? (uw & 0xffff0000u) : (uw << 16));
+          const float dh = rwv[i] * dhv[e];
+          const float sg = __builtin_amdgcn_rcpf(1.0f + __expf(-gv));  // 1 ulp; dg, du are rounded to bf16
+          dg[e] = dh * uv * sg * (1.0f + gv * (1.0f - sg));
+          du[e] = dh * gv * sg;
+        }
+        bf16_t* out = reinterpret_cast<bf16_t*>(rowp[r]);
+        *reinterpret_cast<u32x2_t*>(out + n) = u32x2_t{pack_bf16x2(dg[0], dg[1]), pack_bf16x2(dg[2], dg[3])};
+        *reinterpret_cast<u32x2_t*>(out + g.du_off + n) = u32x2_t{pack_bf16x2(du[0], du[1]), pack_bf16x2(du[2], du[3])};
+      }
     }
   }
 }
