@@ -78,8 +78,6 @@ __device__ __forceinline__ bf16x8_t xq_km_frag(const char* reg, int k0, int c0, 
 // Direct-load sources of one wave.  Wave w fills rows 64 w .. 64 w + 63 of an
 // NT region, or k rows 16 w .. 16 w + 15 of a KM region (load i: rows
 // 16 w + 2 i + (l >> 5)).
-constexpr int XQ_EPI_U = 8;  // rows per thread whose g, u loads are in flight together (SwiGLU backward epilogue)
-
 struct XQLoad {
   const bf16_t* a;        // A base (KM: + group column offset)
   int64_t a_ld;           // KM: elements per k row
@@ -466,11 +464,31 @@ __global__ __launch_bounds__(256) void xgemm_q_kernel(const XGemm g) {
   }
   // SwiGLU backward: dh stays fp32 until dg and du are formed, so each column
   // half (128 columns, owned by the waves with wn == half) is staged as fp32
-  // in turn; 16-byte unit u of row m at unit u ^ (m & 31).
+  // in turn; 16-byte unit u of row m at unit u ^ (m & 31).  Thread tid serves
+  // rows (tid >> 4) + 16 i and columns n0 + 128 half + 8 (tid & 15) + {0..7};
+  // the g, u and row weights of all its rows in the half are loaded before
+  // the staging, so their HBM latency overlaps it.
   const bf16_t* Gs = static_cast<const bf16_t*>(g.Gs);
   const bf16_t* Us = static_cast<const bf16_t*>(g.Us);
   rowp[tid] = my_rowp;
+  const int cc = tid & 15, rq = tid >> 4;
   for (int half = 0; half < 2; ++half) {
+    const int n = n0 + half * 128 + cc * 8;
+    const bool col_ok = n < g.N;
+    u32x4_t gp[16], up[16];
+    float rwv[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = rq + 16 * i;
+      gp[i] = up[i] = u32x4_t{0u, 0u, 0u, 0u};
+      rwv[i] = 0.0f;
+      if (r < rows && col_ok) {
+        const int64_t ogu = (int64_t)(row0 + r) * g.ld_gu + (int64_t)grp * g.gu_group_col + n;
+        gp[i] = *reinterpret_cast<const u32x4_t*>(Gs + ogu);
+        up[i] = *reinterpret_cast<const u32x4_t*>(Us + ogu);
+        rwv[i] = g.row_w ? g.row_w[row0 + r] : 1.0f;
+      }
+    }
     if (half) xq_sync();  // the first half's reads are done
     if (wn == half) {
 #pragma unroll
@@ -487,46 +505,34 @@ __global__ __launch_bounds__(256) void xgemm_q_kernel(const XGemm g) {
       }
     }
     xq_sync();
-    // rows r = (tid >> 5) + 8 i in batches of XQ_EPI_U: the batch's g, u and
-    // row weights are loaded first, so their latencies overlap
-    const int cc = tid & 31, n = n0 + half * 128 + cc * 4;
-    const bool col_ok = n < g.N;
-    for (int rb = tid >> 5; rb < rows; rb += 8 * XQ_EPI_U) {
-      u32x2_t gp[XQ_EPI_U], up[XQ_EPI_U];
-      float rwv[XQ_EPI_U];
 #pragma unroll
-      for (int i = 0; i < XQ_EPI_U; ++i) {
-        const int r = rb + 8 * i;
-        gp[i] = up[i] = u32x2_t{0u, 0u};
-        rwv[i] = 0.0f;
-        if (r < rows && col_ok) {
-          const int64_t ogu = (int64_t)(row0 + r) * g.ld_gu + (int64_t)grp * g.gu_group_col + n;
-          gp[i] = *reinterpret_cast<const u32x2_t*>(Gs + ogu);
-          up[i] = *reinterpret_cast<const u32x2_t*>(Us + ogu);
-          rwv[i] = g.row_w ? g.row_w[row0 + r] : 1.0f;
-        }
-      }
+    for (int i = 0; i < 16; ++i) {
+      const int r = rq + 16 * i;
+      if (r >= rows || !col_ok) continue;
+      const float4 d0 = *reinterpret_cast<const float4*>(sm + r * 512 + (((2 * cc) ^ (r & 31)) << 4));
+      const float4 d1 = *reinterpret_cast<const float4*>(sm + r * 512 + (((2 * cc + 1) ^ (r & 31)) << 4));
+      const float dhv[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+      const uint32_t gw[4] = {gp[i].x, gp[i].y, gp[i].z, gp[i].w};
+      const uint32_t uw[4] = {up[i].x, up[i].y, up[i].z, up[i].w};
+      uint32_t dgw[4], duw[4];
 #pragma unroll
-      for (int i = 0; i < XQ_EPI_U; ++i) {
-        const int r = rb + 8 * i;
-        if (r >= rows || !col_ok) continue;
-        const float4 dh4 = *reinterpret_cast<const float4*>(sm + r * 512 + ((cc ^ (r & 31)) << 4));
-        const float dhv[4] = {dh4.x, dh4.y, dh4.z, dh4.w};
-        float dg[4], du[4];
+      for (int e2 = 0; e2 < 4; ++e2) {
+        float dg[2], du[2];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t gw = (e < 2) ? gp[i].x : gp[i].y, uw = (e < 2) ? up[i].x : up[i].y;
-          const float gv = __uint_as_float((e & 1) ? (gw & 0xffff0000u) : (gw << 16));
-          const float uv = __uint_as_float((e & 1) ? (uw & 0xffff0000u) : (uw << 16));
-          const float dh = rwv[i] * dhv[e];
+        for (int h = 0; h < 2; ++h) {
+          const float gv = __uint_as_float(h ? (gw[e2] & 0xffff0000u) : (gw[e2] << 16));
+          const float uv = __uint_as_float(h ? (uw[e2] & 0xffff0000u) : (uw[e2] << 16));
+          const float dh = rwv[i] * dhv[2 * e2 + h];
           const float sg = __builtin_amdgcn_rcpf(1.0f + __expf(-gv));  // 1 ulp; dg, du are rounded to bf16
-          dg[e] = dh * uv * sg * (1.0f + gv * (1.0f - sg));
-          du[e] = dh * gv * sg;
+          dg[h] = dh * uv * sg * (1.0f + gv * (1.0f - sg));
+          du[h] = dh * gv * sg;
         }
-        bf16_t* out = reinterpret_cast<bf16_t*>(rowp[r]);
-        *reinterpret_cast<u32x2_t*>(out + n) = u32x2_t{pack_bf16x2(dg[0], dg[1]), pack_bf16x2(dg[2], dg[3])};
-        *reinterpret_cast<u32x2_t*>(out + g.du_off + n) = u32x2_t{pack_bf16x2(du[0], du[1]), pack_bf16x2(du[2], du[3])};
+        dgw[e2] = pack_bf16x2(dg[0], dg[1]);
+        duw[e2] = pack_bf16x2(du[0], du[1]);
       }
+      bf16_t* out = reinterpret_cast<bf16_t*>(rowp[r]);
+      *reinterpret_cast<u32x4_t*>(out + n) = u32x4_t{dgw[0], dgw[1], dgw[2], dgw[3]};
+      *reinterpret_cast<u32x4_t*>(out + g.du_off + n) = u32x4_t{duw[0], duw[1], duw[2], duw[3]};
     }
   }
 }
@@ -563,9 +569,8 @@ bool xgemm_q_ok(const XGemm& g, int epi) {
     return g.ldc % 8 == 0 && g.msplit % 4 == 0 && g.sched_mode == XS_WGRAD &&
            (g.ksplit <= 1 || (g.part && xq_al16(g.part)));
   if (epi == XE_SWIGLU_BWD)
-    return g.ldc % 4 == 0 && g.c_group_col % 4 == 0 && (reinterpret_cast<uintptr_t>(g.C) & 7) == 0 &&
-           g.du_off % 4 == 0 && g.ld_gu % 4 == 0 && g.gu_group_col % 4 == 0 &&
-           (reinterpret_cast<uintptr_t>(g.Gs) & 7) == 0 && (reinterpret_cast<uintptr_t>(g.Us) & 7) == 0;
+    return g.ldc % 8 == 0 && g.c_group_col % 8 == 0 && xq_al16(g.C) && g.du_off % 8 == 0 && g.ld_gu % 8 == 0 &&
+           g.gu_group_col % 8 == 0 && xq_al16(g.Gs) && xq_al16(g.Us);
   return g.ldc % 8 == 0 && g.c_group_col % 8 == 0 && xq_al16(g.C);
 }
 
