@@ -260,7 +260,8 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=30,
+                    help="untimed steps first; the clock settles into its loaded state within a few tens of ms")
     ap.add_argument("--config", default="c3", choices=FWD_ONLY)
     ap.add_argument("--fwd-bwd-config", default="c4", choices=sorted(CONFIGS),
                     help="training-step workload reported under fwd_bwd")

@@ -423,6 +423,8 @@ __global__ __launch_bounds__(256) void gemm_qw_kernel(const GemmDesc g0, const G
     // LDS -> global: lane cc of a row group stores 16-byte chunk cc of its row
     bf16_t* C = static_cast<bf16_t*>(pass == 0 ? g.C : ((pass == 1 && g.Gs) ? g.Gs : g.Us));
     const int n = n0 + cc * 8;
+    // unrolled so that the LDS reads of several rows are in flight together
+#pragma unroll 4
     for (int r = rr; r < rows; r += RPP) {
       const int pu = (2 * cc) ^ (r & 31);
       u32x4_t v = *reinterpret_cast<const u32x4_t*>(qw_smem + r * ROWB + ((pu >> 1) << 4));

@@ -454,6 +454,7 @@ __global__ __launch_bounds__(256) void xgemm_q_kernel(const XGemm g) {
     xq_sync();
     // 32 lanes per row, 16 bytes each; 8 rows per pass
     const int cc = tid & 31, n = n0 + cc * 8;
+#pragma unroll 4
     for (int r = tid >> 5; r < rows; r += 8) {
       const int pu = (2 * cc) ^ (r & 31);
       u32x4_t v = *reinterpret_cast<const u32x4_t*>(sm + r * 512 + ((pu >> 1) << 4));
