@@ -23,99 +23,126 @@ typedef float g_f32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned int g_u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int GATE_THREADS = 256;
+// MFMA gate: 4 waves when one 32-expert tile covers E, else 8 (the second four
+// take the odd expert tiles of the same K quarters)
+constexpr int GM_WAVES_MAX = 8;
+constexpr int gm_waves(int nt) { return nt >= 2 ? 8 : 4; }
 constexpr int GATE_KC = 32;        // SIMT: K chunk staged through LDS
 constexpr int GM_TOK = 32;         // MFMA: tokens per block
 constexpr int MAX_EPL = 4;         // experts per lane in routing (E <= 256)
 
 // ------------------------------------------------------------------ routing
 // Routes tokens [t0, t0 + ntok) whose fp32 logits sit in LDS rows lg[t*ldl].
-// Wave w takes tokens w, w+nw, ...; lane l holds expert l (E <= 64) or
-// experts l, l+64, ... (E <= 256).
+// Wave w takes batches of route_ntok(EPL) consecutive tokens (w, w + nw, ... in
+// batch units) and routes the tokens of a batch together, so the LDS round
+// trips of its tokens overlap.  Lane l holds expert l (E <= 64) or experts
+// l, l+64, ... (E <= 256).
 //
 // Selection by rank: every expert's biased score goes to a per-wave LDS row;
 // each lane counts the experts that beat its own under the order (value
 // desc, id asc).  Rank < k selects the expert and is its output slot j, so
 // the result equals k rounds of arg-max with that tie rule.  The renormalising
 // sum then runs over slots j = 0..k-1 in order, as in the oracle.
-// wscr: per-wave LDS scratch of 64 * MAX_EPL + MAX_TOPK floats.
+// wscr: per-wave LDS scratch of route_ntok(EPL) * route_row(EPL) floats.
 //
 // Lanes of one wave exchange values through LDS: a wave's LDS operations
 // complete in issue order, so waiting for this wave's LDS counter (and a
 // compiler barrier) is enough.  A memory fence would also wait for the
 // token's global output stores.
+// Tokens a wave routes together, and scratch floats per token (biased
+// scores of the lane's experts, then the selected scores by slot).
+constexpr int route_ntok(int epl) { return epl == 1 ? 4 : 2; }
+constexpr int route_row(int epl) { return 64 * epl + MAX_TOPK; }
+
 __device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 template <int EPL>  // experts per lane: 1 for E <= 64, MAX_EPL otherwise
 __device__ __forceinline__ void route_tokens_t(const float* lg, int ldl, int ntok, int t0, const float* bias_s, int E,
                                                int k, float route_scale, int xdtype, const GateOut& out, int* hist,
                                                float* wscr_all) {
+  constexpr int NT = route_ntok(EPL), ROUTE_ROW = route_row(EPL);
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int nw = blockDim.x >> 6;
-  float* wb = wscr_all + wave * (64 * MAX_EPL + MAX_TOPK);   // biased scores [E]
-  float* ws = wb + 64 * MAX_EPL;                              // selected scores by slot [k]
+  float* wscr = wscr_all + wave * NT * ROUTE_ROW;   // token t: biased scores [E], then selected scores by slot [k]
   const int e4 = (E + 3) & ~3;
-  for (int t = wave; t < ntok; t += nw) {
-    const float* row = lg + t * ldl;
-    float sv[EPL], bv[EPL];
+  for (int tb = wave * NT; tb < ntok; tb += nw * NT) {
+    float sv[NT][EPL], bv[NT][EPL];
 #pragma unroll
-    for (int q = 0; q < EPL; ++q) {
-      const int e = lane + 64 * q;
-      sv[q] = 0.0f;
-      bv[q] = -INFINITY;
-      if (e < E) {
-        sv[q] = route_sigmoid(row[e]);
-        bv[q] = sv[q] + bias_s[e];
+    for (int t = 0; t < NT; ++t) {
+      const bool tok = tb + t < ntok;
+      const float* row = lg + (tb + t) * ldl;
+#pragma unroll
+      for (int q = 0; q < EPL; ++q) {
+        const int e = lane + 64 * q;
+        sv[t][q] = 0.0f;
+        bv[t][q] = -INFINITY;
+        if (tok && e < E) {
+          sv[t][q] = route_sigmoid(row[e]);
+          bv[t][q] = sv[t][q] + bias_s[e];
+        }
+        if (e < e4) wscr[t * ROUTE_ROW + e] = bv[t][q];
       }
-      if (e < e4) wb[e] = bv[q];
     }
     wave_lds_sync();
-    int rank[EPL];
+    int rank[NT][EPL];
 #pragma unroll
-    for (int q = 0; q < EPL; ++q) rank[q] = 0;
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int q = 0; q < EPL; ++q) rank[t][q] = 0;
     for (int c = 0; c < e4; c += 4) {
-      const float4 v = *reinterpret_cast<const float4*>(wb + c);
-      const float vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int t = 0; t < NT; ++t) {
+        const float4 v = *reinterpret_cast<const float4*>(wscr + t * ROUTE_ROW + c);
+        const float vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-        for (int q = 0; q < EPL; ++q) {
-          const int e = lane + 64 * q;
-          // branch-free: (value desc, id asc) order
-          rank[q] += (int)(vv[i] > bv[q]) | ((int)(vv[i] == bv[q]) & (int)(c + i < e));
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+          for (int q = 0; q < EPL; ++q) {
+            const int e = lane + 64 * q;
+            // branch-free: (value desc, id asc) order
+            rank[t][q] += (int)(vv[i] > bv[t][q]) | ((int)(vv[i] == bv[t][q]) & (int)(c + i < e));
+          }
         }
       }
     }
 #pragma unroll
-    for (int q = 0; q < EPL; ++q) {
-      const int e = lane + 64 * q;
-      if (e < E && rank[q] < k) ws[rank[q]] = sv[q];
-    }
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int q = 0; q < EPL; ++q) {
+        const int e = lane + 64 * q;
+        if (tb + t < ntok && e < E && rank[t][q] < k) wscr[t * ROUTE_ROW + 64 * EPL + rank[t][q]] = sv[t][q];
+      }
     wave_lds_sync();
-    float ssum = 0.0f;
-    for (int j = 0; j < k; ++j) ssum += ws[j];
-    const float den = ssum < 1e-10f ? 1e-10f : ssum;
-    const int64_t o = (int64_t)(t0 + t) * k;
 #pragma unroll
-    for (int q = 0; q < EPL; ++q) {
-      const int e = lane + 64 * q;
-      if (e < E && rank[q] < k) {
-        const int j = rank[q];
-        const float w = sv[q] / den * route_scale;
-        out.idx[o + j] = e;
-        if (out.idx64) out.idx64[o + j] = e;
-        out.weights[o + j] = w;
-        if (out.weights_x) {
-          if (xdtype == DSMOE_BF16)
-            static_cast<bf16_t*>(out.weights_x)[o + j] = f2bf(w);
-          else
-            static_cast<float*>(out.weights_x)[o + j] = w;
+    for (int t = 0; t < NT; ++t) {
+      if (tb + t >= ntok) break;
+      const float* ws = wscr + t * ROUTE_ROW + 64 * EPL;
+      float ssum = 0.0f;
+      for (int j = 0; j < k; ++j) ssum += ws[j];
+      const float den = ssum < 1e-10f ? 1e-10f : ssum;
+      const int64_t o = (int64_t)(t0 + tb + t) * k;
+#pragma unroll
+      for (int q = 0; q < EPL; ++q) {
+        const int e = lane + 64 * q;
+        if (e < E && rank[t][q] < k) {
+          const int j = rank[t][q];
+          const float w = sv[t][q] / den * route_scale;
+          out.idx[o + j] = e;
+          if (out.idx64) out.idx64[o + j] = e;
+          out.weights[o + j] = w;
+          if (out.weights_x) {
+            if (xdtype == DSMOE_BF16)
+              static_cast<bf16_t*>(out.weights_x)[o + j] = f2bf(w);
+            else
+              static_cast<float*>(out.weights_x)[o + j] = w;
+          }
+          if (out.sel_scores) out.sel_scores[o + j] = sv[t][q];
+          if (hist) atomicAdd(&hist[e], 1);
         }
-        if (out.sel_scores) out.sel_scores[o + j] = sv[q];
-        if (hist) atomicAdd(&hist[e], 1);
       }
     }
-    // the next token reuses wb/ws: make sure every lane finished reading them
+    // the next batch reuses the scratch: make sure every lane finished reading it
     wave_lds_sync();
   }
 }
@@ -158,12 +185,16 @@ __device__ __forceinline__ void split3(const g_f32x4_t& a, const g_f32x4_t& b, g
   __builtin_memcpy(&lo, l, 16);
 }
 
-constexpr int ROUTE_SCR = GATE_THREADS / 64 * (64 * MAX_EPL + MAX_TOPK);  // floats of routing scratch
+// floats of routing scratch (per wave, the larger of the two layouts)
+constexpr int ROUTE_SCR = GM_WAVES_MAX *
+                          (route_ntok(1) * route_row(1) > route_ntok(MAX_EPL) * route_row(MAX_EPL)
+                               ? route_ntok(1) * route_row(1)
+                               : route_ntok(MAX_EPL) * route_row(MAX_EPL));
 
 // LDS: part[4][GM_TOK][EP+1] fp32 partial logits (reused for the reduced
 // logits), bias[E], hist[E], routing scratch.
 template <int NT>
-__global__ __launch_bounds__(GATE_THREADS) void gate_mfma_kernel(const bf16_t* __restrict__ x,
+__global__ __launch_bounds__(gm_waves(NT) * 64) void gate_mfma_kernel(const bf16_t* __restrict__ x,
                                                                  const float* __restrict__ gw,
                                                                  const float* __restrict__ bias, int T, int D, int E,
                                                                  int k, float route_scale, GateOut out) {
@@ -176,67 +207,93 @@ __global__ __launch_bounds__(GATE_THREADS) void gate_mfma_kernel(const bf16_t* _
   // 16-byte aligned offset from the LDS base (pointer arithmetic keeps the
   // accesses in the LDS address space)
   float* rscr = gsm + ((4 * GM_TOK * LDP + 2 * E + 3) & ~3);
+  constexpr int NWV = gm_waves(NT);
+  constexpr int NTH = NWV * 64;
+  // wave w: K quarter w & 3; expert tiles ni = w >> 2, w >> 2 + NWV / 4, ...
+  constexpr int TSTEP = NWV / 4;
+  constexpr int NTW = (NT + TSTEP - 1) / TSTEP;       // expert tiles per wave (upper bound)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int quarter = wave & 3, tfirst = wave >> 2;
   const int t0 = blockIdx.x * GM_TOK;
-  for (int e = tid; e < E; e += GATE_THREADS) {
+  for (int e = tid; e < E; e += NTH) {
     bias_s[e] = bias[e];
     hist[e] = 0;
   }
   const int kq = D / 4;
-  const int kbeg = wave * kq;
+  const int kbeg = quarter * kq;
   const int m = lane & 31;
   const int row = min(t0 + m, T - 1);
   const bf16_t* xr = x + (int64_t)row * D + (lane >> 5) * 8;
-  const float* wr[NT];
+  const float* wr[NTW];
 #pragma unroll
-  for (int ni = 0; ni < NT; ++ni) wr[ni] = gw + (int64_t)min(ni * 32 + m, E - 1) * D + (lane >> 5) * 8;
+  for (int i = 0; i < NTW; ++i) {
+    const int ni = min(tfirst + i * TSTEP, NT - 1);
+    wr[i] = gw + (int64_t)min(ni * 32 + m, E - 1) * D + (lane >> 5) * 8;
+  }
+  const int ntw = min(NTW, (NT - tfirst + TSTEP - 1) / TSTEP);   // this wave's tiles
 
-  g_f32x16_t acc[NT];
+  g_f32x16_t acc[NTW];
 #pragma unroll
-  for (int ni = 0; ni < NT; ++ni)
+  for (int i = 0; i < NTW; ++i)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[ni][r] = 0.0f;
+    for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
 
-  // K loop in chunks of PF steps: the loads of a whole chunk are issued before
-  // its MFMAs, so PF global round trips overlap (the loop is latency-bound
-  // otherwise: one block streams all of W_gate).
-  constexpr int PF = (NT <= 2) ? 8 : 2;
+  // K loop in chunks of PF steps of 16, double-buffered: the loads of chunk
+  // c + 1 are issued before the MFMAs of chunk c, so the global round trips
+  // overlap the split and MFMA work (the loop is latency-bound otherwise:
+  // every block streams all of W_gate).
+  constexpr int PF = (NTW <= 2) ? 4 : 2;
   const int kend = kbeg + kq;
-  for (int k0 = kbeg; k0 < kend; k0 += 16 * PF) {
-    g_bf16x8_t a[PF];
-    g_f32x4_t w0[PF][NT], w1[PF][NT];
+  g_bf16x8_t a[2][PF];
+  g_f32x4_t w0[2][PF][NTW], w1[2][PF][NTW];
+  auto load = [&](int buf, int k0) {
 #pragma unroll
     for (int p = 0; p < PF; ++p) {
       const int kk = min(k0 + 16 * p, kend - 16);
-      a[p] = *reinterpret_cast<const g_bf16x8_t*>(xr + kk);
+      a[buf][p] = *reinterpret_cast<const g_bf16x8_t*>(xr + kk);
 #pragma unroll
-      for (int ni = 0; ni < NT; ++ni) {
-        w0[p][ni] = *reinterpret_cast<const g_f32x4_t*>(wr[ni] + kk);
-        w1[p][ni] = *reinterpret_cast<const g_f32x4_t*>(wr[ni] + kk + 4);
+      for (int ni = 0; ni < NTW; ++ni) {
+        w0[buf][p][ni] = *reinterpret_cast<const g_f32x4_t*>(wr[ni] + kk);
+        w1[buf][p][ni] = *reinterpret_cast<const g_f32x4_t*>(wr[ni] + kk + 4);
       }
     }
+  };
+  auto compute = [&](int buf, int k0) {
 #pragma unroll
     for (int p = 0; p < PF; ++p) {
       if (k0 + 16 * p >= kend) break;
 #pragma unroll
-      for (int ni = 0; ni < NT; ++ni) {
+      for (int ni = 0; ni < NTW; ++ni) {
+        if (ni >= ntw) break;
         g_bf16x8_t hi, mid, lo;
-        split3(w0[p][ni], w1[p][ni], hi, mid, lo);
-        acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lo, a[p], acc[ni], 0, 0, 0);
-        acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mid, a[p], acc[ni], 0, 0, 0);
-        acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(hi, a[p], acc[ni], 0, 0, 0);
+        split3(w0[buf][p][ni], w1[buf][p][ni], hi, mid, lo);
+        acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lo, a[buf][p], acc[ni], 0, 0, 0);
+        acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mid, a[buf][p], acc[ni], 0, 0, 0);
+        acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(hi, a[buf][p], acc[ni], 0, 0, 0);
       }
     }
+  };
+  constexpr int CH = 16 * PF;
+  load(0, kbeg);
+  for (int k0 = kbeg; k0 < kend; k0 += 2 * CH) {
+    if (k0 + CH < kend) load(1, k0 + CH);
+    compute(0, k0);
+    if (k0 + CH >= kend) break;
+    if (k0 + 2 * CH < kend) load(0, k0 + 2 * CH);
+    compute(1, k0 + CH);
   }
   // lane holds token m, experts ni*32 + 8*(r/4) + 4*(lane/32) + r%4
-  float* pw = part + wave * GM_TOK * LDP + m * LDP;
+  float* pw = part + quarter * GM_TOK * LDP + m * LDP;
 #pragma unroll
-  for (int ni = 0; ni < NT; ++ni)
+  for (int i = 0; i < NTW; ++i) {
+    if (i >= ntw) break;
+    const int ni = tfirst + i * TSTEP;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) pw[ni * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)] = acc[ni][r];
+    for (int r = 0; r < 16; ++r) pw[ni * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)] = acc[i][r];
+  }
   __syncthreads();
   const int ntok = min(GM_TOK, T - t0);
-  for (int i = tid; i < GM_TOK * E; i += GATE_THREADS) {
+  for (int i = tid; i < GM_TOK * E; i += NTH) {
     const int t = i / E, e = i - t * E;
     const int o = t * LDP + e;
     const float v = ((part[o] + part[GM_TOK * LDP + o]) + part[2 * GM_TOK * LDP + o]) + part[3 * GM_TOK * LDP + o];
@@ -367,7 +424,7 @@ static int launch_gate_mfma(const void* x, const float* gw, const float* bias, c
   auto kern = gate_mfma_kernel<NT>;
   int rc = set_lds((const void*)kern, lds);
   if (rc) return rc;
-  hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(d.T, GM_TOK)), dim3(GATE_THREADS), lds, st,
+  hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(d.T, GM_TOK)), dim3(gm_waves(NT) * 64), lds, st,
                      static_cast<const bf16_t*>(x), gw, bias, d.T, d.D, d.E, d.k, d.route_scale, out);
   return check_launch("gate_mfma");
 }
