@@ -5,9 +5,10 @@
 //   rank_kernel     one wave per 64 tokens: for each expert a wave ballot gives
 //                   every slot its rank among the block's earlier tokens, and
 //                   the block histogram (no atomics, deterministic).
-//   scan_kernel     one block: per-expert exclusive scan over block histograms,
+//   scan_kernel     one block of 16 waves: per-expert exclusive scans over the
+//                   block histograms (wave prefix sums, 64 blocks at a time),
 //                   counts, offsets (E+1), and the M-tile schedule used by the
-//                   grouped GEMMs (tiles of PERM_BM rows inside each expert).
+//                   grouped GEMMs (tiles of bm rows inside each expert).
 //   scatter_kernel  pos = offsets[e] + blockbase[b][e] + rank; writes the
 //                   sorted order, its inverse and optional weight gather.
 //   gather_rows     x_sorted[p] = x[sorted_token[p]] with 16-byte accesses.
@@ -18,20 +19,21 @@ namespace dsmoe {
 constexpr int RANK_TOKENS = 64;  // one wave64 per block, one token per lane
 constexpr int MAX_K = 16;
 
+template <int KB>  // bound on k (slots compared per expert)
 __global__ __launch_bounds__(64) void rank_kernel(const int32_t* __restrict__ idx, int T, int k, int E,
                                                   int32_t* __restrict__ blockhist, int32_t* __restrict__ local_rank) {
   const int lane = threadIdx.x;
   const int t = blockIdx.x * RANK_TOKENS + lane;
-  int ex[MAX_K];
+  int ex[KB];
 #pragma unroll
-  for (int j = 0; j < MAX_K; ++j) ex[j] = -1;
+  for (int j = 0; j < KB; ++j) ex[j] = -1;
   if (t < T)
     for (int j = 0; j < k; ++j) ex[j] = idx[(int64_t)t * k + j];
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   for (int e = 0; e < E; ++e) {
     int jsel = -1;
 #pragma unroll
-    for (int j = 0; j < MAX_K; ++j)
+    for (int j = 0; j < KB; ++j)
       if (ex[j] == e) jsel = j;
     const uint64_t mask = __ballot(jsel >= 0);
     if (jsel >= 0) local_rank[(int64_t)t * k + jsel] = __popcll(mask & below);
@@ -39,46 +41,60 @@ __global__ __launch_bounds__(64) void rank_kernel(const int32_t* __restrict__ id
   }
 }
 
-// Single block.  LDS: cnt[E], off[E+1], tiles[E+1].
-__global__ __launch_bounds__(256) void scan_kernel(const int32_t* __restrict__ blockhist, int nb, int E, int bm,
-                                                   int32_t* __restrict__ blockbase, int32_t* __restrict__ counts,
-                                                   int32_t* __restrict__ offsets, MTile* __restrict__ sched,
-                                                   int32_t* __restrict__ sched_count) {
+// Inclusive prefix sum over the 64 lanes of a wave (exact integer adds).
+__device__ __forceinline__ int32_t wave_incl_scan(int32_t x, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int32_t y = __shfl_up(x, d, 64);
+    if (lane >= d) x += y;
+  }
+  return x;
+}
+
+// Single block.  LDS: cnt[E], off[E+1], tiles[E+1].  Wave w scans experts
+// w, w + nw, ...: lane b holds block b's count of the expert, 64 blocks at a
+// time, carried across chunks.  Wave 0 then scans counts and tile counts over
+// the experts, 64 at a time.  Integer sums: the same values as a serial scan.
+__global__ __launch_bounds__(1024) void scan_kernel(const int32_t* __restrict__ blockhist, int nb, int E, int bm,
+                                                    int32_t* __restrict__ blockbase, int32_t* __restrict__ counts,
+                                                    int32_t* __restrict__ offsets, MTile* __restrict__ sched,
+                                                    int32_t* __restrict__ sched_count) {
   extern __shared__ int32_t sh[];
   int32_t* cnt = sh;
   int32_t* off = sh + E;
   int32_t* til = off + E + 1;
-  const int tid = threadIdx.x;
-  for (int e = tid; e < E; e += blockDim.x) {
-    int32_t run = 0;
-    int b = 0;
-    for (; b + 4 <= nb; b += 4) {
-      int32_t v0 = blockhist[(int64_t)(b + 0) * E + e], v1 = blockhist[(int64_t)(b + 1) * E + e];
-      int32_t v2 = blockhist[(int64_t)(b + 2) * E + e], v3 = blockhist[(int64_t)(b + 3) * E + e];
-      blockbase[(int64_t)(b + 0) * E + e] = run; run += v0;
-      blockbase[(int64_t)(b + 1) * E + e] = run; run += v1;
-      blockbase[(int64_t)(b + 2) * E + e] = run; run += v2;
-      blockbase[(int64_t)(b + 3) * E + e] = run; run += v3;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+  for (int e = wave; e < E; e += nw) {
+    int32_t carry = 0;
+    for (int b0 = 0; b0 < nb; b0 += 64) {
+      const int b = b0 + lane;
+      const int32_t v = b < nb ? blockhist[(int64_t)b * E + e] : 0;
+      const int32_t x = wave_incl_scan(v, lane);
+      if (b < nb) blockbase[(int64_t)b * E + e] = carry + x - v;
+      carry += __shfl(x, 63, 64);
     }
-    for (; b < nb; ++b) {
-      int32_t v = blockhist[(int64_t)b * E + e];
-      blockbase[(int64_t)b * E + e] = run;
-      run += v;
-    }
-    cnt[e] = run;
+    if (lane == 0) cnt[e] = carry;
   }
   __syncthreads();
-  if (tid == 0) {
-    int32_t o = 0, tl = 0;
-    for (int e = 0; e < E; ++e) {
-      off[e] = o;
-      til[e] = tl;
-      o += cnt[e];
-      tl += (cnt[e] + bm - 1) / bm;
+  if (wave == 0) {
+    int32_t co = 0, ct = 0;
+    for (int e0 = 0; e0 < E; e0 += 64) {
+      const int e = e0 + lane;
+      const int32_t c = e < E ? cnt[e] : 0;
+      const int32_t tc = (c + bm - 1) / bm;
+      const int32_t xo = wave_incl_scan(c, lane), xt = wave_incl_scan(tc, lane);
+      if (e < E) {
+        off[e] = co + xo - c;
+        til[e] = ct + xt - tc;
+      }
+      co += __shfl(xo, 63, 64);
+      ct += __shfl(xt, 63, 64);
     }
-    off[E] = o;
-    til[E] = tl;
-    *sched_count = tl;
+    if (lane == 0) {
+      off[E] = co;
+      til[E] = ct;
+      *sched_count = ct;
+    }
   }
   __syncthreads();
   for (int e = tid; e <= E; e += blockDim.x) {
@@ -199,9 +215,14 @@ int launch_permute(const int32_t* idx, const dsmoe_dims& d, int bm, const Permut
                    float* sorted_w, hipStream_t st) {
   const int nb = (int)cdiv(d.T, RANK_TOKENS);
   const int64_t N = (int64_t)d.T * d.k;
-  if (nb > 0) hipLaunchKernelGGL(rank_kernel, dim3(nb), dim3(64), 0, st, idx, d.T, d.k, d.E, s.blockhist, s.local_rank);
+  if (nb > 0) {
+    if (d.k <= 8)
+      hipLaunchKernelGGL(rank_kernel<8>, dim3(nb), dim3(64), 0, st, idx, d.T, d.k, d.E, s.blockhist, s.local_rank);
+    else
+      hipLaunchKernelGGL(rank_kernel<MAX_K>, dim3(nb), dim3(64), 0, st, idx, d.T, d.k, d.E, s.blockhist, s.local_rank);
+  }
   const size_t lds = sizeof(int32_t) * (3 * d.E + 2);
-  hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(256), lds, st, s.blockhist, nb, d.E, bm, s.blockbase, counts, offsets,
+  hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), lds, st, s.blockhist, nb, d.E, bm, s.blockbase, counts, offsets,
                      s.sched, s.sched_count);
   if (N > 0)
     hipLaunchKernelGGL(scatter_kernel, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, st, idx, s.local_rank, s.blockbase,
