@@ -5,7 +5,7 @@
 // reference adds expert outputs in ascending expert id) and the shared add of
 // models/moe.py:100-102.  Accumulation is fp32 with one final rounding; the k
 // rows of a token are contiguous (slot order), so every access is a coalesced
-// 16-byte vector.
+// 16-byte vector.  A token's slot order is computed once, by k threads.
 #include "common.h"
 
 namespace dsmoe {
@@ -57,38 +57,75 @@ __device__ __forceinline__ void order_by_expert(const int32_t* idx_row, int k, i
   }
 }
 
-// One thread per (token, VEC-wide column chunk).
-template <typename T, int VEC>
+// One block per token.  Threads j < k put slot j at its ascending-expert
+// position q (stable for equal ids) with its weight, in LDS; then each thread
+// takes VEC-wide column chunks c, c + blockDim, ... and issues the loads of the
+// token's k rows before the fp32 accumulation in q order.
+template <typename T, int VEC, int KB>
 __global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ o_slots, const float* __restrict__ w,
                                                       const int32_t* __restrict__ idx, const T* __restrict__ shared,
                                                       int T_, int D, int k, T* __restrict__ y) {
   using V = Vec<T, VEC>;
   using VT = typename V::type;
+  __shared__ int ord_s[KB];
+  __shared__ float w_s[KB];
+  const int64_t t = blockIdx.x;
+  if ((int)threadIdx.x < k) {
+    const int j = threadIdx.x;
+    const int e = idx[t * k + j];
+    int q = 0;
+    for (int jj = 0; jj < k; ++jj) {
+      const int ee = idx[t * k + jj];
+      q += (ee < e) || (ee == e && jj < j);
+    }
+    ord_s[q] = j;
+    w_s[q] = w[t * k + j];
+  }
+  __syncthreads();
   const int cpr = D / VEC;
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (int64_t)T_ * cpr) return;
-  const int64_t t = i / cpr;
-  const int c = (int)(i - t * cpr);
-  int ord[CMB_MAX_K];
-  order_by_expert(idx + t * k, k, ord);
-  float acc[VEC];
+  for (int c = threadIdx.x; c < cpr; c += blockDim.x) {
+    VT ov[KB];
 #pragma unroll
-  for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
-  for (int q = 0; q < k; ++q) {
-    const int j = ord[q];
-    const float wj = w[t * k + j];
-    float f[VEC];
-    V::to_f(reinterpret_cast<const VT*>(o_slots + (t * k + j) * (int64_t)D)[c], f);
+    for (int q = 0; q < KB; ++q)
+      if (q < k) ov[q] = reinterpret_cast<const VT*>(o_slots + (t * k + ord_s[q]) * (int64_t)D)[c];
+    VT sv;
+    if (shared) sv = reinterpret_cast<const VT*>(shared + t * (int64_t)D)[c];
+    float acc[VEC];
 #pragma unroll
-    for (int v = 0; v < VEC; ++v) acc[v] = fmaf(wj, f[v], acc[v]);
+    for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
+#pragma unroll
+    for (int q = 0; q < KB; ++q) {
+      if (q >= k) break;
+      const float wj = w_s[q];
+      float f[VEC];
+      V::to_f(ov[q], f);
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) acc[v] = fmaf(wj, f[v], acc[v]);
+    }
+    if (shared) {
+      float f[VEC];
+      V::to_f(sv, f);
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) acc[v] += f[v];
+    }
+    reinterpret_cast<VT*>(y + t * (int64_t)D)[c] = V::from_f(acc);
   }
-  if (shared) {
-    float f[VEC];
-    V::to_f(reinterpret_cast<const VT*>(shared + t * (int64_t)D)[c], f);
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) acc[v] += f[v];
-  }
-  reinterpret_cast<VT*>(y + t * (int64_t)D)[c] = V::from_f(acc);
+}
+
+template <typename T, int VEC>
+static void launch_combine_vec(const void* o_slots, const float* w, const int32_t* idx, const void* shared,
+                               const dsmoe_dims& d, void* y, hipStream_t st) {
+  const int cpr = d.D / VEC;
+  const int threads = cpr >= 256 ? 256 : (int)(cdiv(cpr, 64) * 64);
+  auto o = static_cast<const T*>(o_slots);
+  auto sh = static_cast<const T*>(shared);
+  auto yy = static_cast<T*>(y);
+  if (d.k <= 8)
+    hipLaunchKernelGGL((combine_kernel<T, VEC, 8>), dim3((unsigned)d.T), dim3(threads), 0, st, o, w, idx, sh, d.T, d.D,
+                       d.k, yy);
+  else
+    hipLaunchKernelGGL((combine_kernel<T, VEC, CMB_MAX_K>), dim3((unsigned)d.T), dim3(threads), 0, st, o, w, idx, sh,
+                       d.T, d.D, d.k, yy);
 }
 
 template <typename T>
@@ -118,10 +155,7 @@ int launch_combine(const void* o_slots, const float* w, const int32_t* idx, cons
                     reinterpret_cast<uintptr_t>(shared)) & 15) == 0;
   if (d.dtype == DSMOE_BF16) {
     if (d.D % 8 == 0 && al) {
-      const int64_t n = (int64_t)d.T * (d.D / 8);
-      hipLaunchKernelGGL((combine_kernel<uint16_t, 8>), dim3((unsigned)cdiv(n, 256)), dim3(256), 0, st,
-                         static_cast<const uint16_t*>(o_slots), w, idx, static_cast<const uint16_t*>(shared), d.T, d.D,
-                         d.k, static_cast<uint16_t*>(y));
+      launch_combine_vec<uint16_t, 8>(o_slots, w, idx, shared, d, y, st);
     } else {
       const int64_t n = (int64_t)d.T * d.D;
       hipLaunchKernelGGL(combine_scalar_kernel<uint16_t>, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, st,
@@ -130,10 +164,7 @@ int launch_combine(const void* o_slots, const float* w, const int32_t* idx, cons
     }
   } else {
     if (d.D % 4 == 0 && al) {
-      const int64_t n = (int64_t)d.T * (d.D / 4);
-      hipLaunchKernelGGL((combine_kernel<float, 4>), dim3((unsigned)cdiv(n, 256)), dim3(256), 0, st,
-                         static_cast<const float*>(o_slots), w, idx, static_cast<const float*>(shared), d.T, d.D, d.k,
-                         static_cast<float*>(y));
+      launch_combine_vec<float, 4>(o_slots, w, idx, shared, d, y, st);
     } else {
       const int64_t n = (int64_t)d.T * d.D;
       hipLaunchKernelGGL(combine_scalar_kernel<float>, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, st,
