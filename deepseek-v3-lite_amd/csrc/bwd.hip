@@ -130,43 +130,56 @@ struct Vec16<float> {
 };
 
 // dx[t] per token (one block): same order and rounding as dx_final_kernel.
-template <typename T>
+// Threads j < k put slot j at its ascending-expert position q in LDS (with
+// its expert and dlogit); the k slot rows of a column chunk are loaded
+// together before the fp32 sums.
+template <typename T, int KB>
 __global__ __launch_bounds__(256) void dx_final_vec_kernel(const T* __restrict__ dx_slots, const T* __restrict__ dx_shared,
                                                            const float* __restrict__ dlog, const int32_t* __restrict__ idx,
                                                            const float* __restrict__ gw, int D, int k,
                                                            T* __restrict__ dx) {
   constexpr int V = Vec16<T>::N;
+  __shared__ int ord_s[KB], ev_s[KB];
+  __shared__ float dl_s[KB];
   const int64_t t = blockIdx.x;
-  int ord[MAX_TOPK], ev[MAX_TOPK];
-  for (int j = 0; j < k; ++j) {  // ascending expert id (insertion sort, k <= 16)
+  if ((int)threadIdx.x < k) {
+    const int j = threadIdx.x;
     const int e = idx[t * k + j];
-    int p = j;
-    while (p > 0 && ev[p - 1] > e) {
-      ev[p] = ev[p - 1];
-      ord[p] = ord[p - 1];
-      --p;
+    int q = 0;
+    for (int jj = 0; jj < k; ++jj) {
+      const int ee = idx[t * k + jj];
+      q += (ee < e) || (ee == e && jj < j);
     }
-    ev[p] = e;
-    ord[p] = j;
+    ord_s[q] = j;
+    ev_s[q] = e;
+    dl_s[q] = dlog[t * k + j];
   }
+  __syncthreads();
   for (int c = threadIdx.x; c * V < D; c += blockDim.x) {
     const int d = c * V;
-    float acc[V], v[V];
+    float acc[V], v[KB][V];
 #pragma unroll
     for (int i = 0; i < V; ++i) acc[i] = 0.0f;
-    for (int q = 0; q < k; ++q) {
-      Vec16<T>::load(dx_slots + (t * k + ord[q]) * (int64_t)D + d, v);
 #pragma unroll
-      for (int i = 0; i < V; ++i) acc[i] += v[i];
+    for (int q = 0; q < KB; ++q)
+      if (q < k) Vec16<T>::load(dx_slots + (t * k + ord_s[q]) * (int64_t)D + d, v[q]);
+#pragma unroll
+    for (int q = 0; q < KB; ++q) {
+      if (q >= k) break;
+#pragma unroll
+      for (int i = 0; i < V; ++i) acc[i] += v[q][i];
     }
     if (dx_shared) {
-      Vec16<T>::load(dx_shared + t * (int64_t)D + d, v);
+      float sv[V];
+      Vec16<T>::load(dx_shared + t * (int64_t)D + d, sv);
 #pragma unroll
-      for (int i = 0; i < V; ++i) acc[i] += v[i];
+      for (int i = 0; i < V; ++i) acc[i] += sv[i];
     }
-    for (int q = 0; q < k; ++q) {
-      const float dl = dlog[t * k + ord[q]];
-      const float* grow = gw + (int64_t)ev[q] * D + d;
+#pragma unroll
+    for (int q = 0; q < KB; ++q) {
+      if (q >= k) break;
+      const float dl = dl_s[q];
+      const float* grow = gw + (int64_t)ev_s[q] * D + d;
 #pragma unroll
       for (int i = 0; i < V; i += 4) {
         const float4 w4 = *reinterpret_cast<const float4*>(grow + i);
@@ -196,15 +209,33 @@ __global__ __launch_bounds__(256) void dwgate_vec_kernel(const T* __restrict__ x
   const int d = (blockIdx.x * 64 + l) * V;
   const bool live = d < D;
   const int p0 = offsets[e], p1 = offsets[e + 1];
-  float acc[V], v[V];
+  float acc[V];
 #pragma unroll
   for (int i = 0; i < V; ++i) acc[i] = 0.0f;
   if (live) {
-    for (int p = p0 + grp; p < p1; p += 4) {
-      const float w = dlog[sorted_slot[p]];
-      Vec16<T>::load(x + (int64_t)sorted_token[p] * D + d, v);
+    // rows p0 + grp, p0 + grp + 4, ... in ascending order; the loads of U rows
+    // are issued before their FMAs so the index -> value round trips overlap
+    constexpr int U = 8;
+    for (int p = p0 + grp; p < p1; p += 4 * U) {
+      int slot[U], tok[U];
 #pragma unroll
-      for (int i = 0; i < V; ++i) acc[i] = fmaf(w, v[i], acc[i]);
+      for (int u = 0; u < U; ++u) {
+        const int pp = p + 4 * u;
+        slot[u] = pp < p1 ? sorted_slot[pp] : -1;
+        tok[u] = pp < p1 ? sorted_token[pp] : 0;
+      }
+      float wv[U], xv[U][V];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        wv[u] = slot[u] >= 0 ? dlog[slot[u]] : 0.0f;
+        Vec16<T>::load(x + (int64_t)tok[u] * D + d, xv[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (slot[u] < 0) break;
+#pragma unroll
+        for (int i = 0; i < V; ++i) acc[i] = fmaf(wv[u], xv[u][i], acc[i]);
+      }
     }
   }
   if (grp > 0) {
@@ -220,6 +251,43 @@ __global__ __launch_bounds__(256) void dwgate_vec_kernel(const T* __restrict__ x
     float* o = dgw + (int64_t)e * D + d;
 #pragma unroll
     for (int i = 0; i < V; i += 4) *reinterpret_cast<float4*>(o + i) = make_float4(acc[i], acc[i + 1], acc[i + 2], acc[i + 3]);
+  }
+}
+
+// bf16, one wave per token: dy[t] is read once, 16 bytes per lane, and the
+// k dot products with the token's slot rows accumulate together.
+template <int KB>
+__global__ __launch_bounds__(256) void dw_dot_tok_kernel(const bf16_t* __restrict__ dy, const bf16_t* __restrict__ o_slots,
+                                                         int T, int k, int D, float* __restrict__ dw) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const int vpr = D / 8;
+  const uint4* a = reinterpret_cast<const uint4*>(dy + t * D);
+  float acc[KB];
+#pragma unroll
+  for (int j = 0; j < KB; ++j) acc[j] = 0.0f;
+  for (int c = lane; c < vpr; c += 64) {
+    float af[8];
+    Vec16<bf16_t>::load(reinterpret_cast<const bf16_t*>(a + c), af);
+    float bv[KB][8];
+#pragma unroll
+    for (int j = 0; j < KB; ++j)
+      if (j < k) Vec16<bf16_t>::load(o_slots + (t * k + j) * D + c * 8, bv[j]);
+#pragma unroll
+    for (int j = 0; j < KB; ++j) {
+      if (j >= k) break;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[j] = fmaf(af[i], bv[j][i], acc[j]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < KB; ++j) {
+    if (j >= k) break;
+    float v = acc[j];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    if (lane == 0) dw[t * k + j] = v;
   }
 }
 
@@ -263,6 +331,12 @@ int launch_dw_dot(const void* dy, const void* o_slots, int64_t N, int k, int D, 
                   hipStream_t st) {
   if (N == 0) return DSMOE_OK;
   const unsigned grid = (unsigned)cdiv(N, 4);
+  if (dtype == DSMOE_BF16 && D % 8 == 0 && al16p(dy) && al16p(o_slots) && k <= 8) {
+    const int T = (int)(N / k);
+    hipLaunchKernelGGL(dw_dot_tok_kernel<8>, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, st,
+                       static_cast<const bf16_t*>(dy), static_cast<const bf16_t*>(o_slots), T, k, D, dw);
+    return check_launch("dw_dot");
+  }
   if (dtype == DSMOE_BF16)
     hipLaunchKernelGGL(dw_dot_kernel<bf16_t>, dim3(grid), dim3(256), 0, st, static_cast<const bf16_t*>(dy),
                        static_cast<const bf16_t*>(o_slots), N, k, D, dw);
@@ -307,14 +381,25 @@ int launch_dx_final(const void* dx_slots, const void* dx_shared, const float* dl
   const int V = dtype == DSMOE_BF16 ? 8 : 4;
   if (D % V == 0 && al16p(dx_slots) && al16p(dx) && al16p(gw) && (!dx_shared || al16p(dx_shared))) {
     const unsigned threads = (unsigned)std::min<int64_t>(256, cdiv(cdiv(D, V), 64) * 64);
-    if (dtype == DSMOE_BF16)
-      hipLaunchKernelGGL(dx_final_vec_kernel<bf16_t>, dim3((unsigned)T), dim3(threads), 0, st,
-                         static_cast<const bf16_t*>(dx_slots), static_cast<const bf16_t*>(dx_shared), dlog, idx, gw, D,
-                         k, static_cast<bf16_t*>(dx));
-    else
-      hipLaunchKernelGGL(dx_final_vec_kernel<float>, dim3((unsigned)T), dim3(threads), 0, st,
-                         static_cast<const float*>(dx_slots), static_cast<const float*>(dx_shared), dlog, idx, gw, D, k,
-                         static_cast<float*>(dx));
+    if (dtype == DSMOE_BF16) {
+      if (k <= 8)
+        hipLaunchKernelGGL((dx_final_vec_kernel<bf16_t, 8>), dim3((unsigned)T), dim3(threads), 0, st,
+                           static_cast<const bf16_t*>(dx_slots), static_cast<const bf16_t*>(dx_shared), dlog, idx, gw,
+                           D, k, static_cast<bf16_t*>(dx));
+      else
+        hipLaunchKernelGGL((dx_final_vec_kernel<bf16_t, MAX_TOPK>), dim3((unsigned)T), dim3(threads), 0, st,
+                           static_cast<const bf16_t*>(dx_slots), static_cast<const bf16_t*>(dx_shared), dlog, idx, gw,
+                           D, k, static_cast<bf16_t*>(dx));
+    } else {
+      if (k <= 8)
+        hipLaunchKernelGGL((dx_final_vec_kernel<float, 8>), dim3((unsigned)T), dim3(threads), 0, st,
+                           static_cast<const float*>(dx_slots), static_cast<const float*>(dx_shared), dlog, idx, gw, D,
+                           k, static_cast<float*>(dx));
+      else
+        hipLaunchKernelGGL((dx_final_vec_kernel<float, MAX_TOPK>), dim3((unsigned)T), dim3(threads), 0, st,
+                           static_cast<const float*>(dx_slots), static_cast<const float*>(dx_shared), dlog, idx, gw, D,
+                           k, static_cast<float*>(dx));
+    }
     return check_launch("dx_final_vec");
   }
   const unsigned grid = (unsigned)cdiv((int64_t)T * D, 256);
