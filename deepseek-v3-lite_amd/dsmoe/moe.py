@@ -32,6 +32,19 @@ def _flt(t: torch.Tensor) -> torch.Tensor:
     return t if t.dtype == torch.float32 else t.float()
 
 
+def _compute_dtype(x: torch.Tensor) -> torch.dtype:
+    """Arithmetic dtype of the expert GEMMs.  Under a bf16 autocast region
+    (the reference's training step, training/pretrain.py:212-213) fp32
+    activations and weights are cast to bf16, as autocast does for the
+    reference's matmul/bmm calls (models/moe.py:128-131,175-178); the output
+    and ``_last_weights`` keep x's dtype.  Other autocast dtypes leave fp32."""
+    dt = x.device.type
+    if (x.dtype == torch.float32 and torch.is_autocast_enabled(dt)
+            and torch.get_autocast_dtype(dt) == torch.bfloat16):
+        return torch.bfloat16
+    return x.dtype
+
+
 class AuxLossFreeGate(nn.Module):
     """Sigmoid top-k router with a non-trainable fp32 bias (models/moe.py:7-37)."""
 
@@ -103,6 +116,7 @@ class DeepSeekMoE(nn.Module):
         self._last_weights: Optional[torch.Tensor] = None
         self._last_indices: Optional[torch.Tensor] = None
         self._last_counts: Optional[torch.Tensor] = None
+        self._counts_of: Optional[torch.Tensor] = None  # the _last_indices _last_counts was computed from
         self._stack_dtype: Optional[torch.dtype] = None
 
     # -------------------------------------------------------------- forward
@@ -123,14 +137,16 @@ class DeepSeekMoE(nn.Module):
             raise RuntimeError("dsmoe.DeepSeekMoE.forward needs a ROCm GPU tensor; there is no CPU implementation")
         shape = x.shape
         flat = x.reshape(-1, self.dim)
-        w1, w2, w3, s1, s2, s3 = self._expert_weights(flat.dtype)
-        y, idx64, wx, counts = ops.moe_layer(flat, _flt(self.gate.weight), _flt(self.gate.bias), w1, w2, w3, s1, s2,
-                                             s3, k=self.gate.topk, route_scale=self.gate.route_scale)
-        self._last_weights = wx.detach()
+        cdt = _compute_dtype(flat)
+        w1, w2, w3, s1, s2, s3 = self._expert_weights(cdt)
+        y, idx64, wx, counts = ops.moe_layer(flat.to(cdt), _flt(self.gate.weight), _flt(self.gate.bias), w1, w2, w3,
+                                             s1, s2, s3, k=self.gate.topk, route_scale=self.gate.route_scale)
+        self._last_weights = wx.detach().to(flat.dtype)
         self._last_indices = idx64.detach()
         self._last_counts = counts.detach()
-        self._stack_dtype = flat.dtype
-        return y.view(shape)
+        self._counts_of = self._last_indices
+        self._stack_dtype = cdt
+        return y.to(flat.dtype).view(shape)
 
     # -------------------------------------------------------------- stacked views (read on access)
     def _stack(self, mods, name):
@@ -167,7 +183,10 @@ class DeepSeekMoE(nn.Module):
     def _counts(self) -> torch.Tensor:
         """Per-expert counts of the latest routing: the kernel histogram when the
         latest forward produced one, else bincount of _last_indices."""
-        if self._last_counts is not None:
+        # The reference assigns _last_indices directly (e.g. to plant a
+        # routing in tests); the kernel histogram only describes the indices
+        # of the forward that produced it.
+        if self._last_counts is not None and self._counts_of is self._last_indices:
             return self._last_counts
         return torch.bincount(self._last_indices.flatten(), minlength=self.n_routed_experts)
 
@@ -191,9 +210,3 @@ class DeepSeekMoE(nn.Module):
             return
         self.gate.update_bias(self._counts(), speed=speed)
 
-    def __setattr__(self, name, value):
-        # The reference assigns _last_indices/_last_weights directly (e.g. to
-        # plant a routing in tests); drop the cached histogram when it does.
-        if name in ("_last_indices", "_last_weights") and "_last_counts" in self.__dict__:
-            object.__setattr__(self, "_last_counts", None)
-        super().__setattr__(name, value)

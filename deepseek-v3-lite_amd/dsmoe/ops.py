@@ -140,62 +140,99 @@ def update_bias_(counts: torch.Tensor, bias: torch.Tensor, speed: float, upper: 
 
 
 # ---------------------------------------------------------------------------- whole layer
-class _MoELayerFn(torch.autograd.Function):
-    """Forward = dsmoe_moe_fwd, backward = dsmoe_moe_bwd.  The forward
-    workspace (routing, sorted order, pre-activations, expert outputs) is kept
-    on ctx for the backward."""
+def _layer_weights(weights: Sequence[torch.Tensor], E: int, S: int):
+    """Splits the flat weight list [w1 x E, w2 x E, w3 x E, sw1 x S, sw2 x S, sw3 x S]."""
+    return (weights[:E], weights[E:2 * E], weights[2 * E:3 * E], weights[3 * E:3 * E + S],
+            weights[3 * E + S:3 * E + 2 * S], weights[3 * E + 2 * S:])
 
-    @staticmethod
-    def forward(ctx, meta, x, gate_w, gate_bias, *weights):
-        E, S, k, I, I_s, rs, training = meta
-        dev = x.device
-        T, D = x.shape
-        d = L.make_dims(T, D, E, k, I, S, I_s, x.dtype, rs)
-        lib = L.load()
-        ws = _ws(lib.dsmoe_moe_fwd_workspace_size(d, int(training)), dev)
-        y = torch.empty_like(x)
-        idx64 = torch.empty(T, k, dtype=torch.int64, device=dev)
-        wx = torch.empty(T, k, dtype=x.dtype, device=dev)
-        counts = torch.empty(E, dtype=torch.int32, device=dev)
-        w1, w2, w3 = weights[:E], weights[E:2 * E], weights[2 * E:3 * E]
-        s1, s2, s3 = weights[3 * E:3 * E + S], weights[3 * E + S:3 * E + 2 * S], weights[3 * E + 2 * S:]
-        p1, k1 = L.ptr_array(w1); p2, k2 = L.ptr_array(w2); p3, k3 = L.ptr_array(w3)
-        q1, j1 = L.ptr_array(s1); q2, j2 = L.ptr_array(s2); q3, j3 = L.ptr_array(s3)
-        rc = lib.dsmoe_moe_fwd(L.ptr(x), L.ptr(gate_w), L.ptr(gate_bias), p1, p2, p3, q1, q2, q3, d, int(training),
-                               L.ptr(y), L.ptr(idx64), L.ptr(wx), L.ptr(counts), None, L.ptr(ws), ws.numel(),
-                               L.stream_ptr(dev))
-        L.check(rc, "dsmoe_moe_fwd")
-        ctx.meta = meta
-        ctx.ws = ws
-        ctx.save_for_backward(x, gate_w, *weights)
-        ctx.mark_non_differentiable(idx64, wx, counts)
-        return y, idx64, wx, counts
 
-    @staticmethod
-    def backward(ctx, dy, *_unused):
-        E, S, k, I, I_s, rs, training = ctx.meta
-        if not training:
-            raise RuntimeError("dsmoe: forward ran without saving activations for backward")
-        x, gate_w, *weights = ctx.saved_tensors
-        dev = x.device
-        T, D = x.shape
-        d = L.make_dims(T, D, E, k, I, S, I_s, x.dtype, rs)
-        lib = L.load()
-        bws = _ws(lib.dsmoe_moe_bwd_workspace_size(d), dev)
-        dy = _c(dy)
-        dx = torch.empty_like(x)
-        dgw = torch.empty(E, D, dtype=torch.float32, device=dev)
-        dws = [torch.empty_like(w) for w in weights]
-        w1, w2, w3 = weights[:E], weights[E:2 * E], weights[2 * E:3 * E]
-        s1, s2, s3 = weights[3 * E:3 * E + S], weights[3 * E + S:3 * E + 2 * S], weights[3 * E + 2 * S:]
-        g1, g2, g3 = dws[:E], dws[E:2 * E], dws[2 * E:3 * E]
-        h1, h2, h3 = dws[3 * E:3 * E + S], dws[3 * E + S:3 * E + 2 * S], dws[3 * E + 2 * S:]
-        arrs = [L.ptr_array(a) for a in (w1, w2, w3, s1, s2, s3, g1, g2, g3, h1, h2, h3)]
-        rc = lib.dsmoe_moe_bwd(L.ptr(x), L.ptr(gate_w), *[a[0] for a in arrs[:6]], d, L.ptr(dy), L.ptr(ctx.ws),
-                               L.ptr(dx), L.ptr(dgw), *[a[0] for a in arrs[6:]], L.ptr(bws), bws.numel(),
-                               L.stream_ptr(dev))
-        L.check(rc, "dsmoe_moe_bwd")
-        return (None, dx, dgw, None, *dws)
+def _fwd_ws_bytes(T: int, D: int, E: int, S: int, k: int, I: int, I_s: int, dtype, rs: float, training: bool) -> int:
+    d = L.make_dims(T, D, E, k, I, S, I_s, dtype, rs)
+    return max(int(L.load().dsmoe_moe_fwd_workspace_size(d, int(training))), 256)
+
+
+# The layer is registered as two torch.library operators, so torch.compile
+# traces it as one node (shapes from the fake implementations below) instead
+# of breaking the graph at a ctypes call, and autograd (including activation
+# checkpoint recompute) sees an ordinary differentiable op.  The forward
+# returns its workspace (routing, sorted order, pre-activations, expert
+# outputs) as a fifth output; the backward consumes it.
+@torch.library.custom_op("dsmoe::moe_fwd", mutates_args=(), device_types="cuda")
+def moe_fwd_op(x: torch.Tensor, gate_w: torch.Tensor, gate_bias: torch.Tensor, weights: List[torch.Tensor], E: int,
+               S: int, k: int, I: int, I_s: int, route_scale: float,
+               training: bool) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """dsmoe_moe_fwd: returns (y, idx64, weights_x, counts int32, workspace u8)."""
+    dev = x.device
+    T, D = x.shape
+    d = L.make_dims(T, D, E, k, I, S, I_s, x.dtype, route_scale)
+    lib = L.load()
+    ws = _ws(_fwd_ws_bytes(T, D, E, S, k, I, I_s, x.dtype, route_scale, training), dev)
+    y = torch.empty_like(x)
+    idx64 = torch.empty(T, k, dtype=torch.int64, device=dev)
+    wx = torch.empty(T, k, dtype=x.dtype, device=dev)
+    counts = torch.empty(E, dtype=torch.int32, device=dev)
+    w1, w2, w3, s1, s2, s3 = _layer_weights(weights, E, S)
+    p1, k1 = L.ptr_array(w1); p2, k2 = L.ptr_array(w2); p3, k3 = L.ptr_array(w3)
+    q1, j1 = L.ptr_array(s1); q2, j2 = L.ptr_array(s2); q3, j3 = L.ptr_array(s3)
+    rc = lib.dsmoe_moe_fwd(L.ptr(x), L.ptr(gate_w), L.ptr(gate_bias), p1, p2, p3, q1, q2, q3, d, int(training),
+                           L.ptr(y), L.ptr(idx64), L.ptr(wx), L.ptr(counts), None, L.ptr(ws), ws.numel(),
+                           L.stream_ptr(dev))
+    L.check(rc, "dsmoe_moe_fwd")
+    return y, idx64, wx, counts, ws
+
+
+@moe_fwd_op.register_fake
+def _moe_fwd_fake(x, gate_w, gate_bias, weights, E, S, k, I, I_s, route_scale, training):
+    T, D = x.shape
+    nbytes = _fwd_ws_bytes(int(T), int(D), int(E), int(S), int(k), int(I), int(I_s), x.dtype, route_scale, training)
+    return (torch.empty_like(x), x.new_empty((T, k), dtype=torch.int64), x.new_empty((T, k)),
+            x.new_empty((E,), dtype=torch.int32), x.new_empty((nbytes,), dtype=torch.uint8))
+
+
+@torch.library.custom_op("dsmoe::moe_bwd", mutates_args=(), device_types="cuda")
+def moe_bwd_op(x: torch.Tensor, gate_w: torch.Tensor, weights: List[torch.Tensor], dy: torch.Tensor,
+               ws: torch.Tensor, E: int, S: int, k: int, I: int, I_s: int, route_scale: float) -> List[torch.Tensor]:
+    """dsmoe_moe_bwd: returns [dx, dgate_w (fp32), dW for every entry of weights]."""
+    dev = x.device
+    T, D = x.shape
+    d = L.make_dims(T, D, E, k, I, S, I_s, x.dtype, route_scale)
+    lib = L.load()
+    bws = _ws(lib.dsmoe_moe_bwd_workspace_size(d), dev)
+    dx = torch.empty_like(x)
+    dgw = torch.empty(E, D, dtype=torch.float32, device=dev)
+    dws = [torch.empty_like(w) for w in weights]
+    arrs = [L.ptr_array(a) for a in (*_layer_weights(weights, E, S), *_layer_weights(dws, E, S))]
+    rc = lib.dsmoe_moe_bwd(L.ptr(x), L.ptr(gate_w), *[a[0] for a in arrs[:6]], d, L.ptr(dy), L.ptr(ws),
+                           L.ptr(dx), L.ptr(dgw), *[a[0] for a in arrs[6:]], L.ptr(bws), bws.numel(),
+                           L.stream_ptr(dev))
+    L.check(rc, "dsmoe_moe_bwd")
+    return [dx, dgw, *dws]
+
+
+@moe_bwd_op.register_fake
+def _moe_bwd_fake(x, gate_w, weights, dy, ws, E, S, k, I, I_s, route_scale):
+    return [torch.empty_like(x), gate_w.new_empty((E, x.shape[1]), dtype=torch.float32),
+            *[torch.empty_like(w) for w in weights]]
+
+
+def _moe_fwd_setup(ctx, inputs, output):
+    x, gate_w, gate_bias, weights, E, S, k, I, I_s, rs, training = inputs
+    ctx.meta = (E, S, k, I, I_s, rs, training)
+    ctx.save_for_backward(x, gate_w, output[4], *weights)
+
+
+def _moe_fwd_backward(ctx, dy, _didx, _dwx, _dcounts, _dws):
+    E, S, k, I, I_s, rs, training = ctx.meta
+    x, gate_w, ws, *weights = ctx.saved_tensors
+    if dy is None:
+        return None, None, None, [None] * len(weights), None, None, None, None, None, None, None
+    if not training:
+        raise RuntimeError("dsmoe: forward ran without saving activations for backward")
+    g = moe_bwd_op(x, gate_w, list(weights), _c(dy), ws, E, S, k, I, I_s, rs)
+    return g[0], g[1], None, list(g[2:]), None, None, None, None, None, None, None
+
+
+torch.library.register_autograd("dsmoe::moe_fwd", _moe_fwd_backward, setup_context=_moe_fwd_setup)
 
 
 def moe_layer(x: torch.Tensor, gate_w: torch.Tensor, gate_bias: torch.Tensor, w1: Sequence[torch.Tensor],
@@ -208,15 +245,18 @@ def moe_layer(x: torch.Tensor, gate_w: torch.Tensor, gate_bias: torch.Tensor, w1
     E, S = len(w1), len(sw1)
     I = w1[0].shape[0]
     I_s = sw1[0].shape[0] if S else 0
-    if training is None:
-        training = torch.is_grad_enabled() and (x.requires_grad or gate_w.requires_grad or
-                                                any(w.requires_grad for w in (*w1, *w2, *w3, *sw1, *sw2, *sw3)))
-    for w in (*w1, *w2, *w3, *sw1, *sw2, *sw3):
+    weights = [*w1, *w2, *w3, *sw1, *sw2, *sw3]
+    needs_grad = x.requires_grad or gate_w.requires_grad
+    for w in weights:
         if w.dtype != x.dtype:
             raise ValueError(f"dsmoe: expert weight dtype {w.dtype} differs from activation dtype {x.dtype}")
-    meta = (E, S, int(k), int(I), int(I_s), float(route_scale), bool(training))
-    ws = [_c(w) for w in (*w1, *w2, *w3, *sw1, *sw2, *sw3)]
-    return _MoELayerFn.apply(meta, _c(x), _c(gate_w), _c(gate_bias), *ws)
+        needs_grad = needs_grad or w.requires_grad
+    if training is None:
+        training = torch.is_grad_enabled() and needs_grad
+    ws = [_c(w) for w in weights]
+    y, idx64, wx, counts, _ = moe_fwd_op(_c(x), _c(gate_w), _c(gate_bias), ws, E, S, int(k), int(I), int(I_s),
+                                         float(route_scale), bool(training))
+    return y, idx64, wx, counts
 
 
 # ---------------------------------------------------------------------------- operator seam

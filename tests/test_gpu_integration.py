@@ -1,0 +1,87 @@
+"""The drop-in layer inside the reference's training step
+(training/pretrain.py:172-175,212-213; models/transformer.py:80-85):
+
+* bf16 autocast over fp32 parameters gives exactly the explicit bf16 layer
+  (bf16-rounded weights and activations) with the output, ``_last_weights``
+  and every gradient back in fp32;
+* activation checkpointing (``use_reentrant=False``) recomputes the forward
+  with identical routing, so outputs and gradients are bit-identical to the
+  plain run;
+* ``torch.compile(fullgraph=True)`` traces the layer as one operator (no
+  graph break) and gives the eager results bit for bit.
+"""
+import pytest
+import torch
+
+from tests import _cases as CS
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+CASE32 = CS.Case("integ_fp32", 384, 256, 8, 128, 2, 1, 128, torch.float32, "normal")
+CASE16 = CS.Case("integ_bf16", 384, 256, 8, 128, 2, 1, 128, torch.bfloat16, "normal")
+
+
+def _grads(m):
+    return {n: p.grad.detach().clone() for n, p in m.named_parameters()}
+
+
+def _step(m, x, dy, fn=None):
+    xin = x.detach().clone().to(DEV).requires_grad_(True)
+    y = (m if fn is None else fn)(xin)
+    (y.float() * dy.to(DEV).float()).sum().backward()
+    torch.cuda.synchronize()
+    return y.detach(), xin.grad.detach(), _grads(m)
+
+
+def test_bf16_autocast_over_fp32_parameters():
+    from dsmoe import DeepSeekMoE
+    x, p, dy = CS.make_inputs(CASE32, with_dy=True)
+    m32 = CS.load_module(CASE32, p, DEV, DeepSeekMoE)
+    xin = x.clone().to(DEV).requires_grad_(True)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y = m32(xin)
+    assert y.dtype == torch.float32 and m32._last_weights.dtype == torch.float32
+    (y * dy.to(DEV)).sum().backward()
+    torch.cuda.synchronize()
+    # the explicit bf16 layer on the same (bf16-rounded) values
+    m16 = CS.load_module(CASE16, p, DEV, DeepSeekMoE)
+    y16, dx16, g16 = _step(m16, x.to(torch.bfloat16), dy)
+    assert torch.equal(y, y16.float())
+    assert torch.equal(m32._last_indices, m16._last_indices)
+    assert torch.equal(m32._last_weights, m16._last_weights.float())
+    assert xin.grad.dtype == torch.float32 and torch.equal(xin.grad, dx16.float())
+    for n, prm in m32.named_parameters():
+        assert prm.grad.dtype == torch.float32, n
+        assert torch.equal(prm.grad, g16[n].float()), n
+
+
+def test_activation_checkpoint_recompute_is_identical():
+    from torch.utils.checkpoint import checkpoint
+    from dsmoe import DeepSeekMoE
+    x, p, dy = CS.make_inputs(CASE16, with_dy=True)
+    m = CS.load_module(CASE16, p, DEV, DeepSeekMoE)
+    y0, dx0, g0 = _step(m, x, dy)
+    idx0 = m._last_indices.clone()
+    m.zero_grad(set_to_none=True)
+    y1, dx1, g1 = _step(m, x, dy, fn=lambda t: checkpoint(m, t, use_reentrant=False))
+    assert torch.equal(y0, y1) and torch.equal(dx0, dx1)
+    assert torch.equal(idx0, m._last_indices)
+    for n in g0:
+        assert torch.equal(g0[n], g1[n]), n
+
+
+def test_torch_compile_traces_the_layer_as_one_op():
+    import torch._dynamo
+    from dsmoe import DeepSeekMoE
+    x, p, dy = CS.make_inputs(CASE16, with_dy=True)
+    m = CS.load_module(CASE16, p, DEV, DeepSeekMoE)
+    y0, dx0, g0 = _step(m, x, dy)
+    m.zero_grad(set_to_none=True)
+    torch._dynamo.reset()
+    cm = torch.compile(m, backend="aot_eager", fullgraph=True)
+    y1, dx1, g1 = _step(m, x, dy, fn=cm)
+    assert torch.equal(y0, y1) and torch.equal(dx0, dx1)
+    for n in g0:
+        assert torch.equal(g0[n], g1[n]), n
+    # the side state is set by the compiled forward too
+    assert m._last_indices.shape == (CASE16.T, CASE16.k) and m._last_weights.dtype == torch.bfloat16

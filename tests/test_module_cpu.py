@@ -109,3 +109,66 @@ def test_enforce_triton_env_var_compat(monkeypatch, env, cfg, expect, warned):
 
 def test_next_pow2():
     assert [next_pow2(n) for n in (0, 1, 2, 3, 64, 65, 384)] == [1, 1, 2, 4, 64, 128, 512]
+
+
+def test_planted_routing_replaces_the_forward_histogram(small_cfg):
+    """A forward leaves the kernel histogram beside _last_indices; planting new
+    indices (as the reference's tests do) must switch the counts to them."""
+    moe = DeepSeekMoE(small_cfg)
+    moe._last_indices = torch.zeros(8, 2, dtype=torch.long)
+    moe._last_weights = torch.ones(8, 2) / 2
+    moe._last_counts = torch.tensor([16, 0, 0, 0], dtype=torch.int32)
+    moe._counts_of = moe._last_indices
+    assert torch.equal(moe._counts(), torch.tensor([16, 0, 0, 0], dtype=torch.int32))
+    moe._last_indices = torch.full((8, 2), 3, dtype=torch.long)
+    assert torch.equal(moe._counts(), torch.tensor([0, 0, 0, 16]))
+
+
+def test_checkpoint_manager_roundtrip(small_cfg, tmp_path):
+    """utils/checkpoint.py:17-55,78-88: the state_dict is saved with
+    safetensors after the manager's shared-storage de-duplication and loaded
+    back with strict key checking.  Every key must survive the de-duplication
+    (no two entries share storage) and load into a fresh layer unchanged."""
+    from safetensors.torch import load_file, save_file
+    src = DeepSeekMoE(small_cfg)
+    with torch.no_grad():
+        src.gate.bias.copy_(torch.tensor([0.5, -0.25, 0.0, 1.0]))
+    state = src.state_dict()
+    seen, kept = set(), {}
+    for k, v in state.items():          # the manager's de-duplication by data_ptr
+        if v.data_ptr() in seen:
+            continue
+        seen.add(v.data_ptr())
+        kept[k] = v.contiguous()
+    assert set(kept) == set(state)
+    path = tmp_path / "model_step_1.safetensors"
+    save_file(kept, str(path))
+    dst = DeepSeekMoE(small_cfg)
+    missing, unexpected = dst.load_state_dict(load_file(str(path)), strict=False)
+    assert not missing and not unexpected
+    for k, v in dst.state_dict().items():
+        assert torch.equal(v, state[k]), k
+    assert dst.gate.bias.dtype == torch.float32
+
+
+def test_layer_operator_shapes_without_a_gpu():
+    """The layer's torch.library operators (what torch.compile traces) give
+    the real outputs' shapes and dtypes from their fake implementations."""
+    import dsmoe.ops  # noqa: F401  (registers dsmoe::moe_fwd / dsmoe::moe_bwd)
+    T, D, E, S, k, I, I_s = 96, 128, 8, 1, 2, 64, 96
+    m = dict(device="meta", dtype=torch.bfloat16)
+    x = torch.empty(T, D, **m)
+    gw, gb = torch.empty(E, D, device="meta"), torch.empty(E, device="meta")
+    ws = ([torch.empty(I, D, **m) for _ in range(E)] + [torch.empty(D, I, **m) for _ in range(E)] +
+          [torch.empty(I, D, **m) for _ in range(E)] +
+          [torch.empty(I_s, D, **m), torch.empty(D, I_s, **m), torch.empty(I_s, D, **m)])
+    y, idx, wx, counts, work = torch.ops.dsmoe.moe_fwd(x, gw, gb, ws, E, S, k, I, I_s, 1.0, True)
+    assert y.shape == (T, D) and y.dtype == torch.bfloat16
+    assert idx.shape == (T, k) and idx.dtype == torch.int64
+    assert wx.shape == (T, k) and wx.dtype == torch.bfloat16
+    assert counts.shape == (E,) and counts.dtype == torch.int32
+    assert work.dtype == torch.uint8 and work.numel() >= 256
+    g = torch.ops.dsmoe.moe_bwd(x, gw, ws, y, work, E, S, k, I, I_s, 1.0)
+    assert len(g) == 2 + len(ws)
+    assert g[0].shape == (T, D) and g[1].shape == (E, D) and g[1].dtype == torch.float32
+    assert all(a.shape == w.shape and a.dtype == w.dtype for a, w in zip(g[2:], ws))
