@@ -1,5 +1,6 @@
 // extern "C" entry points of libdsmoe.so (declared in include/dsmoe.h).
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <initializer_list>
 #include <mutex>
@@ -125,7 +126,7 @@ static FwdLayout fwd_layout(const dsmoe_dims& d, int training, void* base) {
   L.sorted_token = c.take<int32_t>(N);
   L.slot_pos = c.take<int32_t>(N);
   L.sorted_w = training ? c.take<float>(N) : nullptr;
-  permute_scratch_carve(c, d, TILE_M, &L.ps);
+  permute_scratch_carve(c, d, SK_BM, &L.ps);  // the smallest schedule tile height
   L.h = c.take<char>((size_t)N * d.I * es);
   L.g = training ? c.take<char>((size_t)N * d.I * es) : nullptr;
   L.u = training ? c.take<char>((size_t)N * d.I * es) : nullptr;
@@ -333,6 +334,30 @@ size_t dsmoe_moe_fwd_workspace_size(const dsmoe_dims* dims, int training) {
   return fwd_layout(*dims, training, nullptr).total;
 }
 
+// Few-row (decode) GEMM path: tokens per call up to which it is taken, and
+// an environment switch (DSMOE_DECODE_GEMM=0) that keeps the quad-wave path.
+constexpr int SK_MAX_T = SK_BM;
+static bool decode_gemm_on() {
+  static bool on = [] {
+    const char* s = std::getenv("DSMOE_DECODE_GEMM");
+    return !(s && std::atoi(s) == 0);
+  }();
+  return on;
+}
+
+// Routed problem gr on the few-row kernel, with the dense shared problem gd
+// in the same launch when that kernel takes it too (else on the general path).
+static int launch_sk_pair(const GemmDesc& gr, const GemmDesc& gd, bool has_gd, int epi, int dtype, bool mf,
+                          hipStream_t st) {
+  if (!has_gd) return launch_gemm_sk(gr, epi, nullptr, st);
+  GemmDesc d1 = gd;
+  d1.bm = SK_BM;
+  if (gemm_sk_ok(d1)) return launch_gemm_sk_pair(gr, d1, epi, nullptr, st);
+  const int rc = launch_gemm_sk(gr, epi, nullptr, st);
+  if (rc) return rc;
+  return launch_grouped_gemm(gd, epi, dtype, nullptr, gemm_mfma_eligible(gd, dtype, mf), st);
+}
+
 int dsmoe_moe_fwd(const void* x, const float* gate_w, const float* gate_bias, const void* const* w1,
                   const void* const* w2, const void* const* w3, const void* const* sw1, const void* const* sw2,
                   const void* const* sw3, const dsmoe_dims* dims, int training, void* y, int64_t* idx64,
@@ -372,7 +397,16 @@ int dsmoe_moe_fwd(const void* x, const float* gate_w, const float* gate_bias, co
   g2.A = L.h; g2.lda = d.I; g2.a_rows = N; g2.B0 = L.ptrs + 2 * d.E; g2.ldb = d.I; g2.kseg = d.I;
   g2.N = d.D; g2.K = d.I; g2.C = L.o_slots; g2.ldc = d.D; g2.c_map = L.sorted_slot;
   const bool mfr = gemm_mfma_eligible(g1, d.dtype, mf) && gemm_mfma_eligible(g2, d.dtype, mf);
-  const int bm = gemm_tile_m(mfr);
+  // Decode shapes (at most SK_MAX_T tokens, inference): every routed and
+  // shared row tile fits the few-row kernel, which streams the weights once.
+  bool sk = false;
+  if (!training && d.dtype == DSMOE_BF16 && d.T <= SK_MAX_T && mf && decode_gemm_on()) {
+    GemmDesc t1 = g1, t2 = g2;
+    t1.bm = t2.bm = SK_BM;
+    t1.Gs = t1.Us = nullptr;
+    sk = gemm_sk_ok(t1) && gemm_sk_ok(t2);
+  }
+  const int bm = sk ? SK_BM : gemm_tile_m(mfr);
   // (b) permute (counts come from the scan: exact bincount, no atomics)
   tm.begin(ST_PERMUTE);
   rc = launch_permute(L.idx, d, bm, L.ps, L.offsets, L.sorted_slot, L.sorted_token, L.slot_pos, counts,
@@ -407,15 +441,18 @@ int dsmoe_moe_fwd(const void* x, const float* gate_w, const float* gate_bias, co
     s2.N = d.D; s2.K = d.S * d.I_s; s2.C = L.shared_out; s2.ldc = d.D;
     s2.bm = gemm_tile_m(gemm_mfma_eligible(s2, d.dtype, mf));
   }
+  if (sk) g1.Gs = g1.Us = s1.Gs = s1.Us = nullptr;  // inference: no pre-activation saves
   tm.begin(ST_GEMM1);
-  rc = d.S ? launch_grouped_gemm_pair(g1, s1, EPI_SWIGLU, d.dtype, nullptr, mfr, mf, st)
-           : launch_grouped_gemm(g1, EPI_SWIGLU, d.dtype, nullptr, mfr, st);
+  rc = sk ? launch_sk_pair(g1, s1, d.S > 0, EPI_SWIGLU, d.dtype, mf, st)
+          : d.S ? launch_grouped_gemm_pair(g1, s1, EPI_SWIGLU, d.dtype, nullptr, mfr, mf, st)
+                : launch_grouped_gemm(g1, EPI_SWIGLU, d.dtype, nullptr, mfr, st);
   tm.end();
   if (rc) return rc;
   // down projections: routed rows written back in slot order (t*k + j)
   tm.begin(ST_GEMM2);
-  rc = d.S ? launch_grouped_gemm_pair(g2, s2, EPI_STORE, d.dtype, nullptr, mfr, mf, st)
-           : launch_grouped_gemm(g2, EPI_STORE, d.dtype, nullptr, mfr, st);
+  rc = sk ? launch_sk_pair(g2, s2, d.S > 0, EPI_STORE, d.dtype, mf, st)
+          : d.S ? launch_grouped_gemm_pair(g2, s2, EPI_STORE, d.dtype, nullptr, mfr, mf, st)
+                : launch_grouped_gemm(g2, EPI_STORE, d.dtype, nullptr, mfr, st);
   tm.end();
   if (rc) return rc;
   // (d) combine

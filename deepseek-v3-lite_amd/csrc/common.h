@@ -164,6 +164,12 @@ int launch_gemm_qw(const GemmDesc& g, int epi, const float* row_scale, hipStream
 int launch_gemm_qw_pair(const GemmDesc& gr, const GemmDesc& gd, int epi, const float* row_scale, hipStream_t st);
 int launch_grouped_gemm(const GemmDesc& g, int epi, int dtype, const float* row_scale, bool allow_mfma,
                         hipStream_t st);
+// Few-row grouped GEMM (decode): row tiles of SK_BM rows, weights streamed
+// once.  The routed schedule must be built with bm = SK_BM; no G/U saves.
+constexpr int SK_BM = 64;
+bool gemm_sk_ok(const GemmDesc& g);
+int launch_gemm_sk(const GemmDesc& g, int epi, const float* row_scale, hipStream_t st);
+int launch_gemm_sk_pair(const GemmDesc& gr, const GemmDesc& gd, int epi, const float* row_scale, hipStream_t st);
 // gr (routed or dense) then the dense gd (same epilogue): one quad-wave launch
 // when that kernel takes both, else two launches.  row_scale applies to gr.
 int launch_grouped_gemm_pair(const GemmDesc& gr, const GemmDesc& gd, int epi, int dtype, const float* row_scale,

@@ -169,6 +169,11 @@ def _run_layer(case, x, p):
     (CS.C3.with_tokens(1024), None),
     (CS.C3, 192),
     (CS.C3_DECODE, None),
+    # decode-size calls (few-row GEMM path): one token; a skewed routing that
+    # sends every token to two experts (37-row tiles); no shared experts
+    (CS.Case("dec_t1", 1, 2048, 64, 1408, 6, 2, 1408, torch.bfloat16), None),
+    (CS.Case("dec_t37_skew", 37, 512, 8, 256, 2, 1, 384, torch.bfloat16, "skew"), None),
+    (CS.Case("dec_t64_noshared", 64, 1024, 16, 512, 4, 0, 0, torch.bfloat16, "normal"), None),
 ], ids=lambda v: getattr(v, "name", str(v)))
 def test_layer_forward_vs_oracle(case, sample):
     """Full-size configs are checked on a seeded token sample: each token's
