@@ -91,6 +91,7 @@ static int validate(const dsmoe_dims* d, bool need_experts) {
 // ---------------------------------------------------------------- layer workspace layout
 struct FwdLayout {
   const void** ptrs;  // [w1 E][w3 E][w2 E][sw1 S][sw3 S][sw2 S]
+  float* gate_part;   // partial logits of a K-split gate, or nullptr
   int32_t* idx;
   float* w;
   float* sel;
@@ -126,6 +127,7 @@ static FwdLayout fwd_layout(const dsmoe_dims& d, int training, void* base) {
   L.sorted_token = c.take<int32_t>(N);
   L.slot_pos = c.take<int32_t>(N);
   L.sorted_w = training ? c.take<float>(N) : nullptr;
+  L.gate_part = gate_part_floats(d) ? c.take<float>(gate_part_floats(d)) : nullptr;
   permute_scratch_carve(c, d, SK_BM, &L.ps);  // the smallest schedule tile height
   L.h = c.take<char>((size_t)N * d.I * es);
   L.g = training ? c.take<char>((size_t)N * d.I * es) : nullptr;
@@ -385,7 +387,7 @@ int dsmoe_moe_fwd(const void* x, const float* gate_w, const float* gate_bias, co
   // (a) gate
   GateOut go{logits, L.idx, idx64, L.w, weights_x, L.sel, nullptr};
   tm.begin(ST_GATE);
-  rc = launch_gate(x, nullptr, gate_w, gate_bias, d, go, st);
+  rc = launch_gate(x, nullptr, gate_w, gate_bias, d, go, st, L.gate_part);
   tm.end();
   if (rc) return rc;
   // GEMM descriptors; the routed schedule height follows the kernel choice

@@ -143,8 +143,12 @@ struct PermuteScratch {
 };
 
 // ---------------------------------------------------------------- launchers
+// part (optional): workspace of gate_part_floats(d) floats for a K-split gate
+// (partial logits, then a routing kernel); nullptr keeps one fused launch.
 int launch_gate(const void* x, const float* logits_in, const float* gw, const float* bias, const dsmoe_dims& d,
-                const GateOut& out, hipStream_t st);
+                const GateOut& out, hipStream_t st, float* part = nullptr);
+int gate_k_splits(const dsmoe_dims& d);
+size_t gate_part_floats(const dsmoe_dims& d);
 void launch_fill_i32(int32_t* p, int n, int32_t v, hipStream_t st);
 int64_t sched_bound(int64_t rows, int groups, int bm);
 size_t permute_scratch_carve(Carver& c, const dsmoe_dims& d, int bm, PermuteScratch* out);

@@ -13,6 +13,8 @@
 // Routing.  One wave per token, one lane per expert (E <= 64; E <= 256 with
 // several experts per lane): sigmoid in double rounded once, + bias, then k
 // rounds of a wave-wide arg-max ordered by (value desc, expert id asc).
+#include <cstdlib>
+
 #include "common.h"
 
 namespace dsmoe {
@@ -33,101 +35,117 @@ constexpr int MAX_EPL = 4;         // experts per lane in routing (E <= 256)
 
 // ------------------------------------------------------------------ routing
 // Routes tokens [t0, t0 + ntok) whose fp32 logits sit in LDS rows lg[t*ldl].
-// Wave w takes batches of route_ntok(EPL) consecutive tokens (w, w + nw, ... in
-// batch units) and routes the tokens of a batch together, so the LDS round
-// trips of its tokens overlap.  Lane l holds expert l (E <= 64) or experts
-// l, l+64, ... (E <= 256).
+// Wave w routes tokens in batches of route_ntok(EPL): w, w + nw, ... in batch
+// units.  Lane l holds expert l (E <= 64) or
+// experts l, l + 64, ... (E <= 256) in registers.
 //
-// Selection by rank: every expert's biased score goes to a per-wave LDS row;
-// each lane counts the experts that beat its own under the order (value
-// desc, id asc).  Rank < k selects the expert and is its output slot j, so
-// the result equals k rounds of arg-max with that tie rule.  The renormalising
-// sum then runs over slots j = 0..k-1 in order, as in the oracle.
-// wscr: per-wave LDS scratch of route_ntok(EPL) * route_row(EPL) floats.
-//
-// Lanes of one wave exchange values through LDS: a wave's LDS operations
-// complete in issue order, so waiting for this wave's LDS counter (and a
-// compiler barrier) is enough.  A memory fence would also wait for the
-// token's global output stores.
-// Tokens a wave routes together, and scratch floats per token (biased
-// scores of the lane's experts, then the selected scores by slot).
+// Selection: k rounds of a wave arg-max over the biased scores under the
+// order (value desc, id asc): a DPP max gives the round's value m, a ballot of
+// the lanes holding m and its lowest set bit give the lowest expert id with
+// that value, which takes slot j of the round and drops out.  This is the
+// oracle's k rounds of arg-max with the same tie rule.  The renormalising sum
+// runs over slots j = 0..k-1 in order, as in the oracle.
 constexpr int route_ntok(int epl) { return epl == 1 ? 4 : 2; }
 constexpr int route_row(int epl) { return 64 * epl + MAX_TOPK; }
 
-__device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+// Maximum over the 64 lanes (every lane gets it).  Row (16-lane) shifts, then
+// the row broadcasts of lanes 15 and 31, leave the maximum in lane 63.
+__device__ __forceinline__ float wave_max_f32(float v) {
+  const int b = __float_as_int(v);
+  float t;
+  t = __int_as_float(__builtin_amdgcn_update_dpp(b, __float_as_int(v), 0x111, 0xf, 0xf, false));  // row_shr:1
+  v = fmaxf(v, t);
+  t = __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x112, 0xf, 0xf, false));
+  v = fmaxf(v, t);
+  t = __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x114, 0xf, 0xf, false));
+  v = fmaxf(v, t);
+  t = __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x118, 0xf, 0xf, false));
+  v = fmaxf(v, t);
+  t = __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x142, 0xa, 0xf, false));  // row_bcast:15
+  v = fmaxf(v, t);
+  t = __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x143, 0xc, 0xf, false));  // row_bcast:31
+  v = fmaxf(v, t);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
 
 template <int EPL>  // experts per lane: 1 for E <= 64, MAX_EPL otherwise
 __device__ __forceinline__ void route_tokens_t(const float* lg, int ldl, int ntok, int t0, const float* bias_s, int E,
                                                int k, float route_scale, int xdtype, const GateOut& out, int* hist,
-                                               float* wscr_all) {
-  constexpr int NT = route_ntok(EPL), ROUTE_ROW = route_row(EPL);
+                                               float* /*unused scratch*/) {
+  // NB tokens per wave are routed side by side: their sigmoid, max and
+  // ballot chains are independent, so their latencies overlap.
+  constexpr int NB = route_ntok(EPL);
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int nw = blockDim.x >> 6;
-  float* wscr = wscr_all + wave * NT * ROUTE_ROW;   // token t: biased scores [E], then selected scores by slot [k]
-  const int e4 = (E + 3) & ~3;
-  for (int tb = wave * NT; tb < ntok; tb += nw * NT) {
-    float sv[NT][EPL], bv[NT][EPL];
+  for (int tb = wave * NB; tb < ntok; tb += nw * NB) {
+    float sv[NB][EPL], bv[NB][EPL];
+    int slot[NB][EPL];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const bool tok = tb + t < ntok;
-      const float* row = lg + (tb + t) * ldl;
+    for (int b = 0; b < NB; ++b)
 #pragma unroll
       for (int q = 0; q < EPL; ++q) {
         const int e = lane + 64 * q;
-        sv[t][q] = 0.0f;
-        bv[t][q] = -INFINITY;
-        if (tok && e < E) {
-          sv[t][q] = route_sigmoid(row[e]);
-          bv[t][q] = sv[t][q] + bias_s[e];
+        sv[b][q] = 0.0f;
+        bv[b][q] = -INFINITY;
+        slot[b][q] = -1;
+        if (tb + b < ntok && e < E) {
+          sv[b][q] = route_sigmoid(lg[(tb + b) * ldl + e]);
+          bv[b][q] = sv[b][q] + bias_s[e];
         }
-        if (e < e4) wscr[t * ROUTE_ROW + e] = bv[t][q];
       }
-    }
-    wave_lds_sync();
-    int rank[NT][EPL];
+    float ssum[NB];
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
+    for (int b = 0; b < NB; ++b) ssum[b] = 0.0f;
+    for (int j = 0; j < k; ++j) {
+      float m[NB];
 #pragma unroll
-      for (int q = 0; q < EPL; ++q) rank[t][q] = 0;
-    for (int c = 0; c < e4; c += 4) {
+      for (int b = 0; b < NB; ++b) {
+        float lm = bv[b][0];
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const float4 v = *reinterpret_cast<const float4*>(wscr + t * ROUTE_ROW + c);
-        const float vv[4] = {v.x, v.y, v.z, v.w};
+        for (int q = 1; q < EPL; ++q) lm = fmaxf(lm, bv[b][q]);
+        m[b] = wave_max_f32(lm);
+      }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+      for (int b = 0; b < NB; ++b) {
+        int win = -1;
+#pragma unroll
+        for (int q = 0; q < EPL; ++q) {
+          const uint64_t bl = __ballot(slot[b][q] < 0 && lane + 64 * q < E && bv[b][q] == m[b]);
+          if (win < 0 && bl) win = __ffsll((unsigned long long)bl) - 1 + 64 * q;
+        }
+        if (win < 0) {
+          // only NaN scores left: the lowest unselected expert id
 #pragma unroll
           for (int q = 0; q < EPL; ++q) {
-            const int e = lane + 64 * q;
-            // branch-free: (value desc, id asc) order
-            rank[t][q] += (int)(vv[i] > bv[t][q]) | ((int)(vv[i] == bv[t][q]) & (int)(c + i < e));
+            const uint64_t bl = __ballot(slot[b][q] < 0 && lane + 64 * q < E);
+            if (win < 0 && bl) win = __ffsll((unsigned long long)bl) - 1 + 64 * q;
           }
         }
+        win = __builtin_amdgcn_readfirstlane(win);
+        const int wl = win & 63, wq = win >> 6;
+#pragma unroll
+        for (int q = 0; q < EPL; ++q)
+          if (q == wq) {
+            ssum[b] += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sv[b][q]), wl));
+            if (lane == wl) {
+              slot[b][q] = j;
+              bv[b][q] = -INFINITY;
+            }
+          }
       }
     }
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
+    for (int b = 0; b < NB; ++b) {
+      if (tb + b >= ntok) break;   // padding tokens of the last batch write nothing
+      const float den = ssum[b] < 1e-10f ? 1e-10f : ssum[b];
+      const int64_t o = (int64_t)(t0 + tb + b) * k;
 #pragma unroll
       for (int q = 0; q < EPL; ++q) {
         const int e = lane + 64 * q;
-        if (tb + t < ntok && e < E && rank[t][q] < k) wscr[t * ROUTE_ROW + 64 * EPL + rank[t][q]] = sv[t][q];
-      }
-    wave_lds_sync();
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      if (tb + t >= ntok) break;
-      const float* ws = wscr + t * ROUTE_ROW + 64 * EPL;
-      float ssum = 0.0f;
-      for (int j = 0; j < k; ++j) ssum += ws[j];
-      const float den = ssum < 1e-10f ? 1e-10f : ssum;
-      const int64_t o = (int64_t)(t0 + tb + t) * k;
-#pragma unroll
-      for (int q = 0; q < EPL; ++q) {
-        const int e = lane + 64 * q;
-        if (e < E && rank[t][q] < k) {
-          const int j = rank[t][q];
-          const float w = sv[t][q] / den * route_scale;
+        if (slot[b][q] >= 0) {
+          const int j = slot[b][q];
+          const float w = sv[b][q] / den * route_scale;
           out.idx[o + j] = e;
           if (out.idx64) out.idx64[o + j] = e;
           out.weights[o + j] = w;
@@ -137,13 +155,11 @@ __device__ __forceinline__ void route_tokens_t(const float* lg, int ldl, int nto
             else
               static_cast<float*>(out.weights_x)[o + j] = w;
           }
-          if (out.sel_scores) out.sel_scores[o + j] = sv[t][q];
+          if (out.sel_scores) out.sel_scores[o + j] = sv[b][q];
           if (hist) atomicAdd(&hist[e], 1);
         }
       }
     }
-    // the next batch reuses the scratch: make sure every lane finished reading it
-    wave_lds_sync();
   }
 }
 
@@ -197,7 +213,8 @@ template <int NT>
 __global__ __launch_bounds__(gm_waves(NT) * 64) void gate_mfma_kernel(const bf16_t* __restrict__ x,
                                                                  const float* __restrict__ gw,
                                                                  const float* __restrict__ bias, int T, int D, int E,
-                                                                 int k, float route_scale, GateOut out) {
+                                                                 int k, float route_scale, GateOut out,
+                                                                 float* __restrict__ part_out, int ks) {
   constexpr int EP = NT * 32;
   constexpr int LDP = EP + 1;
   extern __shared__ float gsm[];
@@ -214,13 +231,17 @@ __global__ __launch_bounds__(gm_waves(NT) * 64) void gate_mfma_kernel(const bf16
   constexpr int NTW = (NT + TSTEP - 1) / TSTEP;       // expert tiles per wave (upper bound)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int quarter = wave & 3, tfirst = wave >> 2;
-  const int t0 = blockIdx.x * GM_TOK;
+  // K split (part_out != nullptr): block b takes token tile b / ks and the
+  // K range of split b % ks, and writes partial logits instead of routing.
+  const int split = part_out ? (int)(blockIdx.x % ks) : 0;
+  const int t0 = (part_out ? (int)(blockIdx.x / ks) : (int)blockIdx.x) * GM_TOK;
   for (int e = tid; e < E; e += NTH) {
     bias_s[e] = bias[e];
     hist[e] = 0;
   }
-  const int kq = D / 4;
-  const int kbeg = quarter * kq;
+  const int dk = part_out ? D / ks : D;
+  const int kq = dk / 4;
+  const int kbeg = split * dk + quarter * kq;
   const int m = lane & 31;
   const int row = min(t0 + m, T - 1);
   const bf16_t* xr = x + (int64_t)row * D + (lane >> 5) * 8;
@@ -298,8 +319,13 @@ __global__ __launch_bounds__(gm_waves(NT) * 64) void gate_mfma_kernel(const bf16
     const int o = t * LDP + e;
     const float v = ((part[o] + part[GM_TOK * LDP + o]) + part[2 * GM_TOK * LDP + o]) + part[3 * GM_TOK * LDP + o];
     part[o] = v;
-    if (out.logits && t < ntok) out.logits[(int64_t)(t0 + t) * E + e] = v;
+    if (part_out) {
+      if (t < ntok) part_out[((int64_t)split * T + t0 + t) * E + e] = v;
+    } else if (out.logits && t < ntok) {
+      out.logits[(int64_t)(t0 + t) * E + e] = v;
+    }
   }
+  if (part_out) return;
   __syncthreads();
   route_tokens(part, LDP, ntok, t0, bias_s, E, k, route_scale, DSMOE_BF16, out, out.counts ? hist : nullptr, rscr);
   __syncthreads();
@@ -393,6 +419,38 @@ __global__ void fill_i32_kernel(int32_t* p, int n, int32_t v) {
   if (i < n) p[i] = v;
 }
 
+// Routing after a K-split gate: logits = sum of the ks partial logits in
+// split order (0, 1, ...), optionally written out, then route_tokens.
+constexpr int RP_TOK = 16;       // tokens per block (four per wave)
+__global__ __launch_bounds__(256) void route_partials_kernel(const float* __restrict__ part, int ks,
+                                                             const float* __restrict__ bias, int T, int E, int k,
+                                                             float route_scale, int xdtype, GateOut out) {
+  extern __shared__ float rsm[];
+  const int ldl = E + 1;
+  float* lg = rsm;                               // [RP_TOK][E + 1]
+  float* bias_s = lg + RP_TOK * ldl;             // [E]
+  int* hist = reinterpret_cast<int*>(bias_s + E);
+  const int tid = threadIdx.x;
+  const int t0 = blockIdx.x * RP_TOK;
+  const int ntok = min(RP_TOK, T - t0);
+  for (int e = tid; e < E; e += blockDim.x) {
+    bias_s[e] = bias[e];
+    hist[e] = 0;
+  }
+  for (int i = tid; i < ntok * E; i += blockDim.x) {
+    const int t = i / E, e = i - t * E;
+    const float* p = part + (int64_t)(t0 + t) * E + e;
+    float v = p[0];
+    for (int sp = 1; sp < ks; ++sp) v += p[(int64_t)sp * T * E];
+    lg[t * ldl + e] = v;
+    if (out.logits) out.logits[(int64_t)(t0 + t) * E + e] = v;
+  }
+  __syncthreads();
+  route_tokens(lg, ldl, ntok, t0, bias_s, E, k, route_scale, xdtype, out, out.counts ? hist : nullptr, nullptr);
+  __syncthreads();
+  flush_hist(hist, E, out.counts);
+}
+
 static int set_lds(const void* kern, size_t lds) {
   if (lds > 64 * 1024 &&
       hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
@@ -418,19 +476,43 @@ static int launch_gate_t(const void* x, const float* logits_in, const float* gw,
 
 template <int NT>
 static int launch_gate_mfma(const void* x, const float* gw, const float* bias, const dsmoe_dims& d, const GateOut& out,
-                            hipStream_t st) {
+                            float* part, int ks, hipStream_t st) {
   const size_t lds = sizeof(float) * (4 * GM_TOK * (NT * 32 + 1) + d.E) + sizeof(int) * ((d.E + 3) & ~3) +
                      sizeof(float) * ROUTE_SCR;
   auto kern = gate_mfma_kernel<NT>;
   int rc = set_lds((const void*)kern, lds);
   if (rc) return rc;
-  hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(d.T, GM_TOK)), dim3(gm_waves(NT) * 64), lds, st,
-                     static_cast<const bf16_t*>(x), gw, bias, d.T, d.D, d.E, d.k, d.route_scale, out);
-  return check_launch("gate_mfma");
+  const int64_t blocks = cdiv(d.T, GM_TOK) * (part ? ks : 1);
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(gm_waves(NT) * 64), lds, st, static_cast<const bf16_t*>(x), gw,
+                     bias, d.T, d.D, d.E, d.k, d.route_scale, out, part, ks);
+  rc = check_launch("gate_mfma");
+  if (rc || !part) return rc;
+  const size_t rlds = sizeof(float) * (RP_TOK * (d.E + 1) + d.E) + sizeof(int) * d.E;
+  hipLaunchKernelGGL(route_partials_kernel, dim3((unsigned)cdiv(d.T, RP_TOK)), dim3(256), rlds, st, part, ks, bias,
+                     d.T, d.E, d.k, d.route_scale, (int)DSMOE_BF16, out);
+  return check_launch("route_partials");
+}
+
+int gate_k_splits(const dsmoe_dims& d) {
+  static const int forced = [] {
+    const char* s = std::getenv("DSMOE_GATE_KS");
+    return s ? std::atoi(s) : 0;
+  }();
+  const int64_t tiles = cdiv(d.T, GM_TOK);
+  int ks = forced > 0 ? forced : 1;
+  if (forced <= 0)
+    while (ks < 16 && tiles * ks * 2 <= 256) ks *= 2;   // fill the 256 CUs when there are few token tiles
+  while (ks > 1 && d.D % (64 * ks) != 0) ks >>= 1;
+  return ks;
+}
+
+size_t gate_part_floats(const dsmoe_dims& d) {
+  const int ks = gate_k_splits(d);
+  return ks > 1 ? (size_t)ks * d.T * d.E : 0;
 }
 
 int launch_gate(const void* x, const float* logits_in, const float* gw, const float* bias, const dsmoe_dims& d,
-                const GateOut& out, hipStream_t st) {
+                const GateOut& out, hipStream_t st, float* part) {
   if (out.counts) {
     hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)cdiv(d.E, 256)), dim3(256), 0, st, out.counts, d.E, 0);
   }
@@ -440,12 +522,14 @@ int launch_gate(const void* x, const float* logits_in, const float* gw, const fl
                     (reinterpret_cast<uintptr_t>(gw) & 15) == 0;
   if (mfma) {
     const int nt = (int)cdiv(d.E, 32);
+    const int ks = part ? gate_k_splits(d) : 1;
+    float* pp = ks > 1 ? part : nullptr;
     switch (nt) {
-      case 1: return launch_gate_mfma<1>(x, gw, bias, d, out, st);
-      case 2: return launch_gate_mfma<2>(x, gw, bias, d, out, st);
-      case 3: return launch_gate_mfma<3>(x, gw, bias, d, out, st);
-      case 4: return launch_gate_mfma<4>(x, gw, bias, d, out, st);
-      default: return launch_gate_mfma<8>(x, gw, bias, d, out, st);
+      case 1: return launch_gate_mfma<1>(x, gw, bias, d, out, pp, ks, st);
+      case 2: return launch_gate_mfma<2>(x, gw, bias, d, out, pp, ks, st);
+      case 3: return launch_gate_mfma<3>(x, gw, bias, d, out, pp, ks, st);
+      case 4: return launch_gate_mfma<4>(x, gw, bias, d, out, pp, ks, st);
+      default: return launch_gate_mfma<8>(x, gw, bias, d, out, pp, ks, st);
     }
   }
   if (d.dtype == DSMOE_BF16) {

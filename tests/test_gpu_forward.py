@@ -73,6 +73,33 @@ def test_route_from_logits_bit_exact(T, E, k):
     assert np.array_equal(_np(out["counts"]), c)
 
 
+@pytest.mark.parametrize("T,E,k", [(1, 4, 2), (5, 64, 6), (333, 16, 4), (70, 256, 8)])
+def test_route_writes_only_the_token_rows(T, E, k):
+    """Tokens are routed in batches per wave; the padding slots of a partly
+    filled batch must write nothing past row T of any output."""
+    from dsmoe import _lib as L
+    g = torch.Generator().manual_seed(5 * T + E)
+    logits = torch.randn(T, E, generator=g).to(DEV)
+    bias = (torch.randn(E, generator=g) * 0.01).to(DEV)
+    pad = 8
+    idx = torch.full((T + pad, k), -7, dtype=torch.int32, device=DEV)
+    idx64 = torch.full((T + pad, k), -7, dtype=torch.int64, device=DEV)
+    w = torch.full((T + pad, k), -7.0, device=DEV)
+    wx = torch.full((T + pad, k), -7.0, device=DEV)
+    sel = torch.full((T + pad, k), -7.0, device=DEV)
+    counts = torch.zeros(E, dtype=torch.int32, device=DEV)
+    d = L.make_dims(T, 1, E, k, 1, 0, 0, torch.float32, 1.0)
+    rc = L.load().dsmoe_route_from_logits(L.ptr(logits), L.ptr(bias), d, L.ptr(idx), L.ptr(idx64), L.ptr(w),
+                                          L.ptr(wx), L.ptr(sel), L.ptr(counts), L.stream_ptr(logits.device))
+    L.check(rc, "dsmoe_route_from_logits")
+    torch.cuda.synchronize()
+    for t in (idx, idx64, w, wx, sel):
+        assert (t[T:] == -7).all()
+    assert int(counts.sum()) == T * k
+    ridx, _, _, rc_ = RC.route(logits.cpu().numpy(), bias.cpu().numpy(), k, 1.0)
+    assert np.array_equal(_np(idx[:T]), ridx) and np.array_equal(_np(counts), rc_)
+
+
 # --------------------------------------------------------------------- permute
 @pytest.mark.parametrize("T,E,k", [(1, 4, 2), (64, 4, 2), (65, 4, 2), (1000, 16, 4), (8192, 64, 6), (3000, 256, 8),
                                    (8192, 16, 4)])
