@@ -422,6 +422,7 @@ __global__ void fill_i32_kernel(int32_t* p, int n, int32_t v) {
 // Routing after a K-split gate: logits = sum of the ks partial logits in
 // split order (0, 1, ...), optionally written out, then route_tokens.
 constexpr int RP_TOK = 16;       // tokens per block (four per wave)
+constexpr int GATE_KS_MAX = 16;  // K splits at most
 __global__ __launch_bounds__(256) void route_partials_kernel(const float* __restrict__ part, int ks,
                                                              const float* __restrict__ bias, int T, int E, int k,
                                                              float route_scale, int xdtype, GateOut out) {
@@ -440,8 +441,14 @@ __global__ __launch_bounds__(256) void route_partials_kernel(const float* __rest
   for (int i = tid; i < ntok * E; i += blockDim.x) {
     const int t = i / E, e = i - t * E;
     const float* p = part + (int64_t)(t0 + t) * E + e;
-    float v = p[0];
-    for (int sp = 1; sp < ks; ++sp) v += p[(int64_t)sp * T * E];
+    // every split's load is issued before the adds (one memory latency)
+    float pv[GATE_KS_MAX];
+#pragma unroll
+    for (int sp = 0; sp < GATE_KS_MAX; ++sp) pv[sp] = sp < ks ? p[(int64_t)sp * T * E] : 0.0f;
+    float v = pv[0];
+#pragma unroll
+    for (int sp = 1; sp < GATE_KS_MAX; ++sp)
+      if (sp < ks) v += pv[sp];
     lg[t * ldl + e] = v;
     if (out.logits) out.logits[(int64_t)(t0 + t) * E + e] = v;
   }
@@ -499,9 +506,9 @@ int gate_k_splits(const dsmoe_dims& d) {
     return s ? std::atoi(s) : 0;
   }();
   const int64_t tiles = cdiv(d.T, GM_TOK);
-  int ks = forced > 0 ? forced : 1;
+  int ks = forced > 0 ? min(forced, GATE_KS_MAX) : 1;
   if (forced <= 0)
-    while (ks < 16 && tiles * ks * 2 <= 256) ks *= 2;   // fill the 256 CUs when there are few token tiles
+    while (ks < GATE_KS_MAX && tiles * ks * 2 <= 256) ks *= 2;   // fill the 256 CUs when there are few token tiles
   while (ks > 1 && d.D % (64 * ks) != 0) ks >>= 1;
   return ks;
 }

@@ -2,7 +2,8 @@
 // Restates models/moe.py:107-117 (argsort, bincount, offsets) and the row
 // gather flat[sorted_token_ids] of models/moe.py:127,150.
 //
-//   rank_kernel     one wave per 64 tokens: for each expert a wave ballot gives
+//   rank_kernel     one workgroup per 64 tokens (a rank block), its four waves
+//                   splitting the experts: for each expert a wave ballot gives
 //                   every slot its rank among the block's earlier tokens, and
 //                   the block histogram (no atomics, deterministic).
 //   scan_kernel     one block of 16 waves: per-expert exclusive scans over the
@@ -11,6 +12,8 @@
 //                   grouped GEMMs (tiles of bm rows inside each expert).
 //   scatter_kernel  pos = offsets[e] + blockbase[b][e] + rank; writes the
 //                   sorted order, its inverse and optional weight gather.
+//   permute_small_kernel  the three stages in one workgroup for calls of at
+//                   most PERMUTE_SMALL_T tokens (decode), one launch.
 //   gather_rows     x_sorted[p] = x[sorted_token[p]] with 16-byte accesses.
 #include "common.h"
 
@@ -19,26 +22,37 @@ namespace dsmoe {
 constexpr int RANK_TOKENS = 64;  // one wave64 per block, one token per lane
 constexpr int MAX_K = 16;
 
+// Ranks of the slots of rank block b (one wave, lane = token) for experts
+// e0, e0 + estep, ...: for each expert a wave ballot gives every slot its rank
+// among the block's earlier tokens, and the block's count of that expert.
 template <int KB>  // bound on k (slots compared per expert)
-__global__ __launch_bounds__(64) void rank_kernel(const int32_t* __restrict__ idx, int T, int k, int E,
-                                                  int32_t* __restrict__ blockhist, int32_t* __restrict__ local_rank) {
-  const int lane = threadIdx.x;
-  const int t = blockIdx.x * RANK_TOKENS + lane;
+__device__ __forceinline__ void rank_experts(const int32_t* __restrict__ idx, int T, int k, int E, int b, int e0,
+                                             int estep, int32_t* __restrict__ blockhist,
+                                             int32_t* __restrict__ local_rank) {
+  const int lane = threadIdx.x & 63;
+  const int t = b * RANK_TOKENS + lane;
   int ex[KB];
 #pragma unroll
   for (int j = 0; j < KB; ++j) ex[j] = -1;
   if (t < T)
     for (int j = 0; j < k; ++j) ex[j] = idx[(int64_t)t * k + j];
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int e = 0; e < E; ++e) {
+  for (int e = e0; e < E; e += estep) {
     int jsel = -1;
 #pragma unroll
     for (int j = 0; j < KB; ++j)
       if (ex[j] == e) jsel = j;
     const uint64_t mask = __ballot(jsel >= 0);
     if (jsel >= 0) local_rank[(int64_t)t * k + jsel] = __popcll(mask & below);
-    if (lane == 0) blockhist[(int64_t)blockIdx.x * E + e] = __popcll(mask);
+    if (lane == 0) blockhist[(int64_t)b * E + e] = __popcll(mask);
   }
+}
+
+// One rank block (64 tokens) per workgroup; its four waves split the experts.
+template <int KB>
+__global__ __launch_bounds__(256) void rank_kernel(const int32_t* __restrict__ idx, int T, int k, int E,
+                                                   int32_t* __restrict__ blockhist, int32_t* __restrict__ local_rank) {
+  rank_experts<KB>(idx, T, k, E, blockIdx.x, threadIdx.x >> 6, blockDim.x >> 6, blockhist, local_rank);
 }
 
 // Inclusive prefix sum over the 64 lanes of a wave (exact integer adds).
@@ -51,15 +65,15 @@ __device__ __forceinline__ int32_t wave_incl_scan(int32_t x, int lane) {
   return x;
 }
 
-// Single block.  LDS: cnt[E], off[E+1], tiles[E+1].  Wave w scans experts
-// w, w + nw, ...: lane b holds block b's count of the expert, 64 blocks at a
-// time, carried across chunks.  Wave 0 then scans counts and tile counts over
-// the experts, 64 at a time.  Integer sums: the same values as a serial scan.
-__global__ __launch_bounds__(1024) void scan_kernel(const int32_t* __restrict__ blockhist, int nb, int E, int bm,
-                                                    int32_t* __restrict__ blockbase, int32_t* __restrict__ counts,
-                                                    int32_t* __restrict__ offsets, MTile* __restrict__ sched,
-                                                    int32_t* __restrict__ sched_count) {
-  extern __shared__ int32_t sh[];
+// Scan over the block histograms by one workgroup.  LDS sh: cnt[E],
+// off[E+1], tiles[E+1].  Wave w scans experts w, w + nw, ...: lane b holds
+// block b's count of the expert, 64 blocks at a time, carried across chunks.
+// Wave 0 then scans counts and tile counts over the experts, 64 at a time.
+// Integer sums: the same values as a serial scan.
+__device__ __forceinline__ void scan_body(const int32_t* __restrict__ blockhist, int nb, int E, int bm,
+                                          int32_t* __restrict__ blockbase, int32_t* __restrict__ counts,
+                                          int32_t* __restrict__ offsets, MTile* __restrict__ sched,
+                                          int32_t* __restrict__ sched_count, int32_t* sh) {
   int32_t* cnt = sh;
   int32_t* off = sh + E;
   int32_t* til = off + E + 1;
@@ -114,12 +128,23 @@ __global__ __launch_bounds__(1024) void scan_kernel(const int32_t* __restrict__ 
   }
 }
 
-__global__ void scatter_kernel(const int32_t* __restrict__ idx, const int32_t* __restrict__ local_rank,
-                               const int32_t* __restrict__ blockbase, const int32_t* __restrict__ offsets, int T, int k,
-                               int E, int32_t* __restrict__ sorted_slot, int32_t* __restrict__ sorted_token,
-                               int32_t* __restrict__ slot_pos, const float* __restrict__ w, float* __restrict__ sorted_w) {
-  const int64_t s = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (s >= (int64_t)T * k) return;
+__global__ __launch_bounds__(1024) void scan_kernel(const int32_t* __restrict__ blockhist, int nb, int E, int bm,
+                                                    int32_t* __restrict__ blockbase, int32_t* __restrict__ counts,
+                                                    int32_t* __restrict__ offsets, MTile* __restrict__ sched,
+                                                    int32_t* __restrict__ sched_count) {
+  extern __shared__ int32_t sh[];
+  scan_body(blockhist, nb, E, bm, blockbase, counts, offsets, sched, sched_count, sh);
+}
+
+// Slot s: pos = offsets[e] + blockbase[b][e] + rank; writes the sorted order,
+// its inverse and the optional weight gather.
+__device__ __forceinline__ void scatter_slot(int64_t s, const int32_t* __restrict__ idx,
+                                             const int32_t* __restrict__ local_rank,
+                                             const int32_t* __restrict__ blockbase,
+                                             const int32_t* __restrict__ offsets, int k, int E,
+                                             int32_t* __restrict__ sorted_slot, int32_t* __restrict__ sorted_token,
+                                             int32_t* __restrict__ slot_pos, const float* __restrict__ w,
+                                             float* __restrict__ sorted_w) {
   const int t = (int)(s / k);
   const int e = idx[s];
   if ((unsigned)e >= (unsigned)E) return;  // ids are validated upstream; never write out of bounds
@@ -129,6 +154,45 @@ __global__ void scatter_kernel(const int32_t* __restrict__ idx, const int32_t* _
   sorted_token[pos] = t;
   slot_pos[s] = pos;
   if (sorted_w) sorted_w[pos] = w[s];
+}
+
+__global__ void scatter_kernel(const int32_t* __restrict__ idx, const int32_t* __restrict__ local_rank,
+                               const int32_t* __restrict__ blockbase, const int32_t* __restrict__ offsets, int T, int k,
+                               int E, int32_t* __restrict__ sorted_slot, int32_t* __restrict__ sorted_token,
+                               int32_t* __restrict__ slot_pos, const float* __restrict__ w, float* __restrict__ sorted_w) {
+  const int64_t s = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (s >= (int64_t)T * k) return;
+  scatter_slot(s, idx, local_rank, blockbase, offsets, k, E, sorted_slot, sorted_token, slot_pos, w, sorted_w);
+}
+
+// Small calls (decode): rank, scan and scatter in one workgroup of 16 waves,
+// with workgroup barriers (which order the global scratch writes) between
+// the stages.  The waves share out (rank block, expert phase) pairs.
+constexpr int PERMUTE_SMALL_T = 256;
+template <int KB>
+__global__ __launch_bounds__(1024) void permute_small_kernel(const int32_t* __restrict__ idx, int T, int k, int E,
+                                                             int bm, int32_t* __restrict__ blockhist,
+                                                             int32_t* __restrict__ local_rank,
+                                                             int32_t* __restrict__ blockbase,
+                                                             int32_t* __restrict__ counts,
+                                                             int32_t* __restrict__ offsets, MTile* __restrict__ sched,
+                                                             int32_t* __restrict__ sched_count,
+                                                             int32_t* __restrict__ sorted_slot,
+                                                             int32_t* __restrict__ sorted_token,
+                                                             int32_t* __restrict__ slot_pos,
+                                                             const float* __restrict__ w, float* __restrict__ sorted_w) {
+  extern __shared__ int32_t sh[];
+  const int nb = (T + RANK_TOKENS - 1) / RANK_TOKENS;
+  const int nw = blockDim.x >> 6, wave = threadIdx.x >> 6;
+  const int per_b = max(1, nw / max(nb, 1));
+  for (int pr = wave; pr < nb * per_b; pr += nw)
+    rank_experts<KB>(idx, T, k, E, pr / per_b, pr % per_b, per_b, blockhist, local_rank);
+  __syncthreads();
+  scan_body(blockhist, nb, E, bm, blockbase, counts, offsets, sched, sched_count, sh);
+  __syncthreads();
+  const int64_t N = (int64_t)T * k;
+  for (int64_t s = threadIdx.x; s < N; s += blockDim.x)
+    scatter_slot(s, idx, local_rank, blockbase, offsets, k, E, sorted_slot, sorted_token, slot_pos, w, sorted_w);
 }
 
 // Row gather with 16-byte vectors; row_bytes % 16 == 0.
@@ -215,13 +279,22 @@ int launch_permute(const int32_t* idx, const dsmoe_dims& d, int bm, const Permut
                    float* sorted_w, hipStream_t st) {
   const int nb = (int)cdiv(d.T, RANK_TOKENS);
   const int64_t N = (int64_t)d.T * d.k;
-  if (nb > 0) {
-    if (d.k <= 8)
-      hipLaunchKernelGGL(rank_kernel<8>, dim3(nb), dim3(64), 0, st, idx, d.T, d.k, d.E, s.blockhist, s.local_rank);
-    else
-      hipLaunchKernelGGL(rank_kernel<MAX_K>, dim3(nb), dim3(64), 0, st, idx, d.T, d.k, d.E, s.blockhist, s.local_rank);
-  }
   const size_t lds = sizeof(int32_t) * (3 * d.E + 2);
+  if (d.T <= PERMUTE_SMALL_T) {
+    if (d.k <= 8)
+      hipLaunchKernelGGL(permute_small_kernel<8>, dim3(1), dim3(1024), lds, st, idx, d.T, d.k, d.E, bm, s.blockhist,
+                         s.local_rank, s.blockbase, counts, offsets, s.sched, s.sched_count, sorted_slot, sorted_token,
+                         slot_pos, w, sorted_w);
+    else
+      hipLaunchKernelGGL(permute_small_kernel<MAX_K>, dim3(1), dim3(1024), lds, st, idx, d.T, d.k, d.E, bm,
+                         s.blockhist, s.local_rank, s.blockbase, counts, offsets, s.sched, s.sched_count, sorted_slot,
+                         sorted_token, slot_pos, w, sorted_w);
+    return check_launch("permute_small");
+  }
+  if (d.k <= 8)
+    hipLaunchKernelGGL(rank_kernel<8>, dim3(nb), dim3(256), 0, st, idx, d.T, d.k, d.E, s.blockhist, s.local_rank);
+  else
+    hipLaunchKernelGGL(rank_kernel<MAX_K>, dim3(nb), dim3(256), 0, st, idx, d.T, d.k, d.E, s.blockhist, s.local_rank);
   hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), lds, st, s.blockhist, nb, d.E, bm, s.blockbase, counts, offsets,
                      s.sched, s.sched_count);
   if (N > 0)
