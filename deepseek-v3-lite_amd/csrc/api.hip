@@ -29,7 +29,7 @@ int check_launch(const char* what) {
 }
 
 // ---------------------------------------------------------------- pointer tables
-constexpr int PTR_CHUNK = 192;  // pointers per upload launch (kernel argument space)
+constexpr int PTR_CHUNK = 480;  // pointers per upload launch (3.8 KB of the 4 KB kernel argument space)
 
 struct PtrChunk {
   const void* p[PTR_CHUNK];

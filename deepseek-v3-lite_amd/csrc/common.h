@@ -149,6 +149,8 @@ int launch_gate(const void* x, const float* logits_in, const float* gw, const fl
                 const GateOut& out, hipStream_t st, float* part = nullptr);
 int gate_k_splits(const dsmoe_dims& d);
 size_t gate_part_floats(const dsmoe_dims& d);
+constexpr int GATE_KS_MAX = 16;      // K splits of the gate at most
+constexpr int PERMUTE_SMALL_T = 256; // calls of at most this many tokens permute in one workgroup
 void launch_fill_i32(int32_t* p, int n, int32_t v, hipStream_t st);
 int64_t sched_bound(int64_t rows, int groups, int bm);
 size_t permute_scratch_carve(Carver& c, const dsmoe_dims& d, int bm, PermuteScratch* out);

@@ -15,7 +15,7 @@
 // rounds of a wave-wide arg-max ordered by (value desc, expert id asc).
 #include <cstdlib>
 
-#include "common.h"
+#include "route.h"
 
 namespace dsmoe {
 
@@ -27,156 +27,9 @@ typedef unsigned int g_u32x4_t __attribute__((ext_vector_type(4)));
 constexpr int GATE_THREADS = 256;
 // MFMA gate: 4 waves when one 32-expert tile covers E, else 8 (the second four
 // take the odd expert tiles of the same K quarters)
-constexpr int GM_WAVES_MAX = 8;
 constexpr int gm_waves(int nt) { return nt >= 2 ? 8 : 4; }
 constexpr int GATE_KC = 32;        // SIMT: K chunk staged through LDS
 constexpr int GM_TOK = 32;         // MFMA: tokens per block
-constexpr int MAX_EPL = 4;         // experts per lane in routing (E <= 256)
-
-// ------------------------------------------------------------------ routing
-// Routes tokens [t0, t0 + ntok) whose fp32 logits sit in LDS rows lg[t*ldl].
-// Wave w routes tokens in batches of route_ntok(EPL): w, w + nw, ... in batch
-// units.  Lane l holds expert l (E <= 64) or
-// experts l, l + 64, ... (E <= 256) in registers.
-//
-// Selection: k rounds of a wave arg-max over the biased scores under the
-// order (value desc, id asc): a DPP max gives the round's value m, a ballot of
-// the lanes holding m and its lowest set bit give the lowest expert id with
-// that value, which takes slot j of the round and drops out.  This is the
-// oracle's k rounds of arg-max with the same tie rule.  The renormalising sum
-// runs over slots j = 0..k-1 in order, as in the oracle.
-constexpr int route_ntok(int epl) { return epl == 1 ? 4 : 2; }
-constexpr int route_row(int epl) { return 64 * epl + MAX_TOPK; }
-
-// Maximum over the 64 lanes (every lane gets it).  Row (16-lane) shifts, then
-// the row broadcasts of lanes 15 and 31, leave the maximum in lane 63.
-__device__ __forceinline__ float wave_max_f32(float v) {
-  const int b = __float_as_int(v);
-  float t;
-  t = __int_as_float(__builtin_amdgcn_update_dpp(b, __float_as_int(v), 0x111, 0xf, 0xf, false));  // row_shr:1
-  v = fmaxf(v, t);
-  t = __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x112, 0xf, 0xf, false));
-  v = fmaxf(v, t);
-  t = __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x114, 0xf, 0xf, false));
-  v = fmaxf(v, t);
-  t = __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x118, 0xf, 0xf, false));
-  v = fmaxf(v, t);
-  t = __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x142, 0xa, 0xf, false));  // row_bcast:15
-  v = fmaxf(v, t);
-  t = __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x143, 0xc, 0xf, false));  // row_bcast:31
-  v = fmaxf(v, t);
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
-
-template <int EPL>  // experts per lane: 1 for E <= 64, MAX_EPL otherwise
-__device__ __forceinline__ void route_tokens_t(const float* lg, int ldl, int ntok, int t0, const float* bias_s, int E,
-                                               int k, float route_scale, int xdtype, const GateOut& out, int* hist,
-                                               float* /*unused scratch*/) {
-  // NB tokens per wave are routed side by side: their sigmoid, max and
-  // ballot chains are independent, so their latencies overlap.
-  constexpr int NB = route_ntok(EPL);
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int nw = blockDim.x >> 6;
-  for (int tb = wave * NB; tb < ntok; tb += nw * NB) {
-    float sv[NB][EPL], bv[NB][EPL];
-    int slot[NB][EPL];
-#pragma unroll
-    for (int b = 0; b < NB; ++b)
-#pragma unroll
-      for (int q = 0; q < EPL; ++q) {
-        const int e = lane + 64 * q;
-        sv[b][q] = 0.0f;
-        bv[b][q] = -INFINITY;
-        slot[b][q] = -1;
-        if (tb + b < ntok && e < E) {
-          sv[b][q] = route_sigmoid(lg[(tb + b) * ldl + e]);
-          bv[b][q] = sv[b][q] + bias_s[e];
-        }
-      }
-    float ssum[NB];
-#pragma unroll
-    for (int b = 0; b < NB; ++b) ssum[b] = 0.0f;
-    for (int j = 0; j < k; ++j) {
-      float m[NB];
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        float lm = bv[b][0];
-#pragma unroll
-        for (int q = 1; q < EPL; ++q) lm = fmaxf(lm, bv[b][q]);
-        m[b] = wave_max_f32(lm);
-      }
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        int win = -1;
-#pragma unroll
-        for (int q = 0; q < EPL; ++q) {
-          const uint64_t bl = __ballot(slot[b][q] < 0 && lane + 64 * q < E && bv[b][q] == m[b]);
-          if (win < 0 && bl) win = __ffsll((unsigned long long)bl) - 1 + 64 * q;
-        }
-        if (win < 0) {
-          // only NaN scores left: the lowest unselected expert id
-#pragma unroll
-          for (int q = 0; q < EPL; ++q) {
-            const uint64_t bl = __ballot(slot[b][q] < 0 && lane + 64 * q < E);
-            if (win < 0 && bl) win = __ffsll((unsigned long long)bl) - 1 + 64 * q;
-          }
-        }
-        win = __builtin_amdgcn_readfirstlane(win);
-        const int wl = win & 63, wq = win >> 6;
-#pragma unroll
-        for (int q = 0; q < EPL; ++q)
-          if (q == wq) {
-            ssum[b] += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sv[b][q]), wl));
-            if (lane == wl) {
-              slot[b][q] = j;
-              bv[b][q] = -INFINITY;
-            }
-          }
-      }
-    }
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      if (tb + b >= ntok) break;   // padding tokens of the last batch write nothing
-      const float den = ssum[b] < 1e-10f ? 1e-10f : ssum[b];
-      const int64_t o = (int64_t)(t0 + tb + b) * k;
-#pragma unroll
-      for (int q = 0; q < EPL; ++q) {
-        const int e = lane + 64 * q;
-        if (slot[b][q] >= 0) {
-          const int j = slot[b][q];
-          const float w = sv[b][q] / den * route_scale;
-          out.idx[o + j] = e;
-          if (out.idx64) out.idx64[o + j] = e;
-          out.weights[o + j] = w;
-          if (out.weights_x) {
-            if (xdtype == DSMOE_BF16)
-              static_cast<bf16_t*>(out.weights_x)[o + j] = f2bf(w);
-            else
-              static_cast<float*>(out.weights_x)[o + j] = w;
-          }
-          if (out.sel_scores) out.sel_scores[o + j] = sv[b][q];
-          if (hist) atomicAdd(&hist[e], 1);
-        }
-      }
-    }
-  }
-}
-
-__device__ __forceinline__ void route_tokens(const float* lg, int ldl, int ntok, int t0, const float* bias_s, int E,
-                                             int k, float route_scale, int xdtype, const GateOut& out, int* hist,
-                                             float* wscr_all) {
-  if (E <= 64)
-    route_tokens_t<1>(lg, ldl, ntok, t0, bias_s, E, k, route_scale, xdtype, out, hist, wscr_all);
-  else
-    route_tokens_t<MAX_EPL>(lg, ldl, ntok, t0, bias_s, E, k, route_scale, xdtype, out, hist, wscr_all);
-}
-
-__device__ __forceinline__ void flush_hist(const int* hist, int E, int32_t* counts) {
-  if (!counts) return;
-  for (int e = threadIdx.x; e < E; e += blockDim.x)
-    if (hist[e]) atomicAdd(&counts[e], hist[e]);
-}
 
 // ------------------------------------------------------------------ MFMA logits (bf16 x)
 // Splits 8 consecutive fp32 weights into three bf16x8 vectors whose sum is exact.
@@ -201,11 +54,6 @@ __device__ __forceinline__ void split3(const g_f32x4_t& a, const g_f32x4_t& b, g
   __builtin_memcpy(&lo, l, 16);
 }
 
-// floats of routing scratch (per wave, the larger of the two layouts)
-constexpr int ROUTE_SCR = GM_WAVES_MAX *
-                          (route_ntok(1) * route_row(1) > route_ntok(MAX_EPL) * route_row(MAX_EPL)
-                               ? route_ntok(1) * route_row(1)
-                               : route_ntok(MAX_EPL) * route_row(MAX_EPL));
 
 // LDS: part[4][GM_TOK][EP+1] fp32 partial logits (reused for the reduced
 // logits), bias[E], hist[E], routing scratch.
@@ -221,9 +69,6 @@ __global__ __launch_bounds__(gm_waves(NT) * 64) void gate_mfma_kernel(const bf16
   float* part = gsm;                                   // [4][GM_TOK][LDP]
   float* bias_s = part + 4 * GM_TOK * LDP;
   int* hist = reinterpret_cast<int*>(bias_s + E);
-  // 16-byte aligned offset from the LDS base (pointer arithmetic keeps the
-  // accesses in the LDS address space)
-  float* rscr = gsm + ((4 * GM_TOK * LDP + 2 * E + 3) & ~3);
   constexpr int NWV = gm_waves(NT);
   constexpr int NTH = NWV * 64;
   // wave w: K quarter w & 3; expert tiles ni = w >> 2, w >> 2 + NWV / 4, ...
@@ -327,7 +172,7 @@ __global__ __launch_bounds__(gm_waves(NT) * 64) void gate_mfma_kernel(const bf16
   }
   if (part_out) return;
   __syncthreads();
-  route_tokens(part, LDP, ntok, t0, bias_s, E, k, route_scale, DSMOE_BF16, out, out.counts ? hist : nullptr, rscr);
+  route_tokens(part, LDP, ntok, t0, bias_s, E, k, route_scale, DSMOE_BF16, out, out.counts ? hist : nullptr);
   __syncthreads();
   flush_hist(hist, E, out.counts);
 }
@@ -347,7 +192,6 @@ __global__ __launch_bounds__(GATE_THREADS) void gate_kernel(const XT* __restrict
   float* lg = ws + GATE_KC * (EC + 4);          // [TB][E+1]
   float* bias_s = lg + TB * (E + 1);            // [E]
   int* hist = reinterpret_cast<int*>(bias_s + E);  // [E]
-  float* rscr = smem + ((GATE_KC * (TB + 4) + GATE_KC * (EC + 4) + TB * (E + 1) + 2 * E + 3) & ~3);
 
   const int tid = threadIdx.x;
   const int t0 = blockIdx.x * TB;
@@ -409,7 +253,7 @@ __global__ __launch_bounds__(GATE_THREADS) void gate_kernel(const XT* __restrict
       out.logits[(int64_t)(t0 + t) * E + e] = lg[t * ldl + e];
     }
   }
-  route_tokens(lg, ldl, ntok, t0, bias_s, E, k, route_scale, xdtype, out, out.counts ? hist : nullptr, rscr);
+  route_tokens(lg, ldl, ntok, t0, bias_s, E, k, route_scale, xdtype, out, out.counts ? hist : nullptr);
   __syncthreads();
   flush_hist(hist, E, out.counts);
 }
@@ -421,9 +265,8 @@ __global__ void fill_i32_kernel(int32_t* p, int n, int32_t v) {
 
 // Routing after a K-split gate: logits = sum of the ks partial logits in
 // split order (0, 1, ...), optionally written out, then route_tokens.
-constexpr int RP_TOK = 16;       // tokens per block (four per wave)
-constexpr int GATE_KS_MAX = 16;  // K splits at most
-__global__ __launch_bounds__(256) void route_partials_kernel(const float* __restrict__ part, int ks,
+constexpr int RP_TOK = 4;        // tokens per block: one wave routes them as one batch
+__global__ __launch_bounds__(64) void route_partials_kernel(const float* __restrict__ part, int ks,
                                                              const float* __restrict__ bias, int T, int E, int k,
                                                              float route_scale, int xdtype, GateOut out) {
   extern __shared__ float rsm[];
@@ -453,7 +296,7 @@ __global__ __launch_bounds__(256) void route_partials_kernel(const float* __rest
     if (out.logits) out.logits[(int64_t)(t0 + t) * E + e] = v;
   }
   __syncthreads();
-  route_tokens(lg, ldl, ntok, t0, bias_s, E, k, route_scale, xdtype, out, out.counts ? hist : nullptr, nullptr);
+  route_tokens(lg, ldl, ntok, t0, bias_s, E, k, route_scale, xdtype, out, out.counts ? hist : nullptr);
   __syncthreads();
   flush_hist(hist, E, out.counts);
 }
@@ -471,7 +314,7 @@ static int launch_gate_t(const void* x, const float* logits_in, const float* gw,
   constexpr int TX = EC / 4;
   constexpr int TB = (GATE_THREADS / TX) * 4;
   const size_t lds = sizeof(float) * (GATE_KC * (TB + 4) + GATE_KC * (EC + 4) + TB * (d.E + 1) + d.E) +
-                     sizeof(int) * d.E + 16 + sizeof(float) * ROUTE_SCR;
+                     sizeof(int) * d.E + 16;
   auto kern = gate_kernel<XT, EC, FROM_LOGITS>;
   int rc = set_lds((const void*)kern, lds);
   if (rc) return rc;
@@ -484,8 +327,7 @@ static int launch_gate_t(const void* x, const float* logits_in, const float* gw,
 template <int NT>
 static int launch_gate_mfma(const void* x, const float* gw, const float* bias, const dsmoe_dims& d, const GateOut& out,
                             float* part, int ks, hipStream_t st) {
-  const size_t lds = sizeof(float) * (4 * GM_TOK * (NT * 32 + 1) + d.E) + sizeof(int) * ((d.E + 3) & ~3) +
-                     sizeof(float) * ROUTE_SCR;
+  const size_t lds = sizeof(float) * (4 * GM_TOK * (NT * 32 + 1) + d.E) + sizeof(int) * ((d.E + 3) & ~3);
   auto kern = gate_mfma_kernel<NT>;
   int rc = set_lds((const void*)kern, lds);
   if (rc) return rc;
@@ -495,7 +337,7 @@ static int launch_gate_mfma(const void* x, const float* gw, const float* bias, c
   rc = check_launch("gate_mfma");
   if (rc || !part) return rc;
   const size_t rlds = sizeof(float) * (RP_TOK * (d.E + 1) + d.E) + sizeof(int) * d.E;
-  hipLaunchKernelGGL(route_partials_kernel, dim3((unsigned)cdiv(d.T, RP_TOK)), dim3(256), rlds, st, part, ks, bias,
+  hipLaunchKernelGGL(route_partials_kernel, dim3((unsigned)cdiv(d.T, RP_TOK)), dim3(64), rlds, st, part, ks, bias,
                      d.T, d.E, d.k, d.route_scale, (int)DSMOE_BF16, out);
   return check_launch("route_partials");
 }
@@ -518,6 +360,11 @@ size_t gate_part_floats(const dsmoe_dims& d) {
   return ks > 1 ? (size_t)ks * d.T * d.E : 0;
 }
 
+static bool gate_mfma_ok(const void* x, const float* gw, const dsmoe_dims& d) {
+  return d.dtype == DSMOE_BF16 && d.D % 64 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+         (reinterpret_cast<uintptr_t>(gw) & 15) == 0;
+}
+
 int launch_gate(const void* x, const float* logits_in, const float* gw, const float* bias, const dsmoe_dims& d,
                 const GateOut& out, hipStream_t st, float* part) {
   if (out.counts) {
@@ -525,8 +372,7 @@ int launch_gate(const void* x, const float* logits_in, const float* gw, const fl
   }
   if (d.T == 0) return check_launch("gate(fill)");
   if (logits_in) return launch_gate_t<float, 64, true>(nullptr, logits_in, gw, bias, d, out, st);
-  const bool mfma = d.dtype == DSMOE_BF16 && d.D % 64 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
-                    (reinterpret_cast<uintptr_t>(gw) & 15) == 0;
+  const bool mfma = gate_mfma_ok(x, gw, d);
   if (mfma) {
     const int nt = (int)cdiv(d.E, 32);
     const int ks = part ? gate_k_splits(d) : 1;

@@ -168,7 +168,6 @@ __global__ void scatter_kernel(const int32_t* __restrict__ idx, const int32_t* _
 // Small calls (decode): rank, scan and scatter in one workgroup of 16 waves,
 // with workgroup barriers (which order the global scratch writes) between
 // the stages.  The waves share out (rank block, expert phase) pairs.
-constexpr int PERMUTE_SMALL_T = 256;
 template <int KB>
 __global__ __launch_bounds__(1024) void permute_small_kernel(const int32_t* __restrict__ idx, int T, int k, int E,
                                                              int bm, int32_t* __restrict__ blockhist,
@@ -328,3 +327,4 @@ int launch_sched_from_offsets(const int64_t* offsets64, int E, int bm, int64_t r
 }
 
 }  // namespace dsmoe
+
