@@ -78,16 +78,48 @@ __device__ __forceinline__ void scan_body(const int32_t* __restrict__ blockhist,
   int32_t* off = sh + E;
   int32_t* til = off + E + 1;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
-  for (int e = wave; e < E; e += nw) {
-    int32_t carry = 0;
-    for (int b0 = 0; b0 < nb; b0 += 64) {
-      const int b = b0 + lane;
-      const int32_t v = b < nb ? blockhist[(int64_t)b * E + e] : 0;
-      const int32_t x = wave_incl_scan(v, lane);
-      if (b < nb) blockbase[(int64_t)b * E + e] = carry + x - v;
-      carry += __shfl(x, 63, 64);
+  const int epw = wave < E ? (E - wave + nw - 1) / nw : 0;   // experts of this wave
+  const int nch = (nb + 63) / 64;                            // 64-block chunks per expert
+  constexpr int PRE = 16;
+  if (nch == 0) {
+    for (int e = wave; e < E; e += nw)
+      if (lane == 0) cnt[e] = 0;
+  } else if (epw * nch <= PRE) {
+    // every (expert, chunk) value of this wave is loaded before the scans, so
+    // the global round trips overlap instead of following each other
+    int32_t v[PRE];
+#pragma unroll
+    for (int i = 0; i < PRE; ++i) {
+      v[i] = 0;
+      if (i < epw * nch) {
+        const int e = wave + (i / nch) * nw, b = (i % nch) * 64 + lane;
+        if (b < nb) v[i] = blockhist[(int64_t)b * E + e];
+      }
     }
-    if (lane == 0) cnt[e] = carry;
+    int32_t carry = 0;
+#pragma unroll
+    for (int i = 0; i < PRE; ++i) {
+      if (i < epw * nch) {
+        const int e = wave + (i / nch) * nw, c = i % nch, b = c * 64 + lane;
+        if (c == 0) carry = 0;
+        const int32_t x = wave_incl_scan(v[i], lane);
+        if (b < nb) blockbase[(int64_t)b * E + e] = carry + x - v[i];
+        carry += __shfl(x, 63, 64);
+        if (c == nch - 1 && lane == 0) cnt[e] = carry;
+      }
+    }
+  } else {
+    for (int e = wave; e < E; e += nw) {
+      int32_t carry = 0;
+      for (int b0 = 0; b0 < nb; b0 += 64) {
+        const int b = b0 + lane;
+        const int32_t v = b < nb ? blockhist[(int64_t)b * E + e] : 0;
+        const int32_t x = wave_incl_scan(v, lane);
+        if (b < nb) blockbase[(int64_t)b * E + e] = carry + x - v;
+        carry += __shfl(x, 63, 64);
+      }
+      if (lane == 0) cnt[e] = carry;
+    }
   }
   __syncthreads();
   if (wave == 0) {
