@@ -607,8 +607,11 @@ int dsmoe_moe_bwd(const void* x, const float* gate_w, const void* const* w1, con
                           (const void**)B.dsw1, st);
   if (rc) return rc;
   // gate gradient path: d weights -> d logits
-  rc = launch_dw_dot(dy, F.o_slots, N, d.k, d.D, d.dtype, B.dw, st);
-  if (!rc && B.dy_w) rc = launch_scale_gather_rows(dy, F.sorted_token, F.sorted_w, N, d.D, B.dy_w, st);
+  rc = launch_prep_tok(dy, F.o_slots, F.w, F.slot_pos, d.T, d.k, d.D, d.dtype, B.dw, B.dy_w, st);
+  if (rc == DSMOE_ERR_UNSUPPORTED) {
+    rc = launch_dw_dot(dy, F.o_slots, N, d.k, d.D, d.dtype, B.dw, st);
+    if (!rc && B.dy_w) rc = launch_scale_gather_rows(dy, F.sorted_token, F.sorted_w, N, d.D, B.dy_w, st);
+  }
   if (!rc) rc = launch_gate_bwd(B.dw, F.sel, d.T, d.k, d.route_scale, B.dlog, st);
   if (!rc) rc = launch_sched32(F.offsets, d.E, BWD_BM, B.sched, B.sched_count, st);
   tm.end();

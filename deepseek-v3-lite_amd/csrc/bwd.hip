@@ -291,7 +291,72 @@ __global__ __launch_bounds__(256) void dw_dot_tok_kernel(const bf16_t* __restric
   }
 }
 
+// dw and the weighted dY rows in one pass, one wave per token: dY_t is read
+// once; for each slot j of the token, dw[t k + j] = <dY_t, o_slot> (the
+// dw_dot_tok_kernel sums, in the same order) and dy_w[slot_pos[t k + j]] =
+// bf16(w[t k + j] * dY_t) (scale_gather_kernel's rounding).
+template <int KB>
+__global__ __launch_bounds__(256) void prep_tok_kernel(const bf16_t* __restrict__ dy, const bf16_t* __restrict__ o_slots,
+                                                       const float* __restrict__ w,
+                                                       const int32_t* __restrict__ slot_pos, int T, int k, int D,
+                                                       float* __restrict__ dw, bf16_t* __restrict__ dy_w) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const int vpr = D / 8;
+  float ws[KB];
+  int64_t pos[KB];
+#pragma unroll
+  for (int j = 0; j < KB; ++j) {
+    ws[j] = 0.0f;
+    pos[j] = 0;
+    if (j < k) {
+      ws[j] = w[t * k + j];
+      pos[j] = slot_pos[t * k + j];
+    }
+  }
+  float acc[KB];
+#pragma unroll
+  for (int j = 0; j < KB; ++j) acc[j] = 0.0f;
+  for (int c = lane; c < vpr; c += 64) {
+    float af[8];
+    Vec16<bf16_t>::load(dy + t * D + c * 8, af);
+    float bv[KB][8];
+#pragma unroll
+    for (int j = 0; j < KB; ++j)
+      if (j < k) Vec16<bf16_t>::load(o_slots + (t * k + j) * D + c * 8, bv[j]);
+#pragma unroll
+    for (int j = 0; j < KB; ++j) {
+      if (j >= k) break;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[j] = fmaf(af[i], bv[j][i], acc[j]);
+      float sv[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sv[i] = af[i] * ws[j];
+      Vec16<bf16_t>::store(dy_w + pos[j] * D + c * 8, sv);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < KB; ++j) {
+    if (j >= k) break;
+    float v = acc[j];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    if (lane == 0) dw[t * k + j] = v;
+  }
+}
+
 static bool al16p(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+int launch_prep_tok(const void* dy, const void* o_slots, const float* w, const int32_t* slot_pos, int T, int k, int D,
+                    int dtype, float* dw, void* dy_w, hipStream_t st) {
+  if (!(dtype == DSMOE_BF16 && D % 8 == 0 && k <= 8 && dy_w && al16p(dy) && al16p(o_slots) && al16p(dy_w)))
+    return DSMOE_ERR_UNSUPPORTED;
+  if (T == 0) return DSMOE_OK;
+  hipLaunchKernelGGL(prep_tok_kernel<8>, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, st, static_cast<const bf16_t*>(dy),
+                     static_cast<const bf16_t*>(o_slots), w, slot_pos, T, k, D, dw, static_cast<bf16_t*>(dy_w));
+  return check_launch("prep_tok");
+}
 
 // ---------------------------------------------------------------- launchers
 // dst[p] = bf16(w[p] * src[rows[p]]), 8 columns per thread: one fp32 product

@@ -274,6 +274,11 @@ int launch_scale_gather_rows(const void* src, const int32_t* rows, const float* 
 int xgemm_pick_ksplit(int64_t tiles, int64_t k_len);
 int64_t xgemm_tiles(int64_t M, int64_t N, int groups);
 int launch_dw_dot(const void* dy, const void* o_slots, int64_t N, int k, int D, int dtype, float* dw, hipStream_t st);
+// launch_dw_dot and launch_scale_gather_rows (rows by token, slot weights) in
+// one pass; DSMOE_ERR_UNSUPPORTED (nothing launched) when the shape or
+// alignment does not fit (bf16, D % 8, k <= 8, 16-byte rows).
+int launch_prep_tok(const void* dy, const void* o_slots, const float* w, const int32_t* slot_pos, int T, int k, int D,
+                    int dtype, float* dw, void* dy_w, hipStream_t st);
 int launch_gate_bwd(const float* dw, const float* sel, int T, int k, float rs, float* dlog, hipStream_t st);
 int launch_dwgate(const void* x, const float* dlog, const int32_t* sorted_slot, const int32_t* sorted_token,
                   const int32_t* offsets, int E, int D, int dtype, float* dgw, hipStream_t st);
