@@ -265,7 +265,7 @@ __global__ void fill_i32_kernel(int32_t* p, int n, int32_t v) {
 
 // Routing after a K-split gate: logits = sum of the ks partial logits in
 // split order (0, 1, ...), optionally written out, then route_tokens.
-constexpr int RP_TOK = 4;        // tokens per block: one wave routes them as one batch
+constexpr int RP_TOK = 1;        // tokens per block (one wave): small calls, spread over the CUs
 __global__ __launch_bounds__(64) void route_partials_kernel(const float* __restrict__ part, int ks,
                                                              const float* __restrict__ bias, int T, int E, int k,
                                                              float route_scale, int xdtype, GateOut out) {
@@ -296,7 +296,7 @@ __global__ __launch_bounds__(64) void route_partials_kernel(const float* __restr
     if (out.logits) out.logits[(int64_t)(t0 + t) * E + e] = v;
   }
   __syncthreads();
-  route_tokens(lg, ldl, ntok, t0, bias_s, E, k, route_scale, xdtype, out, out.counts ? hist : nullptr);
+  route_tokens<1, 1>(lg, ldl, ntok, t0, bias_s, E, k, route_scale, xdtype, out, out.counts ? hist : nullptr);
   __syncthreads();
   flush_hist(hist, E, out.counts);
 }

@@ -42,12 +42,12 @@ __device__ __forceinline__ float wave_max_f32(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
-template <int EPL>  // experts per lane: 1 for E <= 64, MAX_EPL otherwise
+// EPL: experts per lane (1 for E <= 64, MAX_EPL otherwise); NB: tokens a
+// wave routes side by side (their sigmoid, max and ballot chains are
+// independent, so their latencies overlap).
+template <int EPL, int NB = route_ntok(EPL)>
 __device__ __forceinline__ void route_tokens_t(const float* lg, int ldl, int ntok, int t0, const float* bias_s, int E,
                                                int k, float route_scale, int xdtype, const GateOut& out, int* hist) {
-  // NB tokens per wave are routed side by side: their sigmoid, max and
-  // ballot chains are independent, so their latencies overlap.
-  constexpr int NB = route_ntok(EPL);
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int nw = blockDim.x >> 6;
@@ -136,12 +136,13 @@ __device__ __forceinline__ void route_tokens_t(const float* lg, int ldl, int nto
   }
 }
 
+template <int NB1 = route_ntok(1), int NB4 = route_ntok(MAX_EPL)>
 __device__ __forceinline__ void route_tokens(const float* lg, int ldl, int ntok, int t0, const float* bias_s, int E,
                                              int k, float route_scale, int xdtype, const GateOut& out, int* hist) {
   if (E <= 64)
-    route_tokens_t<1>(lg, ldl, ntok, t0, bias_s, E, k, route_scale, xdtype, out, hist);
+    route_tokens_t<1, NB1>(lg, ldl, ntok, t0, bias_s, E, k, route_scale, xdtype, out, hist);
   else
-    route_tokens_t<MAX_EPL>(lg, ldl, ntok, t0, bias_s, E, k, route_scale, xdtype, out, hist);
+    route_tokens_t<MAX_EPL, NB4>(lg, ldl, ntok, t0, bias_s, E, k, route_scale, xdtype, out, hist);
 }
 
 __device__ __forceinline__ void flush_hist(const int* hist, int E, int32_t* counts) {
