@@ -154,6 +154,26 @@ def stage_times(step, steps: int):
     return {kname: v / steps for kname, v in stages.items()}
 
 
+def stage_times_flushed(step, steps: int, dev):
+    """stage_times with the caches flushed before every call: a 512 MiB write
+    (twice the 256 MB MALL) between calls, outside the library's events, so
+    the HBM-bound stages read their inputs from HBM."""
+    import torch
+    import dsmoe._lib as L
+    scratch = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    L.timing_enable(True)
+    try:
+        for i in range(steps):
+            scratch.fill_(i & 0xFF)
+            step()
+        torch_sync()
+        stages, _ncalls = L.timing_read()
+    finally:
+        L.timing_enable(False)
+    del scratch
+    return {kname: v / steps for kname, v in stages.items()}
+
+
 def stage_rooflines(cfg, stage_ms):
     """Per-stage rates against the stage's roof.  Algorithmic bytes / flops
     per forward (bf16 activations and expert weights, fp32 gate):
@@ -302,7 +322,10 @@ def main() -> int:
         ms, wall = time_steps(step, args.steps, args.warmup)
         log(f"[bench] timed {args.steps} steps: {ms:.3f} ms/step (host wall {wall:.3f} ms/step)")
         stage_ms = stage_times(step, args.steps)
+        flushed_ms = stage_times_flushed(step, args.steps, dev)
     log(f"[bench] stages (ms/call): " + ", ".join(f"{a}={b:.4f}" for a, b in stage_ms.items()))
+    log(f"[bench] stages, caches flushed before each call (ms/call): " +
+        ", ".join(f"{a}={b:.4f}" for a, b in flushed_ms.items()))
 
     N = T * k
     stages = stage_rooflines(cfg, stage_ms)
@@ -340,6 +363,10 @@ def main() -> int:
         "grouped_gemm_frac": (gemm_flops / (gemm_ms * 1e-3) / 1e12) / PEAK_BF16_TFLOPS if gemm_ms > 0 else None,
         "stage_ms": stage_ms,
         "stages": stages,
+        # the same stages with L2 and MALL flushed before each call (HBM-bound
+        # stages then read their inputs from HBM)
+        "stages_flushed": {kname: v for kname, v in stage_rooflines(cfg, flushed_ms).items()
+                           if kname in ("gate", "permute", "combine")},
     }
     if not args.no_decode and args.config == "c3":
         result["decode"] = decode_bench(dev, max(10, args.steps), max(3, args.warmup))
