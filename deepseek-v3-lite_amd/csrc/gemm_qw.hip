@@ -380,13 +380,19 @@ __global__ __launch_bounds__(256) void gemm_qw_kernel(const GemmDesc g0, const G
   constexpr int ROWB = BN * 2;       // staged row bytes
   constexpr int LPR = ROWB / 16;     // lanes per row in the write-back
   constexpr int RPP = 256 / LPR;     // rows per write-back pass
-  const int npass = (EPI == EPI_SWIGLU) ? 1 + (g.Gs ? 1 : 0) + (g.Us ? 1 : 0) : 1;
+  // Passes: the output (h or the down projection), then, when training
+  // saves the pre-activations, g and u together (two staged tiles of 64 KB).
+  const bool gu2 = EPI == EPI_SWIGLU && g.Gs && g.Us;
+  const int npass = (EPI == EPI_SWIGLU) ? (gu2 ? 2 : 1 + (g.Gs ? 1 : 0) + (g.Us ? 1 : 0)) : 1;
   const int64_t ccol = (int64_t)grp * g.c_group_col;
   const int rr = tid / LPR, cc = tid % LPR;
   // Output rows of the tile: the c_map entries are fetched once, ahead of the
-  // staging writes, and kept in LDS past the staged tile (a map lookup per
+  // staging writes, and kept in LDS past the staged tiles (a map lookup per
   // write-back pass would wait on global memory every pass).
-  int32_t* crow_tab = reinterpret_cast<int32_t*>(qw_smem + 256 * ROWB);
+  static_assert(2 * 256 * QWCfg<EPI_SWIGLU>::BN * 2 <= 128 * 1024 && 256 * QWCfg<EPI_STORE>::BN * 2 <= 128 * 1024,
+                "staged tiles below the row table");
+  int32_t* crow_tab = reinterpret_cast<int32_t*>(qw_smem + 128 * 1024);
+  char* stage_u = qw_smem + 256 * ROWB;   // second staged tile (u in the g|u pass)
   const int32_t my_crow = (g.c_map && tid < rows) ? g.c_map[row0 + tid] : row0 + tid;
   for (int pass = 0; pass < npass; ++pass) {
     // registers -> LDS
@@ -416,6 +422,13 @@ __global__ __launch_bounds__(256) void gemm_qw_kernel(const GemmDesc g0, const G
           w.x = pack_bf16x2(v[0], v[1]);
           w.y = pack_bf16x2(v[2], v[3]);
           *reinterpret_cast<uint2*>(qw_smem + m * ROWB + ((u ^ (m & 31)) << 3)) = w;
+          if (EPI == EPI_SWIGLU && gu2 && pass == 1) {
+            // u beside g
+            uint2 wu;
+            wu.x = pack_bf16x2(acc[NB - 1][j][ni][q * 4 + 0], acc[NB - 1][j][ni][q * 4 + 1]);
+            wu.y = pack_bf16x2(acc[NB - 1][j][ni][q * 4 + 2], acc[NB - 1][j][ni][q * 4 + 3]);
+            *reinterpret_cast<uint2*>(stage_u + m * ROWB + ((u ^ (m & 31)) << 3)) = wu;
+          }
         }
     }
     if (pass == 0) crow_tab[tid] = my_crow;
@@ -431,6 +444,16 @@ __global__ __launch_bounds__(256) void gemm_qw_kernel(const GemmDesc g0, const G
       if (r & 1) v = u32x4_t{v.z, v.w, v.x, v.y};
       if (n < g.N) {
         *reinterpret_cast<u32x4_t*>(C + (int64_t)crow_tab[r] * g.ldc + ccol + n) = v;
+      }
+    }
+    if (EPI == EPI_SWIGLU && gu2 && pass == 1) {
+      bf16_t* U = static_cast<bf16_t*>(g.Us);
+#pragma unroll 4
+      for (int r = rr; r < rows; r += RPP) {
+        const int pu = (2 * cc) ^ (r & 31);
+        u32x4_t v = *reinterpret_cast<const u32x4_t*>(stage_u + r * ROWB + ((pu >> 1) << 4));
+        if (r & 1) v = u32x4_t{v.z, v.w, v.x, v.y};
+        if (n < g.N) *reinterpret_cast<u32x4_t*>(U + (int64_t)crow_tab[r] * g.ldc + ccol + n) = v;
       }
     }
     if (pass + 1 < npass) qw_sync();
