@@ -29,13 +29,6 @@ int check_launch(const char* what) {
 }
 
 // ---------------------------------------------------------------- pointer tables
-constexpr int PTR_CHUNK = 480;  // pointers per upload launch (3.8 KB of the 4 KB kernel argument space)
-
-struct PtrChunk {
-  const void* p[PTR_CHUNK];
-  int32_t n;
-  int32_t off;
-};
 
 __global__ void set_ptrs_kernel(PtrChunk c, const void** dst) {
   for (int i = threadIdx.x; i < c.n; i += blockDim.x) dst[c.off + i] = c.p[i];
@@ -377,9 +370,22 @@ int dsmoe_moe_fwd(const void* x, const float* gate_w, const float* gate_bias, co
   const int64_t N = (int64_t)d.T * d.k;
   StageTimer tm(st);
 
+  // The weight pointer table goes to the device with the gate launch when it
+  // fits one argument chunk and the MFMA gate runs, else with its own launch.
+  const int ntab = 3 * d.E + 3 * d.S;
+  const bool tab_in_gate = ntab <= PTR_CHUNK && gate_uses_mfma(x, gate_w, d);
+  PtrChunk tabc;
+  tabc.n = 0;
+  tabc.off = 0;
   tm.begin(ST_TABLES);
-  rc = upload_ptr_lists({{w1, d.E}, {w3, d.E}, {w2, d.E}, {sw1, d.S}, {sw3, d.S}, {sw2, d.S}}, L.ptrs, st);
-  if (rc) return rc;
+  if (tab_in_gate) {
+    for (const auto& l : {std::make_pair(w1, d.E), std::make_pair(w3, d.E), std::make_pair(w2, d.E),
+                          std::make_pair(sw1, d.S), std::make_pair(sw3, d.S), std::make_pair(sw2, d.S)})
+      for (int i = 0; i < l.second; ++i) tabc.p[tabc.n++] = l.first[i];
+  } else {
+    rc = upload_ptr_lists({{w1, d.E}, {w3, d.E}, {w2, d.E}, {sw1, d.S}, {sw3, d.S}, {sw2, d.S}}, L.ptrs, st);
+    if (rc) return rc;
+  }
   const bool mf = all_aligned16(w1, d.E) && all_aligned16(w2, d.E) && all_aligned16(w3, d.E) &&
                   (d.S == 0 || (all_aligned16(sw1, d.S) && all_aligned16(sw2, d.S) && all_aligned16(sw3, d.S)));
 
@@ -387,7 +393,7 @@ int dsmoe_moe_fwd(const void* x, const float* gate_w, const float* gate_bias, co
   // (a) gate
   GateOut go{logits, L.idx, idx64, L.w, weights_x, L.sel, nullptr};
   tm.begin(ST_GATE);
-  rc = launch_gate(x, nullptr, gate_w, gate_bias, d, go, st, L.gate_part);
+  rc = launch_gate(x, nullptr, gate_w, gate_bias, d, go, st, L.gate_part, tab_in_gate ? &tabc : nullptr, L.ptrs);
   tm.end();
   if (rc) return rc;
   // GEMM descriptors; the routed schedule height follows the kernel choice

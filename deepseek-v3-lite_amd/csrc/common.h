@@ -143,10 +143,23 @@ struct PermuteScratch {
 };
 
 // ---------------------------------------------------------------- launchers
+// A chunk of a device pointer table passed by value as a kernel argument
+// (within the 4 KB argument space): dst[off + i] = p[i] for i < n.
+constexpr int PTR_CHUNK = 448;
+struct PtrChunk {
+  const void* p[PTR_CHUNK];
+  int32_t n;
+  int32_t off;
+};
+
 // part (optional): workspace of gate_part_floats(d) floats for a K-split gate
 // (partial logits, then a routing kernel); nullptr keeps one fused launch.
+// tables (optional, MFMA gate only): a pointer table written by the gate
+// launch itself (workgroup 0) into tab_dst, saving the upload launch.
 int launch_gate(const void* x, const float* logits_in, const float* gw, const float* bias, const dsmoe_dims& d,
-                const GateOut& out, hipStream_t st, float* part = nullptr);
+                const GateOut& out, hipStream_t st, float* part = nullptr, const PtrChunk* tables = nullptr,
+                const void** tab_dst = nullptr);
+bool gate_uses_mfma(const void* x, const float* gw, const dsmoe_dims& d);
 int gate_k_splits(const dsmoe_dims& d);
 size_t gate_part_floats(const dsmoe_dims& d);
 constexpr int GATE_KS_MAX = 16;      // K splits of the gate at most

@@ -62,7 +62,8 @@ __global__ __launch_bounds__(gm_waves(NT) * 64) void gate_mfma_kernel(const bf16
                                                                  const float* __restrict__ gw,
                                                                  const float* __restrict__ bias, int T, int D, int E,
                                                                  int k, float route_scale, GateOut out,
-                                                                 float* __restrict__ part_out, int ks) {
+                                                                 float* __restrict__ part_out, int ks,
+                                                                 const PtrChunk tables, const void** tab_dst) {
   constexpr int EP = NT * 32;
   constexpr int LDP = EP + 1;
   extern __shared__ float gsm[];
@@ -76,6 +77,8 @@ __global__ __launch_bounds__(gm_waves(NT) * 64) void gate_mfma_kernel(const bf16
   constexpr int NTW = (NT + TSTEP - 1) / TSTEP;       // expert tiles per wave (upper bound)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int quarter = wave & 3, tfirst = wave >> 2;
+  if (blockIdx.x == 0)
+    for (int i = threadIdx.x; i < tables.n; i += blockDim.x) tab_dst[tables.off + i] = tables.p[i];
   // K split (part_out != nullptr): block b takes token tile b / ks and the
   // K range of split b % ks, and writes partial logits instead of routing.
   const int split = part_out ? (int)(blockIdx.x % ks) : 0;
@@ -326,14 +329,17 @@ static int launch_gate_t(const void* x, const float* logits_in, const float* gw,
 
 template <int NT>
 static int launch_gate_mfma(const void* x, const float* gw, const float* bias, const dsmoe_dims& d, const GateOut& out,
-                            float* part, int ks, hipStream_t st) {
+                            float* part, int ks, hipStream_t st, const PtrChunk* tables, const void** tab_dst) {
+  PtrChunk none;
+  none.n = 0;
+  none.off = 0;
   const size_t lds = sizeof(float) * (4 * GM_TOK * (NT * 32 + 1) + d.E) + sizeof(int) * ((d.E + 3) & ~3);
   auto kern = gate_mfma_kernel<NT>;
   int rc = set_lds((const void*)kern, lds);
   if (rc) return rc;
   const int64_t blocks = cdiv(d.T, GM_TOK) * (part ? ks : 1);
   hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(gm_waves(NT) * 64), lds, st, static_cast<const bf16_t*>(x), gw,
-                     bias, d.T, d.D, d.E, d.k, d.route_scale, out, part, ks);
+                     bias, d.T, d.D, d.E, d.k, d.route_scale, out, part, ks, tables ? *tables : none, tab_dst);
   rc = check_launch("gate_mfma");
   if (rc || !part) return rc;
   const size_t rlds = sizeof(float) * (RP_TOK * (d.E + 1) + d.E) + sizeof(int) * d.E;
@@ -365,8 +371,12 @@ static bool gate_mfma_ok(const void* x, const float* gw, const dsmoe_dims& d) {
          (reinterpret_cast<uintptr_t>(gw) & 15) == 0;
 }
 
+bool gate_uses_mfma(const void* x, const float* gw, const dsmoe_dims& d) { return d.T > 0 && gate_mfma_ok(x, gw, d); }
+
 int launch_gate(const void* x, const float* logits_in, const float* gw, const float* bias, const dsmoe_dims& d,
-                const GateOut& out, hipStream_t st, float* part) {
+                const GateOut& out, hipStream_t st, float* part, const PtrChunk* tables, const void** tab_dst) {
+  if (tables && (logits_in || !gate_uses_mfma(x, gw, d)))
+    return fail(DSMOE_ERR_INVALID, "gate: a pointer table rides only with the MFMA gate");
   if (out.counts) {
     hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)cdiv(d.E, 256)), dim3(256), 0, st, out.counts, d.E, 0);
   }
@@ -378,11 +388,11 @@ int launch_gate(const void* x, const float* logits_in, const float* gw, const fl
     const int ks = part ? gate_k_splits(d) : 1;
     float* pp = ks > 1 ? part : nullptr;
     switch (nt) {
-      case 1: return launch_gate_mfma<1>(x, gw, bias, d, out, pp, ks, st);
-      case 2: return launch_gate_mfma<2>(x, gw, bias, d, out, pp, ks, st);
-      case 3: return launch_gate_mfma<3>(x, gw, bias, d, out, pp, ks, st);
-      case 4: return launch_gate_mfma<4>(x, gw, bias, d, out, pp, ks, st);
-      default: return launch_gate_mfma<8>(x, gw, bias, d, out, pp, ks, st);
+      case 1: return launch_gate_mfma<1>(x, gw, bias, d, out, pp, ks, st, tables, tab_dst);
+      case 2: return launch_gate_mfma<2>(x, gw, bias, d, out, pp, ks, st, tables, tab_dst);
+      case 3: return launch_gate_mfma<3>(x, gw, bias, d, out, pp, ks, st, tables, tab_dst);
+      case 4: return launch_gate_mfma<4>(x, gw, bias, d, out, pp, ks, st, tables, tab_dst);
+      default: return launch_gate_mfma<8>(x, gw, bias, d, out, pp, ks, st, tables, tab_dst);
     }
   }
   if (d.dtype == DSMOE_BF16) {
