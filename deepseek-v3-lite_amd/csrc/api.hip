@@ -377,19 +377,18 @@ int dsmoe_moe_fwd(const void* x, const float* gate_w, const float* gate_bias, co
   PtrChunk tabc;
   tabc.n = 0;
   tabc.off = 0;
-  tm.begin(ST_TABLES);
   if (tab_in_gate) {
     for (const auto& l : {std::make_pair(w1, d.E), std::make_pair(w3, d.E), std::make_pair(w2, d.E),
                           std::make_pair(sw1, d.S), std::make_pair(sw3, d.S), std::make_pair(sw2, d.S)})
       for (int i = 0; i < l.second; ++i) tabc.p[tabc.n++] = l.first[i];
   } else {
+    tm.begin(ST_TABLES);
     rc = upload_ptr_lists({{w1, d.E}, {w3, d.E}, {w2, d.E}, {sw1, d.S}, {sw3, d.S}, {sw2, d.S}}, L.ptrs, st);
+    tm.end();
     if (rc) return rc;
   }
   const bool mf = all_aligned16(w1, d.E) && all_aligned16(w2, d.E) && all_aligned16(w3, d.E) &&
                   (d.S == 0 || (all_aligned16(sw1, d.S) && all_aligned16(sw2, d.S) && all_aligned16(sw3, d.S)));
-
-  tm.end();
   // (a) gate
   GateOut go{logits, L.idx, idx64, L.w, weights_x, L.sel, nullptr};
   tm.begin(ST_GATE);
