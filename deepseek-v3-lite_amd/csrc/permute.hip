@@ -55,15 +55,22 @@ __global__ __launch_bounds__(256) void rank_kernel(const int32_t* __restrict__ i
   rank_experts<KB>(idx, T, k, E, blockIdx.x, threadIdx.x >> 6, blockDim.x >> 6, blockhist, local_rank);
 }
 
-// Inclusive prefix sum over the 64 lanes of a wave (exact integer adds).
-__device__ __forceinline__ int32_t wave_incl_scan(int32_t x, int lane) {
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int32_t y = __shfl_up(x, d, 64);
-    if (lane >= d) x += y;
-  }
+// Inclusive prefix sum over the 64 lanes of a wave (exact integer adds), on
+// DPP: row (16-lane) shifts by 1, 2, 4, 8 (lanes without a source add 0),
+// then the row broadcasts of lane 15 (into rows 1 and 3) and lane 31 (into
+// rows 2 and 3).
+__device__ __forceinline__ int32_t wave_incl_scan(int32_t x, int /*lane*/) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31
   return x;
 }
+
+// Lane 63's value in every lane.
+__device__ __forceinline__ int32_t wave_last(int32_t x) { return __builtin_amdgcn_readlane(x, 63); }
 
 // Scan over the block histograms by one workgroup.  LDS sh: cnt[E],
 // off[E+1], tiles[E+1].  Wave w scans experts w, w + nw, ...: lane b holds
@@ -104,7 +111,7 @@ __device__ __forceinline__ void scan_body(const int32_t* __restrict__ blockhist,
         if (c == 0) carry = 0;
         const int32_t x = wave_incl_scan(v[i], lane);
         if (b < nb) blockbase[(int64_t)b * E + e] = carry + x - v[i];
-        carry += __shfl(x, 63, 64);
+        carry += wave_last(x);
         if (c == nch - 1 && lane == 0) cnt[e] = carry;
       }
     }
@@ -116,7 +123,7 @@ __device__ __forceinline__ void scan_body(const int32_t* __restrict__ blockhist,
         const int32_t v = b < nb ? blockhist[(int64_t)b * E + e] : 0;
         const int32_t x = wave_incl_scan(v, lane);
         if (b < nb) blockbase[(int64_t)b * E + e] = carry + x - v;
-        carry += __shfl(x, 63, 64);
+        carry += wave_last(x);
       }
       if (lane == 0) cnt[e] = carry;
     }
@@ -133,8 +140,8 @@ __device__ __forceinline__ void scan_body(const int32_t* __restrict__ blockhist,
         off[e] = co + xo - c;
         til[e] = ct + xt - tc;
       }
-      co += __shfl(xo, 63, 64);
-      ct += __shfl(xt, 63, 64);
+      co += wave_last(xo);
+      ct += wave_last(xt);
     }
     if (lane == 0) {
       off[E] = co;
