@@ -219,6 +219,9 @@ def _moe_fwd_setup(ctx, inputs, output):
     x, gate_w, gate_bias, weights, E, S, k, I, I_s, rs, training = inputs
     ctx.meta = (E, S, k, I, I_s, rs, training)
     ctx.save_for_backward(x, gate_w, output[4], *weights)
+    # only y carries a gradient; without this autograd would materialise zero
+    # gradients for the other outputs, the workspace included (GBs per step)
+    ctx.set_materialize_grads(False)
 
 
 def _moe_fwd_backward(ctx, dy, _didx, _dwx, _dcounts, _dws):
