@@ -507,22 +507,23 @@ static BwdLayout bwd_layout(const dsmoe_dims& d, void* base) {
   BwdLayout B;
   const int64_t N = (int64_t)d.T * d.k;
   const int es = elem_size(d.dtype);
-  // pointer tables: each group is one contiguous block (uploaded in one call)
-  const void** rt = c.take<const void*>(5 * d.E);
+  // pointer tables: one contiguous block, routed weights, shared weights,
+  // routed gradients, shared gradients (uploaded in one call, in this order)
+  const void** rt = c.take<const void*>(8 * d.E + 8 * d.S);
   B.w1 = rt;
   B.w3 = rt + d.E;
   B.w2 = rt + 2 * d.E;
   B.w13 = rt + 3 * d.E;
-  const void** st = c.take<const void*>(5 * d.S + 1);
+  const void** st = rt + 5 * d.E;
   B.sw1 = st;
   B.sw3 = st + d.S;
   B.sw2 = st + 2 * d.S;
   B.sw13 = st + 3 * d.S;
-  void** ro = c.take<void*>(3 * d.E);
+  void** ro = const_cast<void**>(st + 5 * d.S);
   B.dw1 = ro;
   B.dw3 = ro + d.E;
   B.dw2 = ro + 2 * d.E;
-  void** so = c.take<void*>(3 * d.S + 1);
+  void** so = ro + 3 * d.E;
   B.dsw1 = so;
   B.dsw3 = so + d.S;
   B.dsw2 = so + 2 * d.S;
@@ -600,16 +601,13 @@ int dsmoe_moe_bwd(const void* x, const float* gate_w, const void* const* w1, con
                                 all_aligned16((const void* const*)dsw2, d.S) &&
                                 all_aligned16((const void* const*)dsw3, d.S)));
   tm.begin(ST_BWD_PREP);
-  // each table group is contiguous in the workspace, in this order
-  rc = upload_ptr_lists({{w1, d.E}, {w3, d.E}, {w2, d.E}, {w13h.data(), 2 * d.E}}, B.w1, st);
-  if (!rc && d.S) rc = upload_ptr_lists({{sw1, d.S}, {sw3, d.S}, {sw2, d.S}, {sw13h.data(), 2 * d.S}}, B.sw1, st);
-  if (!rc)
-    rc = upload_ptr_lists({{(const void* const*)dw1, d.E}, {(const void* const*)dw3, d.E}, {(const void* const*)dw2, d.E}},
-                          (const void**)B.dw1, st);
-  if (!rc && d.S)
-    rc = upload_ptr_lists({{(const void* const*)dsw1, d.S}, {(const void* const*)dsw3, d.S},
-                           {(const void* const*)dsw2, d.S}},
-                          (const void**)B.dsw1, st);
+  // the four table groups are one contiguous block, in this order
+  rc = upload_ptr_lists({{w1, d.E}, {w3, d.E}, {w2, d.E}, {w13h.data(), 2 * d.E},
+                         {sw1, d.S}, {sw3, d.S}, {sw2, d.S}, {sw13h.data(), 2 * d.S},
+                         {(const void* const*)dw1, d.E}, {(const void* const*)dw3, d.E}, {(const void* const*)dw2, d.E},
+                         {(const void* const*)dsw1, d.S}, {(const void* const*)dsw3, d.S},
+                         {(const void* const*)dsw2, d.S}},
+                        B.w1, st);
   if (rc) return rc;
   // gate gradient path: d weights -> d logits
   rc = launch_prep_tok(dy, F.o_slots, F.w, F.slot_pos, d.T, d.k, d.D, d.dtype, B.dw, B.dy_w, st);
