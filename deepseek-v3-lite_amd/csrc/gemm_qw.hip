@@ -3,28 +3,28 @@
 // stream in with direct global->LDS loads.
 //
 // Same contract and tile enumeration as gemm_mfma_kernel (gemm.hip).  The
-// shape follows from three gfx950 limits measured on MI355X:
-//  * L2 -> LDS direct loads are request-bound: a 64-byte row piece moves half
-//    the bytes per request of a 128-byte piece.  K therefore advances in slabs
-//    of 64 bf16 (one 128-byte cache line per row and operand).
-//  * LDS bandwidth (about 128 B/clk/CU): a 128 x 128 wave tile reads 8
-//    fragments per 16 MFMAs, against 12 for the 64 x 128 tiles of an 8-wave
-//    layout; with the direct-load writes this keeps LDS near 70 % busy at
-//    full MFMA rate.
+// shape follows from gfx950 limits measured on MI355X:
+//  * 512 VGPRs per lane: a 128 x 128 wave tile (256 accumulator registers)
+//    is the largest a wave can hold, and it reads the fewest LDS bytes per
+//    MFMA (8 fragments per 16 MFMAs).  It leaves room for one wave per SIMD.
+//  * L2 -> LDS direct loads move whole 128-byte rows best, so K advances in
+//    slabs of 64 bf16 (one cache line per row and operand).
 //  * 160 KB of LDS: a slab is 32 KB per operand (256 rows of 128 bytes).  A
 //    (activation rows, mostly L2 / MALL hits) cycles through a ring of two
-//    slots, B (weights, streamed from HBM) through a ring of three, so B
-//    loads are issued a slab earlier than A loads.
+//    slots, B (weights, streamed from HBM) through a ring of three.
 //
 // Per slab kb a wave runs four 16-wide K steps.  Fragments are read two steps
 // ahead of their MFMAs through three register sets, so LDS latency hides
 // behind MFMAs.  After the MFMAs of step 1 each wave waits for its LDS reads
 // of slab kb and its own direct loads of slab kb + 1; the workgroup barrier
-// then makes slab kb + 1 visible and frees slab kb's slots, into which A of
-// slab kb + 2 and B of slab kb + 3 are loaded, one direct load after every
-// second MFMA of steps 2 and 3.  Loads past the last slab re-read the last slab into the free slot
-// (never read), so the loop body has no branches and the wait counts stay
-// exact; they are drained before the epilogue.
+// then makes slab kb + 1 visible and frees slab kb's slots.  The refills of
+// slab kb + 2 are spread over the whole slab: B(kb + 2) during steps 0 and 1
+// (into slab kb - 1's slot, freed by the previous barrier), A(kb + 2) during
+// steps 2 and 3, four loads per step, one after every fourth MFMA.  Loads are
+// addressed as a wave-uniform base in SGPRs plus 32-bit per-lane offsets.
+// Loads past the last slab re-read the last slab into the free slot (never
+// read), so the loop body has no branches and the wait counts stay exact;
+// they are drained before the epilogue.
 //
 // Ragged tiles: the wave in row group wm owns the 32-row sub-tiles wm,
 // wm + 2, wm + 4 and wm + 6 of the block, so the valid rows of a partly
@@ -62,41 +62,39 @@ struct QWCfg {
   static constexpr int BN = (EPI == EPI_SWIGLU) ? 128 : 256;  // output columns per block
 };
 
-// Direct-load sources of one wave (wave-uniform bases, per-lane offsets).
-// Wave w fills rows 64 w .. 64 w + 63 of both operand regions of a slab.
+// Direct-load sources of one wave (wave-uniform bases, per-lane byte
+// offsets).  Wave w fills rows 64 w .. 64 w + 63 of both operand regions of
+// a slab.
 struct QWLoad {
-  const bf16_t* a;         // A
-  const bf16_t* b0;        // this wave's B table entry, K segment 0
-  const bf16_t* b1;        // last K segment
-  uint32_t offa[QW_LD];    // per-lane element offsets of the 8 A loads
+  const char* a;           // A
+  const char* b0;          // this wave's B table entry, K segment 0
+  const char* b1;          // last K segment
+  uint32_t offa[QW_LD];    // per-lane byte offsets of the 8 A loads
   uint32_t offb[QW_LD];    // and of the 8 B loads
   int kseg;                // K at which b1 takes over (0x7fffffff: one segment)
   int lds_off;             // byte offset of this wave's 8 KB inside an operand region
   int nk;                  // number of slabs
 };
 
-// Direct loads I0 .. I1-1 of this wave for A of slab ka (ring slot ka % 2),
-// and for B of slab kb (slot kb % 3).  Past the last slab the last slab is
-// reloaded into the (free) slot instead.
-template <int I0, int I1>
-__device__ __forceinline__ void qw_issue_a(const QWLoad& L, int ka) {
+// Direct load i (0 .. 7) of this wave for A of slab ka (ring slot ka % 2) /
+// for B of slab kb (slot kb % 3).  Past the last slab the last slab is
+// reloaded into the (free) slot instead, so the loop body has no branches and
+// the wait counts stay exact.
+__device__ __forceinline__ void qw_load_a(const QWLoad& L, int ka, int i) {
   extern __shared__ __attribute__((aligned(16))) char qw_smem[];
   const uint32_t da = lds_addr(qw_smem) + L.lds_off + (ka & 1) * QW_REG;
   const int k0 = min(ka, L.nk - 1) * QW_BK;
-#pragma unroll
-  for (int i = I0; i < I1; ++i) dma16(L.a + L.offa[i] + k0, da + i * 1024);
+  dma16s(L.a + 2 * k0, L.offa[i], da + i * 1024);
 }
 
-template <int I0, int I1>
-__device__ __forceinline__ void qw_issue_b(const QWLoad& L, int kb) {
+__device__ __forceinline__ void qw_load_b(const QWLoad& L, int kb, int i) {
   extern __shared__ __attribute__((aligned(16))) char qw_smem[];
   const uint32_t db = lds_addr(qw_smem) + L.lds_off + QW_BOFF + (kb % QW_BSLOTS) * QW_REG;
   const int k0 = min(kb, L.nk - 1) * QW_BK;
   const bool hi = k0 >= L.kseg;
-  const bf16_t* src = hi ? L.b1 : L.b0;
+  const char* src = hi ? L.b1 : L.b0;
   const int kin = hi ? k0 - L.kseg : k0;
-#pragma unroll
-  for (int i = I0; i < I1; ++i) dma16(src + L.offb[i] + kin, db + i * 1024);
+  dma16s(src + 2 * kin, L.offb[i], db + i * 1024);
 }
 
 // Fragments of K step s (0..3) of slab kb: A sub-tiles j < NMI (rows
@@ -123,58 +121,26 @@ __device__ __forceinline__ void qw_read(int kb, int s, int wm, int wn, int lane,
   }
 }
 
-// MFMAs T0 .. T1-1 of one K step, in the order t = (j * NB + b) * TN + ni.
-template <int EPI, int NMI, int T0 = 0, int T1 = NMI * QWCfg<EPI>::NB * QWCfg<EPI>::TN>
+// MFMAs T0 .. T1-1 of one K step (MMAS per step, in the order
+// t = (j * NB + b) * TN + ni).  With NL > 0, load i of the step's NL direct
+// loads (index LI0 + i of A (LK 0) or B (LK 1) of slab kl) follows MFMA
+// floor(i * MMAS / NL), so the loads are spread evenly over the step.
+template <int EPI, int NMI, int T0, int T1, int NL, int LK, int LI0>
 __device__ __forceinline__ void qw_mma(const bf16x8_t (&fa)[4], const bf16x8_t (&fb)[QWCfg<EPI>::NB][QWCfg<EPI>::TN],
-                                       f32x16_t (&acc)[QWCfg<EPI>::NB][4][QWCfg<EPI>::TN]) {
-  using CF = QWCfg<EPI>;
-#pragma unroll
-  for (int t = T0; t < T1; ++t) {
-    const int j = t / (CF::NB * CF::TN), b = (t / CF::TN) % CF::NB, ni = t % CF::TN;
-    acc[b][j][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[b][ni], fa[j], acc[b][j][ni], 0, 0, 0);
-  }
-}
-
-// Refill load i (0 .. 2 QW_LD - 1) of slab kb's freed slots: A(kb + 2) for
-// i < QW_LD, then B(kb + 3).
-__device__ __forceinline__ void qw_issue_one(const QWLoad& L, int kb, int i) {
-  extern __shared__ __attribute__((aligned(16))) char qw_smem[];
-  if (i < QW_LD) {
-    const uint32_t da = lds_addr(qw_smem) + L.lds_off + (kb & 1) * QW_REG;
-    const int k0 = min(kb + 2, L.nk - 1) * QW_BK;
-    dma16(L.a + L.offa[i] + k0, da + i * 1024);
-  } else {
-    const uint32_t db = lds_addr(qw_smem) + L.lds_off + QW_BOFF + ((kb + 3) % QW_BSLOTS) * QW_REG;
-    const int k0 = min(kb + 3, L.nk - 1) * QW_BK;
-    const bool hi = k0 >= L.kseg;
-    const bf16_t* src = hi ? L.b1 : L.b0;
-    const int kin = hi ? k0 - L.kseg : k0;
-    dma16(src + L.offb[i - QW_LD] + kin, db + (i - QW_LD) * 1024);
-  }
-}
-
-// MFMAs T0 .. T1-1 of one K step of steps 2-3 (BASE: index of the step's
-// first MFMA within steps 2-3), each followed by its share of the refill
-// loads: MFMA g of the 2 MMAS is followed by loads [g n / 2 MMAS, (g + 1) n /
-// 2 MMAS), n = 2 QW_LD.
-template <int EPI, int NMI, int BASE, int T0, int T1>
-__device__ __forceinline__ void qw_mma_refill(const bf16x8_t (&fa)[4], const bf16x8_t (&fb)[QWCfg<EPI>::NB][QWCfg<EPI>::TN],
-                                              f32x16_t (&acc)[QWCfg<EPI>::NB][4][QWCfg<EPI>::TN], const QWLoad& L,
-                                              int kb) {
+                                       f32x16_t (&acc)[QWCfg<EPI>::NB][4][QWCfg<EPI>::TN], const QWLoad& L, int kl) {
   using CF = QWCfg<EPI>;
   constexpr int MMAS = NMI * CF::NB * CF::TN;
-  constexpr int NL = 2 * QW_LD;
 #pragma unroll
   for (int t = T0; t < T1; ++t) {
     const int j = t / (CF::NB * CF::TN), b = (t / CF::TN) % CF::NB, ni = t % CF::TN;
     acc[b][j][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[b][ni], fa[j], acc[b][j][ni], 0, 0, 0);
-    const int g = BASE + t;
-    const int l0 = g * NL / (2 * MMAS), l1 = (g + 1) * NL / (2 * MMAS);
-    if (l1 > l0) {
-      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = l0; i < l1; ++i) qw_issue_one(L, kb, i);
-      __builtin_amdgcn_sched_barrier(0);
+    for (int i = 0; i < NL; ++i) {
+      if ((i * MMAS / (NL > 0 ? NL : 1)) == t) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (LK == 0) qw_load_a(L, kl, LI0 + i); else qw_load_b(L, kl, LI0 + i);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
   }
 }
@@ -185,16 +151,10 @@ __device__ __forceinline__ void qw_sync() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// Main loop for a wave with NMI active row sub-tiles.  On entry slab 0 is
-// visible to every wave, and A of slab 1 and B of slabs 1 and 2 are in
-// flight, in that order.
-//
 // Fragment reads run two K steps ahead of their MFMAs through three register
 // sets (step t of the kernel uses set t % 3; the four steps of a slab rotate
 // through the sets, so the roles shift by one set per slab and the loop body
-// covers three slabs).  The workgroup barrier of slab kb sits after its step
-// 1: by then the reads of steps 2 and 3 of slab kb are in flight and can be
-// waited for, and the reads of slab kb + 1 may start.
+// covers three slabs).
 template <int EPI, int NMI>
 struct QWPipe {
   using CF = QWCfg<EPI>;
@@ -207,61 +167,82 @@ __device__ __forceinline__ void qw_read_set(QWPipe<EPI, NMI>& P, int kb, int s, 
   qw_read<EPI, NMI>(kb, s, wm, wn, lane, P.fa[SET], P.fb[SET]);
 }
 
-// One slab whose step 0 uses register set S0 (steps use S0, S0+1, S0+2, S0 mod 3).
+// One slab; its step 0 uses register set S0 (steps use S0, S0+1, S0+2, S0
+// mod 3).  On entry slab kb is visible to every wave and this wave's loads of
+// A(kb + 1) and B(kb + 1) are in flight (older ones complete).
+//
+// The refill loads of slab kb + 2 are spread over the whole slab, four after
+// every quarter of a K step's MFMAs: B(kb + 2) during steps 0 and 1 (its slot,
+// that of slab kb - 1, was freed by the previous barrier) and A(kb + 2) during
+// steps 2 and 3 (its slot is slab kb's, freed by this slab's barrier).  Load
+// bursts stall the issuing wave while the L2 -> LDS path drains, and with one
+// wave per SIMD a stalled wave idles its MFMA pipe; spread over all four steps
+// the path runs at half the rate of a two-step spread.
+//
+// The barrier sits after step 1: by then every read of slab kb has been
+// issued (steps 2 and 3 are read during steps 0 and 1); the wave waits for
+// them and for its own loads of slab kb + 1 (only the 8 B(kb + 2) loads are
+// younger), and after the barrier slab kb + 1 is visible and slab kb's slots
+// are free.
 template <int EPI, int NMI, int S0>
 __device__ __forceinline__ void qw_slab(QWPipe<EPI, NMI>& P, const QWLoad& L, int kb, int wm, int wn, int lane,
                                         f32x16_t (&acc)[QWCfg<EPI>::NB][4][QWCfg<EPI>::TN]) {
   using CF = QWCfg<EPI>;
-  constexpr int MMAS = NMI * CF::NB * CF::TN;   // MFMAs per K step
+  constexpr int MMAS = NMI * CF::NB * CF::TN;  // MFMAs per K step
   constexpr int A0 = S0 % 3, A1 = (S0 + 1) % 3, A2 = (S0 + 2) % 3;
-  // step 0: read step 2
+  constexpr int NL = QW_LD / 2;                // direct loads per K step
+  // step 0: read step 2, B(kb + 2) loads 0-3
   __builtin_amdgcn_sched_barrier(0);
   qw_read_set<EPI, NMI, A2>(P, kb, 2, wm, wn, lane);
   __builtin_amdgcn_sched_barrier(0);
-  qw_mma<EPI, NMI>(P.fa[A0], P.fb[A0], acc);
-  // step 1: read step 3 (into the set step 0 just used)
+  if constexpr (MMAS > 0) {
+    qw_mma<EPI, NMI, 0, MMAS, NL, 1, 0>(P.fa[A0], P.fb[A0], acc, L, kb + 2);
+  } else {
+#pragma unroll
+    for (int i = 0; i < NL; ++i) qw_load_b(L, kb + 2, i);
+  }
+  // step 1: read step 3 (into the set step 0 just used), B(kb + 2) loads 4-7
   __builtin_amdgcn_sched_barrier(0);
   qw_read_set<EPI, NMI, A0>(P, kb, 3, wm, wn, lane);
   __builtin_amdgcn_sched_barrier(0);
-  qw_mma<EPI, NMI>(P.fa[A1], P.fb[A1], acc);
+  if constexpr (MMAS > 0) {
+    qw_mma<EPI, NMI, 0, MMAS, NL, 1, NL>(P.fa[A1], P.fb[A1], acc, L, kb + 2);
+  } else {
+#pragma unroll
+    for (int i = 0; i < NL; ++i) qw_load_b(L, kb + 2, NL + i);
+  }
   __builtin_amdgcn_sched_barrier(0);
-  // Every read of slab kb has been issued; wait for them, and for this
-  // wave's loads of A and B of slab kb + 1: each slab issues A(kb + 2) before
-  // B(kb + 3), so only the 8 loads of B(kb + 2) may be younger and still in
-  // flight.  After the barrier slab kb + 1 is visible and the slots of slab
-  // kb are free for A of kb + 2 and B of kb + 3.
   wait_lgkm0();
   wait_vm<QW_LD>();
   qw_sync();
-  // Steps 2 and 3 refill the freed slots, A(kb + 2) first, then B(kb + 3),
-  // with the 16 direct loads spread evenly over their MFMAs (bursts of loads
-  // stall the wave at issue while the L2 -> LDS path drains, and with one
-  // wave per SIMD a stalled wave idles its MFMA pipe).  Step 0 of slab kb + 1
-  // is read after the first four MFMAs of step 2 (into the set step 1 used),
-  // step 1 of kb + 1 before step 3 (into the set step 2 used).
+  // steps 2 and 3: A(kb + 2) loads; step 0 of slab kb + 1 is read after the
+  // first four MFMAs of step 2 (into the set step 1 used), step 1 of kb + 1
+  // before step 3 (into the set step 2 used)
   if constexpr (MMAS > 0) {
     constexpr int H = MMAS < 4 ? MMAS : 4;
-    qw_mma_refill<EPI, NMI, 0, 0, H>(P.fa[A2], P.fb[A2], acc, L, kb);
+    qw_mma<EPI, NMI, 0, H, NL, 0, 0>(P.fa[A2], P.fb[A2], acc, L, kb + 2);
     __builtin_amdgcn_sched_barrier(0);
     qw_read_set<EPI, NMI, A1>(P, kb + 1, 0, wm, wn, lane);
     __builtin_amdgcn_sched_barrier(0);
-    qw_mma_refill<EPI, NMI, 0, H, MMAS>(P.fa[A2], P.fb[A2], acc, L, kb);
+    qw_mma<EPI, NMI, H, MMAS, NL, 0, 0>(P.fa[A2], P.fb[A2], acc, L, kb + 2);
     __builtin_amdgcn_sched_barrier(0);
     qw_read_set<EPI, NMI, A2>(P, kb + 1, 1, wm, wn, lane);
     __builtin_amdgcn_sched_barrier(0);
-    qw_mma_refill<EPI, NMI, MMAS, 0, MMAS>(P.fa[A0], P.fb[A0], acc, L, kb);
+    qw_mma<EPI, NMI, 0, MMAS, NL, 0, NL>(P.fa[A0], P.fb[A0], acc, L, kb + 2);
   } else {
-    qw_issue_a<0, QW_LD>(L, kb + 2);
-    qw_issue_b<0, QW_LD>(L, kb + 3);
+#pragma unroll
+    for (int i = 0; i < QW_LD; ++i) qw_load_a(L, kb + 2, i);
   }
 }
 
+// Main loop for a wave with NMI active row sub-tiles.  On entry slab 0 is
+// visible to every wave and A(1), B(1) are in flight.  No scalar load may be
+// in flight at the loop head: scalar loads return out of order, and a pending
+// one would turn every LDS wait in the loop into a full drain.
 template <int EPI, int NMI>
 __device__ __forceinline__ void qw_loop(const QWLoad& L, int wm, int wn, int lane,
                                         f32x16_t (&acc)[QWCfg<EPI>::NB][4][QWCfg<EPI>::TN]) {
-  // Slab kb's step 0 uses set (4 kb) % 3 = kb % 3.  No scalar load may be in
-  // flight at the loop head: scalar loads return out of order, and a pending
-  // one would turn every LDS wait in the loop into a full drain.
+  // slab kb's step 0 uses set (4 kb) % 3 = kb % 3
   QWPipe<EPI, NMI> P;
   qw_read_set<EPI, NMI, 0>(P, 0, 0, wm, wn, lane);
   qw_read_set<EPI, NMI, 1>(P, 0, 1, wm, wn, lane);
@@ -315,11 +296,11 @@ __global__ __launch_bounds__(256) void gemm_qw_kernel(const GemmDesc g0, const G
   QWLoad L;
   L.nk = g.K / QW_BK;
   L.lds_off = wave * QW_LD * 1024;
-  L.a = static_cast<const bf16_t*>(g.A);
+  L.a = static_cast<const char*>(g.A);
   {
     const void* const* tab = ((NB == 2 && wave >= 2) ? g.B1 : g.B0) + (int64_t)grp * g.nseg;
-    L.b0 = static_cast<const bf16_t*>(tab[0]);
-    L.b1 = static_cast<const bf16_t*>(tab[g.nseg - 1]);
+    L.b0 = static_cast<const char*>(tab[0]);
+    L.b1 = static_cast<const char*>(tab[g.nseg - 1]);
     L.kseg = g.nseg > 1 ? g.kseg : 0x7fffffff;
   }
 #pragma unroll
@@ -328,9 +309,9 @@ __global__ __launch_bounds__(256) void gemm_qw_kernel(const GemmDesc g0, const G
     const int c = (lane & 7) ^ ((r >> 1) & 7);
     const int ra = min(r, rows - 1);
     const int64_t arow = g.a_map ? (int64_t)g.a_map[row0 + ra] : (int64_t)(row0 + ra);
-    L.offa[i] = (uint32_t)(arow * g.lda + c * 8);
+    L.offa[i] = (uint32_t)(2 * (arow * g.lda + c * 8));
     const int bn = (NB == 2) ? n0 + (r & 127) : n0 + r;
-    L.offb[i] = (uint32_t)((int64_t)min(bn, g.N - 1) * g.ldb + c * 8);
+    L.offb[i] = (uint32_t)(2 * ((int64_t)min(bn, g.N - 1) * g.ldb + c * 8));
   }
 
   f32x16_t acc[NB][4][TN];
@@ -343,15 +324,19 @@ __global__ __launch_bounds__(256) void gemm_qw_kernel(const GemmDesc g0, const G
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[b][j][ni][r] = 0.0f;
 
-  // ---- prologue: slab 0 visible to all waves; then A(1), B(1), B(2) in
-  // flight, in that order
-  qw_issue_a<0, QW_LD>(L, 0);
-  qw_issue_b<0, QW_LD>(L, 0);
-  wait_vm<0>();
+  // ---- prologue: A(0), B(0) and A(1), B(1) in flight together (slab 1 is
+  // the last slab reloaded when there is only one); slab 0 visible to all
+  // waves
+#pragma unroll
+  for (int i = 0; i < QW_LD; ++i) qw_load_a(L, 0, i);
+#pragma unroll
+  for (int i = 0; i < QW_LD; ++i) qw_load_b(L, 0, i);
+#pragma unroll
+  for (int i = 0; i < QW_LD; ++i) qw_load_a(L, 1, i);
+#pragma unroll
+  for (int i = 0; i < QW_LD; ++i) qw_load_b(L, 1, i);
+  wait_vm<2 * QW_LD>();
   qw_sync();
-  qw_issue_a<0, QW_LD>(L, 1);
-  qw_issue_b<0, QW_LD>(L, 1);
-  qw_issue_b<0, QW_LD>(L, 2);
 
   // active sub-tiles of this wave: j with (2j + wm) * 32 < rows
   const int nsub = (int)cdiv(rows, 32);

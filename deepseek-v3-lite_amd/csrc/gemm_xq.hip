@@ -193,32 +193,24 @@ __device__ __forceinline__ void xq_mma(const bf16x8_t (&fa)[4], const bf16x8_t (
     acc[t / 4][t % 4] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[t % 4], fa[t / 4], acc[t / 4][t % 4], 0, 0, 0);
 }
 
-// MFMAs T0 .. T1-1 of one K step of steps 2-3 (BASE: index of the step's
-// first MFMA within steps 2-3), each followed by its share of the refill
-// loads A(kb + 2) (loads 0 .. XQ_LD-1) and B(kb + 3): MFMA g of the 2 MMAS is
-// followed by loads [g n / 2 MMAS, (g + 1) n / 2 MMAS), n = 2 XQ_LD.
-template <int AMODE, int NMI, int BASE, int T0, int T1>
-__device__ __forceinline__ void xq_mma_refill(const bf16x8_t (&fa)[4], const bf16x8_t (&fb)[4], f32x16_t (&acc)[4][4],
-                                              const XQLoad& L, int kb, int lane) {
+// MFMAs T0 .. T1-1 of one K step (MMAS per step, t = j * 4 + ni).  With
+// NL > 0, load i of the step's NL direct loads (index LI0 + i of A (LK 0) or
+// B (LK 1) of slab kl) follows MFMA floor(i * MMAS / NL).
+template <int AMODE, int NMI, int T0, int T1, int NL, int LK, int LI0>
+__device__ __forceinline__ void xq_mma_ld(const bf16x8_t (&fa)[4], const bf16x8_t (&fb)[4], f32x16_t (&acc)[4][4],
+                                          const XQLoad& L, int kl, int lane) {
   constexpr int MMAS = NMI * 4;
-  constexpr int NL = 2 * XQ_LD;
   constexpr int BM = AMODE == XA_ROWS ? XB_W_NN : XB_ACT_KMAJOR;
 #pragma unroll
   for (int t = T0; t < T1; ++t) {
     acc[t / 4][t % 4] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[t % 4], fa[t / 4], acc[t / 4][t % 4], 0, 0, 0);
-    const int g = BASE + t;
-    const int l0 = g * NL / (2 * MMAS), l1 = (g + 1) * NL / (2 * MMAS);
-    if (l1 > l0) {
-      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = l0; i < l1; ++i) {
-        if (i < XQ_LD) {
-          xq_issue_a_one<AMODE>(L, kb + 2, lane, i);
-        } else {
-          xq_issue_b_one<BM>(L, kb + 3, lane, i - XQ_LD);
-        }
+    for (int i = 0; i < NL; ++i) {
+      if ((i * MMAS / (NL > 0 ? NL : 1)) == t) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (LK == 0) xq_issue_a_one<AMODE>(L, kl, lane, LI0 + i); else xq_issue_b_one<BM>(L, kl, lane, LI0 + i);
+        __builtin_amdgcn_sched_barrier(0);
       }
-      __builtin_amdgcn_sched_barrier(0);
     }
   }
 }
@@ -234,44 +226,56 @@ struct XQPipe {
   bf16x8_t fb[3][4];
 };
 
-// One slab whose step 0 uses register set S0 (see qw_slab in gemm_qw.hip:
-// reads run two steps ahead; the barrier follows step 1; steps 2 and 3 load
-// A(kb + 2) and B(kb + 3) into the slots slab kb frees).
+// One slab whose step 0 uses register set S0 (the schedule of qw_slab in
+// gemm_qw.hip: reads run two steps ahead; the barrier follows step 1; the
+// refills of slab kb + 2 are spread over the slab, B(kb + 2) during steps 0
+// and 1 into slab kb - 1's slot, A(kb + 2) during steps 2 and 3 into slab
+// kb's).
 template <int AMODE, int NMI, int S0>
 __device__ __forceinline__ void xq_slab(XQPipe& P, const XQLoad& L, int kb, int wm, int wn, int lane,
                                         f32x16_t (&acc)[4][4]) {
   constexpr int MMAS = NMI * 4;
   constexpr int A0 = S0 % 3, A1 = (S0 + 1) % 3, A2 = (S0 + 2) % 3;
+  constexpr int NL = XQ_LD / 2;
+  constexpr int BM = AMODE == XA_ROWS ? XB_W_NN : XB_ACT_KMAJOR;
   __builtin_amdgcn_sched_barrier(0);
   xq_read<AMODE, NMI>(kb, 2, wm, wn, lane, P.fa[A2], P.fb[A2]);
   __builtin_amdgcn_sched_barrier(0);
-  xq_mma<NMI>(P.fa[A0], P.fb[A0], acc);
+  if constexpr (MMAS > 0) {
+    xq_mma_ld<AMODE, NMI, 0, MMAS, NL, 1, 0>(P.fa[A0], P.fb[A0], acc, L, kb + 2, lane);
+  } else {
+#pragma unroll
+    for (int i = 0; i < NL; ++i) xq_issue_b_one<BM>(L, kb + 2, lane, i);
+  }
   __builtin_amdgcn_sched_barrier(0);
   xq_read<AMODE, NMI>(kb, 3, wm, wn, lane, P.fa[A0], P.fb[A0]);
   __builtin_amdgcn_sched_barrier(0);
-  xq_mma<NMI>(P.fa[A1], P.fb[A1], acc);
+  if constexpr (MMAS > 0) {
+    xq_mma_ld<AMODE, NMI, 0, MMAS, NL, 1, NL>(P.fa[A1], P.fb[A1], acc, L, kb + 2, lane);
+  } else {
+#pragma unroll
+    for (int i = 0; i < NL; ++i) xq_issue_b_one<BM>(L, kb + 2, lane, NL + i);
+  }
   __builtin_amdgcn_sched_barrier(0);
   // all reads of slab kb issued: wait for them and for this wave's loads of
-  // A(kb + 1) and B(kb + 1) (only B(kb + 2), issued after A(kb + 1), may be
-  // younger); then slab kb + 1 is visible and slab kb's slots are free
+  // A(kb + 1) and B(kb + 1) (only the 8 B(kb + 2) loads are younger); then
+  // slab kb + 1 is visible and slab kb's slots are free
   wait_lgkm0();
   wait_vm<XQ_LD>();
   xq_sync();
-  // refill loads spread evenly over the MFMAs of steps 2 and 3 (see qw_slab)
   if constexpr (MMAS > 0) {
     constexpr int H = MMAS < 4 ? MMAS : 4;
-    xq_mma_refill<AMODE, NMI, 0, 0, H>(P.fa[A2], P.fb[A2], acc, L, kb, lane);
+    xq_mma_ld<AMODE, NMI, 0, H, NL, 0, 0>(P.fa[A2], P.fb[A2], acc, L, kb + 2, lane);
     __builtin_amdgcn_sched_barrier(0);
     xq_read<AMODE, NMI>(kb + 1, 0, wm, wn, lane, P.fa[A1], P.fb[A1]);
     __builtin_amdgcn_sched_barrier(0);
-    xq_mma_refill<AMODE, NMI, 0, H, MMAS>(P.fa[A2], P.fb[A2], acc, L, kb, lane);
+    xq_mma_ld<AMODE, NMI, H, MMAS, NL, 0, 0>(P.fa[A2], P.fb[A2], acc, L, kb + 2, lane);
     __builtin_amdgcn_sched_barrier(0);
     xq_read<AMODE, NMI>(kb + 1, 1, wm, wn, lane, P.fa[A2], P.fb[A2]);
     __builtin_amdgcn_sched_barrier(0);
-    xq_mma_refill<AMODE, NMI, MMAS, 0, MMAS>(P.fa[A0], P.fb[A0], acc, L, kb, lane);
+    xq_mma_ld<AMODE, NMI, 0, MMAS, NL, 0, NL>(P.fa[A0], P.fb[A0], acc, L, kb + 2, lane);
   } else {
     xq_issue_a<AMODE, 0, XQ_LD>(L, kb + 2, lane);
-    xq_issue_b<AMODE == XA_ROWS ? XB_W_NN : XB_ACT_KMAJOR, 0, XQ_LD>(L, kb + 3, lane);
   }
 }
 
@@ -375,14 +379,14 @@ __global__ __launch_bounds__(256) void xgemm_q_kernel(const XGemm g) {
       for (int r = 0; r < 16; ++r) acc[j][ni][r] = 0.0f;
 
   if (L.nk > 0) {
-    // ---- prologue: slab 0 visible to all waves; then A(1), B(1), B(2) in flight
+    // ---- prologue: A(0), B(0) and A(1), B(1) in flight together; slab 0
+    // visible to all waves
     xq_issue_a<AMODE, 0, XQ_LD>(L, 0, lane);
     xq_issue_b<BM, 0, XQ_LD>(L, 0, lane);
-    wait_vm<0>();
-    xq_sync();
     xq_issue_a<AMODE, 0, XQ_LD>(L, 1, lane);
     xq_issue_b<BM, 0, XQ_LD>(L, 1, lane);
-    xq_issue_b<BM, 0, XQ_LD>(L, 2, lane);
+    wait_vm<2 * XQ_LD>();
+    xq_sync();
     // active row sub-tiles of this wave; none when its 128 columns all lie
     // past N (the last column tile of N = 1408, for instance)
     const int nsub = (int)cdiv(rows, 32);

@@ -58,6 +58,13 @@ __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_base) {
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gptr), "{m0}"(lds_base) : "memory");
 }
 
+// The same load addressed as a wave-uniform 64-bit base (SGPRs) plus a
+// 32-bit per-lane byte offset: no 64-bit address arithmetic in VGPRs, and the
+// per-lane offsets stay 32-bit registers.
+__device__ __forceinline__ void dma16s(const char* base, uint32_t off, uint32_t lds_base) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(base), "{m0}"(lds_base) : "memory");
+}
+
 // Two fp32 values rounded to nearest-even bf16 and packed (lo = a), one
 // v_cvt_pk_bf16_f32 on gfx950.
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
