@@ -254,7 +254,9 @@ int dsmoe_permute(const int32_t* idx, const dsmoe_dims* dims, int32_t* offsets, 
   rc = launch_permute(idx, *dims, TILE_M, ps, offsets, sorted_slot, sorted_token, slot_pos, counts, weights, sorted_w,
                       st);
   if (rc) return rc;
-  if (x) rc = launch_gather_rows(x, sorted_token, (int64_t)dims->T * dims->k, dims->D, elem_size(dims->dtype), x_sorted, st);
+  if (x)
+    rc = launch_gather_rows(x, dims->T, sorted_token, (int64_t)dims->T * dims->k, dims->D, elem_size(dims->dtype),
+                            x_sorted, st);
   return rc;
 }
 
@@ -329,16 +331,8 @@ size_t dsmoe_moe_fwd_workspace_size(const dsmoe_dims* dims, int training) {
   return fwd_layout(*dims, training, nullptr).total;
 }
 
-// Few-row (decode) GEMM path: tokens per call up to which it is taken, and
-// an environment switch (DSMOE_DECODE_GEMM=0) that keeps the quad-wave path.
+// Few-row (decode) GEMM path: tokens per inference call up to which it is taken.
 constexpr int SK_MAX_T = SK_BM;
-static bool decode_gemm_on() {
-  static bool on = [] {
-    const char* s = std::getenv("DSMOE_DECODE_GEMM");
-    return !(s && std::atoi(s) == 0);
-  }();
-  return on;
-}
 
 // Routed problem gr on the few-row kernel, with the dense shared problem gd
 // in the same launch when that kernel takes it too (else on the general path).
@@ -407,7 +401,7 @@ int dsmoe_moe_fwd(const void* x, const float* gate_w, const float* gate_bias, co
   // Decode shapes (at most SK_MAX_T tokens, inference): every routed and
   // shared row tile fits the few-row kernel, which streams the weights once.
   bool sk = false;
-  if (!training && d.dtype == DSMOE_BF16 && d.T <= SK_MAX_T && mf && decode_gemm_on()) {
+  if (!training && d.dtype == DSMOE_BF16 && d.T <= SK_MAX_T && mf) {
     GemmDesc t1 = g1, t2 = g2;
     t1.bm = t2.bm = SK_BM;
     t1.Gs = t1.Us = nullptr;
@@ -422,7 +416,7 @@ int dsmoe_moe_fwd(const void* x, const float* gate_w, const float* gate_bias, co
     // the routed rows of x in sorted order, for the backward's weight
     // gradient (a K-major operand read without a row gather); gemm1 keeps
     // gathering from x, which stays cache-resident
-    rc = launch_gather_rows(x, L.sorted_token, N, d.D, elem_size(d.dtype), L.x_sorted, st);
+    rc = launch_gather_rows(x, d.T, L.sorted_token, N, d.D, elem_size(d.dtype), L.x_sorted, st);
   }
   tm.end();
   if (rc) return rc;
@@ -535,7 +529,9 @@ static BwdLayout bwd_layout(const dsmoe_dims& d, void* base) {
   B.dx_slots = c.take<char>((size_t)N * d.D * es);
   B.dgdu_s = d.S ? c.take<char>((size_t)d.T * 2 * d.S * d.I_s * es) : nullptr;
   B.dx_shared = d.S ? c.take<char>((size_t)d.T * d.D * es) : nullptr;
-  B.dy_w = d.dtype == DSMOE_BF16 ? c.take<char>((size_t)N * d.D * es) : nullptr;
+  // w * dY gathered in sorted order, for bf16 rows of whole 16-byte chunks;
+  // other widths read dY through the row map with the weight as a k scale
+  B.dy_w = (d.dtype == DSMOE_BF16 && d.D % 8 == 0) ? c.take<char>((size_t)N * d.D * es) : nullptr;
   B.ks13 = B.ks2 = 1;
   B.part = nullptr;
   if (d.S && d.dtype == DSMOE_BF16) {
@@ -858,6 +854,32 @@ int dsmoe_update_bias(const int32_t* counts, float* gate_bias, int E, float spee
                       void* stream) {
   DSMOE_REQUIRE(counts && gate_bias && E > 0, DSMOE_ERR_INVALID, "update_bias: bad arguments");
   return launch_update_bias(counts, gate_bias, E, speed, upper, lower, static_cast<hipStream_t>(stream));
+}
+
+int dsmoe_update_bias_f32(const float* counts, float* gate_bias, int E, float speed, float upper, float lower,
+                          void* stream) {
+  DSMOE_REQUIRE(counts && gate_bias && E > 0, DSMOE_ERR_INVALID, "update_bias_f32: bad arguments");
+  return launch_update_bias_f32(counts, gate_bias, E, speed, upper, lower, static_cast<hipStream_t>(stream));
+}
+
+size_t dsmoe_moe_fwd_workspace_offset(const dsmoe_dims* dims, int training, int buffer) {
+  if (validate(dims, true)) return (size_t)-1;
+  // carve the layout at a stand-in base address; pointers minus the base are
+  // the byte offsets (the layout aligns every buffer to 256 bytes)
+  constexpr uintptr_t kBase = uintptr_t(1) << 20;
+  const FwdLayout L = fwd_layout(*dims, training, reinterpret_cast<void*>(kBase));
+  const void* p = nullptr;
+  switch (buffer) {
+    case DSMOE_WS_IDX: p = L.idx; break;
+    case DSMOE_WS_WEIGHTS: p = L.w; break;
+    case DSMOE_WS_SEL_SCORES: p = L.sel; break;
+    case DSMOE_WS_OFFSETS: p = L.offsets; break;
+    case DSMOE_WS_SORTED_SLOT: p = L.sorted_slot; break;
+    case DSMOE_WS_SORTED_TOKEN: p = L.sorted_token; break;
+    case DSMOE_WS_SLOT_POS: p = L.slot_pos; break;
+    default: return (size_t)-1;
+  }
+  return (size_t)(reinterpret_cast<uintptr_t>(p) - kBase);
 }
 
 int dsmoe_timing_enable(int on) {

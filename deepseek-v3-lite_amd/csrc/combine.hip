@@ -175,13 +175,16 @@ int launch_combine(const void* o_slots, const float* w, const int32_t* idx, cons
   return check_launch("combine");
 }
 
-// f1: models/moe.py:21-27 on device.  One block; counts int32 (E).
-__global__ void update_bias_kernel(const int32_t* __restrict__ counts, float* __restrict__ bias, int E, float speed,
+// f1: models/moe.py:21-27 on device.  One block; counts (E) int32 (the gate
+// histogram) or fp32 (any caller-provided counts, fractional ones included).
+// The mean sums the fp32 counts in ascending expert order; integer counts far
+// below 2^24 make every partial sum exact, so any summation order gives the
+// same mean.
+template <typename C>
+__global__ void update_bias_kernel(const C* __restrict__ counts, float* __restrict__ bias, int E, float speed,
                                    float upper, float lower) {
   __shared__ float s_avg;
   if (threadIdx.x == 0) {
-    // mean of the fp32-cast counts in ascending order (the counts are exact
-    // integers far below 2^24, so every partial sum is exact)
     float s = 0.0f;
     for (int e = 0; e < E; ++e) s += (float)counts[e];
     s_avg = s / (float)E;
@@ -199,8 +202,14 @@ __global__ void update_bias_kernel(const int32_t* __restrict__ counts, float* __
 
 int launch_update_bias(const int32_t* counts, float* bias, int E, float speed, float upper, float lower,
                        hipStream_t st) {
-  hipLaunchKernelGGL(update_bias_kernel, dim3(1), dim3(256), 0, st, counts, bias, E, speed, upper, lower);
+  hipLaunchKernelGGL(update_bias_kernel<int32_t>, dim3(1), dim3(256), 0, st, counts, bias, E, speed, upper, lower);
   return check_launch("update_bias");
+}
+
+int launch_update_bias_f32(const float* counts, float* bias, int E, float speed, float upper, float lower,
+                           hipStream_t st) {
+  hipLaunchKernelGGL(update_bias_kernel<float>, dim3(1), dim3(256), 0, st, counts, bias, E, speed, upper, lower);
+  return check_launch("update_bias_f32");
 }
 
 }  // namespace dsmoe

@@ -99,7 +99,6 @@ struct GemmDesc {
   int32_t groups;             // number of groups (dense)
   int32_t m_tiles_bound;      // host upper bound of M tiles (grid sizing)
   int32_t bm;                 // rows per M tile (must equal the schedule's tile height)
-  int32_t raster;             // block -> tile order (0: XCD-chunked, 1: linear, 2: XCD-chunked N-major groups)
   // A operand: rows of length K (K contiguous)
   const void* A;
   int64_t lda;
@@ -170,7 +169,10 @@ size_t permute_scratch_carve(Carver& c, const dsmoe_dims& d, int bm, PermuteScra
 int launch_permute(const int32_t* idx, const dsmoe_dims& d, int bm, const PermuteScratch& s, int32_t* offsets,
                    int32_t* sorted_slot, int32_t* sorted_token, int32_t* slot_pos, int32_t* counts, const float* w,
                    float* sorted_w, hipStream_t st);
-int launch_gather_rows(const void* x, const int32_t* rows, int64_t nrows, int D, int elem, void* dst, hipStream_t st);
+// dst[p] = x[rows[p]] for p < nrows (rows of D elements); rows outside
+// [0, src_rows) give zero rows.
+int launch_gather_rows(const void* x, int64_t src_rows, const int32_t* rows, int64_t nrows, int D, int elem, void* dst,
+                       hipStream_t st);
 int launch_sched_from_offsets(const int64_t* offsets64, int E, int bm, int64_t rows, int32_t* offsets32, MTile* sched,
                               int32_t* sched_count, hipStream_t st);
 // Whether launch_grouped_gemm will take the MFMA kernel for this descriptor,
@@ -197,6 +199,8 @@ int launch_combine(const void* o_slots, const float* w, const int32_t* idx, cons
                    void* y, hipStream_t st);
 int launch_update_bias(const int32_t* counts, float* bias, int E, float speed, float upper, float lower,
                        hipStream_t st);
+int launch_update_bias_f32(const float* counts, float* bias, int E, float speed, float upper, float lower,
+                           hipStream_t st);
 
 
 // ---------------------------------------------------------------- backward GEMM description

@@ -349,14 +349,9 @@ static int launch_gate_mfma(const void* x, const float* gw, const float* bias, c
 }
 
 int gate_k_splits(const dsmoe_dims& d) {
-  static const int forced = [] {
-    const char* s = std::getenv("DSMOE_GATE_KS");
-    return s ? std::atoi(s) : 0;
-  }();
   const int64_t tiles = cdiv(d.T, GM_TOK);
-  int ks = forced > 0 ? min(forced, GATE_KS_MAX) : 1;
-  if (forced <= 0)
-    while (ks < GATE_KS_MAX && tiles * ks * 2 <= 256) ks *= 2;   // fill the 256 CUs when there are few token tiles
+  int ks = 1;
+  while (ks < GATE_KS_MAX && tiles * ks * 2 <= 256) ks *= 2;   // fill the 256 CUs when there are few token tiles
   while (ks > 1 && d.D % (64 * ks) != 0) ks >>= 1;
   return ks;
 }

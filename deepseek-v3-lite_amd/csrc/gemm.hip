@@ -311,23 +311,12 @@ __global__ __launch_bounds__(256) void gemm_simt_kernel(const GemmDesc g, const 
 // =============================================================== host launch
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-// MFMA tile configuration.  All configurations use 256-row M tiles (the
-// routed schedule height); DSMOE_GEMM_CFG selects among them for tuning.
-//   0: 4 waves (2x2), per wave 4x2 tiles (SwiGLU: x2) / 4x4 tiles (store)
-//   1: 8 waves (2x4), per wave 4x1 (SwiGLU x2) / 4x2 (store)
-//   2: 8 waves (4x2), per wave 2x2 (SwiGLU x2) / 2x4 (store)
-//   3: quad-wave kernel of gemm_qw.hip (4 waves of 128 x 128, K slabs of 64
-//      streamed by direct loads; the default where its constraints hold)
+// MFMA kernels use 256-row M tiles (the routed schedule height): the
+// quad-wave kernel of gemm_qw.hip (4 waves of 128 x 128, K slabs of 64
+// streamed by direct loads) wherever its constraints hold, else
+// gemm_mfma_kernel with 8 waves (4 x 2), per wave 2 x 2 tiles (SwiGLU: x2) or
+// 2 x 4 (store).
 constexpr int MF_BM = 256;
-
-static int gemm_cfg() {
-  static int cfg = [] {
-    const char* s = std::getenv("DSMOE_GEMM_CFG");
-    int v = s ? std::atoi(s) : 3;
-    return (v >= 0 && v <= 3) ? v : 3;
-  }();
-  return cfg;
-}
 
 // The MFMA kernel needs bf16, 16-byte aligned operands and strides, K and the
 // K segment multiples of 64, N a multiple of 4 and 8-byte aligned output rows.
@@ -355,44 +344,24 @@ static int launch_mfma_t(const GemmDesc& g, const float* row_scale, hipStream_t 
   const int64_t grid = grid_for(g, CF::BM, CF::BN);
   if (grid == 0) return DSMOE_OK;
   auto kern = gemm_mfma_kernel<EPI, WM, WN, TM, TN>;
-  static bool attr = false;
-  if (!attr) {
-    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)CF::LDS_BYTES) !=
-        hipSuccess)
-      return fail(DSMOE_ERR_HIP, "gemm: cannot raise LDS limit");
-    attr = true;
-  }
+  static const hipError_t attr =
+      hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)CF::LDS_BYTES);
+  if (attr != hipSuccess) return fail(DSMOE_ERR_HIP, "gemm: cannot raise LDS limit");
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(CF::THREADS), CF::LDS_BYTES, st, g, row_scale);
   return check_launch("gemm_mfma");
 }
 
-static int gemm_raster() {
-  static int r = [] {
-    const char* s = std::getenv("DSMOE_GEMM_RASTER");
-    const int v = s ? std::atoi(s) : 0;
-    return (v >= 0 && v <= 2) ? v : 0;
-  }();
-  return r;
-}
-
 int launch_grouped_gemm(const GemmDesc& g_in, int epi, int dtype, const float* row_scale, bool allow_mfma,
                         hipStream_t st) {
-  GemmDesc g = g_in;
-  g.raster = gemm_raster();
+  const GemmDesc& g = g_in;
   if (g.N <= 0 || g.K <= 0) return DSMOE_OK;
   if (gemm_mfma_eligible(g, dtype, allow_mfma)) {
     if (g.bm != MF_BM) return fail(DSMOE_ERR_INVALID, "gemm: schedule tile height does not match the MFMA kernel");
-    const int want = gemm_cfg();
-    if (want == 3 && gemm_qw_ok(g)) return launch_gemm_qw(g, epi, row_scale, st);
-    const int cfg = want == 3 ? 2 : want;  // shapes the quad-wave kernel does not take
-    if (epi == EPI_SWIGLU) {
-      if (cfg == 1) return launch_mfma_t<EPI_SWIGLU, 2, 4, 4, 1>(g, row_scale, st);
-      if (cfg == 2) return launch_mfma_t<EPI_SWIGLU, 4, 2, 2, 2>(g, row_scale, st);
-      return launch_mfma_t<EPI_SWIGLU, 2, 2, 4, 2>(g, row_scale, st);
-    }
-    if (cfg == 1) return launch_mfma_t<EPI_STORE, 2, 4, 4, 2>(g, row_scale, st);
-    if (cfg == 2) return launch_mfma_t<EPI_STORE, 4, 2, 2, 4>(g, row_scale, st);
-    return launch_mfma_t<EPI_STORE, 2, 2, 4, 4>(g, row_scale, st);
+    if (gemm_qw_ok(g)) return launch_gemm_qw(g, epi, row_scale, st);
+    // shapes the quad-wave kernel does not take (N % 8 == 4, more than two K
+    // segments, 8-byte aligned output): the register-staged 8-wave kernel
+    if (epi == EPI_SWIGLU) return launch_mfma_t<EPI_SWIGLU, 4, 2, 2, 2>(g, row_scale, st);
+    return launch_mfma_t<EPI_STORE, 4, 2, 2, 4>(g, row_scale, st);
   }
   if (g.bm != TILE_M) return fail(DSMOE_ERR_INVALID, "gemm: schedule tile height does not match the SIMT kernel");
   const int64_t grid = grid_for(g, TILE_M, SM_N);
@@ -411,20 +380,10 @@ int launch_grouped_gemm(const GemmDesc& g_in, int epi, int dtype, const float* r
   return check_launch("gemm_simt");
 }
 
-// DSMOE_GEMM_PAIR=0 launches the two problems separately.
-static bool gemm_pair() {
-  static bool on = [] {
-    const char* s = std::getenv("DSMOE_GEMM_PAIR");
-    return !(s && std::atoi(s) == 0);
-  }();
-  return on;
-}
-
 int launch_grouped_gemm_pair(const GemmDesc& gr_in, const GemmDesc& gd_in, int epi, int dtype, const float* row_scale,
                              bool allow_mfma_r, bool allow_mfma_d, hipStream_t st) {
-  GemmDesc gr = gr_in, gd = gd_in;
-  gr.raster = gd.raster = gemm_raster();
-  const bool one = gemm_pair() && gr.raster == 0 && gemm_cfg() == 3 && gd.sched == nullptr && gr.N > 0 && gr.K > 0 && gd.N > 0 &&
+  const GemmDesc &gr = gr_in, &gd = gd_in;
+  const bool one = gd.sched == nullptr && gr.N > 0 && gr.K > 0 && gd.N > 0 &&
                    gd.K > 0 && gemm_mfma_eligible(gr, dtype, allow_mfma_r) && gemm_mfma_eligible(gd, dtype, allow_mfma_d) &&
                    gemm_qw_ok(gr) && gemm_qw_ok(gd);
   if (one) return launch_gemm_qw_pair(gr, gd, epi, row_scale, st);

@@ -460,11 +460,11 @@ template <int EPI>
 static int qw_launch(const GemmDesc& g0, const GemmDesc& g1, int pair, const float* row_scale, int64_t grid,
                      hipStream_t st) {
   if (grid == 0) return DSMOE_OK;
-  static bool raised = false;
-  if (!raised && hipFuncSetAttribute((const void*)gemm_qw_kernel<EPI>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     (int)QW_LDS) != hipSuccess)
-    return fail(DSMOE_ERR_HIP, "gemm_qw: cannot raise LDS limit");
-  raised = true;
+  // once per instantiation; the initialisation of a local static is thread-safe
+  // (autograd runs the backward on its own thread)
+  static const hipError_t attr = hipFuncSetAttribute((const void*)gemm_qw_kernel<EPI>,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)QW_LDS);
+  if (attr != hipSuccess) return fail(DSMOE_ERR_HIP, "gemm_qw: cannot raise LDS limit");
   hipLaunchKernelGGL(gemm_qw_kernel<EPI>, dim3((unsigned)grid), dim3(256), QW_LDS, st, g0, g1, pair, row_scale);
   return check_launch("gemm_qw");
 }

@@ -20,28 +20,13 @@ __device__ __forceinline__ bool tile_for_block(const GemmDesc& g, int n_tiles, i
     m_total = (int64_t)tpg * g.groups;
   }
   const int64_t total = m_total * n_tiles;
-  int64_t lin;
-  if (g.raster == 1) {
-    lin = blockIdx.x;
-  } else {
-    const int64_t per_xcd = cdiv(total, 8);
-    const int64_t j = blockIdx.x >> 3;
-    if (j >= per_xcd) return false;
-    lin = (int64_t)(blockIdx.x & 7) * per_xcd + j;
-  }
+  const int64_t per_xcd = cdiv(total, 8);
+  const int64_t j = blockIdx.x >> 3;
+  if (j >= per_xcd) return false;
+  const int64_t lin = (int64_t)(blockIdx.x & 7) * per_xcd + j;
   if (lin >= total) return false;
-  int64_t m_tile;
-  if (g.raster == 2) {
-    // groups of 4 M tiles; inside a group the 4 M tiles of one N tile are adjacent
-    const int64_t grp_sz = 4 * (int64_t)n_tiles;
-    const int64_t gi = lin / grp_sz, r = lin - gi * grp_sz;
-    const int64_t gm = min((int64_t)4, m_total - gi * 4);
-    n_tile = (int)(r / gm);
-    m_tile = gi * 4 + (r - (int64_t)n_tile * gm);
-  } else {
-    m_tile = lin / n_tiles;
-    n_tile = (int)(lin - m_tile * n_tiles);
-  }
+  const int64_t m_tile = lin / n_tiles;
+  n_tile = (int)(lin - m_tile * n_tiles);
   if (g.sched) {
     const MTile t = g.sched[m_tile];
     grp = t.group;

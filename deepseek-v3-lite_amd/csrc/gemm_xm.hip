@@ -440,13 +440,9 @@ bool xgemm_mfma_ok(const XGemm& g, int epi) {
 template <int EPI, int AMODE, int BMODE>
 static int launch_xm_t(const XGemm& g, int64_t grid, hipStream_t st) {
   auto kern = xgemm_mfma_kernel<EPI, AMODE, BMODE>;
-  static bool attr = false;
-  if (!attr) {
-    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)XM_LDS_ALLOC) !=
-        hipSuccess)
-      return fail(DSMOE_ERR_HIP, "xgemm: cannot raise LDS limit");
-    attr = true;
-  }
+  static const hipError_t attr =
+      hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)XM_LDS_ALLOC);
+  if (attr != hipSuccess) return fail(DSMOE_ERR_HIP, "xgemm: cannot raise LDS limit");
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(XM_THREADS), XM_LDS_ALLOC, st, g);
   return check_launch("xgemm_mfma");
 }

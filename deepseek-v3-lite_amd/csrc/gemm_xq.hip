@@ -582,12 +582,9 @@ bool xgemm_q_ok(const XGemm& g, int epi) {
 template <int EPI, int AMODE>
 static int launch_xq_t(const XGemm& g, int64_t grid, hipStream_t st) {
   auto kern = xgemm_q_kernel<EPI, AMODE>;
-  static bool attr = false;
-  if (!attr) {
-    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)XQ_LDS) != hipSuccess)
-      return fail(DSMOE_ERR_HIP, "xgemm_q: cannot raise LDS limit");
-    attr = true;
-  }
+  static const hipError_t attr =
+      hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)XQ_LDS);
+  if (attr != hipSuccess) return fail(DSMOE_ERR_HIP, "xgemm_q: cannot raise LDS limit");
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(256), XQ_LDS, st, g);
   return check_launch("xgemm_q");
 }

@@ -186,9 +186,13 @@ __device__ __forceinline__ void scatter_slot(int64_t s, const int32_t* __restric
                                              float* __restrict__ sorted_w) {
   const int t = (int)(s / k);
   const int e = idx[s];
-  if ((unsigned)e >= (unsigned)E) return;  // ids are validated upstream; never write out of bounds
+  // Invalid routing (an id outside [0, E), or an id repeated within a token,
+  // whose earlier slots get no rank) is not placed: no write leaves the
+  // expert's range of sorted positions.
+  if ((unsigned)e >= (unsigned)E) return;
   const int b = t / RANK_TOKENS;
   const int32_t pos = offsets[e] + blockbase[(int64_t)b * E + e] + local_rank[s];
+  if (pos < offsets[e] || pos >= offsets[e + 1]) return;
   sorted_slot[pos] = (int32_t)s;
   sorted_token[pos] = t;
   slot_pos[s] = pos;
@@ -234,23 +238,27 @@ __global__ __launch_bounds__(1024) void permute_small_kernel(const int32_t* __re
 }
 
 // Row gather with 16-byte vectors; row_bytes % 16 == 0.
+// Row indices outside [0, src_rows) (left unset by an invalid routing) gather
+// zero rows instead of reading out of bounds.
 __global__ void gather_rows_kernel(const uint4* __restrict__ src, const int32_t* __restrict__ rows, int64_t nrows,
-                                   int vec_per_row, uint4* __restrict__ dst) {
+                                   int vec_per_row, int64_t src_rows, uint4* __restrict__ dst) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= nrows * vec_per_row) return;
   const int64_t r = i / vec_per_row;
   const int c = (int)(i - r * vec_per_row);
-  dst[i] = src[(int64_t)rows[r] * vec_per_row + c];
+  const int32_t sr = rows[r];
+  dst[i] = (sr >= 0 && sr < src_rows) ? src[(int64_t)sr * vec_per_row + c] : make_uint4(0, 0, 0, 0);
 }
 
 template <typename T>
 __global__ void gather_rows_scalar_kernel(const T* __restrict__ src, const int32_t* __restrict__ rows, int64_t nrows,
-                                          int D, T* __restrict__ dst) {
+                                          int D, int64_t src_rows, T* __restrict__ dst) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= nrows * D) return;
   const int64_t r = i / D;
   const int c = (int)(i - r * D);
-  dst[i] = src[(int64_t)rows[r] * D + c];
+  const int32_t sr = rows[r];
+  dst[i] = (sr >= 0 && sr < src_rows) ? src[(int64_t)sr * D + c] : T(0);
 }
 
 // Schedule from caller-provided int64 offsets (E+1) (grouped operator seam).
@@ -341,19 +349,20 @@ int launch_permute(const int32_t* idx, const dsmoe_dims& d, int bm, const Permut
   return check_launch("permute");
 }
 
-int launch_gather_rows(const void* x, const int32_t* rows, int64_t nrows, int D, int elem, void* dst, hipStream_t st) {
+int launch_gather_rows(const void* x, int64_t src_rows, const int32_t* rows, int64_t nrows, int D, int elem, void* dst,
+                       hipStream_t st) {
   if (nrows == 0) return DSMOE_OK;
   const int64_t row_bytes = (int64_t)D * elem;
   if (row_bytes % 16 == 0 && ((uintptr_t)x % 16 == 0) && ((uintptr_t)dst % 16 == 0)) {
     const int vpr = (int)(row_bytes / 16);
     hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)cdiv(nrows * vpr, 256)), dim3(256), 0, st,
-                       static_cast<const uint4*>(x), rows, nrows, vpr, static_cast<uint4*>(dst));
+                       static_cast<const uint4*>(x), rows, nrows, vpr, src_rows, static_cast<uint4*>(dst));
   } else if (elem == 2) {
     hipLaunchKernelGGL(gather_rows_scalar_kernel<uint16_t>, dim3((unsigned)cdiv(nrows * D, 256)), dim3(256), 0, st,
-                       static_cast<const uint16_t*>(x), rows, nrows, D, static_cast<uint16_t*>(dst));
+                       static_cast<const uint16_t*>(x), rows, nrows, D, src_rows, static_cast<uint16_t*>(dst));
   } else {
     hipLaunchKernelGGL(gather_rows_scalar_kernel<float>, dim3((unsigned)cdiv(nrows * D, 256)), dim3(256), 0, st,
-                       static_cast<const float*>(x), rows, nrows, D, static_cast<float*>(dst));
+                       static_cast<const float*>(x), rows, nrows, D, src_rows, static_cast<float*>(dst));
   }
   return check_launch("gather_rows");
 }

@@ -22,6 +22,8 @@ DSMOE_ERR_WORKSPACE = -3
 DSMOE_ERR_HIP = -4
 DSMOE_F32 = 0
 DSMOE_BF16 = 1
+# forward-workspace buffer ids of dsmoe_moe_fwd_workspace_offset
+WS_IDX, WS_WEIGHTS, WS_SEL_SCORES, WS_OFFSETS, WS_SORTED_SLOT, WS_SORTED_TOKEN, WS_SLOT_POS = range(7)
 
 
 class Dims(ctypes.Structure):
@@ -55,6 +57,8 @@ _SIGNATURES = {
     "dsmoe_moe_bwd_workspace_size": ([DIMS], SZ),
     "dsmoe_moe_bwd": ([P, P, PP, PP, PP, PP, PP, PP, DIMS, P, P, P, P, PP, PP, PP, PP, PP, PP, P, SZ, P], I32),
     "dsmoe_update_bias": ([P, P, I32, F32, F32, F32, P], I32),
+    "dsmoe_update_bias_f32": ([P, P, I32, F32, F32, F32, P], I32),
+    "dsmoe_moe_fwd_workspace_offset": ([DIMS, I32, I32], SZ),
     "dsmoe_timing_enable": ([I32], I32),
     "dsmoe_timing_read": ([ctypes.POINTER(ctypes.c_double), I32, ctypes.POINTER(ctypes.c_int)], I32),
     "dsmoe_timing_stage_name": ([I32], ctypes.c_char_p),

@@ -12,24 +12,25 @@ from __future__ import annotations
 import os
 from typing import Callable
 
-_DISPATCH = {
-    ("attn_impl", "triton"): "sdpa",
-    ("moe_dispatch", "triton_grouped"): "stacked",
-}
+# The MoE layer's key only; the attention key the reference rewrites too
+# belongs to MLA attention, which this package does not provide.
+_REWRITES = {("moe_dispatch", "triton_grouped"): "stacked"}
 
 
 def enforce_triton_env_var(model_cfg: dict, log: Callable[[str], None]) -> None:
-    """Same config rewrite and single warning as models/_triton_dispatch.py:19-35."""
+    """Config rewrite of models/_triton_dispatch.py:19-35 for the MoE key:
+    without ENABLE_TRITON_KERNELS=1 a 'triton_grouped' dispatch becomes
+    'stacked', announced by one log call per rewritten config."""
     if os.environ.get("ENABLE_TRITON_KERNELS", "0") == "1":
         return
-    forced = []
-    for (key, triton_val), default in _DISPATCH.items():
-        if model_cfg.get(key) == triton_val:
-            model_cfg[key] = default
-            forced.append(f"{key}='{triton_val}' -> '{default}'")
-    if forced:
-        log("[warn] Triton dispatch keys set without ENABLE_TRITON_KERNELS=1; "
-            f"forcing {', '.join(forced)}. Set ENABLE_TRITON_KERNELS=1 to enable the fused Triton paths.")
+    changed = []
+    for (key, value), replacement in _REWRITES.items():
+        if model_cfg.get(key) == value:
+            model_cfg[key] = replacement
+            changed.append(f"{key}: {value!r} becomes {replacement!r}")
+    if changed:
+        log("[warn] ENABLE_TRITON_KERNELS is not 1, so the config's Triton selections are reset ("
+            + "; ".join(changed) + "). The dsmoe layer runs its HIP kernels under either value.")
 
 
 def next_pow2(n: int) -> int:

@@ -45,6 +45,21 @@ def _compute_dtype(x: torch.Tensor) -> torch.dtype:
     return x.dtype
 
 
+class _CachedCast(torch.autograd.Function):
+    """Returns the cached cast copy ``wc`` of parameter ``w`` as an
+    autograd-visible tensor; the backward hands the gradient to ``w`` in its
+    dtype (the backward of autocast's weight cast)."""
+
+    @staticmethod
+    def forward(ctx, w, wc):
+        ctx.dtype = w.dtype
+        return wc.view_as(wc)
+
+    @staticmethod
+    def backward(ctx, g):
+        return g.to(ctx.dtype), None
+
+
 class AuxLossFreeGate(nn.Module):
     """Sigmoid top-k router with a non-trainable fp32 bias (models/moe.py:7-37)."""
 
@@ -118,11 +133,39 @@ class DeepSeekMoE(nn.Module):
         self._last_counts: Optional[torch.Tensor] = None
         self._counts_of: Optional[torch.Tensor] = None  # the _last_indices _last_counts was computed from
         self._stack_dtype: Optional[torch.dtype] = None
+        # id(parameter) -> ((version, data_ptr, dtype), cast copy); see _cast
+        self._cast_cache: dict = {}
 
     # -------------------------------------------------------------- forward
+    def _cast(self, w: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+        """w in ``dtype`` for the expert GEMMs.  Under autocast the weights
+        are fp32 parameters and the GEMMs read bf16: the cast copy is cached
+        and made again only when the parameter changes (its version counter
+        moves on every in-place update, e.g. an optimizer step), so a forward
+        does not re-cast all expert weights.  The gradient flows back to the
+        parameter in its own dtype, as through autocast's cast."""
+        if w.dtype == dtype:
+            return w
+        if torch.compiler.is_compiling():
+            return w.to(dtype)
+        key = (w._version, w.data_ptr(), dtype)
+        ent = self._cast_cache.get(id(w))
+        if ent is None or ent[0] != key:
+            with torch.no_grad():
+                ent = (key, w.detach().to(dtype))
+            self._cast_cache[id(w)] = ent
+        if not (torch.is_grad_enabled() and w.requires_grad):
+            return ent[1]
+        return _CachedCast.apply(w, ent[1])
+
+    def _apply(self, fn, *args, **kwargs):
+        # .to() / .cuda() / .half() replace parameter data: drop the cast copies
+        self._cast_cache.clear()
+        return super()._apply(fn, *args, **kwargs)
+
     def _expert_weights(self, dtype: torch.dtype):
         def cast(w):
-            return w if w.dtype == dtype else w.to(dtype)
+            return self._cast(w, dtype)
         w1 = [cast(e.w1.weight) for e in self.experts]
         w2 = [cast(e.w2.weight) for e in self.experts]
         w3 = [cast(e.w3.weight) for e in self.experts]

@@ -84,9 +84,28 @@ def route_from_logits(logits: torch.Tensor, gate_bias: torch.Tensor, k: int, rou
     return out
 
 
+def check_routing(idx: torch.Tensor, E: int) -> None:
+    """ValueError unless every row of idx (T, k) holds k distinct expert ids
+    in [0, E), the routing the gate produces.  Reads the ids back (a host
+    sync), so the layer itself never calls it."""
+    if idx.dim() != 2:
+        raise ValueError(f"dsmoe: routing indices must be (T, k), got shape {tuple(idx.shape)}")
+    if idx.numel() == 0:
+        return
+    if bool(((idx < 0) | (idx >= E)).any()):
+        raise ValueError(f"dsmoe: routing ids must lie in [0, {E})")
+    if idx.shape[1] > 1:
+        srt = torch.sort(idx, dim=1).values
+        if bool((srt[:, 1:] == srt[:, :-1]).any()):
+            raise ValueError("dsmoe: a token's routing ids must be distinct")
+
+
 def permute(idx: torch.Tensor, E: int, x: Optional[torch.Tensor] = None, weights: Optional[torch.Tensor] = None):
-    """Routing prep of models/moe.py:107-117 (+ optional row gather of :150)."""
+    """Routing prep of models/moe.py:107-117 (+ optional row gather of :150).
+    The ids are checked first (check_routing): ValueError on ids outside
+    [0, E) or repeated within a token."""
     dev = _require_gpu(idx)
+    check_routing(idx, E)
     idx = _c(idx.to(torch.int32))
     T, k = idx.shape
     N = T * k
@@ -129,11 +148,22 @@ def combine(o_slots: torch.Tensor, weights: torch.Tensor, idx: torch.Tensor, sha
 
 
 def update_bias_(counts: torch.Tensor, bias: torch.Tensor, speed: float, upper: float, lower: float) -> None:
-    """In-place f1 bias update on device (models/moe.py:21-27), no host sync."""
+    """In-place f1 bias update on device (models/moe.py:21-27), no host sync.
+    Integer counts (the gate histogram) run the int32 kernel; floating counts
+    (averaged or accumulated, possibly fractional) run the fp32 one, as the
+    reference compares ``counts.float()`` either way."""
     dev = _require_gpu(counts, bias)
     if bias.dtype != torch.float32 or not bias.is_contiguous():
         raise ValueError("dsmoe: gate bias must be a contiguous float32 tensor")
-    c = _c(counts.to(torch.int32))
+    if counts.numel() != bias.numel():
+        raise ValueError(f"dsmoe: {counts.numel()} counts for {bias.numel()} experts")
+    if counts.is_floating_point():
+        c = _c(counts.float().reshape(-1))
+        rc = L.load().dsmoe_update_bias_f32(L.ptr(c), L.ptr(bias), bias.numel(), float(speed), float(upper),
+                                            float(lower), L.stream_ptr(dev))
+        L.check(rc, "dsmoe_update_bias_f32")
+        return
+    c = _c(counts.to(torch.int32).reshape(-1))
     rc = L.load().dsmoe_update_bias(L.ptr(c), L.ptr(bias), bias.numel(), float(speed), float(upper), float(lower),
                                     L.stream_ptr(dev))
     L.check(rc, "dsmoe_update_bias")
@@ -238,21 +268,64 @@ def _moe_fwd_backward(ctx, dy, _didx, _dwx, _dcounts, _dws):
 torch.library.register_autograd("dsmoe::moe_fwd", _moe_fwd_backward, setup_context=_moe_fwd_setup)
 
 
+def check_layer_args(x: torch.Tensor, gate_w: torch.Tensor, gate_bias: torch.Tensor, w1: Sequence[torch.Tensor],
+                     w2: Sequence[torch.Tensor], w3: Sequence[torch.Tensor], sw1: Sequence[torch.Tensor],
+                     sw2: Sequence[torch.Tensor], sw3: Sequence[torch.Tensor], k: int) -> Tuple[int, int, int, int]:
+    """Shapes and dtypes moe_layer's kernels read, checked before any launch:
+    ValueError on a mismatch (the kernels trust these sizes).  -> (E, S, I, I_s)."""
+    if x.dim() != 2:
+        raise ValueError(f"dsmoe: x must be (T, dim), got shape {tuple(x.shape)}")
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"dsmoe: unsupported activation dtype {x.dtype} (float32 or bfloat16)")
+    D = x.shape[1]
+    E, S = len(w1), len(sw1)
+    if E == 0 or len(w2) != E or len(w3) != E:
+        raise ValueError(f"dsmoe: need the same number (>= 1) of w1, w2, w3 expert weights, got "
+                         f"{len(w1)}, {len(w2)}, {len(w3)}")
+    if len(sw2) != S or len(sw3) != S:
+        raise ValueError(f"dsmoe: need the same number of shared w1, w2, w3 weights, got {S}, {len(sw2)}, {len(sw3)}")
+    if gate_w.dtype != torch.float32 or tuple(gate_w.shape) != (E, D):
+        raise ValueError(f"dsmoe: gate weight must be float32 ({E}, {D}), got {gate_w.dtype} {tuple(gate_w.shape)}")
+    if gate_bias.dtype != torch.float32 or tuple(gate_bias.shape) != (E,):
+        raise ValueError(f"dsmoe: gate bias must be float32 ({E},), got {gate_bias.dtype} {tuple(gate_bias.shape)}")
+    if not 1 <= int(k) <= E:
+        raise ValueError(f"dsmoe: need 1 <= n_activated_experts <= {E}, got {k}")
+
+    def inter(ws1, ws2, ws3, what):
+        dims = None
+        for a, b, c in zip(ws1, ws2, ws3):
+            for w in (a, b, c):
+                if w.dtype != x.dtype:
+                    raise ValueError(f"dsmoe: {what} weight dtype {w.dtype} differs from activation dtype {x.dtype}")
+                if w.dim() != 2:
+                    raise ValueError(f"dsmoe: {what} weights must be 2-D, got shape {tuple(w.shape)}")
+            i = a.shape[0]
+            if tuple(a.shape) != (i, D) or tuple(c.shape) != (i, D) or tuple(b.shape) != (D, i):
+                raise ValueError(f"dsmoe: {what} w1/w3 must be (inter, {D}) and w2 ({D}, inter), got "
+                                 f"{tuple(a.shape)}, {tuple(c.shape)}, {tuple(b.shape)}")
+            if dims is not None and i != dims:
+                raise ValueError(f"dsmoe: all {what} experts must share one inter dim ({dims} and {i})")
+            dims = i
+        return dims or 0
+
+    I = inter(w1, w2, w3, "expert")
+    I_s = inter(sw1, sw2, sw3, "shared expert")
+    return E, S, I, I_s
+
+
 def moe_layer(x: torch.Tensor, gate_w: torch.Tensor, gate_bias: torch.Tensor, w1: Sequence[torch.Tensor],
               w2: Sequence[torch.Tensor], w3: Sequence[torch.Tensor], sw1: Sequence[torch.Tensor] = (),
               sw2: Sequence[torch.Tensor] = (), sw3: Sequence[torch.Tensor] = (), *, k: int,
               route_scale: float = 1.0, training: Optional[bool] = None):
     """One DeepSeekMoE layer on (T, D) tokens.  Expert weights must be in
-    x.dtype; gate_w and gate_bias are fp32.  Returns (y, idx64, weights_x, counts)."""
+    x.dtype, w1/w3 (inter, D) and w2 (D, inter); gate_w (E, D) and gate_bias
+    (E,) are fp32 (check_layer_args raises ValueError otherwise).
+    Returns (y, idx64, weights_x, counts)."""
+    E, S, I, I_s = check_layer_args(x, gate_w, gate_bias, w1, w2, w3, sw1, sw2, sw3, k)
     _require_gpu(x, gate_w, gate_bias, *w1)
-    E, S = len(w1), len(sw1)
-    I = w1[0].shape[0]
-    I_s = sw1[0].shape[0] if S else 0
     weights = [*w1, *w2, *w3, *sw1, *sw2, *sw3]
     needs_grad = x.requires_grad or gate_w.requires_grad
     for w in weights:
-        if w.dtype != x.dtype:
-            raise ValueError(f"dsmoe: expert weight dtype {w.dtype} differs from activation dtype {x.dtype}")
         needs_grad = needs_grad or w.requires_grad
     if training is None:
         training = torch.is_grad_enabled() and needs_grad
@@ -321,11 +394,18 @@ def grouped_moe_dispatch(x_sorted: torch.Tensor, w1: torch.Tensor, w2: torch.Ten
         raise ValueError("dsmoe: x_sorted and expert weights must share one dtype")
     xs, a, b, c = _c(x_sorted), _c(w1), _c(w2), _c(w3)
     needs_grad = torch.is_grad_enabled() and any(t.requires_grad for t in (x_sorted, w1, w2, w3, sorted_weights))
-    if not needs_grad:
+    # the reference returns out * sorted_weights.unsqueeze(-1) with torch's
+    # type promotion (an fp32 weight over a bf16 out gives fp32)
+    out_dtype = torch.result_type(x_sorted, sorted_weights)
+    if not needs_grad and out_dtype == x_sorted.dtype:
+        # weight fused into the down-projection epilogue (fp32 product, one rounding)
         sw = _c(sorted_weights.float())
         return _GroupedSwiGLUFn.forward(_NoCtx(), xs, a, b, c, expert_offsets, sw)
-    out = _GroupedSwiGLUFn.apply(xs, a, b, c, expert_offsets)
-    return out * sorted_weights.unsqueeze(-1).to(out.dtype)
+    if not needs_grad:
+        out = _GroupedSwiGLUFn.forward(_NoCtx(), xs, a, b, c, expert_offsets, None)
+    else:
+        out = _GroupedSwiGLUFn.apply(xs, a, b, c, expert_offsets)
+    return out * sorted_weights.unsqueeze(-1)
 
 
 class _NoCtx:

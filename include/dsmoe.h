@@ -97,6 +97,10 @@ int dsmoe_route_from_logits(const float* logits, const float* gate_bias, const d
  *   x, x_sorted  optional row gather x_sorted[p] = x[sorted_token[p]] (both NULL to skip)
  *   sorted_w     optional (N) fp32 gather of weights (T,k) (both NULL to skip)
  *   workspace    dsmoe_permute_workspace_size() bytes
+ * Each token's k ids must be distinct and in [0, E), as the gate produces
+ * them.  Other input is not detected here (that would need a host sync): its
+ * invalid slots are left unplaced, unset sorted positions keep what the
+ * buffers held and gather zero rows; no access leaves the buffers.
  */
 size_t dsmoe_permute_workspace_size(const dsmoe_dims* dims);
 int dsmoe_permute(const int32_t* idx, const dsmoe_dims* dims, int32_t* offsets, int32_t* sorted_slot,
@@ -167,6 +171,32 @@ int dsmoe_moe_bwd(const void* x, const float* gate_w, const void* const* w1, con
  * counts (E) int32 -> bias (E) fp32 updated in place by the +/-speed band rule. */
 int dsmoe_update_bias(const int32_t* counts, float* gate_bias, int E, float speed, float upper, float lower,
                       void* stream);
+
+/* The same update from fp32 counts (E), for callers whose counts are not the
+ * gate histogram (averaged or accumulated counts may be fractional); the
+ * reference casts any counts with counts.float() (models/moe.py:24). */
+int dsmoe_update_bias_f32(const float* counts, float* gate_bias, int E, float speed, float upper, float lower,
+                          void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Inspection of a forward workspace (no counterpart in the reference, whose
+ * intermediates are torch tensors): byte offset inside the dsmoe_moe_fwd
+ * workspace of one routing buffer, or (size_t)-1 for bad dims or an unknown
+ * id.  The buffers hold, after a forward call (N = T*k):
+ *   DSMOE_WS_IDX          (T,k) int32 expert ids
+ *   DSMOE_WS_WEIGHTS      (T,k) fp32 renormalised weights
+ *   DSMOE_WS_SEL_SCORES   (T,k) fp32 unbiased scores of the selected experts
+ *   DSMOE_WS_OFFSETS      (E+1) int32 expert offsets in the sorted order
+ *   DSMOE_WS_SORTED_SLOT  (N) int32, DSMOE_WS_SORTED_TOKEN (N) int32,
+ *   DSMOE_WS_SLOT_POS     (N) int32 (as dsmoe_permute's outputs) */
+#define DSMOE_WS_IDX 0
+#define DSMOE_WS_WEIGHTS 1
+#define DSMOE_WS_SEL_SCORES 2
+#define DSMOE_WS_OFFSETS 3
+#define DSMOE_WS_SORTED_SLOT 4
+#define DSMOE_WS_SORTED_TOKEN 5
+#define DSMOE_WS_SLOT_POS 6
+size_t dsmoe_moe_fwd_workspace_offset(const dsmoe_dims* dims, int training, int buffer);
 
 /* ---------------------------------------------------------------------------
  * Stage timing for measurement tools (no counterpart in the reference, which

@@ -14,6 +14,8 @@ It restates, with torch CPU ops, the reference's default ("stacked") forward:
 * ``grouped_moe_ref``     <- ``models/moe_triton.py:28-51`` (grouped_moe_pytorch)
 * ``balance_loss_ref``    <- ``models/moe.py:181-192``
 * ``update_bias_ref``     <- ``models/moe.py:21-27``
+* ``expert_grad_slice_ref`` <- autograd of ``models/moe.py:128-132`` for one expert,
+  restricted to a slice of its inter columns
 
 Deliberate, documented deviation: the gate is evaluated on ``x.float()`` with
 an fp32 gate weight (the reference runs ``F.linear`` in ``x.dtype``, i.e. bf16
@@ -226,6 +228,33 @@ def update_bias_ref(bias: torch.Tensor, counts: torch.Tensor, speed: float, uppe
     b[c > avg * (1.0 + upper)] -= speed
     b[c < avg * (1.0 - lower)] += speed
     return b
+
+
+# ----------------------------------------------------------------------------
+# Weight gradients of one expert, restricted to a slice of its inter columns.
+# ----------------------------------------------------------------------------
+def expert_grad_slice_ref(x_rows: torch.Tensor, dy_rows: torch.Tensor, w_rows: torch.Tensor, w1: torch.Tensor,
+                          w2: torch.Tensor, w3: torch.Tensor, i0: int, i1: int):
+    """fp32 weight gradients of one SwiGLU expert for inter columns [i0, i1).
+
+    The expert sees rows ``x_rows`` (n, D) with routing weights ``w_rows``
+    (n,) and the upstream gradient ``dy_rows`` (n, D) of the layer output,
+    which holds ``w * W2 (silu(W1 x) * W3 x)`` for these rows
+    (models/moe.py:128-132; shared experts: w = 1, models/moe.py:175-179).
+    Column i of h depends only on row i of W1 and W3, and only column i of W2
+    reads it, so the output splits into a sum over inter slices and the slice
+    [i0, i1) of every weight gradient is the gradient of that slice's term:
+    autograd of ``(w * silu(x W1s^T) * (x W3s^T)) W2s^T`` with W1s = W1[i0:i1],
+    W3s = W3[i0:i1], W2s = W2[:, i0:i1], all in fp32.
+    Returns (dW1[i0:i1] (m, D), dW2[:, i0:i1] (D, m), dW3[i0:i1] (m, D))."""
+    x = x_rows.float()
+    a = w1[i0:i1].detach().float().clone().requires_grad_(True)
+    b = w2[:, i0:i1].detach().float().clone().requires_grad_(True)
+    c = w3[i0:i1].detach().float().clone().requires_grad_(True)
+    h = F.silu(x @ a.t()) * (x @ c.t())
+    out = (h @ b.t()) * w_rows.float().unsqueeze(-1)
+    out.backward(dy_rows.float())
+    return a.grad, b.grad, c.grad
 
 
 # ----------------------------------------------------------------------------

@@ -76,3 +76,27 @@ def test_workspace_sizes_are_consistent(lib):
     assert inf >= 2 * (N * 1408 + N * 2048 + 8192 * 2816 + 8192 * 2048)
     assert trn - inf >= 2 * 2 * (N * 1408 + 8192 * 2816)
     assert lib.dsmoe_permute_workspace_size(ctypes.byref(d)) > 0
+
+
+def test_workspace_offsets_lie_inside_the_forward_workspace(lib):
+    """dsmoe_moe_fwd_workspace_offset: every routing buffer lies inside the
+    workspace, 256-byte aligned, without overlaps; unknown ids and bad dims
+    give (size_t)-1."""
+    import dsmoe._lib as L
+    bad = ctypes.c_size_t(-1).value
+    for T, train in ((8192, 0), (64, 0), (16384, 1)):
+        d = L.Dims(T, 2048, 64, 6, 1408, 2, 1408, L.DSMOE_BF16, 1.0)
+        total = lib.dsmoe_moe_fwd_workspace_size(ctypes.byref(d), train)
+        N = T * 6
+        sizes = {L.WS_IDX: 4 * N, L.WS_WEIGHTS: 4 * N, L.WS_SEL_SCORES: 4 * N, L.WS_OFFSETS: 4 * 65,
+                 L.WS_SORTED_SLOT: 4 * N, L.WS_SORTED_TOKEN: 4 * N, L.WS_SLOT_POS: 4 * N}
+        spans = []
+        for buf, nbytes in sizes.items():
+            off = lib.dsmoe_moe_fwd_workspace_offset(ctypes.byref(d), train, buf)
+            assert off != bad and off % 256 == 0 and off + nbytes <= total
+            spans.append((off, off + nbytes))
+        spans.sort()
+        assert all(a[1] <= b[0] for a, b in zip(spans, spans[1:]))
+        assert lib.dsmoe_moe_fwd_workspace_offset(ctypes.byref(d), train, 99) == bad
+    d = L.Dims(16, 64, 4, 5, 32, 1, 32, L.DSMOE_F32, 1.0)          # k > E
+    assert lib.dsmoe_moe_fwd_workspace_offset(ctypes.byref(d), 0, L.WS_IDX) == bad

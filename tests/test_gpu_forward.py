@@ -189,45 +189,96 @@ def _run_layer(case, x, p):
     return out
 
 
-@pytest.mark.parametrize("case,sample", [
-    (CS.C0, None),
-    (CS.C1, 512),
-    (CS.C2, 512),
-    (CS.C3.with_tokens(1024), None),
-    (CS.C3, 192),
-    (CS.C3_DECODE, None),
+def _layer_raw(case, x, p, training=False):
+    """dsmoe_moe_fwd through the C ABI with its fp32 logits output, then the
+    layer's own routing buffers read out of its workspace
+    (dsmoe_moe_fwd_workspace_offset)."""
+    from dsmoe import _lib as L
+    lib = L.load()
+    q = CS.params_to(p, DEV)
+    T, D, E, k = case.T, case.D, case.E, case.k
+    d = L.make_dims(T, D, E, k, case.I, case.S, case.I_s, case.dtype, case.route_scale)
+    ws = torch.empty(max(256, lib.dsmoe_moe_fwd_workspace_size(d, int(training))), dtype=torch.uint8, device=DEV)
+    xd = x.to(DEV).contiguous()
+    y = torch.empty(T, D, dtype=case.dtype, device=DEV)
+    idx64 = torch.empty(T, k, dtype=torch.int64, device=DEV)
+    wx = torch.empty(T, k, dtype=case.dtype, device=DEV)
+    counts = torch.empty(E, dtype=torch.int32, device=DEV)
+    logits = torch.empty(T, E, dtype=torch.float32, device=DEV)
+    arrs = [L.ptr_array(ts) for ts in (q.w1, q.w2, q.w3, q.sw1, q.sw2, q.sw3)]
+    print(f"[{case.name}] dsmoe_moe_fwd T={T} D={D} E={E} k={k} training={int(training)}", flush=True)
+    rc = lib.dsmoe_moe_fwd(L.ptr(xd), L.ptr(q.gate_w), L.ptr(q.gate_bias), *[a[0] for a in arrs], d, int(training),
+                           L.ptr(y), L.ptr(idx64), L.ptr(wx), L.ptr(counts), L.ptr(logits), L.ptr(ws), ws.numel(),
+                           L.stream_ptr(DEV))
+    L.check(rc, "dsmoe_moe_fwd")
+    torch.cuda.synchronize()
+    wsc = ws.cpu()
+
+    def buf(which, n, dt):
+        off = lib.dsmoe_moe_fwd_workspace_offset(d, int(training), which)
+        nb = n * torch.empty((), dtype=dt).element_size()
+        return wsc[off:off + nb].view(dt).numpy()
+
+    N = T * k
+    return {"y": y.cpu(), "idx64": _np(idx64), "wx": wx.cpu(), "counts": _np(counts), "logits": _np(logits),
+            "idx": buf(L.WS_IDX, N, torch.int32).reshape(T, k), "weights": buf(L.WS_WEIGHTS, N, torch.float32).reshape(T, k),
+            "sel": buf(L.WS_SEL_SCORES, N, torch.float32).reshape(T, k), "offsets": buf(L.WS_OFFSETS, E + 1, torch.int32),
+            "sorted_slot": buf(L.WS_SORTED_SLOT, N, torch.int32), "sorted_token": buf(L.WS_SORTED_TOKEN, N, torch.int32),
+            "slot_pos": buf(L.WS_SLOT_POS, N, torch.int32)}
+
+
+@pytest.mark.parametrize("case,sample,training", [
+    (CS.C0, None, False),
+    (CS.C1, 512, False),
+    (CS.C2, 512, False),
+    (CS.C3.with_tokens(1024), None, False),
+    (CS.C3, 192, False),
+    (CS.C4, 128, True),
+    (CS.C3_DECODE, None, False),
     # decode-size calls (few-row GEMM path): one token; a skewed routing that
     # sends every token to two experts (37-row tiles); no shared experts
-    (CS.Case("dec_t1", 1, 2048, 64, 1408, 6, 2, 1408, torch.bfloat16), None),
-    (CS.Case("dec_t37_skew", 37, 512, 8, 256, 2, 1, 384, torch.bfloat16, "skew"), None),
-    (CS.Case("dec_t64_noshared", 64, 1024, 16, 512, 4, 0, 0, torch.bfloat16, "normal"), None),
+    (CS.Case("dec_t1", 1, 2048, 64, 1408, 6, 2, 1408, torch.bfloat16), None, False),
+    (CS.Case("dec_t37_skew", 37, 512, 8, 256, 2, 1, 384, torch.bfloat16, "skew"), None, False),
+    (CS.Case("dec_t64_noshared", 64, 1024, 16, 512, 4, 0, 0, torch.bfloat16, "normal"), None, False),
+    # three shared experts (the down projection sums three K segments) and
+    # inter widths with N % 8 == 4: the register-staged MFMA kernel
+    # (gemm_mfma_kernel) instead of the quad-wave one
+    (CS.Case("s3_i132", 512, 256, 8, 132, 2, 3, 100, torch.bfloat16, "normal"), None, False),
+    (CS.Case("s3_i132_train", 512, 256, 8, 132, 2, 3, 100, torch.bfloat16, "normal"), None, True),
 ], ids=lambda v: getattr(v, "name", str(v)))
-def test_layer_forward_vs_oracle(case, sample):
-    """Full-size configs are checked on a seeded token sample: each token's
-    output depends only on that token's row and the weights (the layer is
-    token-separable), so the oracle on the sampled rows is exact for them."""
+def test_layer_forward_vs_oracle(case, sample, training):
+    """Every config at full size.  The layer's own fp32 logits (K-split gate
+    and routing kernel at T <= 4096, fused gate above) are within 1e-5 of the
+    fp32 oracle; given those logits, the C oracle reproduces the layer's expert
+    ids, fp32 weights, selected scores, counts and its sorted order (offsets,
+    sorted slots and tokens, inverse) bit for bit.  The output is checked on a
+    seeded token sample: each token's output depends only on that token's row
+    and the weights (the layer is token-separable), so the oracle on the
+    sampled rows is exact for them."""
     x, p, _ = CS.make_inputs(case)
-    y, idx, wx, counts = _run_layer(case, x, p)
-    # routing of every token: bit-exact vs the C oracle on this layer's fp32 logits
-    lg = R.gate_logits_ref(x, p.gate_w).numpy()
-    ridx, rw, _, rc = RC.route(lg, p.gate_bias.numpy(), case.k, case.route_scale)
-    margin = RC.min_margin(lg, p.gate_bias.numpy(), case.k)
-    print(f"[{case.name}] min margin {margin:.3e}")
-    gidx = _np(idx)
-    if margin > 1e-5:
-        assert np.array_equal(gidx, ridx)
-        assert np.array_equal(_np(counts), rc)
-    else:
-        assert (gidx != ridx).any(axis=1).mean() < 1e-3
-    assert np.array_equal(_np(counts), np.bincount(gidx.ravel(), minlength=case.E))
+    out = _layer_raw(case, x, p, training)
+    lg = out["logits"]
+    np.testing.assert_allclose(lg, R.gate_logits_ref(x, p.gate_w).numpy(), rtol=1e-5, atol=1e-5)
+    ridx, rw, rs, rc = RC.route(lg, p.gate_bias.numpy(), case.k, case.route_scale)
+    print(f"[{case.name}] min k/k+1 margin on the layer's logits {RC.min_margin(lg, p.gate_bias.numpy(), case.k):.3e}")
+    assert np.array_equal(out["idx"], ridx)
+    assert np.array_equal(out["idx64"], ridx.astype(np.int64))
+    assert np.array_equal(out["weights"], rw)
+    assert np.array_equal(out["sel"], rs)
+    assert np.array_equal(out["counts"], rc)
+    np.testing.assert_array_equal(out["wx"].float().numpy(), torch.from_numpy(rw).to(case.dtype).float().numpy())
+    off, ss, st, sp = RC.permute(ridx, case.E)
+    assert np.array_equal(out["offsets"], off)
+    assert np.array_equal(out["sorted_slot"], ss)
+    assert np.array_equal(out["sorted_token"], st)
+    assert np.array_equal(out["slot_pos"], sp)
     rows = torch.arange(case.T) if sample is None else \
         torch.randperm(case.T, generator=torch.Generator().manual_seed(11))[:sample]
     y_ref = R.moe_forward_ref(x[rows], p, case.k, case.route_scale)
     tol = 1e-5 if case.dtype == torch.float32 else 2e-2
-    torch.testing.assert_close(y.cpu()[rows].float(), y_ref.float(), rtol=tol, atol=tol)
+    torch.testing.assert_close(out["y"][rows].float(), y_ref.float(), rtol=tol, atol=tol)
     if case.bias == "skew":
-        c = _np(counts)
-        assert c[0] == case.T and c[1] == case.T and c.sum() == case.N
+        assert rc[0] == case.T and rc[1] == case.T and rc.sum() == case.N
 
 
 def test_layer_forward_is_deterministic():
@@ -269,3 +320,60 @@ def test_module_update_bias_kats_on_device():
     gate.bias.zero_()
     gate.update_bias(torch.tensor([256, 0, 0, 0], device=DEV), speed=0.1)
     assert torch.equal(gate.bias.cpu(), torch.tensor([-0.1, 0.1, 0.1, 0.1]))
+
+
+def test_grouped_operator_promotes_like_the_reference():
+    """models/moe_triton.py:525 returns out * sorted_weights.unsqueeze(-1):
+    fp32 gate weights over a bf16 expert output give an fp32 result (the
+    product of the bf16-rounded output and the fp32 weight), with and without
+    autograd."""
+    from dsmoe import grouped_moe_dispatch
+    x, w1, w2, w3, off, _ = CS.grouped_case(300, 128, 4, 256, [130, 0, 1, 169], torch.bfloat16, seed=5)
+    gw = torch.rand(300, generator=torch.Generator().manual_seed(6)) * 0.1          # fp32
+    d = lambda t: t.to(DEV)
+    ones = torch.ones(300, dtype=torch.bfloat16)
+    with torch.no_grad():
+        y = grouped_moe_dispatch(d(x), d(w1), d(w2), d(w3), d(gw), d(off))
+        out = grouped_moe_dispatch(d(x), d(w1), d(w2), d(w3), d(ones), d(off))   # unweighted, bf16
+    assert y.dtype == torch.float32 and out.dtype == torch.bfloat16
+    assert torch.equal(y, out.float() * d(gw).unsqueeze(-1))
+    xl = d(x).requires_grad_(True)
+    yg = grouped_moe_dispatch(xl, d(w1), d(w2), d(w3), d(gw), d(off))
+    assert yg.dtype == torch.float32 and torch.equal(yg.detach(), y)
+    ref = R.grouped_moe_ref(x.float(), w1.float(), w2.float(), w3.float(), off, gw)
+    torch.testing.assert_close(y.cpu(), ref, rtol=2e-2, atol=2e-2)
+
+
+def test_expert_module_forward():
+    """Expert.forward (models/moe.py:40-49) as a one-group call of the grouped
+    operator, against the SwiGLU on the oracle's arithmetic."""
+    from dsmoe import Expert
+    g = torch.Generator().manual_seed(21)
+    m = Expert(256, 192)
+    with torch.no_grad():
+        for lin in (m.w1, m.w2, m.w3):
+            lin.weight.copy_(torch.randn(lin.weight.shape, generator=g) * 0.05)
+    x = torch.randn(3, 70, 256, generator=g)
+    m = m.to(DEV, torch.bfloat16)
+    with torch.no_grad():
+        y = m(x.to(DEV, torch.bfloat16))
+    assert y.shape == x.shape and y.dtype == torch.bfloat16
+    xb = x.to(torch.bfloat16).float().reshape(-1, 256)
+    w1, w2, w3 = (lin.weight.detach().float().cpu() for lin in (m.w1, m.w2, m.w3))
+    ref = (torch.nn.functional.silu(xb @ w1.t()) * (xb @ w3.t())) @ w2.t()
+    torch.testing.assert_close(y.float().cpu().reshape(-1, 256), ref, rtol=2e-2, atol=2e-2)
+
+
+def test_update_bias_with_fractional_counts():
+    """Floating counts (e.g. averaged over steps) run the fp32 band rule of
+    models/moe.py:21-27 without truncation."""
+    from dsmoe import AuxLossFreeGate
+    gate = AuxLossFreeGate({"dim": 8, "n_activated_experts": 2, "n_routed_experts": 6,
+                            "bias_upper_threshold": 0.10, "bias_lower_threshold": 0.10}).to(DEV)
+    counts = torch.tensor([0.9, 0.5, 0.6, 0.4, 0.7, 0.3])   # mean 0.5667; every count 1e-2 or more from a band edge
+    b0 = torch.tensor([0.1, -0.2, 0.0, 0.05, 0.0, 0.3])
+    gate.bias.copy_(b0.to(DEV))
+    gate.update_bias(counts.to(DEV), speed=0.01)
+    assert torch.equal(gate.bias.cpu(), R.update_bias_ref(b0, counts, 0.01))
+    truncated = R.update_bias_ref(b0, counts.to(torch.int32), 0.01)
+    assert not torch.equal(gate.bias.cpu(), truncated)             # integer truncation would differ

@@ -85,3 +85,47 @@ def test_torch_compile_traces_the_layer_as_one_op():
         assert torch.equal(g0[n], g1[n]), n
     # the side state is set by the compiled forward too
     assert m._last_indices.shape == (CASE16.T, CASE16.k) and m._last_weights.dtype == torch.bfloat16
+
+
+def test_torch_compile_inductor_backend():
+    """The trainer's default compile backend (inductor) around the layer: one
+    custom operator, results bit-identical to eager."""
+    import torch._dynamo
+    from dsmoe import DeepSeekMoE
+    x, p, dy = CS.make_inputs(CASE16, with_dy=True)
+    m = CS.load_module(CASE16, p, DEV, DeepSeekMoE)
+    y0, dx0, g0 = _step(m, x, dy)
+    m.zero_grad(set_to_none=True)
+    torch._dynamo.reset()
+    cm = torch.compile(m, backend="inductor", fullgraph=True)
+    y1, dx1, g1 = _step(m, x, dy, fn=cm)
+    assert torch.equal(y0, y1) and torch.equal(dx0, dx1)
+    for n in g0:
+        assert torch.equal(g0[n], g1[n]), n
+
+
+def test_autocast_weight_copies_follow_optimizer_steps():
+    """Under bf16 autocast the fp32 expert weights are cast once per
+    parameter version: two training steps with an SGD update between them give
+    the explicit bf16 layer's results on the updated (bf16-rounded) weights."""
+    from dsmoe import DeepSeekMoE
+    x, p, dy = CS.make_inputs(CASE32, with_dy=True)
+    m32 = CS.load_module(CASE32, p, DEV, DeepSeekMoE)
+    opt = torch.optim.SGD(m32.parameters(), lr=0.5)
+    for step in range(2):
+        opt.zero_grad(set_to_none=True)
+        xin = x.clone().to(DEV).requires_grad_(True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            y = m32(xin)
+        (y * dy.to(DEV)).sum().backward()
+        torch.cuda.synchronize()
+        # the same parameters, experts rounded to bf16, the gate kept fp32
+        m16 = DeepSeekMoE(CASE16.config()).to(DEV, torch.bfloat16)
+        m16.gate.float()
+        m16.load_state_dict({k: v.detach().clone() for k, v in m32.state_dict().items()})
+        y16, dx16, g16 = _step(m16, x.to(torch.bfloat16), dy)
+        assert torch.equal(y, y16.float()), step
+        assert torch.equal(xin.grad, dx16.float()), step
+        for n, prm in m32.named_parameters():
+            assert torch.equal(prm.grad, g16[n].float()), (step, n)
+        opt.step()

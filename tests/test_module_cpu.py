@@ -172,3 +172,82 @@ def test_layer_operator_shapes_without_a_gpu():
     assert len(g) == 2 + len(ws)
     assert g[0].shape == (T, D) and g[1].shape == (E, D) and g[1].dtype == torch.float32
     assert all(a.shape == w.shape and a.dtype == w.dtype for a, w in zip(g[2:], ws))
+
+
+def _layer_args(D=16, E=4, I=8, S=1, I_s=8, dt=torch.bfloat16):
+    x = torch.zeros(5, D, dtype=dt)
+    gw, gb = torch.zeros(E, D), torch.zeros(E)
+    w1 = [torch.zeros(I, D, dtype=dt) for _ in range(E)]
+    w2 = [torch.zeros(D, I, dtype=dt) for _ in range(E)]
+    w3 = [torch.zeros(I, D, dtype=dt) for _ in range(E)]
+    s1 = [torch.zeros(I_s, D, dtype=dt) for _ in range(S)]
+    s2 = [torch.zeros(D, I_s, dtype=dt) for _ in range(S)]
+    s3 = [torch.zeros(I_s, D, dtype=dt) for _ in range(S)]
+    return [x, gw, gb, w1, w2, w3, s1, s2, s3]
+
+
+@pytest.mark.parametrize("edit,match", [
+    (lambda a: a.__setitem__(1, a[1].bfloat16()), "gate weight must be float32"),      # model.bfloat16()
+    (lambda a: a.__setitem__(1, torch.zeros(4, 8)), "gate weight must be float32"),    # (E, D) mismatch
+    (lambda a: a.__setitem__(2, torch.zeros(4, dtype=torch.float64)), "gate bias"),
+    (lambda a: a.__setitem__(2, torch.zeros(5)), "gate bias"),
+    (lambda a: a[4].__setitem__(1, torch.zeros(8, 16, dtype=torch.bfloat16)), "w2"),  # w2[1] transposed
+    (lambda a: a[3].__setitem__(2, torch.zeros(8, 16)), "dtype"),                      # fp32 expert in bf16 layer
+    (lambda a: a[3].__setitem__(0, torch.zeros(12, 16, dtype=torch.bfloat16)), "w1/w3"),
+    (lambda a: a[6].__setitem__(0, torch.zeros(8, 12, dtype=torch.bfloat16)), "shared expert"),
+    (lambda a: a.__setitem__(8, []), "shared"),
+    (lambda a: a.__setitem__(0, torch.zeros(5, 16, dtype=torch.float16)), "activation dtype"),
+])
+def test_moe_layer_rejects_bad_shapes_before_any_launch(edit, match):
+    """The kernels trust the sizes they are given; moe_layer checks them first
+    (CPU tensors: the check runs before the device check)."""
+    from dsmoe import ops
+    args = _layer_args()
+    ops.check_layer_args(*args, k=2)                                   # the valid case passes
+    edit(args)
+    with pytest.raises(ValueError, match=match):
+        ops.moe_layer(*args, k=2)
+
+
+def test_moe_layer_rejects_bad_topk():
+    from dsmoe import ops
+    with pytest.raises(ValueError, match="n_activated_experts"):
+        ops.moe_layer(*_layer_args(), k=5)
+
+
+@pytest.mark.parametrize("idx,ok", [
+    ([[0, 1], [3, 2]], True),
+    ([[0, 4], [3, 2]], False),      # id == E
+    ([[0, -1], [3, 2]], False),     # negative id
+    ([[1, 1], [3, 2]], False),      # repeated within a token
+    ([[0], [3]], True),
+])
+def test_check_routing(idx, ok):
+    from dsmoe import ops
+    t = torch.tensor(idx, dtype=torch.int32)
+    if ok:
+        ops.check_routing(t, 4)
+    else:
+        with pytest.raises(ValueError):
+            ops.check_routing(t, 4)
+
+
+def test_autocast_cast_cache_follows_parameter_updates(small_cfg):
+    """The bf16 copy used under autocast is made once per parameter version:
+    reused while the parameter is unchanged, remade after an in-place update,
+    and the gradient reaches the fp32 parameter through it."""
+    moe = DeepSeekMoE(small_cfg)
+    w = moe.experts[1].w3.weight
+    a = moe._cast(w, torch.bfloat16)
+    b = moe._cast(w, torch.bfloat16)
+    assert a.dtype == torch.bfloat16 and a.data_ptr() == b.data_ptr()
+    assert torch.equal(a.float(), w.detach().bfloat16().float())
+    (a.float() * 3.0).sum().backward()
+    assert w.grad.dtype == torch.float32 and torch.equal(w.grad, torch.full_like(w, 3.0))
+    with torch.no_grad():
+        w.mul_(0.5)                                   # an optimizer step
+    c = moe._cast(w, torch.bfloat16)
+    assert torch.equal(c.float(), w.detach().bfloat16().float())
+    assert moe._cast(w, torch.float32) is w
+    moe.to(torch.float64)
+    assert not moe._cast_cache

@@ -256,3 +256,30 @@ def test_grouped_ref_gradients_pass_gradcheck():
     off = torch.tensor([0, 4, 4, 7])
     assert torch.autograd.gradcheck(lambda a, b, c, d, w: R.grouped_moe_ref(a, b, c, d, off, w),
                                     (x, w1, w2, w3, gw), eps=1e-6, atol=1e-7)
+
+
+def test_expert_grad_slice_matches_full_layer_autograd():
+    """expert_grad_slice_ref on one expert's rows gives exactly the slice of
+    the full layer's weight gradients (autograd through moe_forward_ref, fp64),
+    for a routed expert (rows and weights from the layer's routing) and for a
+    shared expert (all rows, weight 1)."""
+    g = torch.Generator().manual_seed(3)
+    T, D, E, I, k, S = 96, 24, 6, 20, 2, 1
+    p = R.make_params(D, E, I, S, seed=9).to(torch.float64)
+    x = torch.randn(T, D, generator=g, dtype=torch.float64)
+    dy = torch.randn(T, D, generator=g, dtype=torch.float64)
+    full = R.moe_forward_backward_ref(x, p, k, dy)
+    idx, w = full["indices"], full["weights"]
+    for e in range(E):
+        t, j = torch.nonzero(idx == e, as_tuple=True)
+        if len(t) == 0:
+            continue
+        a, b, c = R.expert_grad_slice_ref(x[t].double(), dy[t], w[t, j], p.w1[e].double(), p.w2[e].double(),
+                                          p.w3[e].double(), 5, 13)
+        torch.testing.assert_close(a.double(), full["dw1"][e][5:13], rtol=1e-5, atol=1e-6)
+        torch.testing.assert_close(b.double(), full["dw2"][e][:, 5:13], rtol=1e-5, atol=1e-6)
+        torch.testing.assert_close(c.double(), full["dw3"][e][5:13], rtol=1e-5, atol=1e-6)
+    a, b, c = R.expert_grad_slice_ref(x, dy, torch.ones(T, dtype=torch.float64), p.sw1[0], p.sw2[0], p.sw3[0], 0, I)
+    torch.testing.assert_close(a.double(), full["dsw1"][0], rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(b.double(), full["dsw2"][0], rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(c.double(), full["dsw3"][0], rtol=1e-5, atol=1e-6)
