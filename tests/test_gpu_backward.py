@@ -51,7 +51,8 @@ def _close(a, b, rtol, atol, what):
     assert torch.allclose(a, b, rtol=rtol, atol=atol), f"{what}: max |diff| {err:.3e} (ref max {b.abs().max():.3e})"
 
 
-@pytest.mark.parametrize("name,k,rs", [("c0_fp32.npz", 2, 1.0), ("noshared_scale.npz", 3, 2.5)])
+@pytest.mark.parametrize("name,k,rs", [("c0_fp32.npz", 2, 1.0), ("noshared_scale.npz", 3, 2.5),
+                                       ("e16_k4_fp32.npz", 4, 1.5)])
 def test_backward_matches_reference_golden_fp32(golden_dir, name, k, rs):
     d = dict(np.load(golden_dir / name, allow_pickle=False))
     t = lambda key: torch.from_numpy(d[key])
@@ -119,6 +120,23 @@ def test_backward_bf16_vs_oracle(case):
     for e in torch.nonzero(counts == 0).flatten().tolist():
         for nm in ("dw1", "dw2", "dw3"):
             assert not out[nm][e].any(), f"{nm}[{e}] of an expert with no rows is not zero"
+
+
+def test_backward_matches_reference_golden_bf16(golden_dir):
+    """Against the reference layer's own bf16 forward and backward (fp32 gate,
+    tests/golden/c0_bf16_fwd_bwd.npz): routing exact; y and dx within 2e-2;
+    the token sums (dW_gate, every dW) within 2e-2 x their max magnitude."""
+    d = dict(np.load(golden_dir / "c0_bf16_fwd_bwd.npz", allow_pickle=False))
+    cv = lambda a: torch.from_numpy(a.astype(np.uint16).view(np.int16).copy()).view(torch.bfloat16)
+    st = lambda key: list(cv(d[key]).unbind(0))
+    out = _run(cv(d["x_bits"]), torch.from_numpy(d["gate_w"]), torch.from_numpy(d["gate_bias"]), st("w1_bits"),
+               st("w2_bits"), st("w3_bits"), st("sw1_bits"), st("sw2_bits"), st("sw3_bits"), 2, 1.0, cv(d["dy_bits"]))
+    assert np.array_equal(out["idx"].numpy(), d["last_indices"])
+    _close(out["y"], cv(d["y_bits"]), 2e-2, 2e-2, "y")
+    _close(out["dx"], cv(d["dx_bits"]), 2e-2, 2e-2, "dx")
+    _sum_close(out["dgate_w"], torch.from_numpy(d["dgate_w"]), "dgate_w")
+    for nm in ("dw1", "dw2", "dw3", "dsw1", "dsw2", "dsw3"):
+        _sum_close(torch.stack(out[nm]), cv(d[nm + "_bits"]), nm)
 
 
 def test_backward_is_deterministic():
