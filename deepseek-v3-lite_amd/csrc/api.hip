@@ -251,8 +251,9 @@ int dsmoe_permute(const int32_t* idx, const dsmoe_dims* dims, int32_t* offsets, 
   Carver c(workspace);
   PermuteScratch ps;
   permute_scratch_carve(c, *dims, TILE_M, &ps);
-  rc = launch_permute(idx, *dims, TILE_M, ps, offsets, sorted_slot, sorted_token, slot_pos, counts, weights, sorted_w,
-                      st);
+  rc = launch_permute(idx, *dims,
+                      permute_out(ps, TILE_M, offsets, sorted_slot, sorted_token, slot_pos, counts, weights, sorted_w),
+                      false, st);
   if (rc) return rc;
   if (x)
     rc = launch_gather_rows(x, dims->T, sorted_token, (int64_t)dims->T * dims->k, dims->D, elem_size(dims->dtype),
@@ -383,12 +384,6 @@ int dsmoe_moe_fwd(const void* x, const float* gate_w, const float* gate_bias, co
   }
   const bool mf = all_aligned16(w1, d.E) && all_aligned16(w2, d.E) && all_aligned16(w3, d.E) &&
                   (d.S == 0 || (all_aligned16(sw1, d.S) && all_aligned16(sw2, d.S) && all_aligned16(sw3, d.S)));
-  // (a) gate
-  GateOut go{logits, L.idx, idx64, L.w, weights_x, L.sel, nullptr};
-  tm.begin(ST_GATE);
-  rc = launch_gate(x, nullptr, gate_w, gate_bias, d, go, st, L.gate_part, tab_in_gate ? &tabc : nullptr, L.ptrs);
-  tm.end();
-  if (rc) return rc;
   // GEMM descriptors; the routed schedule height follows the kernel choice
   GemmDesc g1 = desc_zero();
   g1.A = x; g1.lda = d.D; g1.a_rows = d.T; g1.a_map = L.sorted_token;
@@ -408,10 +403,20 @@ int dsmoe_moe_fwd(const void* x, const float* gate_w, const float* gate_bias, co
     sk = gemm_sk_ok(t1) && gemm_sk_ok(t2);
   }
   const int bm = sk ? SK_BM : gemm_tile_m(mfr);
-  // (b) permute (counts come from the scan: exact bincount, no atomics)
+  // (a) gate; the MFMA gate's routing launch also ranks the slots for the
+  // permute (and finishes it for a call of one rank block)
+  const PermuteOut po = permute_out(L.ps, bm, L.offsets, L.sorted_slot, L.sorted_token, L.slot_pos, counts,
+                                    training ? L.w : nullptr, L.sorted_w);
+  GateOut go{logits, L.idx, idx64, L.w, weights_x, L.sel, nullptr};
+  bool ranked = false;
+  tm.begin(ST_GATE);
+  rc = launch_gate(x, nullptr, gate_w, gate_bias, d, go, st, L.gate_part, tab_in_gate ? &tabc : nullptr, L.ptrs, &po,
+                   &ranked);
+  tm.end();
+  if (rc) return rc;
+  // (b) permute (counts are the exact per-expert totals, no atomics)
   tm.begin(ST_PERMUTE);
-  rc = launch_permute(L.idx, d, bm, L.ps, L.offsets, L.sorted_slot, L.sorted_token, L.slot_pos, counts,
-                      training ? L.w : nullptr, L.sorted_w, st);
+  rc = launch_permute(L.idx, d, po, ranked, st);
   if (!rc && training) {
     // the routed rows of x in sorted order, for the backward's weight
     // gradient (a K-major operand read without a row gather); gemm1 keeps

@@ -135,11 +135,34 @@ struct GateOut {
 
 struct PermuteScratch {
   int32_t* blockhist;
-  int32_t* blockbase;
   int32_t* local_rank;
   MTile* sched;
   int32_t* sched_count;
 };
+
+// Tokens are ranked in blocks of RANK_TOKENS (one token per lane of a wave).
+constexpr int RANK_TOKENS = 64;
+
+// Outputs and scratch of the permute stage.  blockhist[b * E + e]: the count
+// of expert e among the tokens of rank block b; local_rank[s]: slot s's rank
+// among the earlier tokens of its rank block routed to the same expert (-1:
+// the slot is not placed).
+struct PermuteOut {
+  int32_t* offsets;       // E + 1
+  int32_t* sorted_slot;   // T * k
+  int32_t* sorted_token;  // T * k
+  int32_t* slot_pos;      // T * k
+  int32_t* counts;        // E, optional
+  const float* w;         // T * k, optional: gathered into sorted_w
+  float* sorted_w;
+  MTile* sched;           // M tiles of bm rows inside each expert
+  int32_t* sched_count;
+  int32_t bm;
+  int32_t* blockhist;
+  int32_t* local_rank;
+};
+PermuteOut permute_out(const PermuteScratch& s, int bm, int32_t* offsets, int32_t* sorted_slot, int32_t* sorted_token,
+                       int32_t* slot_pos, int32_t* counts, const float* w, float* sorted_w);
 
 // ---------------------------------------------------------------- launchers
 // A chunk of a device pointer table passed by value as a kernel argument
@@ -151,24 +174,27 @@ struct PtrChunk {
   int32_t off;
 };
 
-// part (optional): workspace of gate_part_floats(d) floats for a K-split gate
-// (partial logits, then a routing kernel); nullptr keeps one fused launch.
+// part (optional): workspace of gate_part_floats(d) floats.  With it the
+// MFMA gate writes K-split partial logits and a second launch adds them and
+// routes; without it one launch computes and routes whole token tiles.
 // tables (optional, MFMA gate only): a pointer table written by the gate
 // launch itself (workgroup 0) into tab_dst, saving the upload launch.
+// po (optional): the routing launch also ranks the routed slots for the
+// permute (po's scratch), and for a call of one rank block finishes the
+// permute; *ranked tells whether it did (the SIMT gate does not rank).
 int launch_gate(const void* x, const float* logits_in, const float* gw, const float* bias, const dsmoe_dims& d,
                 const GateOut& out, hipStream_t st, float* part = nullptr, const PtrChunk* tables = nullptr,
-                const void** tab_dst = nullptr);
+                const void** tab_dst = nullptr, const PermuteOut* po = nullptr, bool* ranked = nullptr);
 bool gate_uses_mfma(const void* x, const float* gw, const dsmoe_dims& d);
 int gate_k_splits(const dsmoe_dims& d);
 size_t gate_part_floats(const dsmoe_dims& d);
-constexpr int GATE_KS_MAX = 16;      // K splits of the gate at most
-constexpr int PERMUTE_SMALL_T = 256; // calls of at most this many tokens permute in one workgroup
+constexpr int GATE_KS_MAX = 8;       // K splits of the gate at most
 void launch_fill_i32(int32_t* p, int n, int32_t v, hipStream_t st);
 int64_t sched_bound(int64_t rows, int groups, int bm);
 size_t permute_scratch_carve(Carver& c, const dsmoe_dims& d, int bm, PermuteScratch* out);
-int launch_permute(const int32_t* idx, const dsmoe_dims& d, int bm, const PermuteScratch& s, int32_t* offsets,
-                   int32_t* sorted_slot, int32_t* sorted_token, int32_t* slot_pos, int32_t* counts, const float* w,
-                   float* sorted_w, hipStream_t st);
+// The permute of idx into po.  ranked: the slots are already ranked (by the
+// routing launch, launch_gate with po), else a rank launch runs first.
+int launch_permute(const int32_t* idx, const dsmoe_dims& d, const PermuteOut& po, bool ranked, hipStream_t st);
 // dst[p] = x[rows[p]] for p < nrows (rows of D elements); rows outside
 // [0, src_rows) give zero rows.
 int launch_gather_rows(const void* x, int64_t src_rows, const int32_t* rows, int64_t nrows, int D, int elem, void* dst,

@@ -2,19 +2,30 @@
 // renormalisation, per-expert histogram.  Restates models/moe.py:29-37 and
 // the bincount of models/moe.py:114 (see dsmoe.h for the tie rule).
 //
-// Logits.  bf16 x: MFMA.  Each fp32 gate weight is split exactly into three
+// Logits, bf16 x: MFMA.  Each fp32 gate weight is split exactly into three
 // bf16 parts by truncation (w = hi + mid + lo: hi keeps the top 8 significand
-// bits, mid the next 8, lo the last 8), so x.w = x.hi + x.mid + x.lo with
-// every product exact; the MFMA accumulates in fp32.  A block takes 32 tokens
-// and all experts; its 4 waves split D in quarters and the four partial sums
-// are added in a fixed order, so the result is deterministic.  fp32 x: SIMT
-// FMA tiles.
+// bits, mid the next 8, lo the last 8), so x.w = x.lo + x.mid + x.hi with
+// every product exact; the MFMA accumulates in fp32.  A workgroup takes
+// GP_TOK = 128 tokens (wave w: tokens 32w .. 32w + 31) and every expert over
+// one K split of D / ks columns: the workgroup's W rows of each K chunk are
+// loaded once (row-contiguous 16-byte loads), split, and staged in LDS as
+// three bf16 planes (double-buffered, one barrier per chunk), so the split
+// work and the W traffic per workgroup shrink with ks.  With ks splits the
+// partial logits go to a workspace and the routing launch adds them in split
+// order; without a workspace (ks = 1) the workgroup routes its own tokens.
+// fp32 x: SIMT FMA tiles.
 //
 // Routing.  One wave per token, one lane per expert (E <= 64; E <= 256 with
 // several experts per lane): sigmoid in double rounded once, + bias, then k
-// rounds of a wave-wide arg-max ordered by (value desc, expert id asc).
+// rounds of a wave-wide arg-max ordered by (value desc, expert id asc).  The
+// routing launch of the MFMA gate takes rank blocks of 64 tokens and also
+// ranks their slots for the permute (rank.h).
 #include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <vector>
 
+#include "rank.h"
 #include "route.h"
 
 namespace dsmoe {
@@ -25,168 +36,329 @@ typedef float g_f32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned int g_u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int GATE_THREADS = 256;
-// MFMA gate: 4 waves when one 32-expert tile covers E, else 8 (the second four
-// take the odd expert tiles of the same K quarters)
-constexpr int gm_waves(int nt) { return nt >= 2 ? 8 : 4; }
 constexpr int GATE_KC = 32;        // SIMT: K chunk staged through LDS
-constexpr int GM_TOK = 32;         // MFMA: tokens per block
+constexpr int GP_TOK = 128;        // MFMA: tokens per workgroup
+constexpr int GP_THREADS = 512;    // MFMA: 8 waves = 4 token groups x 2 expert halves
 
-// ------------------------------------------------------------------ MFMA logits (bf16 x)
-// Splits 8 consecutive fp32 weights into three bf16x8 vectors whose sum is exact.
-__device__ __forceinline__ void split3(const g_f32x4_t& a, const g_f32x4_t& b, g_bf16x8_t& hi, g_bf16x8_t& mid,
-                                       g_bf16x8_t& lo) {
-  const float w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-  unsigned short h[8], m[8], l[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const uint32_t wb = __float_as_uint(w[i]);
-    const float fh = __uint_as_float(wb & 0xffff0000u);
-    const float r1 = w[i] - fh;                       // exact
-    const uint32_t rb = __float_as_uint(r1);
-    const float fm = __uint_as_float(rb & 0xffff0000u);
-    const float r2 = r1 - fm;                         // exact, <= 8 significant bits
-    h[i] = (unsigned short)(wb >> 16);
-    m[i] = (unsigned short)(rb >> 16);
-    l[i] = (unsigned short)(__float_as_uint(r2) >> 16);
-  }
-  __builtin_memcpy(&hi, h, 16);
-  __builtin_memcpy(&mid, m, 16);
-  __builtin_memcpy(&lo, l, 16);
+// MFMA gate tiling.  A workgroup takes GP_TOK tokens (wave w: token group
+// w & 3 of 32, expert tiles (w >> 2) + 2i of 32) over its K split, in
+// super-chunks of SC columns.  The super-chunk's W rows (all experts) are
+// loaded by every thread (row-contiguous 16-byte loads), split, and staged as
+// three bf16 planes in LDS (at most 96 KB); its x rows are loaded the same way
+// (each wave instruction reads 1 KB of whole rows) and staged as a fourth
+// plane of GP_TOK rows.  Each wave then runs all its MFMAs of the super-chunk
+// from LDS without another barrier, while the loads of the next super-chunk
+// are in flight in registers.
+// The widest super-chunk of NT expert tiles (planes of at most 96 KB).
+constexpr int gp_sc_max(int nt) { return nt <= 2 ? 256 : nt <= 4 ? 128 : 64; }
+
+template <int NT, int SC_ = gp_sc_max(NT)>
+struct GPCfg {
+  static constexpr int EP = NT * 32;                          // experts padded to whole 32-row tiles
+  static constexpr int SC = SC_;                              // super-chunk K
+  static constexpr int ROWB = SC * 2;                         // bytes of one plane row (bf16)
+  static constexpr int SWZ = (ROWB / 16 >= 16 ? 16 : ROWB / 16) - 1;  // 16-byte unit swizzle mask
+  static constexpr int PLANE = EP * ROWB;
+  static constexpr int F4R = SC / 4;                          // float4 loads per W row and super-chunk
+  static constexpr int NLD = EP * F4R / GP_THREADS;           // float4 loads per thread and super-chunk
+  static constexpr int STEPS = SC / 16;                       // MFMA K steps per super-chunk
+  static constexpr int NTW = (NT + 1) / 2;                    // expert tiles per wave (at most)
+  static constexpr int XUR = SC / 8;                          // 16-byte units of one x row
+  static constexpr int NXL = GP_TOK * XUR / GP_THREADS;       // x loads per thread and super-chunk
+  static constexpr int XPLANE = 3 * PLANE;                    // LDS offset of the x plane (GP_TOK rows)
+  static constexpr int LDS = XPLANE + GP_TOK * ROWB;
+};
+
+template <int NT, int SC>
+constexpr size_t gp_lds(bool route) {
+  return route && (size_t)4 * (GP_TOK * (NT * 32 + 1) + 2 * NT * 32) > (size_t)GPCfg<NT, SC>::LDS
+             ? (size_t)4 * (GP_TOK * (NT * 32 + 1) + 2 * NT * 32)
+             : (size_t)GPCfg<NT, SC>::LDS;
 }
 
+// Splits 4 fp32 weights into three bf16x4 words (hi, mid, lo) whose sum is
+// exact: hi = w truncated to bf16, r1 = w - hi (exact, <= 16 significant
+// bits), mid = r1 truncated, lo = r1 - mid (exact, <= 8 significant bits).
+__device__ __forceinline__ void split3x4(const g_f32x4_t& w, uint2& hi, uint2& mid, uint2& lo) {
+  uint32_t h[4], m[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t wb = __float_as_uint(w[i]);
+    const float r1 = w[i] - __uint_as_float(wb & 0xffff0000u);
+    const uint32_t rb = __float_as_uint(r1);
+    const float r2 = r1 - __uint_as_float(rb & 0xffff0000u);
+    h[i] = wb;
+    m[i] = rb;
+    l[i] = __float_as_uint(r2);
+  }
+  hi = make_uint2((h[0] >> 16) | (h[1] & 0xffff0000u), (h[2] >> 16) | (h[3] & 0xffff0000u));
+  mid = make_uint2((m[0] >> 16) | (m[1] & 0xffff0000u), (m[2] >> 16) | (m[3] & 0xffff0000u));
+  lo = make_uint2((l[0] >> 16) | (l[1] & 0xffff0000u), (l[2] >> 16) | (l[3] & 0xffff0000u));
+}
 
-// LDS: part[4][GM_TOK][EP+1] fp32 partial logits (reused for the reduced
-// logits), bias[E], hist[E], routing scratch.
-template <int NT>
-__global__ __launch_bounds__(gm_waves(NT) * 64) void gate_mfma_kernel(const bf16_t* __restrict__ x,
-                                                                 const float* __restrict__ gw,
-                                                                 const float* __restrict__ bias, int T, int D, int E,
-                                                                 int k, float route_scale, GateOut out,
-                                                                 float* __restrict__ part_out, int ks,
-                                                                 const PtrChunk tables, const void** tab_dst) {
-  constexpr int EP = NT * 32;
-  constexpr int LDP = EP + 1;
-  extern __shared__ float gsm[];
-  float* part = gsm;                                   // [4][GM_TOK][LDP]
-  float* bias_s = part + 4 * GM_TOK * LDP;
-  int* hist = reinterpret_cast<int*>(bias_s + E);
-  constexpr int NWV = gm_waves(NT);
-  constexpr int NTH = NWV * 64;
-  // wave w: K quarter w & 3; expert tiles ni = w >> 2, w >> 2 + NWV / 4, ...
-  constexpr int TSTEP = NWV / 4;
-  constexpr int NTW = (NT + TSTEP - 1) / TSTEP;       // expert tiles per wave (upper bound)
+// LDS plane layout: row e of a plane holds the super-chunk's SC bf16 of
+// expert e; its 16-byte unit u sits at unit u ^ (e & SWZ).
+template <class C>
+__device__ __forceinline__ int gp_unit_off(int row, int unit) {
+  return row * C::ROWB + ((unit ^ (row & C::SWZ)) << 4);
+}
+
+// ROUTE = false: partial logits of split blockIdx.x % ks for token tile
+// blockIdx.x / ks go to part[(split * T + t) * E + e].  ROUTE = true (ks = 1):
+// the workgroup routes its tokens (logits in LDS).
+template <int NT, int SC, bool ROUTE>
+__global__ __launch_bounds__(GP_THREADS) void gate_mfma_kernel(const bf16_t* __restrict__ x,
+                                                               const float* __restrict__ gw,
+                                                               const float* __restrict__ bias, int T, int D, int E,
+                                                               int k, float route_scale, GateOut out,
+                                                               float* __restrict__ part, int ks, const PtrChunk tables,
+                                                               const void** tab_dst) {
+  using C = GPCfg<NT, SC>;
+  extern __shared__ __attribute__((aligned(16))) char gsm[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int quarter = wave & 3, tfirst = wave >> 2;
   if (blockIdx.x == 0)
-    for (int i = threadIdx.x; i < tables.n; i += blockDim.x) tab_dst[tables.off + i] = tables.p[i];
-  // K split (part_out != nullptr): block b takes token tile b / ks and the
-  // K range of split b % ks, and writes partial logits instead of routing.
-  const int split = part_out ? (int)(blockIdx.x % ks) : 0;
-  const int t0 = (part_out ? (int)(blockIdx.x / ks) : (int)blockIdx.x) * GM_TOK;
-  for (int e = tid; e < E; e += NTH) {
-    bias_s[e] = bias[e];
-    hist[e] = 0;
-  }
-  const int dk = part_out ? D / ks : D;
-  const int kq = dk / 4;
-  const int kbeg = split * dk + quarter * kq;
+    for (int i = tid; i < tables.n; i += blockDim.x) tab_dst[tables.off + i] = tables.p[i];
+  const int split = (int)(blockIdx.x % ks);
+  const int t0 = (int)(blockIdx.x / ks) * GP_TOK;
+  const int dk = D / ks;
+  const int kbeg = split * dk;
+  const int nsc = dk / C::SC;
+  // W staging: load i of this thread reads float4 c4 of row r0 + i * (GP_THREADS / F4R)
+  constexpr int RSTEP = GP_THREADS / C::F4R;
+  const int c4 = tid % C::F4R, r0 = tid / C::F4R;
+  const float* wsrc = gw + (int64_t)kbeg + c4 * 4;
+  // x staging: load q of this thread reads unit xu of token row xr0 + q * (GP_THREADS / XUR)
+  constexpr int XRSTEP = GP_THREADS / C::XUR;
+  const int xu = tid % C::XUR, xr0 = tid / C::XUR;
+  const bf16_t* xsrc = x + (int64_t)kbeg + xu * 8;
+  const int tg = wave & 3, eh = wave >> 2;
+  const int ntw = (NT - eh + 1) / 2;                  // this wave's expert tiles: eh, eh + 2, ...
+  const bool wave_live = t0 + tg * 32 < T && ntw > 0;
   const int m = lane & 31;
-  const int row = min(t0 + m, T - 1);
-  const bf16_t* xr = x + (int64_t)row * D + (lane >> 5) * 8;
-  const float* wr[NTW];
+  g_f32x4_t wr[C::NLD];
+  g_u32x4_t xv[C::NXL];
+  g_f32x16_t acc[C::NTW];
 #pragma unroll
-  for (int i = 0; i < NTW; ++i) {
-    const int ni = min(tfirst + i * TSTEP, NT - 1);
-    wr[i] = gw + (int64_t)min(ni * 32 + m, E - 1) * D + (lane >> 5) * 8;
-  }
-  const int ntw = min(NTW, (NT - tfirst + TSTEP - 1) / TSTEP);   // this wave's tiles
-
-  g_f32x16_t acc[NTW];
-#pragma unroll
-  for (int i = 0; i < NTW; ++i)
+  for (int i = 0; i < C::NTW; ++i)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
 
-  // K loop in chunks of PF steps of 16, double-buffered: the loads of chunk
-  // c + 1 are issued before the MFMAs of chunk c, so the global round trips
-  // overlap the split and MFMA work (the loop is latency-bound otherwise:
-  // every block streams all of W_gate).
-  constexpr int PF = (NTW <= 2) ? 4 : 2;
-  const int kend = kbeg + kq;
-  g_bf16x8_t a[2][PF];
-  g_f32x4_t w0[2][PF][NTW], w1[2][PF][NTW];
-  auto load = [&](int buf, int k0) {
+  auto xload = [&](int sc) {
 #pragma unroll
-    for (int p = 0; p < PF; ++p) {
-      const int kk = min(k0 + 16 * p, kend - 16);
-      a[buf][p] = *reinterpret_cast<const g_bf16x8_t*>(xr + kk);
+    for (int q = 0; q < C::NXL; ++q)
+      xv[q] = *reinterpret_cast<const g_u32x4_t*>(xsrc + (int64_t)min(t0 + xr0 + q * XRSTEP, T - 1) * D + sc * C::SC);
+  };
+  auto xstage = [&]() {
 #pragma unroll
-      for (int ni = 0; ni < NTW; ++ni) {
-        w0[buf][p][ni] = *reinterpret_cast<const g_f32x4_t*>(wr[ni] + kk);
-        w1[buf][p][ni] = *reinterpret_cast<const g_f32x4_t*>(wr[ni] + kk + 4);
+    for (int q = 0; q < C::NXL; ++q)
+      *reinterpret_cast<g_u32x4_t*>(gsm + C::XPLANE + gp_unit_off<C>(xr0 + q * XRSTEP, xu)) = xv[q];
+  };
+  auto wload = [&](int sc) {
+#pragma unroll
+    for (int i = 0; i < C::NLD; ++i)
+      wr[i] = *reinterpret_cast<const g_f32x4_t*>(wsrc + (int64_t)min(r0 + i * RSTEP, E - 1) * D + sc * C::SC);
+  };
+  auto wstage = [&]() {
+#pragma unroll
+    for (int i = 0; i < C::NLD; ++i) {
+      uint2 hi, mid, lo;
+      split3x4(wr[i], hi, mid, lo);
+      const int o = gp_unit_off<C>(r0 + i * RSTEP, c4 >> 1) + ((c4 & 1) << 3);
+      *reinterpret_cast<uint2*>(gsm + o) = hi;
+      *reinterpret_cast<uint2*>(gsm + C::PLANE + o) = mid;
+      *reinterpret_cast<uint2*>(gsm + 2 * C::PLANE + o) = lo;
+    }
+  };
+  // x fragment: token row tg * 32 + (lane & 31), 8 bf16 at K offset (lane >> 5) * 8 + 16 s
+  auto compute = [&]() {
+    if (!wave_live) return;
+#pragma unroll
+    for (int s = 0; s < C::STEPS; ++s) {
+      const g_bf16x8_t xa =
+          *reinterpret_cast<const g_bf16x8_t*>(gsm + C::XPLANE + gp_unit_off<C>(tg * 32 + m, 2 * s + (lane >> 5)));
+#pragma unroll
+      for (int i = 0; i < C::NTW; ++i) {
+        if (i < ntw) {
+          const int o = gp_unit_off<C>((eh + 2 * i) * 32 + m, 2 * s + (lane >> 5));
+          const g_bf16x8_t bhi = *reinterpret_cast<const g_bf16x8_t*>(gsm + o);
+          const g_bf16x8_t bmid = *reinterpret_cast<const g_bf16x8_t*>(gsm + C::PLANE + o);
+          const g_bf16x8_t blo = *reinterpret_cast<const g_bf16x8_t*>(gsm + 2 * C::PLANE + o);
+          acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(blo, xa, acc[i], 0, 0, 0);
+          acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bmid, xa, acc[i], 0, 0, 0);
+          acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bhi, xa, acc[i], 0, 0, 0);
+        }
       }
     }
   };
-  auto compute = [&](int buf, int k0) {
+
+  // super-chunk sc: stage its W planes and x rows, barrier, issue the loads
+  // of sc + 1 into registers, run the MFMAs, barrier (the planes are
+  // rewritten next)
+  xload(0);
+  wload(0);
+  for (int sc = 0; sc < nsc; ++sc) {
+    wstage();
+    xstage();
+    __syncthreads();
+    if (sc + 1 < nsc) {
+      wload(sc + 1);
+      xload(sc + 1);
+    }
+    compute();
+    __syncthreads();
+  }
+  // lane holds token m of its group, experts ni*32 + 8*(r/4) + 4*(lane/32) + r%4
+  const int t = t0 + tg * 32 + m;
+  if constexpr (!ROUTE) {
+    if (t < T && wave_live) {
+      float* pr = part + ((int64_t)split * T + t) * E;
 #pragma unroll
-    for (int p = 0; p < PF; ++p) {
-      if (k0 + 16 * p >= kend) break;
+      for (int i = 0; i < C::NTW; ++i) {
+        if (i >= ntw) break;
+        const int ni = eh + 2 * i;
 #pragma unroll
-      for (int ni = 0; ni < NTW; ++ni) {
-        if (ni >= ntw) break;
-        g_bf16x8_t hi, mid, lo;
-        split3(w0[buf][p][ni], w1[buf][p][ni], hi, mid, lo);
-        acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lo, a[buf][p], acc[ni], 0, 0, 0);
-        acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mid, a[buf][p], acc[ni], 0, 0, 0);
-        acc[ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(hi, a[buf][p], acc[ni], 0, 0, 0);
+        for (int g = 0; g < 4; ++g) {
+          const int e = ni * 32 + 8 * g + 4 * (lane >> 5);
+          if ((E & 3) == 0) {
+            if (e < E)
+              *reinterpret_cast<g_f32x4_t*>(pr + e) =
+                  g_f32x4_t{acc[i][4 * g], acc[i][4 * g + 1], acc[i][4 * g + 2], acc[i][4 * g + 3]};
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              if (e + q < E) pr[e + q] = acc[i][4 * g + q];
+          }
+        }
       }
     }
-  };
-  constexpr int CH = 16 * PF;
-  load(0, kbeg);
-  for (int k0 = kbeg; k0 < kend; k0 += 2 * CH) {
-    if (k0 + CH < kend) load(1, k0 + CH);
-    compute(0, k0);
-    if (k0 + CH >= kend) break;
-    if (k0 + 2 * CH < kend) load(0, k0 + 2 * CH);
-    compute(1, k0 + CH);
-  }
-  // lane holds token m, experts ni*32 + 8*(r/4) + 4*(lane/32) + r%4
-  float* pw = part + quarter * GM_TOK * LDP + m * LDP;
-#pragma unroll
-  for (int i = 0; i < NTW; ++i) {
-    if (i >= ntw) break;
-    const int ni = tfirst + i * TSTEP;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) pw[ni * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)] = acc[i][r];
-  }
-  __syncthreads();
-  const int ntok = min(GM_TOK, T - t0);
-  for (int i = tid; i < GM_TOK * E; i += NTH) {
-    const int t = i / E, e = i - t * E;
-    const int o = t * LDP + e;
-    const float v = ((part[o] + part[GM_TOK * LDP + o]) + part[2 * GM_TOK * LDP + o]) + part[3 * GM_TOK * LDP + o];
-    part[o] = v;
-    if (part_out) {
-      if (t < ntok) part_out[((int64_t)split * T + t0 + t) * E + e] = v;
-    } else if (out.logits && t < ntok) {
-      out.logits[(int64_t)(t0 + t) * E + e] = v;
+  } else {
+    // the W planes are dead (the loop ended on a barrier): logits in LDS
+    constexpr int LDP = C::EP + 1;
+    float* lg = reinterpret_cast<float*>(gsm);     // [GP_TOK][LDP]
+    float* bias_s = lg + GP_TOK * LDP;
+    int* hist = reinterpret_cast<int*>(bias_s + C::EP);
+    for (int e = tid; e < E; e += blockDim.x) {
+      bias_s[e] = bias[e];
+      hist[e] = 0;
     }
+    if (wave_live) {
+      float* pw = lg + (tg * 32 + m) * LDP;
+#pragma unroll
+      for (int i = 0; i < C::NTW; ++i) {
+        if (i >= ntw) break;
+        const int ni = eh + 2 * i;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) pw[ni * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)] = acc[i][r];
+      }
+    }
+    __syncthreads();
+    const int ntok = min(GP_TOK, T - t0);
+    if (out.logits)
+      for (int i = tid; i < ntok * E; i += blockDim.x) {
+        const int tt = i / E, e = i - tt * E;
+        out.logits[(int64_t)(t0 + tt) * E + e] = lg[tt * LDP + e];
+      }
+    route_tokens(lg, LDP, ntok, t0, bias_s, E, k, route_scale, DSMOE_BF16, out, out.counts ? hist : nullptr);
+    __syncthreads();
+    flush_hist(hist, E, out.counts);
   }
-  if (part_out) return;
-  __syncthreads();
-  route_tokens(part, LDP, ntok, t0, bias_s, E, k, route_scale, DSMOE_BF16, out, out.counts ? hist : nullptr);
-  __syncthreads();
-  flush_hist(hist, E, out.counts);
 }
 
-// ------------------------------------------------------------------ SIMT logits (fp32 x) / given logits
+// Routing launch: logits = the ks partial logits added in split order (ks = 1:
+// given logits), one workgroup of RR_WAVES waves per rank block of
+// RANK_TOKENS tokens (four tokens per wave).  With po.offsets set it also
+// ranks the block's slots (rank.h), and a call of one rank block finishes its
+// permute here.
+// LDS (4-byte words): lg[64][E + 1] | bias[E] | hist[E] | sel[64 k] | rank[64 k] | off[E + 1] | til[E + 1]
+constexpr int RR_WAVES = RANK_TOKENS / 4;
+
+template <int KB>
+__global__ __launch_bounds__(RR_WAVES * 64) void route_rank_kernel(const float* __restrict__ part, int ks,
+                                                                  const float* __restrict__ bias, int T, int E, int k,
+                                                                  float route_scale, int xdtype, GateOut out,
+                                                                  PermuteOut po, int nb) {
+  extern __shared__ __attribute__((aligned(16))) float rsm[];
+  const int ldl = E + 1;
+  float* lg = rsm;
+  float* bias_s = lg + RANK_TOKENS * ldl;
+  int32_t* hist = reinterpret_cast<int32_t*>(bias_s + E);
+  int32_t* sel = hist + E;
+  int32_t* rank_lds = sel + RANK_TOKENS * k;
+  int32_t* off = rank_lds + RANK_TOKENS * k;
+  int32_t* til = off + E + 1;
+  const int tid = threadIdx.x;
+  const int b = blockIdx.x;
+  const int t0 = b * RANK_TOKENS;
+  const int ntok = max(0, min(RANK_TOKENS, T - t0));
+  const bool rank = po.offsets != nullptr;
+  for (int e = tid; e < E; e += blockDim.x) {
+    bias_s[e] = bias[e];
+    hist[e] = 0;
+  }
+  for (int i = tid; i < RANK_TOKENS * k; i += blockDim.x) sel[i] = -1;
+  const int64_t split_stride = (int64_t)T * E;
+  // each thread's loads of every split are issued before the adds (one
+  // memory latency), then added in split order
+  const bool lvec = (reinterpret_cast<uintptr_t>(out.logits) & 15) == 0;
+  if ((E & 3) == 0) {
+    const int E4 = E >> 2;
+    for (int i = tid; i < ntok * E4; i += blockDim.x) {
+      const int tt = i / E4, e = (i - tt * E4) * 4;
+      const float* p = part + (int64_t)(t0 + tt) * E + e;
+      g_f32x4_t pv[GATE_KS_MAX];
+#pragma unroll
+      for (int sp = 0; sp < GATE_KS_MAX; ++sp)
+        if (sp < ks) pv[sp] = *reinterpret_cast<const g_f32x4_t*>(p + sp * split_stride);
+      g_f32x4_t v = pv[0];
+#pragma unroll
+      for (int sp = 1; sp < GATE_KS_MAX; ++sp)
+        if (sp < ks) v += pv[sp];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) lg[tt * ldl + e + q] = v[q];
+      if (out.logits) {
+        float* lo = out.logits + (int64_t)(t0 + tt) * E + e;
+        if (lvec)
+          *reinterpret_cast<g_f32x4_t*>(lo) = v;
+        else
+#pragma unroll
+          for (int q = 0; q < 4; ++q) lo[q] = v[q];
+      }
+    }
+  } else {
+    for (int i = tid; i < ntok * E; i += blockDim.x) {
+      const int tt = i / E, e = i - tt * E;
+      const float* p = part + (int64_t)(t0 + tt) * E + e;
+      float pv[GATE_KS_MAX];
+#pragma unroll
+      for (int sp = 0; sp < GATE_KS_MAX; ++sp)
+        if (sp < ks) pv[sp] = p[sp * split_stride];
+      float v = pv[0];
+#pragma unroll
+      for (int sp = 1; sp < GATE_KS_MAX; ++sp)
+        if (sp < ks) v += pv[sp];
+      lg[tt * ldl + e] = v;
+      if (out.logits) out.logits[(int64_t)(t0 + tt) * E + e] = v;
+    }
+  }
+  __syncthreads();
+  route_tokens(lg, ldl, ntok, t0, bias_s, E, k, route_scale, xdtype, out, (!rank && out.counts) ? hist : nullptr,
+               rank ? sel : nullptr);
+  __syncthreads();
+  if (!rank) {
+    flush_hist(hist, E, out.counts);
+    return;
+  }
+  const bool single = nb <= 1;
+  rank_block<KB>(sel, ntok, k, E, b, po, hist, single ? rank_lds : nullptr);
+  if (single) finish_single_block(sel, rank_lds, ntok, k, E, po, hist, off, til);
+}
+
+// ------------------------------------------------------------------ SIMT logits (fp32 x, or D % 64 != 0)
 // LDS layout (floats): xs[KC][TB+4] | ws[KC][EC+4] | lg[TB][E+1] | bias[E] | hist[E] (int) | routing scratch
-template <typename XT, int EC, bool FROM_LOGITS>
-__global__ __launch_bounds__(GATE_THREADS) void gate_kernel(const XT* __restrict__ x, const float* __restrict__ logits_in,
-                                                            const float* __restrict__ gw, const float* __restrict__ bias,
-                                                            int T, int D, int E, int k, float route_scale, int xdtype,
-                                                            GateOut out) {
+template <typename XT, int EC>
+__global__ __launch_bounds__(GATE_THREADS) void gate_kernel(const XT* __restrict__ x, const float* __restrict__ gw,
+                                                            const float* __restrict__ bias, int T, int D, int E, int k,
+                                                            float route_scale, int xdtype, GateOut out) {
   constexpr int TX = EC / 4;                   // threads along experts
   constexpr int TB = (GATE_THREADS / TX) * 4;  // tokens per block
   extern __shared__ float smem[];
@@ -203,54 +375,46 @@ __global__ __launch_bounds__(GATE_THREADS) void gate_kernel(const XT* __restrict
     bias_s[e] = bias[e];
     hist[e] = 0;
   }
-
-  if constexpr (FROM_LOGITS) {
-    for (int i = tid; i < TB * E; i += GATE_THREADS) {
-      int t = i / E, e = i - t * E;
-      lg[t * ldl + e] = (t0 + t < T) ? logits_in[(int64_t)(t0 + t) * E + e] : 0.0f;
-    }
-  } else {
-    const int tx = tid % TX, ty = tid / TX;
-    for (int e0 = 0; e0 < E; e0 += EC) {
-      float acc[4][4] = {};
-      for (int kc = 0; kc < D; kc += GATE_KC) {
-        for (int i = tid; i < TB * GATE_KC; i += GATE_THREADS) {
-          int t = i / GATE_KC, kk = i - t * GATE_KC;
-          float v = 0.0f;
-          if (t0 + t < T && kc + kk < D) v = to_f<XT>(x[(int64_t)(t0 + t) * D + kc + kk]);
-          xs[kk * (TB + 4) + t] = v;
-        }
-        for (int i = tid; i < EC * GATE_KC; i += GATE_THREADS) {
-          int e = i / GATE_KC, kk = i - e * GATE_KC;
-          float v = 0.0f;
-          if (e0 + e < E && kc + kk < D) v = gw[(int64_t)(e0 + e) * D + kc + kk];
-          ws[kk * (EC + 4) + e] = v;
-        }
-        __syncthreads();
-#pragma unroll 8
-        for (int kk = 0; kk < GATE_KC; ++kk) {
-          float4 a = *reinterpret_cast<const float4*>(&xs[kk * (TB + 4) + ty * 4]);
-          float4 b = *reinterpret_cast<const float4*>(&ws[kk * (EC + 4) + tx * 4]);
-          float av[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], bw[j], acc[i][j]);
-        }
-        __syncthreads();
+  const int tx = tid % TX, ty = tid / TX;
+  for (int e0 = 0; e0 < E; e0 += EC) {
+    float acc[4][4] = {};
+    for (int kc = 0; kc < D; kc += GATE_KC) {
+      for (int i = tid; i < TB * GATE_KC; i += GATE_THREADS) {
+        int t = i / GATE_KC, kk = i - t * GATE_KC;
+        float v = 0.0f;
+        if (t0 + t < T && kc + kk < D) v = to_f<XT>(x[(int64_t)(t0 + t) * D + kc + kk]);
+        xs[kk * (TB + 4) + t] = v;
       }
+      for (int i = tid; i < EC * GATE_KC; i += GATE_THREADS) {
+        int e = i / GATE_KC, kk = i - e * GATE_KC;
+        float v = 0.0f;
+        if (e0 + e < E && kc + kk < D) v = gw[(int64_t)(e0 + e) * D + kc + kk];
+        ws[kk * (EC + 4) + e] = v;
+      }
+      __syncthreads();
+#pragma unroll 8
+      for (int kk = 0; kk < GATE_KC; ++kk) {
+        float4 a = *reinterpret_cast<const float4*>(&xs[kk * (TB + 4) + ty * 4]);
+        float4 b = *reinterpret_cast<const float4*>(&ws[kk * (EC + 4) + tx * 4]);
+        float av[4] = {a.x, a.y, a.z, a.w}, bw[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          int e = e0 + tx * 4 + j;
-          if (e < E) lg[(ty * 4 + i) * ldl + e] = acc[i][j];
-        }
+          for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], bw[j], acc[i][j]);
+      }
+      __syncthreads();
     }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        int e = e0 + tx * 4 + j;
+        if (e < E) lg[(ty * 4 + i) * ldl + e] = acc[i][j];
+      }
   }
   __syncthreads();
   const int ntok = min(TB, T - t0);
-  if (!FROM_LOGITS && out.logits) {
+  if (out.logits) {
     for (int i = tid; i < ntok * E; i += GATE_THREADS) {
       int t = i / E, e = i - t * E;
       out.logits[(int64_t)(t0 + t) * E + e] = lg[t * ldl + e];
@@ -266,100 +430,104 @@ __global__ void fill_i32_kernel(int32_t* p, int n, int32_t v) {
   if (i < n) p[i] = v;
 }
 
-// Routing after a K-split gate: logits = sum of the ks partial logits in
-// split order (0, 1, ...), optionally written out, then route_tokens.
-constexpr int RP_TOK = 1;        // tokens per block (one wave): small calls, spread over the CUs
-__global__ __launch_bounds__(64) void route_partials_kernel(const float* __restrict__ part, int ks,
-                                                             const float* __restrict__ bias, int T, int E, int k,
-                                                             float route_scale, int xdtype, GateOut out) {
-  extern __shared__ float rsm[];
-  const int ldl = E + 1;
-  float* lg = rsm;                               // [RP_TOK][E + 1]
-  float* bias_s = lg + RP_TOK * ldl;             // [E]
-  int* hist = reinterpret_cast<int*>(bias_s + E);
-  const int tid = threadIdx.x;
-  const int t0 = blockIdx.x * RP_TOK;
-  const int ntok = min(RP_TOK, T - t0);
-  for (int e = tid; e < E; e += blockDim.x) {
-    bias_s[e] = bias[e];
-    hist[e] = 0;
-  }
-  for (int i = tid; i < ntok * E; i += blockDim.x) {
-    const int t = i / E, e = i - t * E;
-    const float* p = part + (int64_t)(t0 + t) * E + e;
-    // every split's load is issued before the adds (one memory latency)
-    float pv[GATE_KS_MAX];
-#pragma unroll
-    for (int sp = 0; sp < GATE_KS_MAX; ++sp) pv[sp] = sp < ks ? p[(int64_t)sp * T * E] : 0.0f;
-    float v = pv[0];
-#pragma unroll
-    for (int sp = 1; sp < GATE_KS_MAX; ++sp)
-      if (sp < ks) v += pv[sp];
-    lg[t * ldl + e] = v;
-    if (out.logits) out.logits[(int64_t)(t0 + t) * E + e] = v;
-  }
-  __syncthreads();
-  route_tokens<1, 1>(lg, ldl, ntok, t0, bias_s, E, k, route_scale, xdtype, out, out.counts ? hist : nullptr);
-  __syncthreads();
-  flush_hist(hist, E, out.counts);
-}
-
+// Raises a kernel's dynamic LDS limit to the CU's 160 KB, once per kernel and
+// process (the call costs far more than a launch).
 static int set_lds(const void* kern, size_t lds) {
-  if (lds > 64 * 1024 &&
-      hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+  constexpr size_t kMax = 160 * 1024;
+  if (lds <= 64 * 1024) return DSMOE_OK;
+  if (lds > kMax) return fail(DSMOE_ERR_UNSUPPORTED, "gate: LDS need exceeds 160 KB");
+  static std::mutex mu;
+  static std::vector<const void*> raised;
+  std::lock_guard<std::mutex> lock(mu);
+  for (const void* p : raised)
+    if (p == kern) return DSMOE_OK;
+  if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMax) != hipSuccess)
     return fail(DSMOE_ERR_HIP, "gate: cannot raise LDS limit");
+  raised.push_back(kern);
   return DSMOE_OK;
 }
 
-template <typename XT, int EC, bool FROM_LOGITS>
-static int launch_gate_t(const void* x, const float* logits_in, const float* gw, const float* bias, const dsmoe_dims& d,
-                         const GateOut& out, hipStream_t st) {
+template <typename XT, int EC>
+static int launch_gate_t(const void* x, const float* gw, const float* bias, const dsmoe_dims& d, const GateOut& out,
+                         hipStream_t st) {
   constexpr int TX = EC / 4;
   constexpr int TB = (GATE_THREADS / TX) * 4;
   const size_t lds = sizeof(float) * (GATE_KC * (TB + 4) + GATE_KC * (EC + 4) + TB * (d.E + 1) + d.E) +
                      sizeof(int) * d.E + 16;
-  auto kern = gate_kernel<XT, EC, FROM_LOGITS>;
+  auto kern = gate_kernel<XT, EC>;
   int rc = set_lds((const void*)kern, lds);
   if (rc) return rc;
   int blocks = (int)cdiv(d.T, TB);
-  hipLaunchKernelGGL(kern, dim3(blocks), dim3(GATE_THREADS), lds, st, static_cast<const XT*>(x), logits_in, gw, bias,
-                     d.T, d.D, d.E, d.k, d.route_scale, d.dtype, out);
+  hipLaunchKernelGGL(kern, dim3(blocks), dim3(GATE_THREADS), lds, st, static_cast<const XT*>(x), gw, bias, d.T, d.D,
+                     d.E, d.k, d.route_scale, d.dtype, out);
   return check_launch("gate");
 }
 
-template <int NT>
+// The routing launch over ks partial (or given, ks = 1) logits.
+static int launch_route(const float* part, int ks, const float* bias, const dsmoe_dims& d, const GateOut& out,
+                        const PermuteOut* po, bool* ranked, hipStream_t st) {
+  PermuteOut none;
+  std::memset(static_cast<void*>(&none), 0, sizeof(none));
+  const int nb = (int)cdiv(d.T, RANK_TOKENS);
+  const size_t lds = sizeof(float) * (RANK_TOKENS * (d.E + 1) + 2 * d.E + 2 * RANK_TOKENS * d.k + 2 * (d.E + 1));
+  auto kern = d.k <= 8 ? route_rank_kernel<8> : route_rank_kernel<MAX_TOPK>;
+  int rc = set_lds((const void*)kern, lds);
+  if (rc) return rc;
+  hipLaunchKernelGGL(kern, dim3((unsigned)max(nb, 1)), dim3(RR_WAVES * 64), lds, st, part, ks, bias, d.T, d.E, d.k,
+                     d.route_scale, d.dtype, out, po ? *po : none, nb);
+  rc = check_launch("route");
+  if (!rc && po && ranked) *ranked = true;
+  return rc;
+}
+
+template <int NT, int SC>
 static int launch_gate_mfma(const void* x, const float* gw, const float* bias, const dsmoe_dims& d, const GateOut& out,
-                            float* part, int ks, hipStream_t st, const PtrChunk* tables, const void** tab_dst) {
+                            float* part, const PtrChunk* tables, const void** tab_dst, const PermuteOut* po,
+                            bool* ranked, hipStream_t st) {
   PtrChunk none;
   none.n = 0;
   none.off = 0;
-  const size_t lds = sizeof(float) * (4 * GM_TOK * (NT * 32 + 1) + d.E) + sizeof(int) * ((d.E + 3) & ~3);
-  auto kern = gate_mfma_kernel<NT>;
+  const bool route = part == nullptr;
+  const int ks = route ? 1 : gate_k_splits(d);
+  auto kern = route ? gate_mfma_kernel<NT, SC, true> : gate_mfma_kernel<NT, SC, false>;
+  const size_t lds = gp_lds<NT, SC>(route);
   int rc = set_lds((const void*)kern, lds);
   if (rc) return rc;
-  const int64_t blocks = cdiv(d.T, GM_TOK) * (part ? ks : 1);
-  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(gm_waves(NT) * 64), lds, st, static_cast<const bf16_t*>(x), gw,
-                     bias, d.T, d.D, d.E, d.k, d.route_scale, out, part, ks, tables ? *tables : none, tab_dst);
+  const int64_t blocks = cdiv(d.T, GP_TOK) * ks;
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(GP_THREADS), lds, st, static_cast<const bf16_t*>(x), gw, bias,
+                     d.T, d.D, d.E, d.k, d.route_scale, out, part, ks, tables ? *tables : none, tab_dst);
   rc = check_launch("gate_mfma");
-  if (rc || !part) return rc;
-  const size_t rlds = sizeof(float) * (RP_TOK * (d.E + 1) + d.E) + sizeof(int) * d.E;
-  hipLaunchKernelGGL(route_partials_kernel, dim3((unsigned)cdiv(d.T, RP_TOK)), dim3(64), rlds, st, part, ks, bias,
-                     d.T, d.E, d.k, d.route_scale, (int)DSMOE_BF16, out);
-  return check_launch("route_partials");
+  if (rc || route) return rc;
+  return launch_route(part, ks, bias, d, out, po, ranked, st);
+}
+
+// Super-chunk of the MFMA gate: the widest one for the expert count when it
+// divides D, else 64 columns.
+template <int NT>
+static int launch_gate_mfma_nt(const void* x, const float* gw, const float* bias, const dsmoe_dims& d,
+                               const GateOut& out, float* part, const PtrChunk* tables, const void** tab_dst,
+                               const PermuteOut* po, bool* ranked, hipStream_t st) {
+  if (d.D % gp_sc_max(NT) == 0)
+    return launch_gate_mfma<NT, gp_sc_max(NT)>(x, gw, bias, d, out, part, tables, tab_dst, po, ranked, st);
+  return launch_gate_mfma<NT, 64>(x, gw, bias, d, out, part, tables, tab_dst, po, ranked, st);
+}
+
+static int gate_nt(int E) { return E <= 32 ? 1 : E <= 64 ? 2 : E <= 96 ? 3 : E <= 128 ? 4 : 8; }
+static int gate_sc(const dsmoe_dims& d) {
+  const int w = gp_sc_max(gate_nt(d.E));
+  return d.D % w == 0 ? w : 64;
 }
 
 int gate_k_splits(const dsmoe_dims& d) {
-  const int64_t tiles = cdiv(d.T, GM_TOK);
+  const int64_t tiles = cdiv(d.T, GP_TOK);
+  const int sc = gate_sc(d);
   int ks = 1;
-  while (ks < GATE_KS_MAX && tiles * ks * 2 <= 256) ks *= 2;   // fill the 256 CUs when there are few token tiles
-  while (ks > 1 && d.D % (64 * ks) != 0) ks >>= 1;
+  // about one workgroup per CU; a split keeps whole super-chunks
+  while (ks < GATE_KS_MAX && tiles * ks * 2 <= 256 && d.D % (sc * ks * 2) == 0) ks *= 2;
   return ks;
 }
 
-size_t gate_part_floats(const dsmoe_dims& d) {
-  const int ks = gate_k_splits(d);
-  return ks > 1 ? (size_t)ks * d.T * d.E : 0;
-}
+size_t gate_part_floats(const dsmoe_dims& d) { return (size_t)gate_k_splits(d) * d.T * d.E; }
 
 static bool gate_mfma_ok(const void* x, const float* gw, const dsmoe_dims& d) {
   return d.dtype == DSMOE_BF16 && d.D % 64 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
@@ -369,35 +537,33 @@ static bool gate_mfma_ok(const void* x, const float* gw, const dsmoe_dims& d) {
 bool gate_uses_mfma(const void* x, const float* gw, const dsmoe_dims& d) { return d.T > 0 && gate_mfma_ok(x, gw, d); }
 
 int launch_gate(const void* x, const float* logits_in, const float* gw, const float* bias, const dsmoe_dims& d,
-                const GateOut& out, hipStream_t st, float* part, const PtrChunk* tables, const void** tab_dst) {
+                const GateOut& out, hipStream_t st, float* part, const PtrChunk* tables, const void** tab_dst,
+                const PermuteOut* po, bool* ranked) {
+  if (ranked) *ranked = false;
   if (tables && (logits_in || !gate_uses_mfma(x, gw, d)))
     return fail(DSMOE_ERR_INVALID, "gate: a pointer table rides only with the MFMA gate");
   if (out.counts) {
     hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)cdiv(d.E, 256)), dim3(256), 0, st, out.counts, d.E, 0);
   }
   if (d.T == 0) return check_launch("gate(fill)");
-  if (logits_in) return launch_gate_t<float, 64, true>(nullptr, logits_in, gw, bias, d, out, st);
-  const bool mfma = gate_mfma_ok(x, gw, d);
-  if (mfma) {
-    const int nt = (int)cdiv(d.E, 32);
-    const int ks = part ? gate_k_splits(d) : 1;
-    float* pp = ks > 1 ? part : nullptr;
-    switch (nt) {
-      case 1: return launch_gate_mfma<1>(x, gw, bias, d, out, pp, ks, st, tables, tab_dst);
-      case 2: return launch_gate_mfma<2>(x, gw, bias, d, out, pp, ks, st, tables, tab_dst);
-      case 3: return launch_gate_mfma<3>(x, gw, bias, d, out, pp, ks, st, tables, tab_dst);
-      case 4: return launch_gate_mfma<4>(x, gw, bias, d, out, pp, ks, st, tables, tab_dst);
-      default: return launch_gate_mfma<8>(x, gw, bias, d, out, pp, ks, st, tables, tab_dst);
+  if (logits_in) return launch_route(logits_in, 1, bias, d, out, nullptr, nullptr, st);
+  if (gate_mfma_ok(x, gw, d)) {
+    switch (gate_nt(d.E)) {
+      case 1: return launch_gate_mfma_nt<1>(x, gw, bias, d, out, part, tables, tab_dst, po, ranked, st);
+      case 2: return launch_gate_mfma_nt<2>(x, gw, bias, d, out, part, tables, tab_dst, po, ranked, st);
+      case 3: return launch_gate_mfma_nt<3>(x, gw, bias, d, out, part, tables, tab_dst, po, ranked, st);
+      case 4: return launch_gate_mfma_nt<4>(x, gw, bias, d, out, part, tables, tab_dst, po, ranked, st);
+      default: return launch_gate_mfma_nt<8>(x, gw, bias, d, out, part, tables, tab_dst, po, ranked, st);
     }
   }
   if (d.dtype == DSMOE_BF16) {
-    if (d.E <= 16) return launch_gate_t<bf16_t, 16, false>(x, nullptr, gw, bias, d, out, st);
-    if (d.E <= 32) return launch_gate_t<bf16_t, 32, false>(x, nullptr, gw, bias, d, out, st);
-    return launch_gate_t<bf16_t, 64, false>(x, nullptr, gw, bias, d, out, st);
+    if (d.E <= 16) return launch_gate_t<bf16_t, 16>(x, gw, bias, d, out, st);
+    if (d.E <= 32) return launch_gate_t<bf16_t, 32>(x, gw, bias, d, out, st);
+    return launch_gate_t<bf16_t, 64>(x, gw, bias, d, out, st);
   }
-  if (d.E <= 16) return launch_gate_t<float, 16, false>(x, nullptr, gw, bias, d, out, st);
-  if (d.E <= 32) return launch_gate_t<float, 32, false>(x, nullptr, gw, bias, d, out, st);
-  return launch_gate_t<float, 64, false>(x, nullptr, gw, bias, d, out, st);
+  if (d.E <= 16) return launch_gate_t<float, 16>(x, gw, bias, d, out, st);
+  if (d.E <= 32) return launch_gate_t<float, 32>(x, gw, bias, d, out, st);
+  return launch_gate_t<float, 64>(x, gw, bias, d, out, st);
 }
 
 void launch_fill_i32(int32_t* p, int n, int32_t v, hipStream_t st) {

@@ -2,239 +2,98 @@
 // Restates models/moe.py:107-117 (argsort, bincount, offsets) and the row
 // gather flat[sorted_token_ids] of models/moe.py:127,150.
 //
-//   rank_kernel     one workgroup per 64 tokens (a rank block), its four waves
-//                   splitting the experts: for each expert a wave ballot gives
-//                   every slot its rank among the block's earlier tokens, and
-//                   the block histogram (no atomics, deterministic).
-//   scan_kernel     one block of 16 waves: per-expert exclusive scans over the
-//                   block histograms (wave prefix sums, 64 blocks at a time),
-//                   counts, offsets (E+1), and the M-tile schedule used by the
-//                   grouped GEMMs (tiles of bm rows inside each expert).
-//   scatter_kernel  pos = offsets[e] + blockbase[b][e] + rank; writes the
-//                   sorted order, its inverse and optional weight gather.
-//   permute_small_kernel  the three stages in one workgroup for calls of at
-//                   most PERMUTE_SMALL_T tokens (decode), one launch.
-//   gather_rows     x_sorted[p] = x[sorted_token[p]] with 16-byte accesses.
-#include "common.h"
+// Tokens are taken in rank blocks of RANK_TOKENS = 64 (one token per lane).
+//   rank         for each expert a wave ballot over the block's tokens gives
+//                every slot its rank among the block's earlier tokens routed
+//                to that expert, and the block's count (blockhist).  Done by
+//                rank_kernel here, or by the routing launch of the MFMA gate
+//                for the tokens it has just routed (rank.h).
+//   prefix_scatter_kernel  one workgroup per rank block (per run of rank
+//                blocks when there are more than 256): it sums blockhist over
+//                every block (expert totals, hence offsets) and over the
+//                blocks before its own (its base inside each expert), and
+//                places its slots at pos = offsets[e] + base[e] + rank.
+//                Workgroup 0 also writes counts, offsets and the M-tile
+//                schedule.  Each workgroup reads the whole histogram (nb x E
+//                ints, cache-resident) instead of waiting on a separate scan.
+//   A call of one rank block (T <= 64) is finished by its ranking workgroup:
+//   one launch.
+//   gather_rows  x_sorted[p] = x[sorted_token[p]] with 16-byte accesses.
+#include "rank.h"
 
 namespace dsmoe {
 
-constexpr int RANK_TOKENS = 64;  // one wave64 per block, one token per lane
-constexpr int MAX_K = 16;
-
-// Ranks of the slots of rank block b (one wave, lane = token) for experts
-// e0, e0 + estep, ...: for each expert a wave ballot gives every slot its rank
-// among the block's earlier tokens, and the block's count of that expert.
-template <int KB>  // bound on k (slots compared per expert)
-__device__ __forceinline__ void rank_experts(const int32_t* __restrict__ idx, int T, int k, int E, int b, int e0,
-                                             int estep, int32_t* __restrict__ blockhist,
-                                             int32_t* __restrict__ local_rank) {
-  const int lane = threadIdx.x & 63;
-  const int t = b * RANK_TOKENS + lane;
-  int ex[KB];
-#pragma unroll
-  for (int j = 0; j < KB; ++j) ex[j] = -1;
-  if (t < T)
-    for (int j = 0; j < k; ++j) ex[j] = idx[(int64_t)t * k + j];
-  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int e = e0; e < E; e += estep) {
-    int jsel = -1;
-#pragma unroll
-    for (int j = 0; j < KB; ++j)
-      if (ex[j] == e) jsel = j;
-    const uint64_t mask = __ballot(jsel >= 0);
-    if (jsel >= 0) local_rank[(int64_t)t * k + jsel] = __popcll(mask & below);
-    if (lane == 0) blockhist[(int64_t)b * E + e] = __popcll(mask);
-  }
-}
-
-// One rank block (64 tokens) per workgroup; its four waves split the experts.
+// One rank block per workgroup (4 waves), idx read into LDS; a call of one
+// rank block finishes its permute here.
+// LDS: sel[64 k] | rank[64 k] | hist[E] | off[E + 1] | til[E + 1]
 template <int KB>
-__global__ __launch_bounds__(256) void rank_kernel(const int32_t* __restrict__ idx, int T, int k, int E,
-                                                   int32_t* __restrict__ blockhist, int32_t* __restrict__ local_rank) {
-  rank_experts<KB>(idx, T, k, E, blockIdx.x, threadIdx.x >> 6, blockDim.x >> 6, blockhist, local_rank);
-}
-
-// Inclusive prefix sum over the 64 lanes of a wave (exact integer adds), on
-// DPP: row (16-lane) shifts by 1, 2, 4, 8 (lanes without a source add 0),
-// then the row broadcasts of lane 15 (into rows 1 and 3) and lane 31 (into
-// rows 2 and 3).
-__device__ __forceinline__ int32_t wave_incl_scan(int32_t x, int /*lane*/) {
-  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
-  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
-  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
-  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
-  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15
-  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31
-  return x;
-}
-
-// Lane 63's value in every lane.
-__device__ __forceinline__ int32_t wave_last(int32_t x) { return __builtin_amdgcn_readlane(x, 63); }
-
-// Scan over the block histograms by one workgroup.  LDS sh: cnt[E],
-// off[E+1], tiles[E+1].  Wave w scans experts w, w + nw, ...: lane b holds
-// block b's count of the expert, 64 blocks at a time, carried across chunks.
-// Wave 0 then scans counts and tile counts over the experts, 64 at a time.
-// Integer sums: the same values as a serial scan.
-__device__ __forceinline__ void scan_body(const int32_t* __restrict__ blockhist, int nb, int E, int bm,
-                                          int32_t* __restrict__ blockbase, int32_t* __restrict__ counts,
-                                          int32_t* __restrict__ offsets, MTile* __restrict__ sched,
-                                          int32_t* __restrict__ sched_count, int32_t* sh) {
-  int32_t* cnt = sh;
-  int32_t* off = sh + E;
+__global__ __launch_bounds__(256) void rank_kernel(const int32_t* __restrict__ idx, int T, int k, int E, int nb,
+                                                   PermuteOut po) {
+  extern __shared__ int32_t rsh[];
+  int32_t* sel = rsh;
+  int32_t* rank_lds = sel + RANK_TOKENS * k;
+  int32_t* hist = rank_lds + RANK_TOKENS * k;
+  int32_t* off = hist + E;
   int32_t* til = off + E + 1;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
-  const int epw = wave < E ? (E - wave + nw - 1) / nw : 0;   // experts of this wave
-  const int nch = (nb + 63) / 64;                            // 64-block chunks per expert
-  constexpr int PRE = 16;
-  if (nch == 0) {
-    for (int e = wave; e < E; e += nw)
-      if (lane == 0) cnt[e] = 0;
-  } else if (epw * nch <= PRE) {
-    // every (expert, chunk) value of this wave is loaded before the scans, so
-    // the global round trips overlap instead of following each other
-    int32_t v[PRE];
-#pragma unroll
-    for (int i = 0; i < PRE; ++i) {
-      v[i] = 0;
-      if (i < epw * nch) {
-        const int e = wave + (i / nch) * nw, b = (i % nch) * 64 + lane;
-        if (b < nb) v[i] = blockhist[(int64_t)b * E + e];
-      }
-    }
-    int32_t carry = 0;
-#pragma unroll
-    for (int i = 0; i < PRE; ++i) {
-      if (i < epw * nch) {
-        const int e = wave + (i / nch) * nw, c = i % nch, b = c * 64 + lane;
-        if (c == 0) carry = 0;
-        const int32_t x = wave_incl_scan(v[i], lane);
-        if (b < nb) blockbase[(int64_t)b * E + e] = carry + x - v[i];
-        carry += wave_last(x);
-        if (c == nch - 1 && lane == 0) cnt[e] = carry;
-      }
-    }
-  } else {
-    for (int e = wave; e < E; e += nw) {
-      int32_t carry = 0;
-      for (int b0 = 0; b0 < nb; b0 += 64) {
-        const int b = b0 + lane;
-        const int32_t v = b < nb ? blockhist[(int64_t)b * E + e] : 0;
-        const int32_t x = wave_incl_scan(v, lane);
-        if (b < nb) blockbase[(int64_t)b * E + e] = carry + x - v;
-        carry += wave_last(x);
-      }
-      if (lane == 0) cnt[e] = carry;
-    }
-  }
+  const int b = blockIdx.x;
+  const int t0 = b * RANK_TOKENS;
+  const int ntok = max(0, min(RANK_TOKENS, T - t0));
+  for (int i = threadIdx.x; i < RANK_TOKENS * k; i += blockDim.x)
+    sel[i] = i < ntok * k ? idx[(int64_t)t0 * k + i] : -1;
   __syncthreads();
-  if (wave == 0) {
-    int32_t co = 0, ct = 0;
-    for (int e0 = 0; e0 < E; e0 += 64) {
-      const int e = e0 + lane;
-      const int32_t c = e < E ? cnt[e] : 0;
-      const int32_t tc = (c + bm - 1) / bm;
-      const int32_t xo = wave_incl_scan(c, lane), xt = wave_incl_scan(tc, lane);
-      if (e < E) {
-        off[e] = co + xo - c;
-        til[e] = ct + xt - tc;
-      }
-      co += wave_last(xo);
-      ct += wave_last(xt);
-    }
-    if (lane == 0) {
-      off[E] = co;
-      til[E] = ct;
-      *sched_count = ct;
-    }
-  }
-  __syncthreads();
-  for (int e = tid; e <= E; e += blockDim.x) {
-    offsets[e] = off[e];
-    if (e < E && counts) counts[e] = cnt[e];
-  }
-  for (int e = tid; e < E; e += blockDim.x) {
-    const int32_t c = cnt[e], base = til[e];
-    for (int i = 0; i * bm < c; ++i) {
-      MTile m;
-      m.group = e;
-      m.row0 = off[e] + i * bm;
-      m.rows = min(bm, c - i * bm);
-      m.pad = 0;
-      sched[base + i] = m;
-    }
-  }
+  const bool single = nb <= 1;
+  rank_block<KB>(sel, ntok, k, E, b, po, hist, single ? rank_lds : nullptr);
+  if (single) finish_single_block(sel, rank_lds, ntok, k, E, po, hist, off, til);
 }
 
-__global__ __launch_bounds__(1024) void scan_kernel(const int32_t* __restrict__ blockhist, int nb, int E, int bm,
-                                                    int32_t* __restrict__ blockbase, int32_t* __restrict__ counts,
-                                                    int32_t* __restrict__ offsets, MTile* __restrict__ sched,
-                                                    int32_t* __restrict__ sched_count) {
-  extern __shared__ int32_t sh[];
-  scan_body(blockhist, nb, E, bm, blockbase, counts, offsets, sched, sched_count, sh);
-}
-
-// Slot s: pos = offsets[e] + blockbase[b][e] + rank; writes the sorted order,
-// its inverse and the optional weight gather.
-__device__ __forceinline__ void scatter_slot(int64_t s, const int32_t* __restrict__ idx,
-                                             const int32_t* __restrict__ local_rank,
-                                             const int32_t* __restrict__ blockbase,
-                                             const int32_t* __restrict__ offsets, int k, int E,
-                                             int32_t* __restrict__ sorted_slot, int32_t* __restrict__ sorted_token,
-                                             int32_t* __restrict__ slot_pos, const float* __restrict__ w,
-                                             float* __restrict__ sorted_w) {
-  const int t = (int)(s / k);
-  const int e = idx[s];
-  // Invalid routing (an id outside [0, E), or an id repeated within a token,
-  // whose earlier slots get no rank) is not placed: no write leaves the
-  // expert's range of sorted positions.
-  if ((unsigned)e >= (unsigned)E) return;
-  const int b = t / RANK_TOKENS;
-  const int32_t pos = offsets[e] + blockbase[(int64_t)b * E + e] + local_rank[s];
-  if (pos < offsets[e] || pos >= offsets[e + 1]) return;
-  sorted_slot[pos] = (int32_t)s;
-  sorted_token[pos] = t;
-  slot_pos[s] = pos;
-  if (sorted_w) sorted_w[pos] = w[s];
-}
-
-__global__ void scatter_kernel(const int32_t* __restrict__ idx, const int32_t* __restrict__ local_rank,
-                               const int32_t* __restrict__ blockbase, const int32_t* __restrict__ offsets, int T, int k,
-                               int E, int32_t* __restrict__ sorted_slot, int32_t* __restrict__ sorted_token,
-                               int32_t* __restrict__ slot_pos, const float* __restrict__ w, float* __restrict__ sorted_w) {
-  const int64_t s = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (s >= (int64_t)T * k) return;
-  scatter_slot(s, idx, local_rank, blockbase, offsets, k, E, sorted_slot, sorted_token, slot_pos, w, sorted_w);
-}
-
-// Small calls (decode): rank, scan and scatter in one workgroup of 16 waves,
-// with workgroup barriers (which order the global scratch writes) between
-// the stages.  The waves share out (rank block, expert phase) pairs.
-template <int KB>
-__global__ __launch_bounds__(1024) void permute_small_kernel(const int32_t* __restrict__ idx, int T, int k, int E,
-                                                             int bm, int32_t* __restrict__ blockhist,
-                                                             int32_t* __restrict__ local_rank,
-                                                             int32_t* __restrict__ blockbase,
-                                                             int32_t* __restrict__ counts,
-                                                             int32_t* __restrict__ offsets, MTile* __restrict__ sched,
-                                                             int32_t* __restrict__ sched_count,
-                                                             int32_t* __restrict__ sorted_slot,
-                                                             int32_t* __restrict__ sorted_token,
-                                                             int32_t* __restrict__ slot_pos,
-                                                             const float* __restrict__ w, float* __restrict__ sorted_w) {
-  extern __shared__ int32_t sh[];
-  const int nb = (T + RANK_TOKENS - 1) / RANK_TOKENS;
-  const int nw = blockDim.x >> 6, wave = threadIdx.x >> 6;
-  const int per_b = max(1, nw / max(nb, 1));
-  for (int pr = wave; pr < nb * per_b; pr += nw)
-    rank_experts<KB>(idx, T, k, E, pr / per_b, pr % per_b, per_b, blockhist, local_rank);
+// Expert totals and this workgroup's base from blockhist, then its slots.
+// LDS: cnt[E] | base[E] | off[E + 1] | til[E + 1] | red[2][4][64]
+__global__ __launch_bounds__(256) void prefix_scatter_kernel(const int32_t* __restrict__ idx, int T, int k, int E,
+                                                             int nb, int G, PermuteOut po) {
+  extern __shared__ int32_t psh[];
+  int32_t* cnt = psh;
+  int32_t* base = cnt + E;
+  int32_t* off = base + E;
+  int32_t* til = off + E + 1;
+  int32_t* red = til + E + 1;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int b0 = blockIdx.x * G, b1 = min(nb, b0 + G);
+  for (int e0 = 0; e0 < E; e0 += 64) {
+    const int e = e0 + lane;
+    int32_t tot = 0, pre = 0;
+    if (e < E) {
+#pragma unroll 8
+      for (int b = wave; b < nb; b += 4) {
+        const int32_t v = po.blockhist[(int64_t)b * E + e];
+        tot += v;
+        pre += b < b0 ? v : 0;
+      }
+    }
+    red[wave * 64 + lane] = tot;
+    red[256 + wave * 64 + lane] = pre;
+    __syncthreads();
+    if (wave == 0 && e < E) {
+      cnt[e] = ((red[lane] + red[64 + lane]) + red[128 + lane]) + red[192 + lane];
+      base[e] = ((red[256 + lane] + red[320 + lane]) + red[384 + lane]) + red[448 + lane];
+    }
+    __syncthreads();
+  }
+  scan_experts(cnt, E, po.bm, off, til);
   __syncthreads();
-  scan_body(blockhist, nb, E, bm, blockbase, counts, offsets, sched, sched_count, sh);
-  __syncthreads();
-  const int64_t N = (int64_t)T * k;
-  for (int64_t s = threadIdx.x; s < N; s += blockDim.x)
-    scatter_slot(s, idx, local_rank, blockbase, offsets, k, E, sorted_slot, sorted_token, slot_pos, w, sorted_w);
+  if (blockIdx.x == 0) write_offsets(cnt, off, til, E, po);
+  for (int rb = b0; rb < b1; ++rb) {
+    const int64_t s0 = (int64_t)rb * RANK_TOKENS * k;
+    const int64_t s1 = min((int64_t)T * k, s0 + (int64_t)RANK_TOKENS * k);
+    for (int64_t s = s0 + tid; s < s1; s += blockDim.x) {
+      const int e = idx[s];
+      if ((unsigned)e < (unsigned)E) place_slot(s, e, po.local_rank[s], base[e], off, k, po);
+    }
+    if (rb + 1 < b1) {
+      __syncthreads();
+      for (int e = tid; e < E; e += blockDim.x) base[e] += po.blockhist[(int64_t)rb * E + e];
+      __syncthreads();
+    }
+  }
 }
 
 // Row gather with 16-byte vectors; row_bytes % 16 == 0.
@@ -312,7 +171,6 @@ size_t permute_scratch_carve(Carver& c, const dsmoe_dims& d, int bm, PermuteScra
   const int64_t N = (int64_t)d.T * d.k;
   PermuteScratch s;
   s.blockhist = c.take<int32_t>(nb * d.E);
-  s.blockbase = c.take<int32_t>(nb * d.E);
   s.local_rank = c.take<int32_t>(N);
   s.sched = c.take<MTile>(sched_bound(N, d.E, bm));
   s.sched_count = c.take<int32_t>(1);
@@ -320,33 +178,41 @@ size_t permute_scratch_carve(Carver& c, const dsmoe_dims& d, int bm, PermuteScra
   return c.used();
 }
 
-int launch_permute(const int32_t* idx, const dsmoe_dims& d, int bm, const PermuteScratch& s, int32_t* offsets,
-                   int32_t* sorted_slot, int32_t* sorted_token, int32_t* slot_pos, int32_t* counts, const float* w,
-                   float* sorted_w, hipStream_t st) {
+PermuteOut permute_out(const PermuteScratch& s, int bm, int32_t* offsets, int32_t* sorted_slot, int32_t* sorted_token,
+                       int32_t* slot_pos, int32_t* counts, const float* w, float* sorted_w) {
+  PermuteOut po;
+  po.offsets = offsets;
+  po.sorted_slot = sorted_slot;
+  po.sorted_token = sorted_token;
+  po.slot_pos = slot_pos;
+  po.counts = counts;
+  po.w = w;
+  po.sorted_w = sorted_w;
+  po.sched = s.sched;
+  po.sched_count = s.sched_count;
+  po.bm = bm;
+  po.blockhist = s.blockhist;
+  po.local_rank = s.local_rank;
+  return po;
+}
+
+int launch_permute(const int32_t* idx, const dsmoe_dims& d, const PermuteOut& po, bool ranked, hipStream_t st) {
   const int nb = (int)cdiv(d.T, RANK_TOKENS);
-  const int64_t N = (int64_t)d.T * d.k;
-  const size_t lds = sizeof(int32_t) * (3 * d.E + 2);
-  if (d.T <= PERMUTE_SMALL_T) {
+  if (!ranked) {
+    const size_t lds = sizeof(int32_t) * (2 * RANK_TOKENS * d.k + 3 * d.E + 2);
     if (d.k <= 8)
-      hipLaunchKernelGGL(permute_small_kernel<8>, dim3(1), dim3(1024), lds, st, idx, d.T, d.k, d.E, bm, s.blockhist,
-                         s.local_rank, s.blockbase, counts, offsets, s.sched, s.sched_count, sorted_slot, sorted_token,
-                         slot_pos, w, sorted_w);
+      hipLaunchKernelGGL(rank_kernel<8>, dim3(max(nb, 1)), dim3(256), lds, st, idx, d.T, d.k, d.E, nb, po);
     else
-      hipLaunchKernelGGL(permute_small_kernel<MAX_K>, dim3(1), dim3(1024), lds, st, idx, d.T, d.k, d.E, bm,
-                         s.blockhist, s.local_rank, s.blockbase, counts, offsets, s.sched, s.sched_count, sorted_slot,
-                         sorted_token, slot_pos, w, sorted_w);
-    return check_launch("permute_small");
+      hipLaunchKernelGGL(rank_kernel<MAX_TOPK>, dim3(max(nb, 1)), dim3(256), lds, st, idx, d.T, d.k, d.E, nb, po);
+    const int rc = check_launch("permute(rank)");
+    if (rc) return rc;
   }
-  if (d.k <= 8)
-    hipLaunchKernelGGL(rank_kernel<8>, dim3(nb), dim3(256), 0, st, idx, d.T, d.k, d.E, s.blockhist, s.local_rank);
-  else
-    hipLaunchKernelGGL(rank_kernel<MAX_K>, dim3(nb), dim3(256), 0, st, idx, d.T, d.k, d.E, s.blockhist, s.local_rank);
-  hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), lds, st, s.blockhist, nb, d.E, bm, s.blockbase, counts, offsets,
-                     s.sched, s.sched_count);
-  if (N > 0)
-    hipLaunchKernelGGL(scatter_kernel, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, st, idx, s.local_rank, s.blockbase,
-                       offsets, d.T, d.k, d.E, sorted_slot, sorted_token, slot_pos, w, sorted_w);
-  return check_launch("permute");
+  if (nb <= 1) return DSMOE_OK;   // finished by the ranking workgroup
+  const int G = (int)cdiv(nb, 256);
+  const size_t lds = sizeof(int32_t) * (4 * d.E + 2 + 512);
+  hipLaunchKernelGGL(prefix_scatter_kernel, dim3((unsigned)cdiv(nb, G)), dim3(256), lds, st, idx, d.T, d.k, d.E, nb,
+                     G, po);
+  return check_launch("permute(scatter)");
 }
 
 int launch_gather_rows(const void* x, int64_t src_rows, const int32_t* rows, int64_t nrows, int D, int elem, void* dst,

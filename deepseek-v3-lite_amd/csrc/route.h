@@ -3,6 +3,8 @@
 // Restates models/moe.py:32-36 (AuxLossFreeGate.forward after F.linear).
 #pragma once
 
+#include <stdint.h>
+
 #include "common.h"
 
 namespace dsmoe {
@@ -10,49 +12,57 @@ namespace dsmoe {
 constexpr int MAX_EPL = 4;         // experts per lane in routing (E <= 256)
 
 // Routes tokens [t0, t0 + ntok) whose fp32 logits sit in LDS rows lg[t*ldl].
-// Wave w routes tokens in batches of route_ntok(EPL): w, w + nw, ... in batch
-// units.  Lane l holds expert l (E <= 64) or
-// experts l, l + 64, ... (E <= 256) in registers.
+// Wave w routes tokens in batches of NB: w, w + nw, ... in batch units.  Lane
+// l holds expert l (E <= 64) or experts l, l + 64, ... (E <= 256) in
+// registers.
 //
 // Selection: k rounds of a wave arg-max over the biased scores under the
-// order (value desc, id asc): a DPP max gives the round's value m, a ballot of
-// the lanes holding m and its lowest set bit give the lowest expert id with
-// that value, which takes slot j of the round and drops out.  This is the
-// oracle's k rounds of arg-max with the same tie rule.  The renormalising sum
-// runs over slots j = 0..k-1 in order, as in the oracle.
+// order (value desc, id asc).  Each score is held as an integer key with the
+// same order (route_key), so a round is one integer DPP max (the round's key
+// m) and a ballot of the lanes holding m, whose lowest set bit gives the
+// lowest expert id with that key; that expert takes slot j and its key drops
+// to INT32_MIN.  This is the oracle's k rounds of arg-max with the same tie
+// rule.  The renormalising sum runs over slots j = 0..k-1 in order, as in
+// the oracle.
 constexpr int route_ntok(int epl) { return epl == 1 ? 4 : 2; }
+
+// Order key of a biased score: a signed integer ordered like the score, with
+// -0 folded into +0 (they compare equal) and NaN below every number (a NaN
+// score is taken only when no number is left, lowest id first).  INT32_MIN
+// marks lanes without an expert or already selected.
+__device__ __forceinline__ int32_t route_key(float f) {
+  int32_t b = __float_as_int(f);
+  if (f != f) return INT32_MIN + 1;
+  if (b == INT32_MIN) b = 0;
+  return b >= 0 ? b : b ^ 0x7fffffff;
+}
 
 // Maximum over the 64 lanes (every lane gets it).  Row (16-lane) shifts, then
 // the row broadcasts of lanes 15 and 31, leave the maximum in lane 63.
-__device__ __forceinline__ float wave_max_f32(float v) {
-  const int b = __float_as_int(v);
-  float t;
-  t = __int_as_float(__builtin_amdgcn_update_dpp(b, __float_as_int(v), 0x111, 0xf, 0xf, false));  // row_shr:1
-  v = fmaxf(v, t);
-  t = __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x112, 0xf, 0xf, false));
-  v = fmaxf(v, t);
-  t = __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x114, 0xf, 0xf, false));
-  v = fmaxf(v, t);
-  t = __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x118, 0xf, 0xf, false));
-  v = fmaxf(v, t);
-  t = __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x142, 0xa, 0xf, false));  // row_bcast:15
-  v = fmaxf(v, t);
-  t = __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x143, 0xc, 0xf, false));  // row_bcast:31
-  v = fmaxf(v, t);
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+__device__ __forceinline__ int32_t wave_max_i32(int32_t v) {
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x111, 0xf, 0xf, false));  // row_shr:1
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x112, 0xf, 0xf, false));  // row_shr:2
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x114, 0xf, 0xf, false));  // row_shr:4
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x118, 0xf, 0xf, false));  // row_shr:8
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x142, 0xa, 0xf, false));  // row_bcast:15
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x143, 0xc, 0xf, false));  // row_bcast:31
+  return __builtin_amdgcn_readlane(v, 63);
 }
 
 // EPL: experts per lane (1 for E <= 64, MAX_EPL otherwise); NB: tokens a
 // wave routes side by side (their sigmoid, max and ballot chains are
 // independent, so their latencies overlap).
+// sel (optional, LDS): sel[t * k + j] = the expert of slot j of token t0 + t.
 template <int EPL, int NB = route_ntok(EPL)>
 __device__ __forceinline__ void route_tokens_t(const float* lg, int ldl, int ntok, int t0, const float* bias_s, int E,
-                                               int k, float route_scale, int xdtype, const GateOut& out, int* hist) {
+                                               int k, float route_scale, int xdtype, const GateOut& out, int* hist,
+                                               int32_t* sel = nullptr) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int nw = blockDim.x >> 6;
   for (int tb = wave * NB; tb < ntok; tb += nw * NB) {
-    float sv[NB][EPL], bv[NB][EPL];
+    float sv[NB][EPL];
+    int32_t key[NB][EPL];
     int slot[NB][EPL];
 #pragma unroll
     for (int b = 0; b < NB; ++b)
@@ -60,40 +70,34 @@ __device__ __forceinline__ void route_tokens_t(const float* lg, int ldl, int nto
       for (int q = 0; q < EPL; ++q) {
         const int e = lane + 64 * q;
         sv[b][q] = 0.0f;
-        bv[b][q] = -INFINITY;
+        key[b][q] = INT32_MIN;
         slot[b][q] = -1;
         if (tb + b < ntok && e < E) {
           sv[b][q] = route_sigmoid(lg[(tb + b) * ldl + e]);
-          bv[b][q] = sv[b][q] + bias_s[e];
+          key[b][q] = route_key(sv[b][q] + bias_s[e]);
         }
       }
     float ssum[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) ssum[b] = 0.0f;
     for (int j = 0; j < k; ++j) {
-      float m[NB];
+      int32_t m[NB];
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
-        float lm = bv[b][0];
+        int32_t lm = key[b][0];
 #pragma unroll
-        for (int q = 1; q < EPL; ++q) lm = fmaxf(lm, bv[b][q]);
-        m[b] = wave_max_f32(lm);
+        for (int q = 1; q < EPL; ++q) lm = max(lm, key[b][q]);
+        m[b] = wave_max_i32(lm);
       }
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
+        // the lowest expert id holding the round's key (a token past ntok
+        // has no expert: its rounds pick lane 0 and write nothing)
         int win = -1;
 #pragma unroll
         for (int q = 0; q < EPL; ++q) {
-          const uint64_t bl = __ballot(slot[b][q] < 0 && lane + 64 * q < E && bv[b][q] == m[b]);
+          const uint64_t bl = __ballot(key[b][q] == m[b]);
           if (win < 0 && bl) win = __ffsll((unsigned long long)bl) - 1 + 64 * q;
-        }
-        if (win < 0) {
-          // only NaN scores left: the lowest unselected expert id
-#pragma unroll
-          for (int q = 0; q < EPL; ++q) {
-            const uint64_t bl = __ballot(slot[b][q] < 0 && lane + 64 * q < E);
-            if (win < 0 && bl) win = __ffsll((unsigned long long)bl) - 1 + 64 * q;
-          }
         }
         win = __builtin_amdgcn_readfirstlane(win);
         const int wl = win & 63, wq = win >> 6;
@@ -103,7 +107,7 @@ __device__ __forceinline__ void route_tokens_t(const float* lg, int ldl, int nto
             ssum[b] += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sv[b][q]), wl));
             if (lane == wl) {
               slot[b][q] = j;
-              bv[b][q] = -INFINITY;
+              key[b][q] = INT32_MIN;
             }
           }
       }
@@ -130,19 +134,119 @@ __device__ __forceinline__ void route_tokens_t(const float* lg, int ldl, int nto
           }
           if (out.sel_scores) out.sel_scores[o + j] = sv[b][q];
           if (hist) atomicAdd(&hist[e], 1);
+          if (sel) sel[(tb + b) * k + j] = e;
         }
       }
     }
   }
 }
 
-template <int NB1 = route_ntok(1), int NB4 = route_ntok(MAX_EPL)>
+// Maxima / minima over each 16-lane row of a wave (every lane gets its row's):
+// rotations by 1, 2, 4, 8 within the row.
+__device__ __forceinline__ int32_t row_max_i32(int32_t v) {
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x121, 0xf, 0xf, false));  // row_ror:1
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x122, 0xf, 0xf, false));  // row_ror:2
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x124, 0xf, 0xf, false));  // row_ror:4
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x128, 0xf, 0xf, false));  // row_ror:8
+  return v;
+}
+__device__ __forceinline__ int32_t row_min_i32(int32_t v) {
+  v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x121, 0xf, 0xf, false));
+  v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x122, 0xf, 0xf, false));
+  v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x124, 0xf, 0xf, false));
+  v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x128, 0xf, 0xf, false));
+  return v;
+}
+
+// Routing of E <= 64 experts with four tokens per wave: row r (16 lanes) holds
+// token tb + r, lane c of the row experts c, c + 16, c + 32, c + 48.  A round
+// is a row max of the keys, a row min of the lowest expert id holding it (the
+// tie rule), and a permute that hands the winner's unbiased score to the row
+// for the renormalising sum (slot order, as in the oracle).
+__device__ __forceinline__ void route_tokens_rows(const float* lg, int ldl, int ntok, int t0, const float* bias_s,
+                                                  int E, int k, float route_scale, int xdtype, const GateOut& out,
+                                                  int* hist, int32_t* sel) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nw = blockDim.x >> 6;
+  const int r = lane >> 4, c = lane & 15;
+  for (int tb = wave * 4; tb < ntok; tb += nw * 4) {
+    const int t = tb + r;
+    const bool live = t < ntok;
+    float sv[4];
+    int32_t key[4];
+    int slot[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int e = c + 16 * q;
+      sv[q] = 0.0f;
+      key[q] = INT32_MIN;
+      slot[q] = -1;
+      if (live && e < E) {
+        sv[q] = route_sigmoid(lg[t * ldl + e]);
+        key[q] = route_key(sv[q] + bias_s[e]);
+      }
+    }
+    float ssum = 0.0f;
+    for (int j = 0; j < k; ++j) {
+      const int32_t m = row_max_i32(max(max(key[0], key[1]), max(key[2], key[3])));
+      int32_t cand = 255;
+#pragma unroll
+      for (int q = 3; q >= 0; --q)
+        if (key[q] == m) cand = c + 16 * q;
+      // a row without a live token has only INT32_MIN keys: its rounds pick
+      // expert 0 and write nothing
+      const int32_t win = row_min_i32(cand);
+      const int wq = win >> 4;
+      float wsv = sv[0];
+#pragma unroll
+      for (int q = 1; q < 4; ++q)
+        if (q == wq) wsv = sv[q];
+      ssum += __int_as_float(
+          __builtin_amdgcn_ds_bpermute((r * 16 + (win & 15)) << 2, __float_as_int(wsv)));
+      if (c == (win & 15)) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (q == wq) {
+            slot[q] = j;
+            key[q] = INT32_MIN;
+          }
+      }
+    }
+    if (!live) continue;
+    const float den = ssum < 1e-10f ? 1e-10f : ssum;
+    const int64_t o = (int64_t)(t0 + t) * k;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int e = c + 16 * q;
+      if (slot[q] >= 0) {
+        const int jj = slot[q];
+        const float w = sv[q] / den * route_scale;
+        out.idx[o + jj] = e;
+        if (out.idx64) out.idx64[o + jj] = e;
+        out.weights[o + jj] = w;
+        if (out.weights_x) {
+          if (xdtype == DSMOE_BF16)
+            static_cast<bf16_t*>(out.weights_x)[o + jj] = f2bf(w);
+          else
+            static_cast<float*>(out.weights_x)[o + jj] = w;
+        }
+        if (out.sel_scores) out.sel_scores[o + jj] = sv[q];
+        if (hist) atomicAdd(&hist[e], 1);
+        if (sel) sel[t * k + jj] = e;
+      }
+    }
+  }
+}
+
+template <int NB4 = route_ntok(MAX_EPL)>
 __device__ __forceinline__ void route_tokens(const float* lg, int ldl, int ntok, int t0, const float* bias_s, int E,
-                                             int k, float route_scale, int xdtype, const GateOut& out, int* hist) {
+                                             int k, float route_scale, int xdtype, const GateOut& out, int* hist,
+                                             int32_t* sel = nullptr) {
   if (E <= 64)
-    route_tokens_t<1, NB1>(lg, ldl, ntok, t0, bias_s, E, k, route_scale, xdtype, out, hist);
+    route_tokens_rows(lg, ldl, ntok, t0, bias_s, E, k, route_scale, xdtype, out, hist, sel);
   else
-    route_tokens_t<MAX_EPL, NB4>(lg, ldl, ntok, t0, bias_s, E, k, route_scale, xdtype, out, hist);
+    route_tokens_t<MAX_EPL, NB4>(lg, ldl, ntok, t0, bias_s, E, k, route_scale, xdtype, out, hist, sel);
 }
 
 __device__ __forceinline__ void flush_hist(const int* hist, int E, int32_t* counts) {

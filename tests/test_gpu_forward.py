@@ -102,7 +102,7 @@ def test_route_writes_only_the_token_rows(T, E, k):
 
 # --------------------------------------------------------------------- permute
 @pytest.mark.parametrize("T,E,k", [(1, 4, 2), (64, 4, 2), (65, 4, 2), (1000, 16, 4), (8192, 64, 6), (3000, 256, 8),
-                                   (8192, 16, 4)])
+                                   (8192, 16, 4), (20000, 64, 6)])
 def test_permute_bit_exact(T, E, k):
     rng = np.random.default_rng(T * 31 + E)
     if T == 8192 and E == 16:       # C2-like skew: experts 0 and 1 in every token
@@ -121,6 +121,48 @@ def test_permute_bit_exact(T, E, k):
     assert np.array_equal(_np(out["counts"]), np.diff(off))
     assert torch.equal(out["x_sorted"].cpu(), x[torch.from_numpy(st).long()])
     assert torch.equal(out["sorted_w"].cpu(), w.reshape(-1)[torch.from_numpy(ss).long()])
+
+
+@pytest.mark.parametrize("T", [40, 300])   # one rank block (one launch), and several
+def test_permute_c_abi_skips_invalid_slots(T):
+    """Through the C ABI (ops.permute rejects such ids before the call): a
+    slot whose id lies outside [0, E), or repeats a later slot's id in its
+    token, is not placed; every other slot lands where a stable (expert,
+    token) sort of the placed slots puts it, and offsets and counts count only
+    those."""
+    import dsmoe._lib as L
+    E, k = 8, 3
+    rng = np.random.default_rng(T)
+    idx = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    idx[3, 1] = E + 5
+    idx[7, 0] = -2
+    idx[11, 0] = idx[11, 2]
+    placed = [(t, j) for t in range(T) for j in range(k)
+              if 0 <= idx[t, j] < E and idx[t, j] not in idx[t, j + 1:]]
+    order = sorted(placed, key=lambda tj: (idx[tj], tj[0]))
+    counts = np.bincount([idx[tj] for tj in placed], minlength=E)
+    P = len(placed)
+    N = T * k
+    d = L.make_dims(T, 1, E, k, 1, 0, 0, torch.float32, 1.0)
+    lib = L.load()
+    ws = torch.empty(lib.dsmoe_permute_workspace_size(d), dtype=torch.uint8, device=DEV)
+    gi = torch.from_numpy(idx).to(DEV)
+    off = torch.full((E + 1,), -7, dtype=torch.int32, device=DEV)
+    ss, st, sp = (torch.full((N,), -7, dtype=torch.int32, device=DEV) for _ in range(3))
+    cnt = torch.full((E,), -7, dtype=torch.int32, device=DEV)
+    rc = lib.dsmoe_permute(L.ptr(gi), d, L.ptr(off), L.ptr(ss), L.ptr(st), L.ptr(sp), L.ptr(cnt), None, None, None,
+                           None, L.ptr(ws), ws.numel(), L.stream_ptr(DEV))
+    L.check(rc, "dsmoe_permute")
+    assert np.array_equal(_np(off), np.concatenate([[0], np.cumsum(counts)]))
+    assert np.array_equal(_np(cnt), counts)
+    assert np.array_equal(_np(ss)[:P], [t * k + j for t, j in order])
+    assert np.array_equal(_np(st)[:P], [t for t, _ in order])
+    assert (_np(ss)[P:] == -7).all()
+    spn = _np(sp)
+    for pos, (t, j) in enumerate(order):
+        assert spn[t * k + j] == pos
+    for t, j in ((3, 1), (7, 0), (11, 0)):
+        assert spn[t * k + j] == -7
 
 
 # --------------------------------------------------------------------- grouped operator seam
