@@ -198,6 +198,34 @@ static GemmDesc desc_zero() {
   return g;
 }
 
+// ---------------------------------------------------------------- static permute scratch
+// The scratch of dsmoe_permute_noalloc: a file-scope device array, one copy
+// per GPU (each at its own address), held until the process ends.  In host
+// code `scratch` names a host-side stand-in, so kernels get the device
+// address from hipGetSymbolAddress, fetched once per device with that device
+// current and kept in g_scratch_ptr.
+static __device__ __align__(256) char scratch[DSMOE_PERMUTE_NOALLOC_BYTES];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices] = {};
+
+static int static_scratch(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(DSMOE_ERR_HIP, "permute_noalloc: hipGetDevice failed");
+  if (dev < 0 || dev >= kMaxDevices) return fail(DSMOE_ERR_UNSUPPORTED, "permute_noalloc: device index >= 64");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(DSMOE_ERR_HIP, std::string("permute_noalloc: hipGetSymbolAddress: ") + hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return DSMOE_OK;
+}
+
 }  // namespace dsmoe
 
 using namespace dsmoe;
@@ -259,6 +287,26 @@ int dsmoe_permute(const int32_t* idx, const dsmoe_dims* dims, int32_t* offsets, 
     rc = launch_gather_rows(x, dims->T, sorted_token, (int64_t)dims->T * dims->k, dims->D, elem_size(dims->dtype),
                             x_sorted, st);
   return rc;
+}
+
+int dsmoe_permute_noalloc(const int32_t* idx, const dsmoe_dims* dims, int32_t* offsets, int32_t* sorted_slot,
+                          int32_t* sorted_token, int32_t* slot_pos, int32_t* counts, const void* x, void* x_sorted,
+                          const float* weights, float* sorted_w, void* stream) {
+  int rc = validate(dims, false);
+  if (rc) return rc;
+  const size_t need = dsmoe_permute_workspace_size(dims);
+  if (need > DSMOE_PERMUTE_NOALLOC_BYTES)
+    return fail(DSMOE_ERR_UNSUPPORTED, "permute_noalloc: this call needs " + std::to_string(need) +
+                                           " bytes of scratch, more than the static " +
+                                           std::to_string((size_t)DSMOE_PERMUTE_NOALLOC_BYTES) +
+                                           "; use dsmoe_permute with a workspace");
+  void* ws = nullptr;
+  rc = static_scratch(&ws);
+  if (rc) return rc;
+  // the same launches as dsmoe_permute; no scratch value is read before the
+  // call writes it, so nothing needs clearing between calls
+  return dsmoe_permute(idx, dims, offsets, sorted_slot, sorted_token, slot_pos, counts, x, x_sorted, weights, sorted_w,
+                       ws, DSMOE_PERMUTE_NOALLOC_BYTES, stream);
 }
 
 static size_t grouped_ws(const dsmoe_dims& d, void* base, const void*** ptrs, int32_t** off32, MTile** sched,

@@ -24,6 +24,7 @@ DSMOE_F32 = 0
 DSMOE_BF16 = 1
 # forward-workspace buffer ids of dsmoe_moe_fwd_workspace_offset
 WS_IDX, WS_WEIGHTS, WS_SEL_SCORES, WS_OFFSETS, WS_SORTED_SLOT, WS_SORTED_TOKEN, WS_SLOT_POS = range(7)
+PERMUTE_NOALLOC_BYTES = 2 << 20   # include/dsmoe.h DSMOE_PERMUTE_NOALLOC_BYTES
 
 
 class Dims(ctypes.Structure):
@@ -47,6 +48,7 @@ _SIGNATURES = {
     "dsmoe_route_from_logits": ([P, P, DIMS, P, P, P, P, P, P, P], I32),
     "dsmoe_permute_workspace_size": ([DIMS], SZ),
     "dsmoe_permute": ([P, DIMS, P, P, P, P, P, P, P, P, P, P, SZ, P], I32),
+    "dsmoe_permute_noalloc": ([P, DIMS, P, P, P, P, P, P, P, P, P, P], I32),
     "dsmoe_grouped_swiglu_workspace_size": ([DIMS], SZ),
     "dsmoe_grouped_swiglu_fwd": ([P, PP, PP, PP, P, P, DIMS, P, P, SZ, P], I32),
     "dsmoe_grouped_swiglu_bwd_workspace_size": ([DIMS], SZ),

@@ -107,6 +107,21 @@ int dsmoe_permute(const int32_t* idx, const dsmoe_dims* dims, int32_t* offsets, 
                   int32_t* sorted_token, int32_t* slot_pos, int32_t* counts, const void* x, void* x_sorted,
                   const float* weights, float* sorted_w, void* workspace, size_t workspace_bytes, void* stream);
 
+/* dsmoe_permute without a workspace argument.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops, harnesses that forbid hipMalloc).  The
+ * scratch is a static device array of DSMOE_PERMUTE_NOALLOC_BYTES that the
+ * library holds on each GPU it runs on until the process ends; the call makes
+ * no allocation.  A call needing more scratch than that
+ * (dsmoe_permute_workspace_size(dims) > DSMOE_PERMUTE_NOALLOC_BYTES; about
+ * 400k slots T*k at E = 64) returns DSMOE_ERR_UNSUPPORTED without launching.
+ * Every call on one GPU shares the array: calls that overlap on one GPU (other
+ * streams, other threads) race and must be serialised by the caller. */
+#define DSMOE_PERMUTE_NOALLOC_BYTES (2u << 20)
+int dsmoe_permute_noalloc(const int32_t* idx, const dsmoe_dims* dims, int32_t* offsets, int32_t* sorted_slot,
+                          int32_t* sorted_token, int32_t* slot_pos, int32_t* counts, const void* x, void* x_sorted,
+                          const float* weights, float* sorted_w, void* stream);
+
 /* ---------------------------------------------------------------------------
  * (c) Grouped SwiGLU experts on expert-sorted rows.  Replaces the operator
  * seam triton_grouped_moe_dispatch / _TritonGroupedMoeFunction.forward,

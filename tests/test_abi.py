@@ -100,3 +100,16 @@ def test_workspace_offsets_lie_inside_the_forward_workspace(lib):
         assert lib.dsmoe_moe_fwd_workspace_offset(ctypes.byref(d), train, 99) == bad
     d = L.Dims(16, 64, 4, 5, 32, 1, 32, L.DSMOE_F32, 1.0)          # k > E
     assert lib.dsmoe_moe_fwd_workspace_offset(ctypes.byref(d), 0, L.WS_IDX) == bad
+
+
+def test_permute_noalloc_rejects_calls_beyond_its_static_scratch(lib):
+    """dsmoe_permute_noalloc refuses (before any device call) a shape whose
+    permute scratch exceeds DSMOE_PERMUTE_NOALLOC_BYTES, and names the limit."""
+    import dsmoe._lib as L
+    d = L.Dims(600000, 64, 64, 6, 32, 0, 32, L.DSMOE_BF16, 1.0)
+    assert lib.dsmoe_permute_workspace_size(ctypes.byref(d)) > L.PERMUTE_NOALLOC_BYTES
+    rc = lib.dsmoe_permute_noalloc(None, ctypes.byref(d), None, None, None, None, None, None, None, None, None, None)
+    assert rc == L.DSMOE_ERR_UNSUPPORTED
+    assert str(L.PERMUTE_NOALLOC_BYTES).encode() in lib.dsmoe_last_error()
+    small = L.Dims(8192, 2048, 64, 6, 1408, 2, 1408, L.DSMOE_BF16, 1.0)
+    assert lib.dsmoe_permute_workspace_size(ctypes.byref(small)) <= L.PERMUTE_NOALLOC_BYTES
