@@ -31,6 +31,7 @@ import statistics
 import sys
 import time
 from pathlib import Path
+from typing import Optional
 
 ROOT = Path(__file__).resolve().parent
 for _p in (str(ROOT), str(ROOT / "deepseek-v3-lite_amd")):
@@ -82,10 +83,15 @@ def make_layer(cfg, device, seed: int = 0):
     return x, gate_w, bias, (w1, w2, w3, s1, s2, s3)
 
 
-def cpu_baseline(cfg, x, gate_w, bias, weights, budget_s: float = 16.0, backward: bool = False):
+def cpu_baseline(cfg, x, gate_w, bias, weights, budget_s: float = 16.0, backward: bool = False,
+                 min_tokens: int = 0):
     """Times oracle/moe_ref.py's restatement of the reference stacked forward
-    (models/moe.py:74-179) on this host on a token sample sized to the budget;
-    with ``backward`` the autograd forward+backward of the same path."""
+    (models/moe.py:74-179) on this host on a token sample sized to the budget
+    (at least ``min_tokens``); with ``backward`` the autograd forward+backward
+    of the same path.  A first pass over min(T, 256) tokens is the warm-up and,
+    with the timed sample, gives a fit of the CPU time as fixed + per-token
+    cost (the fixed part is the per-call weight work, which does not shrink
+    with the sample)."""
     import torch
     from oracle import moe_ref as R
     T, D, E, I, k, S, I_s, dt, _ = cfg
@@ -104,22 +110,29 @@ def cpu_baseline(cfg, x, gate_w, bias, weights, budget_s: float = 16.0, backward
             with torch.no_grad():
                 R.moe_forward_ref(xs[:n], p, k)
 
-    n = min(T, 256)
+    n1 = min(T, 256)
     t0 = time.perf_counter()
-    run(n)
+    run(n1)
     dt1 = time.perf_counter() - t0
-    n = int(min(T, max(n, n * (budget_s / 4.0) / max(dt1, 1e-6))))
+    n = int(min(T, max(n1, min_tokens, n1 * (budget_s / 4.0) / max(dt1, 1e-6))))
+    reps = 3 if not backward else 2
     times = []
-    for _ in range(3):
+    for _ in range(reps):
         t0 = time.perf_counter()
         run(n)
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
     what = "forward+backward (autograd) passes" if backward else "forward passes"
-    return {"value": n / med, "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"first {n} of {T} tokens, same weights; median of 3 {what} "
-                      f"({med * 1e3:.1f} ms each) after 1 warm-up; torch {torch.__version__} "
-                      f"{torch.backends.cpu.get_cpu_capability()}"}
+    out = {"value": n / med, "unit": "tokens/s", "cores": cores, "kind": "port",
+           "sample": f"first {n} of {T} tokens, same weights; median of {reps} {what} "
+                     f"({med * 1e3:.1f} ms each) after a {n1}-token warm-up pass; torch {torch.__version__} "
+                     f"{torch.backends.cpu.get_cpu_capability()}"}
+    if n > n1:
+        per_tok = (med - dt1) / (n - n1)
+        fixed = dt1 - per_tok * n1
+        out["fit"] = {"fixed_s": fixed, "per_token_s": per_tok, "from": f"{n1} and {n} tokens",
+                      "full_T_tokens_per_s": T / (fixed + per_tok * T) if fixed + per_tok * T > 0 else None}
+    return out
 
 
 def time_steps(step, steps: int, warmup: int):
@@ -231,6 +244,76 @@ def decode_bench(dev, steps: int, warmup: int):
             "weight_bytes": nbytes, "GB/s": gbs, "frac_hbm": gbs / PEAK_HBM_GBS, "stage_ms": stage_ms}
 
 
+def fwd_bench(name: str, dev, steps: int, warmup: int):
+    """Forward of another BASELINE config (C1, C2 with its skewed bias): step
+    time, routed tokens/s, the grouped GEMMs' rate, per-stage times and the
+    largest expert's share of the slots."""
+    import torch
+    from dsmoe import moe_layer
+    cfg = CONFIGS[name]
+    T, D, E, I, k, S, I_s, dt, bias_kind = cfg
+    log(f"[bench] forward config {name}: T={T} D={D} E={E} I={I} k={k} S={S}x{I_s} {dt} bias={bias_kind}")
+    x, gate_w, bias, (w1, w2, w3, s1, s2, s3) = make_layer(cfg, dev)
+
+    def step():
+        return moe_layer(x, gate_w, bias, w1, w2, w3, s1, s2, s3, k=k, training=False)
+
+    with torch.no_grad():
+        counts = step()[3]
+        ms, wall = time_steps(step, steps, warmup)
+        stage_ms = stage_times(step, steps)
+    N = T * k
+    gemm_flops = 6.0 * N * D * I + 6.0 * T * D * S * I_s
+    gemm_ms = sum(stage_ms.get(s, 0.0) for s in ("gemm1", "gemm2"))
+    tf = gemm_flops / (gemm_ms * 1e-3) / 1e12 if gemm_ms > 0 else None
+    log(f"[bench] {name}: {ms:.4f} ms/step, grouped GEMMs {tf:.0f} TFLOP/s")
+    return {"workload": f"{name}: DeepSeekMoE layer forward, T={T}, dim={D}, {E} routed (inter {I}) top-{k}, "
+                        f"{S} shared (inter {I_s}), {dt}, fp32 gate, gate bias {bias_kind}",
+            "ms_per_step": ms, "tokens_per_s": T / (ms * 1e-3), "grouped_gemm_tflops": tf,
+            "grouped_gemm_frac": tf / PEAK_BF16_TFLOPS if tf else None, "stage_ms": stage_ms,
+            "max_expert_share": float(counts.max().item()) / N}
+
+
+def autocast_bench(dev, steps: int, warmup: int, ref_fwd_ms: float, ref_fwd_bwd_ms: Optional[float]):
+    """The drop-in module (fp32 parameters) under bf16 autocast, the way the
+    reference trains (training/pretrain.py:212-213): C3 forward and, when the
+    bf16-weights training step was timed, the C4 forward+backward to every
+    parameter.  Reported beside the bf16-weights layer times; the module casts
+    its fp32 expert weights once per parameter change, not per call."""
+    import torch
+    from dsmoe import DeepSeekMoE
+    out = {}
+    for name, ref_ms, train in (("c3", ref_fwd_ms, False), ("c4", ref_fwd_bwd_ms, True)):
+        if ref_ms is None:
+            continue
+        T, D, E, I, k, S, I_s, dt, _ = CONFIGS[name]
+        torch.manual_seed(0)
+        mod = DeepSeekMoE({"dim": D, "n_routed_experts": E, "n_shared_experts": S, "n_activated_experts": k,
+                           "moe_inter_dim": I, "shared_inter_dim": I_s}).to(dev)
+        x = torch.randn(T, D, device=dev, dtype=torch.bfloat16)
+        if train:
+            x.requires_grad_(True)
+            dy = torch.randn(T, D, device=dev, dtype=torch.bfloat16)
+            leaves = [x] + [p for p in mod.parameters() if p.requires_grad]
+
+            def step():
+                with torch.autocast("cuda", dtype=torch.bfloat16):
+                    y = mod(x)
+                return torch.autograd.grad(y, leaves, dy)
+            ms, _ = time_steps(step, max(3, steps // 4), max(2, warmup // 4))
+        else:
+            def step():
+                with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+                    return mod(x)
+            ms, _ = time_steps(step, steps, warmup)
+        key = "fwd_bwd_c4" if train else "fwd_c3"
+        out[key] = {"ms_per_step": ms, "bf16_weights_ms_per_step": ref_ms, "ratio": ms / ref_ms}
+        log(f"[bench] autocast {key}: {ms:.4f} ms/step vs {ref_ms:.4f} with bf16 weights ({ms / ref_ms:.3f}x)")
+        del mod, x
+        torch.cuda.empty_cache()
+    return out
+
+
 def torch_sync():
     import torch
     torch.cuda.synchronize()
@@ -271,7 +354,7 @@ def fwd_bwd_bench(name: str, dev, steps: int, warmup: int, with_cpu: bool):
     if with_cpu:
         log("[bench] timing the CPU restatement of the reference path (fwd+bwd) ...")
         out["cpu_baseline"] = cpu_baseline(cfg, x, gate_w, bias, (w1, w2, w3, s1, s2, s3), budget_s=12.0,
-                                           backward=True)
+                                           backward=True, min_tokens=2048)
         out["speedup_vs_cpu"] = out["value"] / out["cpu_baseline"]["value"]
     return out
 
@@ -288,8 +371,13 @@ def main() -> int:
     ap.add_argument("--no-fwd-bwd", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true", help="skip the config-3 decode (T=64) measurement")
+    ap.add_argument("--no-extra-configs", action="store_true", help="skip the C1 / C2 forward figures")
+    ap.add_argument("--no-autocast", action="store_true", help="skip the module-under-autocast figures")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="instead of the layer, run --steps device copies of this many MiB (counter calibration)")
+    ap.add_argument("--dma-mb", type=int, default=0,
+                    help="instead of the layer, run --steps direct global->LDS reads of this many MiB "
+                         "(counter calibration for the GEMMs' load path)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -308,6 +396,17 @@ def main() -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_per_launch": n, "launches": args.steps}), flush=True)
+        return 0
+    if args.dma_mb:
+        import dsmoe._lib as L
+        n = args.dma_mb * (1 << 20)
+        src = torch.ones(n, dtype=torch.uint8, device=dev)
+        sink = torch.empty(args.dma_mb, dtype=torch.int32, device=dev)
+        lib = L.load()
+        for _ in range(args.steps):
+            L.check(lib.dsmoe_probe_dma_read(L.ptr(src), n, L.ptr(sink), L.stream_ptr(dev)), "dsmoe_probe_dma_read")
+        torch.cuda.synchronize()
+        print(json.dumps({"dma_read_bytes_per_launch": n, "launches": args.steps}), flush=True)
         return 0
     cfg = CONFIGS[args.config]
     T, D, E, I, k, S, I_s, dt, bias_kind = cfg
@@ -370,6 +469,8 @@ def main() -> int:
     }
     if not args.no_decode and args.config == "c3":
         result["decode"] = decode_bench(dev, max(10, args.steps), max(3, args.warmup))
+    if not args.no_extra_configs and args.config == "c3":
+        result["configs_fwd"] = {c: fwd_bench(c, dev, args.steps, args.warmup) for c in ("c1", "c2")}
     if not args.no_cpu_baseline:
         log("[bench] timing the CPU restatement of the reference path ...")
         result["cpu_baseline"] = cpu_baseline(cfg, x, gate_w, bias, weights)
@@ -378,6 +479,10 @@ def main() -> int:
         del x, weights, w1, w2, w3, s1, s2, s3
         result["fwd_bwd"] = fwd_bwd_bench(args.fwd_bwd_config, dev, max(3, args.steps // 4), max(1, args.warmup // 2),
                                           not args.no_cpu_baseline)
+    if not args.no_autocast and args.config == "c3":
+        fb = result.get("fwd_bwd")
+        result["autocast"] = autocast_bench(dev, args.steps, args.warmup, ms,
+                                            fb["ms_per_step"] if fb and args.fwd_bwd_config == "c4" else None)
     print(json.dumps(result), flush=True)
     return 0
 

@@ -64,6 +64,7 @@ _SIGNATURES = {
     "dsmoe_timing_enable": ([I32], I32),
     "dsmoe_timing_read": ([ctypes.POINTER(ctypes.c_double), I32, ctypes.POINTER(ctypes.c_int)], I32),
     "dsmoe_timing_stage_name": ([I32], ctypes.c_char_p),
+    "dsmoe_probe_dma_read": ([P, SZ, P, P], I32),
 }
 
 _lib = None

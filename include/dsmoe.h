@@ -224,6 +224,12 @@ int dsmoe_timing_enable(int on);
 int dsmoe_timing_read(double* stage_ms, int max_stages, int* n_calls);
 const char* dsmoe_timing_stage_name(int stage);
 
+/* Traffic-counter calibration for measurement tools (no counterpart in the
+ * reference): reads exactly `bytes` (a multiple of 1 MiB, 16-byte aligned
+ * src) with the direct global -> LDS loads of the grouped GEMMs, one
+ * workgroup per MiB, and writes one word per workgroup to sink. */
+int dsmoe_probe_dma_read(const void* src, size_t bytes, uint32_t* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
