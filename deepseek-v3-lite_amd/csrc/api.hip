@@ -616,9 +616,22 @@ int dsmoe_moe_bwd(const void* x, const float* gate_w, const void* const* w1, con
                   const dsmoe_dims* dims, const void* dy, const void* fwd_workspace, void* dx, float* dgate_w,
                   void* const* dw1, void* const* dw2, void* const* dw3, void* const* dsw1, void* const* dsw2,
                   void* const* dsw3, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!dims) return fail(DSMOE_ERR_INVALID, "dims is NULL");
+  return dsmoe_moe_bwd_ex(x, gate_w, w1, w2, w3, sw1, sw2, sw3, dims, dy, fwd_workspace, dx, dgate_w, dw1, dw2, dw3,
+                          dsw1, dsw2, dsw3, dims->dtype, workspace, workspace_bytes, stream);
+}
+
+int dsmoe_moe_bwd_ex(const void* x, const float* gate_w, const void* const* w1, const void* const* w2,
+                     const void* const* w3, const void* const* sw1, const void* const* sw2, const void* const* sw3,
+                     const dsmoe_dims* dims, const void* dy, const void* fwd_workspace, void* dx, float* dgate_w,
+                     void* const* dw1, void* const* dw2, void* const* dw3, void* const* dsw1, void* const* dsw2,
+                     void* const* dsw3, int dw_dtype, void* workspace, size_t workspace_bytes, void* stream) {
   int rc = validate(dims, true);
   if (rc) return rc;
   const dsmoe_dims& d = *dims;
+  DSMOE_REQUIRE(dw_dtype == d.dtype || dw_dtype == DSMOE_F32, DSMOE_ERR_UNSUPPORTED,
+                "moe_bwd: expert weight gradients are written in the compute dtype or fp32");
+  const int32_t dw_f32 = dw_dtype == DSMOE_F32 && d.dtype != DSMOE_F32;
   DSMOE_REQUIRE(x && gate_w && w1 && w2 && w3 && dy && fwd_workspace && dx && dgate_w && dw1 && dw2 && dw3,
                 DSMOE_ERR_INVALID, "moe_bwd: NULL required pointer");
   DSMOE_REQUIRE(d.S == 0 || (sw1 && sw2 && sw3 && dsw1 && dsw2 && dsw3), DSMOE_ERR_INVALID,
@@ -698,7 +711,7 @@ int dsmoe_moe_bwd(const void* x, const float* gate_w, const void* const* w1, con
   w13.sched_mode = XS_WGRAD; w13.groups = d.E; w13.k_off = F.offsets; w13.M = 2 * d.I; w13.N = d.D; w13.K = (int32_t)N;
   w13.a_mode = XA_KMAJOR; w13.A = B.dgdu; w13.lda = 2 * (int64_t)d.I;
   w13.b_mode = XB_ACT_KMAJOR; w13.Bact = F.x_sorted; w13.ldb = d.D;
-  w13.Ctab0 = B.dw1; w13.Ctab1 = B.dw3; w13.msplit = d.I; w13.ldc = d.D;
+  w13.Ctab0 = B.dw1; w13.Ctab1 = B.dw3; w13.msplit = d.I; w13.ldc = d.D; w13.c_f32 = dw_f32;
   tm.begin(ST_BWD_DW13);
   rc = launch_xgemm(w13, XE_WGRAD, d.dtype, mf, st);
   tm.end();
@@ -712,7 +725,7 @@ int dsmoe_moe_bwd(const void* x, const float* gate_w, const void* const* w1, con
     w2g.A = dy; w2g.a_map = F.sorted_token; w2g.a_kscale = F.sorted_w;
   }
   w2g.b_mode = XB_ACT_KMAJOR; w2g.Bact = F.h; w2g.ldb = d.I;
-  w2g.Ctab0 = B.dw2; w2g.Ctab1 = B.dw2; w2g.msplit = d.D; w2g.ldc = d.I;
+  w2g.Ctab0 = B.dw2; w2g.Ctab1 = B.dw2; w2g.msplit = d.D; w2g.ldc = d.I; w2g.c_f32 = dw_f32;
   tm.begin(ST_BWD_DW2);
   rc = launch_xgemm(w2g, XE_WGRAD, d.dtype, mf, st);
   tm.end();
@@ -744,13 +757,13 @@ int dsmoe_moe_bwd(const void* x, const float* gate_w, const void* const* w1, con
     s13.a_mode = XA_KMAJOR; s13.A = B.dgdu_s; s13.lda = 2 * SIs; s13.a_col = 2 * (int64_t)d.I_s;
     s13.b_mode = XB_ACT_KMAJOR; s13.Bact = x; s13.ldb = d.D;
     s13.Ctab0 = B.dsw1; s13.Ctab1 = B.dsw3; s13.msplit = d.I_s; s13.ldc = d.D;
-    s13.ksplit = B.ks13; s13.part = B.part;
+    s13.ksplit = B.ks13; s13.part = B.part; s13.c_f32 = dw_f32;
     XGemm s2 = xdesc_zero();
     s2.sched_mode = XS_WGRAD; s2.groups = d.S; s2.M = d.D; s2.N = d.I_s; s2.K = d.T;
     s2.a_mode = XA_KMAJOR; s2.A = dy; s2.lda = d.D;
     s2.b_mode = XB_ACT_KMAJOR; s2.Bact = F.hs; s2.ldb = SIs; s2.b_col = d.I_s;
     s2.Ctab0 = B.dsw2; s2.Ctab1 = B.dsw2; s2.msplit = d.D; s2.ldc = d.I_s;
-    s2.ksplit = B.ks2; s2.part = B.part;
+    s2.ksplit = B.ks2; s2.part = B.part; s2.c_f32 = dw_f32;
     tm.begin(ST_BWD_DW_SHARED);
     rc = launch_xgemm(s13, XE_WGRAD, d.dtype, mf, st);
     if (!rc) rc = launch_xgemm(s2, XE_WGRAD, d.dtype, mf, st);

@@ -300,6 +300,9 @@ struct XGemm {
   // parts in ascending i and rounds once.  ksplit <= 1: direct store.
   int32_t ksplit;
   float* part;
+  // XE_WGRAD: the output rows (Ctab0 / Ctab1) are fp32 (fp32 master weights
+  // of a bf16 computation), written unrounded; else the compute dtype.
+  int32_t c_f32;
 };
 
 // Backward grouped GEMM: MFMA kernel when dtype is bf16, allow_mfma is set

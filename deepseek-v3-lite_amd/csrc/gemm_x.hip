@@ -52,9 +52,12 @@ template <typename T, int EPI>
 __device__ __forceinline__ void x_store(const XGemm& g, int grp, int row0, int m, int n, float acc) {
   if (EPI == XE_WGRAD) {
     const int mm = row0 + m;
-    T* out = static_cast<T*>(mm < g.msplit ? g.Ctab0[grp] : g.Ctab1[grp]);
-    const int mr = mm < g.msplit ? mm : mm - g.msplit;
-    out[(int64_t)mr * g.ldc + n] = from_f<T>(acc);
+    void* base = mm < g.msplit ? g.Ctab0[grp] : g.Ctab1[grp];
+    const int64_t o = (int64_t)(mm < g.msplit ? mm : mm - g.msplit) * g.ldc + n;
+    if (g.c_f32)
+      static_cast<float*>(base)[o] = acc;
+    else
+      static_cast<T*>(base)[o] = from_f<T>(acc);
     return;
   }
   const int r = row0 + m;

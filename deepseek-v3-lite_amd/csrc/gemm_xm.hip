@@ -265,13 +265,18 @@ __global__ __launch_bounds__(XM_THREADS) void xgemm_mfma_kernel(const XGemm g) {
 
   // ---- epilogue.  Lane holds tile row m = (wm * 2 + mi) * 32 + (lane & 31)
   // and, per qq, columns n = (wn * 4 + ni) * 32 + 8 qq + 4 (lane >> 5) + {0..3}
-  // (acc registers 4 qq ..).  Split-K partials go straight out as fp32.
-  if (EPI == XE_WGRAD && g.ksplit > 1) {
+  // (acc registers 4 qq ..).  Split-K partials, and fp32 weight gradients,
+  // go straight out as fp32.
+  if (EPI == XE_WGRAD && (g.ksplit > 1 || g.c_f32)) {
 #pragma unroll
     for (int mi = 0; mi < XM_TM; ++mi) {
       const int m = (wm * XM_TM + mi) * 32 + (lane & 31);
       if (m >= rows) continue;
-      float* prow = g.part + (((int64_t)split * g.groups + grp) * g.M + row0 + m) * g.N;
+      const int r = row0 + m;
+      float* prow = g.ksplit > 1
+                        ? g.part + (((int64_t)split * g.groups + grp) * g.M + r) * g.N
+                        : static_cast<float*>(r < g.msplit ? g.Ctab0[grp] : g.Ctab1[grp]) +
+                              (int64_t)(r < g.msplit ? r : r - g.msplit) * g.ldc;
 #pragma unroll
       for (int ni = 0; ni < XM_TN; ++ni)
 #pragma unroll
@@ -380,7 +385,8 @@ __global__ __launch_bounds__(XM_THREADS) void xgemm_mfma_kernel(const XGemm g) {
 }
 
 // Adds the ksplit fp32 partials of a split-K weight gradient in ascending
-// part order and writes the bf16 result (4 columns per thread).
+// part order and writes the result, rounded to bf16 or (c_f32) as fp32 (4
+// columns per thread).
 __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const XGemm g) {
   const int64_t q4 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t per_grp = (int64_t)g.M * (g.N / 4);
@@ -399,8 +405,12 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const XGemm g) {
     s.z += v.z;
     s.w += v.w;
   }
-  bf16_t* out = static_cast<bf16_t*>(m < g.msplit ? g.Ctab0[grp] : g.Ctab1[grp]);
   const int64_t o = (int64_t)(m < g.msplit ? m : m - g.msplit) * g.ldc + n;
+  if (g.c_f32) {
+    *reinterpret_cast<float4*>(static_cast<float*>(m < g.msplit ? g.Ctab0[grp] : g.Ctab1[grp]) + o) = s;
+    return;
+  }
+  bf16_t* out = static_cast<bf16_t*>(m < g.msplit ? g.Ctab0[grp] : g.Ctab1[grp]);
   const uint32_t p0 = (uint32_t)f2bf(s.x) | ((uint32_t)f2bf(s.y) << 16);
   const uint32_t p1 = (uint32_t)f2bf(s.z) | ((uint32_t)f2bf(s.w) << 16);
   *reinterpret_cast<u32x2_t*>(out + o) = u32x2_t{p0, p1};
@@ -430,7 +440,7 @@ bool xgemm_mfma_ok(const XGemm& g, int epi) {
   // the staged epilogue writes 16-byte row pieces (XE_SWIGLU_BWD: 8-byte)
   if (epi == XE_WGRAD)
     return g.ldc % 8 == 0 && g.msplit % 4 == 0 && g.sched_mode == XS_WGRAD &&
-           (g.ksplit <= 1 || (g.part && al16(g.part)));
+           (g.ksplit <= 1 || (g.part && al16(g.part)));   // fp32 rows: ldc % 4 and 16-byte bases (caller)
   if (epi == XE_SWIGLU_BWD)
     return g.ldc % 4 == 0 && g.c_group_col % 4 == 0 && al8(g.C) && g.du_off % 4 == 0 && g.ld_gu % 4 == 0 &&
            g.gu_group_col % 4 == 0 && al8(g.Gs) && al8(g.Us);

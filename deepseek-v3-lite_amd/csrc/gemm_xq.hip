@@ -402,13 +402,18 @@ __global__ __launch_bounds__(256) void xgemm_q_kernel(const XGemm g) {
 
   // ---- epilogue.  Lane holds tile row m = (2j + wm) * 32 + (lane & 31) and,
   // per q, columns n = wn * 128 + 32 ni + 8 q + 4 (lane >> 5) + {0..3}
-  // (registers 4q .. 4q+3).  Split-K partials go straight out as fp32.
-  if (EPI == XE_WGRAD && g.ksplit > 1) {
+  // (registers 4q .. 4q+3).  Split-K partials, and fp32 weight gradients,
+  // go straight out as fp32.
+  if (EPI == XE_WGRAD && (g.ksplit > 1 || g.c_f32)) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int m = (2 * j + wm) * 32 + (lane & 31);
       if (m >= rows) continue;
-      float* prow = g.part + (((int64_t)split * g.groups + grp) * g.M + row0 + m) * g.N;
+      const int r = row0 + m;
+      float* prow = g.ksplit > 1
+                        ? g.part + (((int64_t)split * g.groups + grp) * g.M + r) * g.N
+                        : static_cast<float*>(r < g.msplit ? g.Ctab0[grp] : g.Ctab1[grp]) +
+                              (int64_t)(r < g.msplit ? r : r - g.msplit) * g.ldc;
 #pragma unroll
       for (int ni = 0; ni < 4; ++ni)
 #pragma unroll

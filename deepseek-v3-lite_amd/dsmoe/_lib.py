@@ -57,6 +57,7 @@ _SIGNATURES = {
     "dsmoe_moe_fwd_workspace_size": ([DIMS, I32], SZ),
     "dsmoe_moe_fwd": ([P, P, P, PP, PP, PP, PP, PP, PP, DIMS, I32, P, P, P, P, P, P, SZ, P], I32),
     "dsmoe_moe_bwd_workspace_size": ([DIMS], SZ),
+    "dsmoe_moe_bwd_ex": ([P, P, PP, PP, PP, PP, PP, PP, DIMS, P, P, P, P, PP, PP, PP, PP, PP, PP, I32, P, SZ, P], I32),
     "dsmoe_moe_bwd": ([P, P, PP, PP, PP, PP, PP, PP, DIMS, P, P, P, P, PP, PP, PP, PP, PP, PP, P, SZ, P], I32),
     "dsmoe_update_bias": ([P, P, I32, F32, F32, F32, P], I32),
     "dsmoe_update_bias_f32": ([P, P, I32, F32, F32, F32, P], I32),

@@ -148,15 +148,26 @@ class DeepSeekMoE(nn.Module):
             return w
         if torch.compiler.is_compiling():
             return w.to(dtype)
+        copy = self._cached_copy(w, dtype)
+        if not (torch.is_grad_enabled() and w.requires_grad):
+            return copy
+        return _CachedCast.apply(w, copy)
+
+    def _cached_copy(self, w: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+        """The detached cast copy of w, made again only when w changes."""
         key = (w._version, w.data_ptr(), dtype)
         ent = self._cast_cache.get(id(w))
         if ent is None or ent[0] != key:
             with torch.no_grad():
                 ent = (key, w.detach().to(dtype))
             self._cast_cache[id(w)] = ent
-        if not (torch.is_grad_enabled() and w.requires_grad):
-            return ent[1]
-        return _CachedCast.apply(w, ent[1])
+        return ent[1]
+
+    def _expert_params(self):
+        """Expert weight parameters in the layer operator's order."""
+        return ([e.w1.weight for e in self.experts] + [e.w2.weight for e in self.experts] +
+                [e.w3.weight for e in self.experts] + [e.w1.weight for e in self.shared_experts] +
+                [e.w2.weight for e in self.shared_experts] + [e.w3.weight for e in self.shared_experts])
 
     def _apply(self, fn, *args, **kwargs):
         # .to() / .cuda() / .half() replace parameter data: drop the cast copies
@@ -181,9 +192,23 @@ class DeepSeekMoE(nn.Module):
         shape = x.shape
         flat = x.reshape(-1, self.dim)
         cdt = _compute_dtype(flat)
-        w1, w2, w3, s1, s2, s3 = self._expert_weights(cdt)
+        params = self._expert_params()
+        masters = None
+        if (cdt == torch.bfloat16 and torch.is_grad_enabled() and not torch.compiler.is_compiling() and
+                all(p.dtype == torch.float32 and p.requires_grad for p in params)):
+            # fp32 parameters under bf16 autocast: the GEMMs read the cached
+            # bf16 copies and the backward writes fp32 gradients for the
+            # parameters themselves (no per-parameter cast nodes)
+            masters = params
+            copies = [self._cached_copy(p, cdt) for p in params]
+            E, S = self.n_routed_experts, self.n_shared_experts
+            w1, w2, w3 = copies[:E], copies[E:2 * E], copies[2 * E:3 * E]
+            s1, s2, s3 = copies[3 * E:3 * E + S], copies[3 * E + S:3 * E + 2 * S], copies[3 * E + 2 * S:]
+        else:
+            w1, w2, w3, s1, s2, s3 = self._expert_weights(cdt)
         y, idx64, wx, counts = ops.moe_layer(flat.to(cdt), _flt(self.gate.weight), _flt(self.gate.bias), w1, w2, w3,
-                                             s1, s2, s3, k=self.gate.topk, route_scale=self.gate.route_scale)
+                                             s1, s2, s3, k=self.gate.topk, route_scale=self.gate.route_scale,
+                                             master_weights=masters)
         self._last_weights = wx.detach().to(flat.dtype)
         self._last_indices = idx64.detach()
         self._last_counts = counts.detach()

@@ -186,10 +186,13 @@ def _fwd_ws_bytes(T: int, D: int, E: int, S: int, k: int, I: int, I_s: int, dtyp
 # of breaking the graph at a ctypes call, and autograd (including activation
 # checkpoint recompute) sees an ordinary differentiable op.  The forward
 # returns its workspace (routing, sorted order, pre-activations, expert
-# outputs) as a fifth output; the backward consumes it.
+# outputs) as a fifth output; the backward consumes it.  `masters`, when not
+# empty, are fp32 master copies of `weights` (a bf16 computation under
+# autocast): the forward reads only `weights`, and the expert weight
+# gradients go to the masters, written as fp32 by the backward kernels.
 @torch.library.custom_op("dsmoe::moe_fwd", mutates_args=(), device_types="cuda")
-def moe_fwd_op(x: torch.Tensor, gate_w: torch.Tensor, gate_bias: torch.Tensor, weights: List[torch.Tensor], E: int,
-               S: int, k: int, I: int, I_s: int, route_scale: float,
+def moe_fwd_op(x: torch.Tensor, gate_w: torch.Tensor, gate_bias: torch.Tensor, weights: List[torch.Tensor],
+               masters: List[torch.Tensor], E: int, S: int, k: int, I: int, I_s: int, route_scale: float,
                training: bool) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     """dsmoe_moe_fwd: returns (y, idx64, weights_x, counts int32, workspace u8)."""
     dev = x.device
@@ -212,7 +215,7 @@ def moe_fwd_op(x: torch.Tensor, gate_w: torch.Tensor, gate_bias: torch.Tensor, w
 
 
 @moe_fwd_op.register_fake
-def _moe_fwd_fake(x, gate_w, gate_bias, weights, E, S, k, I, I_s, route_scale, training):
+def _moe_fwd_fake(x, gate_w, gate_bias, weights, masters, E, S, k, I, I_s, route_scale, training):
     T, D = x.shape
     nbytes = _fwd_ws_bytes(int(T), int(D), int(E), int(S), int(k), int(I), int(I_s), x.dtype, route_scale, training)
     return (torch.empty_like(x), x.new_empty((T, k), dtype=torch.int64), x.new_empty((T, k)),
@@ -221,8 +224,10 @@ def _moe_fwd_fake(x, gate_w, gate_bias, weights, E, S, k, I, I_s, route_scale, t
 
 @torch.library.custom_op("dsmoe::moe_bwd", mutates_args=(), device_types="cuda")
 def moe_bwd_op(x: torch.Tensor, gate_w: torch.Tensor, weights: List[torch.Tensor], dy: torch.Tensor,
-               ws: torch.Tensor, E: int, S: int, k: int, I: int, I_s: int, route_scale: float) -> List[torch.Tensor]:
-    """dsmoe_moe_bwd: returns [dx, dgate_w (fp32), dW for every entry of weights]."""
+               ws: torch.Tensor, E: int, S: int, k: int, I: int, I_s: int, route_scale: float,
+               dw_f32: bool) -> List[torch.Tensor]:
+    """dsmoe_moe_bwd_ex: returns [dx, dgate_w (fp32), dW for every entry of
+    weights (fp32 with dw_f32, else the weights' dtype)]."""
     dev = x.device
     T, D = x.shape
     d = L.make_dims(T, D, E, k, I, S, I_s, x.dtype, route_scale)
@@ -230,24 +235,25 @@ def moe_bwd_op(x: torch.Tensor, gate_w: torch.Tensor, weights: List[torch.Tensor
     bws = _ws(lib.dsmoe_moe_bwd_workspace_size(d), dev)
     dx = torch.empty_like(x)
     dgw = torch.empty(E, D, dtype=torch.float32, device=dev)
-    dws = [torch.empty_like(w) for w in weights]
+    dws = [torch.empty(w.shape, dtype=torch.float32 if dw_f32 else w.dtype, device=dev) for w in weights]
     arrs = [L.ptr_array(a) for a in (*_layer_weights(weights, E, S), *_layer_weights(dws, E, S))]
-    rc = lib.dsmoe_moe_bwd(L.ptr(x), L.ptr(gate_w), *[a[0] for a in arrs[:6]], d, L.ptr(dy), L.ptr(ws),
-                           L.ptr(dx), L.ptr(dgw), *[a[0] for a in arrs[6:]], L.ptr(bws), bws.numel(),
-                           L.stream_ptr(dev))
-    L.check(rc, "dsmoe_moe_bwd")
+    rc = lib.dsmoe_moe_bwd_ex(L.ptr(x), L.ptr(gate_w), *[a[0] for a in arrs[:6]], d, L.ptr(dy), L.ptr(ws),
+                              L.ptr(dx), L.ptr(dgw), *[a[0] for a in arrs[6:]],
+                              L.DSMOE_F32 if dw_f32 else L.dtype_code(x.dtype), L.ptr(bws), bws.numel(),
+                              L.stream_ptr(dev))
+    L.check(rc, "dsmoe_moe_bwd_ex")
     return [dx, dgw, *dws]
 
 
 @moe_bwd_op.register_fake
-def _moe_bwd_fake(x, gate_w, weights, dy, ws, E, S, k, I, I_s, route_scale):
+def _moe_bwd_fake(x, gate_w, weights, dy, ws, E, S, k, I, I_s, route_scale, dw_f32):
     return [torch.empty_like(x), gate_w.new_empty((E, x.shape[1]), dtype=torch.float32),
-            *[torch.empty_like(w) for w in weights]]
+            *[w.new_empty(w.shape, dtype=torch.float32 if dw_f32 else w.dtype) for w in weights]]
 
 
 def _moe_fwd_setup(ctx, inputs, output):
-    x, gate_w, gate_bias, weights, E, S, k, I, I_s, rs, training = inputs
-    ctx.meta = (E, S, k, I, I_s, rs, training)
+    x, gate_w, gate_bias, weights, masters, E, S, k, I, I_s, rs, training = inputs
+    ctx.meta = (E, S, k, I, I_s, rs, training, len(masters))
     ctx.save_for_backward(x, gate_w, output[4], *weights)
     # only y carries a gradient; without this autograd would materialise zero
     # gradients for the other outputs, the workspace included (GBs per step)
@@ -255,14 +261,17 @@ def _moe_fwd_setup(ctx, inputs, output):
 
 
 def _moe_fwd_backward(ctx, dy, _didx, _dwx, _dcounts, _dws):
-    E, S, k, I, I_s, rs, training = ctx.meta
+    E, S, k, I, I_s, rs, training, n_masters = ctx.meta
     x, gate_w, ws, *weights = ctx.saved_tensors
+    rest = (None,) * 7
     if dy is None:
-        return None, None, None, [None] * len(weights), None, None, None, None, None, None, None
+        return (None, None, None, [None] * len(weights), [None] * n_masters) + rest
     if not training:
         raise RuntimeError("dsmoe: forward ran without saving activations for backward")
-    g = moe_bwd_op(x, gate_w, list(weights), _c(dy), ws, E, S, k, I, I_s, rs)
-    return g[0], g[1], None, list(g[2:]), None, None, None, None, None, None, None
+    g = moe_bwd_op(x, gate_w, list(weights), _c(dy), ws, E, S, k, I, I_s, rs, n_masters > 0)
+    if n_masters:
+        return (g[0], g[1], None, [None] * len(weights), list(g[2:])) + rest
+    return (g[0], g[1], None, list(g[2:]), []) + rest
 
 
 torch.library.register_autograd("dsmoe::moe_fwd", _moe_fwd_backward, setup_context=_moe_fwd_setup)
@@ -316,22 +325,35 @@ def check_layer_args(x: torch.Tensor, gate_w: torch.Tensor, gate_bias: torch.Ten
 def moe_layer(x: torch.Tensor, gate_w: torch.Tensor, gate_bias: torch.Tensor, w1: Sequence[torch.Tensor],
               w2: Sequence[torch.Tensor], w3: Sequence[torch.Tensor], sw1: Sequence[torch.Tensor] = (),
               sw2: Sequence[torch.Tensor] = (), sw3: Sequence[torch.Tensor] = (), *, k: int,
-              route_scale: float = 1.0, training: Optional[bool] = None):
+              route_scale: float = 1.0, training: Optional[bool] = None,
+              master_weights: Optional[Sequence[torch.Tensor]] = None):
     """One DeepSeekMoE layer on (T, D) tokens.  Expert weights must be in
     x.dtype, w1/w3 (inter, D) and w2 (D, inter); gate_w (E, D) and gate_bias
     (E,) are fp32 (check_layer_args raises ValueError otherwise).
+    master_weights (optional, bf16 x only): fp32 tensors of the same shapes in
+    the order [*w1, *w2, *w3, *sw1, *sw2, *sw3], of which the expert weights
+    are bf16 copies; the expert weight gradients then go to the masters, as
+    fp32 (the gradients of autocast's casts, computed without a cast pass).
     Returns (y, idx64, weights_x, counts)."""
     E, S, I, I_s = check_layer_args(x, gate_w, gate_bias, w1, w2, w3, sw1, sw2, sw3, k)
     _require_gpu(x, gate_w, gate_bias, *w1)
     weights = [*w1, *w2, *w3, *sw1, *sw2, *sw3]
+    masters = list(master_weights) if master_weights is not None else []
+    if masters:
+        if x.dtype != torch.bfloat16 or len(masters) != len(weights):
+            raise ValueError("dsmoe: master_weights need bf16 activations and one fp32 master per expert weight")
+        for m, w in zip(masters, weights):
+            if m.dtype != torch.float32 or m.shape != w.shape:
+                raise ValueError(f"dsmoe: a master weight must be float32 of its copy's shape {tuple(w.shape)}, got "
+                                 f"{m.dtype} {tuple(m.shape)}")
     needs_grad = x.requires_grad or gate_w.requires_grad
-    for w in weights:
+    for w in (*weights, *masters):
         needs_grad = needs_grad or w.requires_grad
     if training is None:
         training = torch.is_grad_enabled() and needs_grad
     ws = [_c(w) for w in weights]
-    y, idx64, wx, counts, _ = moe_fwd_op(_c(x), _c(gate_w), _c(gate_bias), ws, E, S, int(k), int(I), int(I_s),
-                                         float(route_scale), bool(training))
+    y, idx64, wx, counts, _ = moe_fwd_op(_c(x), _c(gate_w), _c(gate_bias), ws, masters, E, S, int(k), int(I),
+                                         int(I_s), float(route_scale), bool(training))
     return y, idx64, wx, counts
 
 

@@ -182,6 +182,18 @@ int dsmoe_moe_bwd(const void* x, const float* gate_w, const void* const* w1, con
                   void* const* dw1, void* const* dw2, void* const* dw3, void* const* dsw1, void* const* dsw2,
                   void* const* dsw3, void* workspace, size_t workspace_bytes, void* stream);
 
+/* The same backward with the expert weight gradients dw1..dsw3 written in
+ * dw_dtype: the compute dtype (as dsmoe_moe_bwd), or DSMOE_F32 for a bf16
+ * computation over fp32 master weights, as under the reference's bf16
+ * autocast (training/pretrain.py:212-213, whose fp32 parameters receive the
+ * casts' gradients): the fp32 accumulators are stored unrounded, with no
+ * separate cast pass. */
+int dsmoe_moe_bwd_ex(const void* x, const float* gate_w, const void* const* w1, const void* const* w2,
+                     const void* const* w3, const void* const* sw1, const void* const* sw2, const void* const* sw3,
+                     const dsmoe_dims* dims, const void* dy, const void* fwd_workspace, void* dx, float* dgate_w,
+                     void* const* dw1, void* const* dw2, void* const* dw3, void* const* dsw1, void* const* dsw2,
+                     void* const* dsw3, int dw_dtype, void* workspace, size_t workspace_bytes, void* stream);
+
 /* f1: aux-loss-free bias update on device (models/moe.py:21-27,194-201).
  * counts (E) int32 -> bias (E) fp32 updated in place by the +/-speed band rule. */
 int dsmoe_update_bias(const int32_t* counts, float* gate_bias, int E, float speed, float upper, float lower,

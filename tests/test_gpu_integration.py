@@ -3,7 +3,8 @@
 
 * bf16 autocast over fp32 parameters gives exactly the explicit bf16 layer
   (bf16-rounded weights and activations) with the output, ``_last_weights``
-  and every gradient back in fp32;
+  and every gradient back in fp32; the expert weight gradients are the same
+  fp32 accumulators unrounded (rounded to bf16 they are the bf16 layer's);
 * activation checkpointing (``use_reentrant=False``) recomputes the forward
   with identical routing, so outputs and gradients are bit-identical to the
   plain run;
@@ -52,7 +53,17 @@ def test_bf16_autocast_over_fp32_parameters():
     assert xin.grad.dtype == torch.float32 and torch.equal(xin.grad, dx16.float())
     for n, prm in m32.named_parameters():
         assert prm.grad.dtype == torch.float32, n
-        assert torch.equal(prm.grad, g16[n].float()), n
+        _same_gradient(n, prm.grad, g16[n])
+
+
+def _same_gradient(name, g32, g16):
+    """The gate gradient is fp32 in both layers (equal); an expert weight's
+    fp32 gradient is the bf16 layer's accumulator before its rounding."""
+    if name.startswith("gate."):
+        assert torch.equal(g32, g16.float()), name
+        return
+    assert torch.equal(g32.to(torch.bfloat16), g16), name
+    assert not torch.equal(g32, g16.float()), name   # unrounded (a bf16 cast pass would make them equal)
 
 
 def test_activation_checkpoint_recompute_is_identical():
@@ -127,5 +138,5 @@ def test_autocast_weight_copies_follow_optimizer_steps():
         assert torch.equal(y, y16.float()), step
         assert torch.equal(xin.grad, dx16.float()), step
         for n, prm in m32.named_parameters():
-            assert torch.equal(prm.grad, g16[n].float()), (step, n)
+            _same_gradient(f"{n} (step {step})" if not n.startswith("gate.") else n, prm.grad, g16[n])
         opt.step()

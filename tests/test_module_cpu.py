@@ -162,16 +162,18 @@ def test_layer_operator_shapes_without_a_gpu():
     ws = ([torch.empty(I, D, **m) for _ in range(E)] + [torch.empty(D, I, **m) for _ in range(E)] +
           [torch.empty(I, D, **m) for _ in range(E)] +
           [torch.empty(I_s, D, **m), torch.empty(D, I_s, **m), torch.empty(I_s, D, **m)])
-    y, idx, wx, counts, work = torch.ops.dsmoe.moe_fwd(x, gw, gb, ws, E, S, k, I, I_s, 1.0, True)
+    y, idx, wx, counts, work = torch.ops.dsmoe.moe_fwd(x, gw, gb, ws, [], E, S, k, I, I_s, 1.0, True)
     assert y.shape == (T, D) and y.dtype == torch.bfloat16
     assert idx.shape == (T, k) and idx.dtype == torch.int64
     assert wx.shape == (T, k) and wx.dtype == torch.bfloat16
     assert counts.shape == (E,) and counts.dtype == torch.int32
     assert work.dtype == torch.uint8 and work.numel() >= 256
-    g = torch.ops.dsmoe.moe_bwd(x, gw, ws, y, work, E, S, k, I, I_s, 1.0)
-    assert len(g) == 2 + len(ws)
-    assert g[0].shape == (T, D) and g[1].shape == (E, D) and g[1].dtype == torch.float32
-    assert all(a.shape == w.shape and a.dtype == w.dtype for a, w in zip(g[2:], ws))
+    for dw_f32 in (False, True):   # weight gradients in the weights' dtype, or fp32 for fp32 masters
+        g = torch.ops.dsmoe.moe_bwd(x, gw, ws, y, work, E, S, k, I, I_s, 1.0, dw_f32)
+        assert len(g) == 2 + len(ws)
+        assert g[0].shape == (T, D) and g[1].shape == (E, D) and g[1].dtype == torch.float32
+        want = torch.float32 if dw_f32 else torch.bfloat16
+        assert all(a.shape == w.shape and a.dtype == want for a, w in zip(g[2:], ws))
 
 
 def _layer_args(D=16, E=4, I=8, S=1, I_s=8, dt=torch.bfloat16):
