@@ -352,6 +352,7 @@ class XGemm:
     Ctab1: Optional[List[Buf]] = None
     msplit: int = 0
     part: Optional[Buf] = None
+    c_f32: bool = False       # XE_WGRAD output rows are fp32
     swiglu_bwd: bool = False
     Gs: Optional[Buf] = None
     Us: Optional[Buf] = None
@@ -457,7 +458,8 @@ def xq_tile(rec: Recorder, g: XGemm, grp, row0, rows, n_tile, kbeg, kend, split,
                 off = krow * g.ldb + grp * g.b_col + col
                 rec.touch(g.Bact, 2 * off[live], 2 * off[live] + 16, what + " B act")
     # epilogue
-    if g.mode == XS_WGRAD and g.ksplit > 1:
+    if g.mode == XS_WGRAD and (g.ksplit > 1 or g.c_f32):
+        # register-direct float4 stores: split-K partials, or fp32 gradient rows
         j = np.arange(4)[:, None, None, None]
         wm = (np.arange(4) >> 1)[None, :, None, None]
         wn = (np.arange(4) & 1)[None, :, None, None]
@@ -465,10 +467,20 @@ def xq_tile(rec: Recorder, g: XGemm, grp, row0, rows, n_tile, kbeg, kend, split,
         m = (2 * j + wm) * 32 + (ln & 31)
         nq = np.arange(16)[None, None, None, :]            # ni * 4 + q
         n = n0 + wn * 128 + (nq >> 2) * 32 + (nq & 3) * 8 + (ln >> 5) * 4
-        ok = (m < rows) & (n < g.N)
-        off = 4 * ((((split * g.groups + grp) * g.M + row0 + m) * g.N) + n)
-        rec.touch(g.part, off[np.broadcast_to(ok, off.shape)], off[np.broadcast_to(ok, off.shape)] + 16,
-                  what + " part")
+        ok = np.broadcast_to((m < rows) & (n < g.N), np.broadcast_shapes(m.shape, n.shape))
+        if g.ksplit > 1:
+            off = 4 * ((((split * g.groups + grp) * g.M + row0 + m) * g.N) + n)
+            off = np.broadcast_to(off, ok.shape)
+            rec.touch(g.part, off[ok], off[ok] + 16, what + " part")
+            return
+        r = np.broadcast_to(row0 + m, ok.shape)
+        nn = np.broadcast_to(n, ok.shape)
+        lo = r < g.msplit
+        for sel, tab, rel in ((ok & lo, g.Ctab0, r), (ok & ~lo, g.Ctab1, r - g.msplit)):
+            if sel.any():
+                buf = rec.index(np.array(tab, dtype=object), grp, what + " Ctab")
+                off = 4 * (rel[sel] * g.ldc + nn[sel])
+                rec.touch(buf, off, off + 16, what + " C fp32")
         return
     rr = row0 + np.arange(rows)
     if g.mode == XS_WGRAD:

@@ -88,14 +88,16 @@ def _forward(rec, T, D, E, k, I, S, I_s, training, counts, sorted_token, sorted_
     return launched
 
 
-def _backward(rec, T, D, E, k, I, S, I_s, counts, sorted_token, sorted_slot, offsets):
-    """dsmoe_moe_bwd's backward GEMMs that take xgemm_q_kernel (csrc/api.hip)."""
+def _backward(rec, T, D, E, k, I, S, I_s, counts, sorted_token, sorted_slot, offsets, dw_f32=False):
+    """dsmoe_moe_bwd's backward GEMMs that take xgemm_q_kernel (csrc/api.hip);
+    dw_f32: dsmoe_moe_bwd_ex with fp32 weight gradients (4-byte dW buffers)."""
     N = T * k
+    we = 4 if dw_f32 else 2
     dy = M.Buf("dy", T * D * 2)
     x = M.Buf("x", T * D * 2)
     w1, w3, w2 = _bufs("w1", E, I * D * 2), _bufs("w3", E, I * D * 2), _bufs("w2", E, D * I * 2)
     w13 = [b for e in range(E) for b in (w1[e], w3[e])]
-    dw1, dw3, dw2 = _bufs("dw1", E, I * D * 2), _bufs("dw3", E, I * D * 2), _bufs("dw2", E, D * I * 2)
+    dw1, dw3, dw2 = _bufs("dw1", E, I * D * we), _bufs("dw3", E, I * D * we), _bufs("dw2", E, D * I * we)
     g_, u_, h = M.Buf("g", N * I * 2), M.Buf("u", N * I * 2), M.Buf("h", N * I * 2)
     x_sorted = M.Buf("x_sorted", N * D * 2)
     dgdu = M.Buf("dgdu", N * 2 * I * 2)
@@ -109,14 +111,16 @@ def _backward(rec, T, D, E, k, I, S, I_s, counts, sorted_token, sorted_slot, off
         ("dx", M.XGemm(mode=M.XS_ROUTED, M=0, N=D, K=2 * I, a_km=False, A=dgdu, lda=2 * I, b_weights=True,
                        Btab=w13, ldb=D, kseg=I, nseg=2, sched=sched, C=dx_slots, ldc=D, c_map=sorted_slot)),
         ("dW13", M.XGemm(mode=M.XS_WGRAD, M=2 * I, N=D, K=N, a_km=True, A=dgdu, lda=2 * I, b_weights=False,
-                         Bact=x_sorted, ldb=D, groups=E, k_off=offsets, Ctab0=dw1, Ctab1=dw3, msplit=I, ldc=D)),
+                         Bact=x_sorted, ldb=D, groups=E, k_off=offsets, Ctab0=dw1, Ctab1=dw3, msplit=I, ldc=D,
+                         c_f32=dw_f32)),
         ("dW2", M.XGemm(mode=M.XS_WGRAD, M=D, N=I, K=N, a_km=True, A=dy_w, lda=D, b_weights=False, Bact=h, ldb=I,
-                        groups=E, k_off=offsets, Ctab0=dw2, Ctab1=dw2, msplit=D, ldc=I)),
+                        groups=E, k_off=offsets, Ctab0=dw2, Ctab1=dw2, msplit=D, ldc=I, c_f32=dw_f32)),
     ]
     if S:
         SIs = S * I_s
         sw1, sw3, sw2 = _bufs("sw1", S, I_s * D * 2), _bufs("sw3", S, I_s * D * 2), _bufs("sw2", S, D * I_s * 2)
-        dsw1, dsw3, dsw2 = _bufs("dsw1", S, I_s * D * 2), _bufs("dsw3", S, I_s * D * 2), _bufs("dsw2", S, D * I_s * 2)
+        dsw1, dsw3, dsw2 = (_bufs("dsw1", S, I_s * D * we), _bufs("dsw3", S, I_s * D * we),
+                            _bufs("dsw2", S, D * I_s * we))
         gs_, us_, hs = M.Buf("gs", T * SIs * 2), M.Buf("us", T * SIs * 2), M.Buf("hs", T * SIs * 2)
         dgdu_s = M.Buf("dgdu_s", T * 2 * SIs * 2)
         ks13 = M.xgemm_pick_ksplit(M.xgemm_tiles(2 * I_s, D, S), T)
@@ -128,10 +132,10 @@ def _backward(rec, T, D, E, k, I, S, I_s, counts, sorted_token, sorted_slot, off
                              du_off=I_s, swiglu_bwd=True, Gs=gs_, Us=us_, ld_gu=SIs, gu_group_col=I_s)),
             ("dW13_s", M.XGemm(mode=M.XS_WGRAD, M=2 * I_s, N=D, K=T, a_km=True, A=dgdu_s, lda=2 * SIs,
                                a_col=2 * I_s, b_weights=False, Bact=x, ldb=D, groups=S, Ctab0=dsw1, Ctab1=dsw3,
-                               msplit=I_s, ldc=D, ksplit=ks13, part=part)),
+                               msplit=I_s, ldc=D, ksplit=ks13, part=part, c_f32=dw_f32)),
             ("dW2_s", M.XGemm(mode=M.XS_WGRAD, M=D, N=I_s, K=T, a_km=True, A=dy, lda=D, b_weights=False, Bact=hs,
                               ldb=SIs, b_col=I_s, groups=S, Ctab0=dsw2, Ctab1=dsw2, msplit=D, ldc=I_s,
-                              ksplit=ks2, part=part)),
+                              ksplit=ks2, part=part, c_f32=dw_f32)),
         ]
         if S <= 1:   # the shared dx sums 2S K segments; the quad-wave kernel takes two
             gemms.append(("dx_s", M.XGemm(mode=M.XS_DENSE, M=0, N=D, K=2 * SIs, a_km=False, A=dgdu_s, lda=2 * SIs,
@@ -175,11 +179,14 @@ def test_forward_gemm_addresses_in_bounds(name, training):
 
 
 @pytest.mark.parametrize("name", ["c0_bf16", "c1", "c2_skew", "c3", "c4", "ragged_empty", "wide_e256", "one_token"])
-def test_backward_gemm_addresses_in_bounds(name):
+@pytest.mark.parametrize("dw_f32", [False, True])
+def test_backward_gemm_addresses_in_bounds(name, dw_f32):
     T, D, E, k, I, S, I_s, kw = CONFIGS[name]
     counts, st, ss, off = _routing(T, E, k, seed=T + E + 1, **kw)
     rec = M.Recorder()
-    assert _backward(rec, T, D, E, k, I, S, I_s, counts, st, ss, off) > 0
+    assert _backward(rec, T, D, E, k, I, S, I_s, counts, st, ss, off, dw_f32=dw_f32) > 0
+    if dw_f32:   # every fp32 gradient row is written to its last byte
+        assert rec.ext["dw1[0]"][1] == I * D * 4 and rec.ext["dw2[0]"][1] == D * I * 4
 
 
 def test_model_catches_a_slab_overrun():
