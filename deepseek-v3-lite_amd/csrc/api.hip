@@ -526,7 +526,8 @@ struct BwdLayout {
   const void** sw1;
   const void** sw3;
   const void** sw2;
-  const void** sw13;  // [sw1_0, sw3_0, sw1_1, sw3_1, ...]: one group, 2S segments
+  const void** sw13;  // [sw1_0, sw3_0, sw1_1, sw3_1, ...]: one group, 2S segments, or the stack below
+  void* sw13_stack;   // bf16, S > 1: the 2S blocks copied into one (2 S I_s, D) matrix (one K segment)
   void** dw1;
   void** dw3;
   void** dw2;
@@ -582,6 +583,9 @@ static BwdLayout bwd_layout(const dsmoe_dims& d, void* base) {
   B.dx_slots = c.take<char>((size_t)N * d.D * es);
   B.dgdu_s = d.S ? c.take<char>((size_t)d.T * 2 * d.S * d.I_s * es) : nullptr;
   B.dx_shared = d.S ? c.take<char>((size_t)d.T * d.D * es) : nullptr;
+  // the shared dx GEMM sums 2S K segments; the quad-wave kernel takes two, so
+  // for S > 1 the shared W1 / W3 blocks are first copied into one matrix
+  B.sw13_stack = (d.S > 1 && d.dtype == DSMOE_BF16) ? c.take<char>((size_t)2 * d.S * d.I_s * d.D * es) : nullptr;
   // w * dY gathered in sorted order, for bf16 rows of whole 16-byte chunks;
   // other widths read dY through the row map with the weight as a k scale
   B.dy_w = (d.dtype == DSMOE_BF16 && d.D % 8 == 0) ? c.take<char>((size_t)N * d.D * es) : nullptr;
@@ -654,6 +658,7 @@ int dsmoe_moe_bwd_ex(const void* x, const float* gate_w, const void* const* w1, 
     sw13h[2 * s] = sw1[s];
     sw13h[2 * s + 1] = sw3[s];
   }
+  if (B.sw13_stack) sw13h[0] = B.sw13_stack;   // one segment: the stacked copy
   // MFMA backward GEMMs need every weight and weight-gradient pointer 16-byte aligned
   const bool mf = all_aligned16(w1, d.E) && all_aligned16(w2, d.E) && all_aligned16(w3, d.E) &&
                   all_aligned16((const void* const*)dw1, d.E) && all_aligned16((const void* const*)dw2, d.E) &&
@@ -749,7 +754,17 @@ int dsmoe_moe_bwd_ex(const void* x, const float* gate_w, const void* const* w1, 
     sx.b_mode = XB_W_NN; sx.Btab = B.sw13; sx.ldb = d.D; sx.kseg = d.I_s; sx.nseg = 2 * d.S;
     sx.C = B.dx_shared; sx.ldc = d.D;
     tm.begin(ST_BWD_DX_SHARED);
-    rc = launch_xgemm(sx, XE_STORE, d.dtype, mf, st);
+    if (B.sw13_stack) {
+      const size_t blk = (size_t)d.I_s * d.D * elem_size(d.dtype);
+      for (int s = 0; s < d.S && !rc; ++s)
+        for (int h = 0; h < 2 && !rc; ++h)
+          if (hipMemcpyAsync(static_cast<char*>(B.sw13_stack) + (2 * s + h) * blk, h ? sw3[s] : sw1[s], blk,
+                             hipMemcpyDeviceToDevice, st) != hipSuccess)
+            rc = fail(DSMOE_ERR_HIP, "moe_bwd: shared weight stack copy failed");
+      sx.kseg = (int32_t)(2 * SIs);
+      sx.nseg = 1;
+    }
+    if (!rc) rc = launch_xgemm(sx, XE_STORE, d.dtype, mf, st);
     tm.end();
     if (rc) return rc;
     XGemm s13 = xdesc_zero();

@@ -137,11 +137,14 @@ def _backward(rec, T, D, E, k, I, S, I_s, counts, sorted_token, sorted_slot, off
                               ldb=SIs, b_col=I_s, groups=S, Ctab0=dsw2, Ctab1=dsw2, msplit=D, ldc=I_s,
                               ksplit=ks2, part=part, c_f32=dw_f32)),
         ]
-        if S <= 1:   # the shared dx sums 2S K segments; the quad-wave kernel takes two
-            gemms.append(("dx_s", M.XGemm(mode=M.XS_DENSE, M=0, N=D, K=2 * SIs, a_km=False, A=dgdu_s, lda=2 * SIs,
-                                          b_weights=True, Btab=[b for s in range(S) for b in (sw1[s], sw3[s])],
-                                          ldb=D, kseg=I_s, nseg=2 * S, dense_rows=T, groups=1,
-                                          C=M.Buf("dx_shared", T * D * 2), ldc=D)))
+        # the shared dx sums 2S K segments: two as they are, more through
+        # the stacked copy of the W1 / W3 blocks (one segment)
+        tab = ([b for s in range(S) for b in (sw1[s], sw3[s])] if S <= 1
+               else [M.Buf("sw13_stack", 2 * SIs * D * 2)])
+        gemms.append(("dx_s", M.XGemm(mode=M.XS_DENSE, M=0, N=D, K=2 * SIs, a_km=False, A=dgdu_s, lda=2 * SIs,
+                                      b_weights=True, Btab=tab, ldb=D, kseg=I_s if S <= 1 else 2 * SIs,
+                                      nseg=2 * S if S <= 1 else 1, dense_rows=T, groups=1,
+                                      C=M.Buf("dx_shared", T * D * 2), ldc=D)))
     n = 0
     for name, g in gemms:
         if M.xq_ok(g):
