@@ -171,7 +171,10 @@ def sched_bound(rows: int, groups: int, bm: int) -> int:
     return rows // bm + groups + 1
 
 
-# ---------------------------------------------------------------- gemm_qw (forward quad-wave kernel)
+# ---------------------------------------------------------------- gemm_qw (forward ping-pong kernel)
+# Loading wave w (0..3) of group 0 loads A rows, wave w of group 1 the same B
+# rows; slabs 0 .. nk - 1 (the model also covers the clamped reloads of the
+# last slab, a superset).
 QW_BM, QW_BK, QW_LD = 256, 64, 8
 
 
@@ -187,7 +190,7 @@ def qw_tile(rec: Recorder, g: Gemm, swiglu: bool, grp: int, row0: int, rows: int
     BN = 128 if swiglu else 256
     n0 = n_tile * BN
     nk = g.K // QW_BK
-    wave = np.arange(4)[:, None, None]
+    wave = np.arange(4)[:, None, None]          # wave in its loading group
     lane = np.arange(64)[None, :, None]
     i = np.arange(QW_LD)[None, None, :]
     r = (wave * QW_LD + i) * 8 + (lane >> 3)
