@@ -314,6 +314,36 @@ def autocast_bench(dev, steps: int, warmup: int, ref_fwd_ms: float, ref_fwd_bwd_
     return out
 
 
+def blas_dense_reference(dev, cfg, steps: int = 30, warmup: int = 10):
+    """The vendor library on the dense problems of the config's grouped GEMMs:
+    torch.matmul (hipBLASLt) of bf16 NT products with all T*k routed rows as one
+    matrix, gate/up (N = 2 I, K = D) and down (N = D, K = I).  Not the MoE
+    layer: a reference point for the grouped GEMMs' fraction of peak at these
+    shapes (no gather, no ragged tiles, no epilogue)."""
+    import torch
+    T, D, E, I, k, S, I_s, dt, _ = cfg
+    N = T * k
+    out = {}
+    for name, (m, n, kk) in (("gate_up", (N, 2 * I, D)), ("down", (N, D, I))):
+        a = torch.randn(m, kk, device=dev, dtype=torch.bfloat16)
+        b = torch.randn(n, kk, device=dev, dtype=torch.bfloat16)
+        for _ in range(warmup):
+            c = a @ b.t()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            c = a @ b.t()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        tf = 2.0 * m * n * kk / (ms * 1e-3) / 1e12
+        out[name] = {"M": m, "N": n, "K": kk, "ms": ms, "TFLOP/s": tf, "frac_mfma": tf / PEAK_BF16_TFLOPS}
+        del a, b, c
+    log("[bench] hipBLASLt dense reference: " + ", ".join(f"{k_} {v['TFLOP/s']:.0f} TFLOP/s" for k_, v in out.items()))
+    return out
+
+
 def torch_sync():
     import torch
     torch.cuda.synchronize()
@@ -471,6 +501,7 @@ def main() -> int:
         result["decode"] = decode_bench(dev, max(10, args.steps), max(3, args.warmup))
     if not args.no_extra_configs and args.config == "c3":
         result["configs_fwd"] = {c: fwd_bench(c, dev, args.steps, args.warmup) for c in ("c1", "c2")}
+        result["blas_dense_reference"] = blas_dense_reference(dev, cfg)
     if not args.no_cpu_baseline:
         log("[bench] timing the CPU restatement of the reference path ...")
         result["cpu_baseline"] = cpu_baseline(cfg, x, gate_w, bias, weights)

@@ -100,7 +100,7 @@ struct FwdLayout {
   void* hs;
   void* gs;
   void* us;
-  void* o_slots;
+  void* o_sorted;   // routed expert outputs (N, D) in sorted order
   void* shared_out;
   void* x_sorted;   // training: routed rows of x in sorted order (the backward's K-major operand)
   size_t total;
@@ -129,7 +129,7 @@ static FwdLayout fwd_layout(const dsmoe_dims& d, int training, void* base) {
   L.hs = d.S ? c.take<char>((size_t)d.T * SIs * es) : nullptr;
   L.gs = (d.S && training) ? c.take<char>((size_t)d.T * SIs * es) : nullptr;
   L.us = (d.S && training) ? c.take<char>((size_t)d.T * SIs * es) : nullptr;
-  L.o_slots = c.take<char>((size_t)N * d.D * es);
+  L.o_sorted = c.take<char>((size_t)N * d.D * es);
   L.shared_out = d.S ? c.take<char>((size_t)d.T * d.D * es) : nullptr;
   L.x_sorted = training ? c.take<char>((size_t)N * d.D * es) : nullptr;
   L.total = c.used();
@@ -372,7 +372,7 @@ int dsmoe_combine_fwd(const void* o_slots, const float* weights, const int32_t* 
   int rc = validate(dims, false);
   if (rc) return rc;
   DSMOE_REQUIRE(o_slots && weights && idx && y, DSMOE_ERR_INVALID, "combine: NULL required pointer");
-  return launch_combine(o_slots, weights, idx, shared, *dims, y, static_cast<hipStream_t>(stream));
+  return launch_combine(o_slots, nullptr, weights, idx, shared, *dims, y, static_cast<hipStream_t>(stream));
 }
 
 size_t dsmoe_moe_fwd_workspace_size(const dsmoe_dims* dims, int training) {
@@ -439,7 +439,9 @@ int dsmoe_moe_fwd(const void* x, const float* gate_w, const float* gate_bias, co
   g1.N = d.I; g1.K = d.D; g1.C = L.h; g1.ldc = d.I; g1.Gs = L.g; g1.Us = L.u;
   GemmDesc g2 = desc_zero();
   g2.A = L.h; g2.lda = d.I; g2.a_rows = N; g2.B0 = L.ptrs + 2 * d.E; g2.ldb = d.I; g2.kseg = d.I;
-  g2.N = d.D; g2.K = d.I; g2.C = L.o_slots; g2.ldc = d.D; g2.c_map = L.sorted_slot;
+  // expert outputs stay in sorted order (rows written whole, in order); the
+  // combine and the backward read slot s at row slot_pos[s]
+  g2.N = d.D; g2.K = d.I; g2.C = L.o_sorted; g2.ldc = d.D;
   const bool mfr = gemm_mfma_eligible(g1, d.dtype, mf) && gemm_mfma_eligible(g2, d.dtype, mf);
   // Decode shapes (at most SK_MAX_T tokens, inference): every routed and
   // shared row tile fits the few-row kernel, which streams the weights once.
@@ -479,7 +481,7 @@ int dsmoe_moe_fwd(const void* x, const float* gate_w, const float* gate_bias, co
   g1.bm = g2.bm = bm;
   // (c) gate/up + SwiGLU: routed rows gathered from x through sorted_token,
   // and the shared experts as S dense groups over all tokens (h_shared =
-  // [h_0 | h_1 | ...]), in one launch when the quad-wave kernel takes both
+  // [h_0 | h_1 | ...]), in one launch when the persistent kernel takes both
   GemmDesc s1 = desc_zero(), s2 = desc_zero();
   if (d.S) {
     s1.dense_rows = d.T; s1.groups = d.S;
@@ -511,7 +513,7 @@ int dsmoe_moe_fwd(const void* x, const float* gate_w, const float* gate_bias, co
   if (rc) return rc;
   // (d) combine
   tm.begin(ST_COMBINE);
-  rc = launch_combine(L.o_slots, L.w, L.idx, L.shared_out, d, y, st);
+  rc = launch_combine(L.o_sorted, L.slot_pos, L.w, L.idx, L.shared_out, d, y, st);
   tm.end();
   tm.call_done(0);
   return rc;
@@ -677,9 +679,9 @@ int dsmoe_moe_bwd_ex(const void* x, const float* gate_w, const void* const* w1, 
                         B.w1, st);
   if (rc) return rc;
   // gate gradient path: d weights -> d logits
-  rc = launch_prep_tok(dy, F.o_slots, F.w, F.slot_pos, d.T, d.k, d.D, d.dtype, B.dw, B.dy_w, st);
+  rc = launch_prep_tok(dy, F.o_sorted, F.slot_pos, F.w, F.slot_pos, d.T, d.k, d.D, d.dtype, B.dw, B.dy_w, st);
   if (rc == DSMOE_ERR_UNSUPPORTED) {
-    rc = launch_dw_dot(dy, F.o_slots, N, d.k, d.D, d.dtype, B.dw, st);
+    rc = launch_dw_dot(dy, F.o_sorted, F.slot_pos, N, d.k, d.D, d.dtype, B.dw, st);
     if (!rc && B.dy_w) rc = launch_scale_gather_rows(dy, F.sorted_token, F.sorted_w, N, d.D, B.dy_w, st);
   }
   if (!rc) rc = launch_gate_bwd(B.dw, F.sel, d.T, d.k, d.route_scale, B.dlog, st);

@@ -17,15 +17,18 @@
 
 namespace dsmoe {
 
+// Slot s's expert output is row row_of[s] of o (the layer keeps them in
+// expert-sorted order, row_of = slot_pos) or row s (row_of null).
 template <typename T>
-__global__ __launch_bounds__(256) void dw_dot_kernel(const T* __restrict__ dy, const T* __restrict__ o_slots, int64_t N,
-                                                     int k, int D, float* __restrict__ dw) {
+__global__ __launch_bounds__(256) void dw_dot_kernel(const T* __restrict__ dy, const T* __restrict__ o_slots,
+                                                     const int32_t* __restrict__ row_of, int64_t N, int k, int D,
+                                                     float* __restrict__ dw) {
   const int lane = threadIdx.x & 63;
   const int64_t s = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (s >= N) return;
   const int64_t t = s / k;
   const T* a = dy + t * D;
-  const T* b = o_slots + s * D;
+  const T* b = o_slots + (row_of ? (int64_t)row_of[s] : s) * D;
   float acc = 0.0f;
   for (int d = lane; d < D; d += 64) acc = fmaf(to_f<T>(a[d]), to_f<T>(b[d]), acc);
 #pragma unroll
@@ -258,11 +261,15 @@ __global__ __launch_bounds__(256) void dwgate_vec_kernel(const T* __restrict__ x
 // k dot products with the token's slot rows accumulate together.
 template <int KB>
 __global__ __launch_bounds__(256) void dw_dot_tok_kernel(const bf16_t* __restrict__ dy, const bf16_t* __restrict__ o_slots,
-                                                         int T, int k, int D, float* __restrict__ dw) {
+                                                         const int32_t* __restrict__ row_of, int T, int k, int D,
+                                                         float* __restrict__ dw) {
   const int lane = threadIdx.x & 63;
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
   const int vpr = D / 8;
+  int64_t orow[KB];
+#pragma unroll
+  for (int j = 0; j < KB; ++j) orow[j] = j < k ? (row_of ? (int64_t)row_of[t * k + j] : t * k + j) : 0;
   const uint4* a = reinterpret_cast<const uint4*>(dy + t * D);
   float acc[KB];
 #pragma unroll
@@ -273,7 +280,7 @@ __global__ __launch_bounds__(256) void dw_dot_tok_kernel(const bf16_t* __restric
     float bv[KB][8];
 #pragma unroll
     for (int j = 0; j < KB; ++j)
-      if (j < k) Vec16<bf16_t>::load(o_slots + (t * k + j) * D + c * 8, bv[j]);
+      if (j < k) Vec16<bf16_t>::load(o_slots + orow[j] * D + c * 8, bv[j]);
 #pragma unroll
     for (int j = 0; j < KB; ++j) {
       if (j >= k) break;
@@ -297,7 +304,7 @@ __global__ __launch_bounds__(256) void dw_dot_tok_kernel(const bf16_t* __restric
 // bf16(w[t k + j] * dY_t) (scale_gather_kernel's rounding).
 template <int KB>
 __global__ __launch_bounds__(256) void prep_tok_kernel(const bf16_t* __restrict__ dy, const bf16_t* __restrict__ o_slots,
-                                                       const float* __restrict__ w,
+                                                       const int32_t* __restrict__ row_of, const float* __restrict__ w,
                                                        const int32_t* __restrict__ slot_pos, int T, int k, int D,
                                                        float* __restrict__ dw, bf16_t* __restrict__ dy_w) {
   const int lane = threadIdx.x & 63;
@@ -305,14 +312,16 @@ __global__ __launch_bounds__(256) void prep_tok_kernel(const bf16_t* __restrict_
   if (t >= T) return;
   const int vpr = D / 8;
   float ws[KB];
-  int64_t pos[KB];
+  int64_t pos[KB], orow[KB];
 #pragma unroll
   for (int j = 0; j < KB; ++j) {
     ws[j] = 0.0f;
     pos[j] = 0;
+    orow[j] = 0;
     if (j < k) {
       ws[j] = w[t * k + j];
       pos[j] = slot_pos[t * k + j];
+      orow[j] = row_of ? (int64_t)row_of[t * k + j] : t * k + j;
     }
   }
   float acc[KB];
@@ -324,7 +333,7 @@ __global__ __launch_bounds__(256) void prep_tok_kernel(const bf16_t* __restrict_
     float bv[KB][8];
 #pragma unroll
     for (int j = 0; j < KB; ++j)
-      if (j < k) Vec16<bf16_t>::load(o_slots + (t * k + j) * D + c * 8, bv[j]);
+      if (j < k) Vec16<bf16_t>::load(o_slots + orow[j] * D + c * 8, bv[j]);
 #pragma unroll
     for (int j = 0; j < KB; ++j) {
       if (j >= k) break;
@@ -348,13 +357,14 @@ __global__ __launch_bounds__(256) void prep_tok_kernel(const bf16_t* __restrict_
 
 static bool al16p(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-int launch_prep_tok(const void* dy, const void* o_slots, const float* w, const int32_t* slot_pos, int T, int k, int D,
-                    int dtype, float* dw, void* dy_w, hipStream_t st) {
+int launch_prep_tok(const void* dy, const void* o_slots, const int32_t* row_of, const float* w, const int32_t* slot_pos,
+                    int T, int k, int D, int dtype, float* dw, void* dy_w, hipStream_t st) {
   if (!(dtype == DSMOE_BF16 && D % 8 == 0 && k <= 8 && dy_w && al16p(dy) && al16p(o_slots) && al16p(dy_w)))
     return DSMOE_ERR_UNSUPPORTED;
   if (T == 0) return DSMOE_OK;
   hipLaunchKernelGGL(prep_tok_kernel<8>, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, st, static_cast<const bf16_t*>(dy),
-                     static_cast<const bf16_t*>(o_slots), w, slot_pos, T, k, D, dw, static_cast<bf16_t*>(dy_w));
+                     static_cast<const bf16_t*>(o_slots), row_of, w, slot_pos, T, k, D, dw,
+                     static_cast<bf16_t*>(dy_w));
   return check_launch("prep_tok");
 }
 
@@ -392,22 +402,22 @@ int launch_scale_gather_rows(const void* src, const int32_t* rows, const float* 
   return check_launch("scale_gather");
 }
 
-int launch_dw_dot(const void* dy, const void* o_slots, int64_t N, int k, int D, int dtype, float* dw,
-                  hipStream_t st) {
+int launch_dw_dot(const void* dy, const void* o_slots, const int32_t* row_of, int64_t N, int k, int D, int dtype,
+                  float* dw, hipStream_t st) {
   if (N == 0) return DSMOE_OK;
   const unsigned grid = (unsigned)cdiv(N, 4);
   if (dtype == DSMOE_BF16 && D % 8 == 0 && al16p(dy) && al16p(o_slots) && k <= 8) {
     const int T = (int)(N / k);
     hipLaunchKernelGGL(dw_dot_tok_kernel<8>, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, st,
-                       static_cast<const bf16_t*>(dy), static_cast<const bf16_t*>(o_slots), T, k, D, dw);
+                       static_cast<const bf16_t*>(dy), static_cast<const bf16_t*>(o_slots), row_of, T, k, D, dw);
     return check_launch("dw_dot");
   }
   if (dtype == DSMOE_BF16)
     hipLaunchKernelGGL(dw_dot_kernel<bf16_t>, dim3(grid), dim3(256), 0, st, static_cast<const bf16_t*>(dy),
-                       static_cast<const bf16_t*>(o_slots), N, k, D, dw);
+                       static_cast<const bf16_t*>(o_slots), row_of, N, k, D, dw);
   else
     hipLaunchKernelGGL(dw_dot_kernel<float>, dim3(grid), dim3(256), 0, st, static_cast<const float*>(dy),
-                       static_cast<const float*>(o_slots), N, k, D, dw);
+                       static_cast<const float*>(o_slots), row_of, N, k, D, dw);
   return check_launch("dw_dot");
 }
 

@@ -58,16 +58,19 @@ __device__ __forceinline__ void order_by_expert(const int32_t* idx_row, int k, i
 }
 
 // One block per token.  Threads j < k put slot j at its ascending-expert
-// position q (stable for equal ids) with its weight, in LDS; then each thread
-// takes VEC-wide column chunks c, c + blockDim, ... and issues the loads of the
-// token's k rows before the fp32 accumulation in q order.
+// position q (stable for equal ids) with its weight and the row of o that
+// holds it, in LDS; then each thread takes VEC-wide column chunks c,
+// c + blockDim, ... and issues the loads of the token's k rows before the fp32
+// accumulation in q order.  Slot s's output is row row_of[s] of o (the layer
+// keeps them in expert-sorted order, row_of = slot_pos) or row s (row_of null).
 template <typename T, int VEC, int KB>
-__global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ o_slots, const float* __restrict__ w,
-                                                      const int32_t* __restrict__ idx, const T* __restrict__ shared,
-                                                      int T_, int D, int k, T* __restrict__ y) {
+__global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ o_slots, const int32_t* __restrict__ row_of,
+                                                      const float* __restrict__ w, const int32_t* __restrict__ idx,
+                                                      const T* __restrict__ shared, int T_, int D, int k,
+                                                      T* __restrict__ y) {
   using V = Vec<T, VEC>;
   using VT = typename V::type;
-  __shared__ int ord_s[KB];
+  __shared__ int row_s[KB];
   __shared__ float w_s[KB];
   const int64_t t = blockIdx.x;
   if ((int)threadIdx.x < k) {
@@ -78,7 +81,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ o_sl
       const int ee = idx[t * k + jj];
       q += (ee < e) || (ee == e && jj < j);
     }
-    ord_s[q] = j;
+    row_s[q] = row_of ? row_of[t * k + j] : (int)(t * k + j);
     w_s[q] = w[t * k + j];
   }
   __syncthreads();
@@ -87,7 +90,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ o_sl
     VT ov[KB];
 #pragma unroll
     for (int q = 0; q < KB; ++q)
-      if (q < k) ov[q] = reinterpret_cast<const VT*>(o_slots + (t * k + ord_s[q]) * (int64_t)D)[c];
+      if (q < k) ov[q] = reinterpret_cast<const VT*>(o_slots + (int64_t)row_s[q] * D)[c];
     VT sv;
     if (shared) sv = reinterpret_cast<const VT*>(shared + t * (int64_t)D)[c];
     float acc[VEC];
@@ -113,23 +116,25 @@ __global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ o_sl
 }
 
 template <typename T, int VEC>
-static void launch_combine_vec(const void* o_slots, const float* w, const int32_t* idx, const void* shared,
-                               const dsmoe_dims& d, void* y, hipStream_t st) {
+static void launch_combine_vec(const void* o_slots, const int32_t* row_of, const float* w, const int32_t* idx,
+                               const void* shared, const dsmoe_dims& d, void* y, hipStream_t st) {
   const int cpr = d.D / VEC;
   const int threads = cpr >= 256 ? 256 : (int)(cdiv(cpr, 64) * 64);
   auto o = static_cast<const T*>(o_slots);
   auto sh = static_cast<const T*>(shared);
   auto yy = static_cast<T*>(y);
   if (d.k <= 8)
-    hipLaunchKernelGGL((combine_kernel<T, VEC, 8>), dim3((unsigned)d.T), dim3(threads), 0, st, o, w, idx, sh, d.T, d.D,
-                       d.k, yy);
-  else
-    hipLaunchKernelGGL((combine_kernel<T, VEC, CMB_MAX_K>), dim3((unsigned)d.T), dim3(threads), 0, st, o, w, idx, sh,
+    hipLaunchKernelGGL((combine_kernel<T, VEC, 8>), dim3((unsigned)d.T), dim3(threads), 0, st, o, row_of, w, idx, sh,
                        d.T, d.D, d.k, yy);
+  else
+    hipLaunchKernelGGL((combine_kernel<T, VEC, CMB_MAX_K>), dim3((unsigned)d.T), dim3(threads), 0, st, o, row_of, w,
+                       idx, sh, d.T, d.D, d.k, yy);
 }
 
 template <typename T>
-__global__ __launch_bounds__(256) void combine_scalar_kernel(const T* __restrict__ o_slots, const float* __restrict__ w,
+__global__ __launch_bounds__(256) void combine_scalar_kernel(const T* __restrict__ o_slots,
+                                                             const int32_t* __restrict__ row_of,
+                                                             const float* __restrict__ w,
                                                              const int32_t* __restrict__ idx,
                                                              const T* __restrict__ shared, int T_, int D, int k,
                                                              T* __restrict__ y) {
@@ -142,34 +147,35 @@ __global__ __launch_bounds__(256) void combine_scalar_kernel(const T* __restrict
   float acc = 0.0f;
   for (int q = 0; q < k; ++q) {
     const int j = ord[q];
-    acc = fmaf(w[t * k + j], to_f<T>(o_slots[(t * k + j) * (int64_t)D + c]), acc);
+    const int64_t r = row_of ? (int64_t)row_of[t * k + j] : t * k + j;
+    acc = fmaf(w[t * k + j], to_f<T>(o_slots[r * D + c]), acc);
   }
   if (shared) acc += to_f<T>(shared[t * (int64_t)D + c]);
   y[t * (int64_t)D + c] = from_f<T>(acc);
 }
 
-int launch_combine(const void* o_slots, const float* w, const int32_t* idx, const void* shared, const dsmoe_dims& d,
-                   void* y, hipStream_t st) {
+int launch_combine(const void* o_slots, const int32_t* row_of, const float* w, const int32_t* idx, const void* shared,
+                   const dsmoe_dims& d, void* y, hipStream_t st) {
   if (d.T == 0) return DSMOE_OK;
   const bool al = ((reinterpret_cast<uintptr_t>(o_slots) | reinterpret_cast<uintptr_t>(y) |
                     reinterpret_cast<uintptr_t>(shared)) & 15) == 0;
   if (d.dtype == DSMOE_BF16) {
     if (d.D % 8 == 0 && al) {
-      launch_combine_vec<uint16_t, 8>(o_slots, w, idx, shared, d, y, st);
+      launch_combine_vec<uint16_t, 8>(o_slots, row_of, w, idx, shared, d, y, st);
     } else {
       const int64_t n = (int64_t)d.T * d.D;
       hipLaunchKernelGGL(combine_scalar_kernel<uint16_t>, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, st,
-                         static_cast<const uint16_t*>(o_slots), w, idx, static_cast<const uint16_t*>(shared), d.T, d.D,
-                         d.k, static_cast<uint16_t*>(y));
+                         static_cast<const uint16_t*>(o_slots), row_of, w, idx, static_cast<const uint16_t*>(shared),
+                         d.T, d.D, d.k, static_cast<uint16_t*>(y));
     }
   } else {
     if (d.D % 4 == 0 && al) {
-      launch_combine_vec<float, 4>(o_slots, w, idx, shared, d, y, st);
+      launch_combine_vec<float, 4>(o_slots, row_of, w, idx, shared, d, y, st);
     } else {
       const int64_t n = (int64_t)d.T * d.D;
       hipLaunchKernelGGL(combine_scalar_kernel<float>, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, st,
-                         static_cast<const float*>(o_slots), w, idx, static_cast<const float*>(shared), d.T, d.D, d.k,
-                         static_cast<float*>(y));
+                         static_cast<const float*>(o_slots), row_of, w, idx, static_cast<const float*>(shared), d.T,
+                         d.D, d.k, static_cast<float*>(y));
     }
   }
   return check_launch("combine");

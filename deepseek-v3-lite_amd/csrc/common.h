@@ -206,9 +206,9 @@ int launch_sched_from_offsets(const int64_t* offsets64, int E, int bm, int64_t r
 // be built with the same height.
 bool gemm_mfma_eligible(const GemmDesc& g, int dtype, bool allow_mfma);
 int gemm_tile_m(bool mfma);
-bool gemm_qw_ok(const GemmDesc& g);
-int launch_gemm_qw(const GemmDesc& g, int epi, const float* row_scale, hipStream_t st);
-int launch_gemm_qw_pair(const GemmDesc& gr, const GemmDesc& gd, int epi, const float* row_scale, hipStream_t st);
+bool gemm_qp_ok(const GemmDesc& g);
+int launch_gemm_qp(const GemmDesc& g, int epi, const float* row_scale, hipStream_t st);
+int launch_gemm_qp_pair(const GemmDesc& gr, const GemmDesc& gd, int epi, const float* row_scale, hipStream_t st);
 int launch_grouped_gemm(const GemmDesc& g, int epi, int dtype, const float* row_scale, bool allow_mfma,
                         hipStream_t st);
 // Few-row grouped GEMM (decode): row tiles of SK_BM rows, weights streamed
@@ -217,12 +217,13 @@ constexpr int SK_BM = 64;
 bool gemm_sk_ok(const GemmDesc& g);
 int launch_gemm_sk(const GemmDesc& g, int epi, const float* row_scale, hipStream_t st);
 int launch_gemm_sk_pair(const GemmDesc& gr, const GemmDesc& gd, int epi, const float* row_scale, hipStream_t st);
-// gr (routed or dense) then the dense gd (same epilogue): one quad-wave launch
+// gr (routed or dense) then the dense gd (same epilogue): one persistent launch
 // when that kernel takes both, else two launches.  row_scale applies to gr.
 int launch_grouped_gemm_pair(const GemmDesc& gr, const GemmDesc& gd, int epi, int dtype, const float* row_scale,
                              bool allow_mfma_r, bool allow_mfma_d, hipStream_t st);
-int launch_combine(const void* o_slots, const float* w, const int32_t* idx, const void* shared, const dsmoe_dims& d,
-                   void* y, hipStream_t st);
+// row_of: slot s's output is row row_of[s] of o_slots (null: row s)
+int launch_combine(const void* o_slots, const int32_t* row_of, const float* w, const int32_t* idx, const void* shared,
+                   const dsmoe_dims& d, void* y, hipStream_t st);
 int launch_update_bias(const int32_t* counts, float* bias, int E, float speed, float upper, float lower,
                        hipStream_t st);
 int launch_update_bias_f32(const float* counts, float* bias, int E, float speed, float upper, float lower,
@@ -319,12 +320,13 @@ int launch_scale_gather_rows(const void* src, const int32_t* rows, const float* 
                              hipStream_t st);
 int xgemm_pick_ksplit(int64_t tiles, int64_t k_len);
 int64_t xgemm_tiles(int64_t M, int64_t N, int groups);
-int launch_dw_dot(const void* dy, const void* o_slots, int64_t N, int k, int D, int dtype, float* dw, hipStream_t st);
+int launch_dw_dot(const void* dy, const void* o_slots, const int32_t* row_of, int64_t N, int k, int D, int dtype,
+                  float* dw, hipStream_t st);
 // launch_dw_dot and launch_scale_gather_rows (rows by token, slot weights) in
 // one pass; DSMOE_ERR_UNSUPPORTED (nothing launched) when the shape or
 // alignment does not fit (bf16, D % 8, k <= 8, 16-byte rows).
-int launch_prep_tok(const void* dy, const void* o_slots, const float* w, const int32_t* slot_pos, int T, int k, int D,
-                    int dtype, float* dw, void* dy_w, hipStream_t st);
+int launch_prep_tok(const void* dy, const void* o_slots, const int32_t* row_of, const float* w, const int32_t* slot_pos,
+                    int T, int k, int D, int dtype, float* dw, void* dy_w, hipStream_t st);
 int launch_gate_bwd(const float* dw, const float* sel, int T, int k, float rs, float* dlog, hipStream_t st);
 int launch_dwgate(const void* x, const float* dlog, const int32_t* sorted_slot, const int32_t* sorted_token,
                   const int32_t* offsets, int E, int D, int dtype, float* dgw, hipStream_t st);

@@ -13,9 +13,9 @@
 // the tile list so the weight tiles of an expert stay in that XCD's L2.  The
 // grid is sized from a host bound; blocks past the device count exit.
 //
-// Kernels (the default bf16 path is gemm_qw_kernel in gemm_qw.hip; this file
-// holds the register-staged MFMA kernel for the shapes that one does not
-// take, the fp32 fallback and the dispatcher):
+// Kernels (the default bf16 path is the persistent gemm_qp_kernel of
+// gemm_qp.hip; this file holds the register-staged MFMA kernel for the shapes
+// that one does not take, the fp32 fallback and the dispatcher):
 //   gemm_mfma_kernel  bf16 on gfx950 v_mfma_f32_32x32x16_bf16.  Block =
 //                     WM x WN waves, each owning TM x TN 32x32 output tiles
 //                     (x2 for SwiGLU: the W1 and W3 tiles of the same columns
@@ -312,10 +312,9 @@ __global__ __launch_bounds__(256) void gemm_simt_kernel(const GemmDesc g, const 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 // MFMA kernels use 256-row M tiles (the routed schedule height): the
-// quad-wave kernel of gemm_qw.hip (4 waves of 128 x 128, K slabs of 64
-// streamed by direct loads) wherever its constraints hold, else
-// gemm_mfma_kernel with 8 waves (4 x 2), per wave 2 x 2 tiles (SwiGLU: x2) or
-// 2 x 4 (store).
+// persistent eight-wave kernel of gemm_qp.hip (K slabs of 64 streamed by
+// direct loads) wherever its constraints hold, else gemm_mfma_kernel with 8
+// waves (4 x 2), per wave 2 x 2 tiles (SwiGLU: x2) or 2 x 4 (store).
 constexpr int MF_BM = 256;
 
 // The MFMA kernel needs bf16, 16-byte aligned operands and strides, K and the
@@ -357,8 +356,8 @@ int launch_grouped_gemm(const GemmDesc& g_in, int epi, int dtype, const float* r
   if (g.N <= 0 || g.K <= 0) return DSMOE_OK;
   if (gemm_mfma_eligible(g, dtype, allow_mfma)) {
     if (g.bm != MF_BM) return fail(DSMOE_ERR_INVALID, "gemm: schedule tile height does not match the MFMA kernel");
-    if (gemm_qw_ok(g)) return launch_gemm_qw(g, epi, row_scale, st);
-    // shapes the quad-wave kernel does not take (N % 8 == 4, more than two K
+    if (gemm_qp_ok(g)) return launch_gemm_qp(g, epi, row_scale, st);
+    // shapes the persistent kernel does not take (N % 8 == 4, more than two K
     // segments, 8-byte aligned output): the register-staged 8-wave kernel
     if (epi == EPI_SWIGLU) return launch_mfma_t<EPI_SWIGLU, 4, 2, 2, 2>(g, row_scale, st);
     return launch_mfma_t<EPI_STORE, 4, 2, 2, 4>(g, row_scale, st);
@@ -385,8 +384,8 @@ int launch_grouped_gemm_pair(const GemmDesc& gr_in, const GemmDesc& gd_in, int e
   const GemmDesc &gr = gr_in, &gd = gd_in;
   const bool one = gd.sched == nullptr && gr.N > 0 && gr.K > 0 && gd.N > 0 &&
                    gd.K > 0 && gemm_mfma_eligible(gr, dtype, allow_mfma_r) && gemm_mfma_eligible(gd, dtype, allow_mfma_d) &&
-                   gemm_qw_ok(gr) && gemm_qw_ok(gd);
-  if (one) return launch_gemm_qw_pair(gr, gd, epi, row_scale, st);
+                   gemm_qp_ok(gr) && gemm_qp_ok(gd);
+  if (one) return launch_gemm_qp_pair(gr, gd, epi, row_scale, st);
   const int rc = launch_grouped_gemm(gr_in, epi, dtype, row_scale, allow_mfma_r, st);
   if (rc) return rc;
   return launch_grouped_gemm(gd_in, epi, dtype, nullptr, allow_mfma_d, st);

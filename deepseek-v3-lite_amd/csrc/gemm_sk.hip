@@ -17,7 +17,7 @@
 // epilogue (SwiGLU or store, optional row scale, output row map) writes
 // 16-byte chunks.
 //
-// Tile enumeration and GemmDesc contract as in gemm_qw.hip, with row tiles of
+// Tile enumeration (gemm_tile.h) and GemmDesc contract as in gemm.hip, with row tiles of
 // SK_BM rows (the routed schedule must be built with bm = SK_BM).
 #include "gemm_tile.h"
 #include "mfma.h"

@@ -1,6 +1,6 @@
-// Backward grouped GEMMs on gfx950: the quad-wave design of gemm_qw.hip
-// (four waves, one per SIMD, each owning 128 x 128 of a 256 x 256 tile; K
-// slabs of 64 streamed into separate A and B LDS rings by direct
+// Backward grouped GEMMs on gfx950, quad-wave design (four waves, one per
+// SIMD, each owning 128 x 128 of a 256 x 256 tile; K slabs of 64 streamed
+// into separate A and B LDS rings by direct
 // global -> LDS loads; fragment reads two K steps ahead of the MFMAs;
 // LDS-staged, whole-row epilogues) extended to operands whose reduction
 // index K is the ROW index of the stored matrix ("K-major", KM):
@@ -226,8 +226,7 @@ struct XQPipe {
   bf16x8_t fb[3][4];
 };
 
-// One slab whose step 0 uses register set S0 (the schedule of qw_slab in
-// gemm_qw.hip: reads run two steps ahead; the barrier follows step 1; the
+// One slab whose step 0 uses register set S0 (reads run two steps ahead; the barrier follows step 1; the
 // refills of slab kb + 2 are spread over the slab, B(kb + 2) during steps 0
 // and 1 into slab kb - 1's slot, A(kb + 2) during steps 2 and 3 into slab
 // kb's).

@@ -3,11 +3,12 @@
 Restates, in numpy, the index arithmetic of the direct-load loaders and the
 epilogue stores of
 
-* ``gemm_qw_kernel``  (deepseek-v3-lite_amd/csrc/gemm_qw.hip, forward gemm1 / gemm2),
+* ``gemm_qp_kernel``  (deepseek-v3-lite_amd/csrc/gemm_qp.hip, forward gemm1 / gemm2, persistent),
 * ``gemm_sk_kernel``  (csrc/gemm_sk.hip, the decode few-row kernel),
 * ``xgemm_q_kernel``  (csrc/gemm_xq.hip, backward dh, dx, dW13, dW2),
 
-including the block -> tile enumeration (csrc/gemm_tile.h), the loads the
+including the block -> tile enumeration (csrc/gemm_tile.h, and the persistent
+workgroups' tile lists of gemm_qp.hip), the staged epilogues' LDS regions, the loads the
 main loops issue past the last K slab (clamped to the last slab), and the
 zero-block redirection of K-major rows past a weight-gradient range.  Every
 access is returned as (buffer, first byte, last byte + 1) per lane, so a test
@@ -171,21 +172,59 @@ def sched_bound(rows: int, groups: int, bm: int) -> int:
     return rows // bm + groups + 1
 
 
-# ---------------------------------------------------------------- gemm_qw (forward ping-pong kernel)
+# ---------------------------------------------------------------- gemm_qp (forward persistent ping-pong kernel)
 # Loading wave w (0..3) of group 0 loads A rows, wave w of group 1 the same B
-# rows; slabs 0 .. nk - 1 (the model also covers the clamped reloads of the
-# last slab, a superset).
+# rows; a tile's loads cover its slabs 0 .. nk - 1 (the loaders then move on
+# to the next tile of the workgroup).
 QW_BM, QW_BK, QW_LD = 256, 64, 8
+QP_STAGE = 8192   # bytes of a slot a wave may stage in (its own 8 KB)
 
 
-def qw_ok(g: Gemm) -> bool:
-    """gemm_qw_ok (alignment of real pointers is not modelled; callers align)."""
+def qp_ok(g: Gemm) -> bool:
+    """gemm_qp_ok (alignment of real pointers is not modelled; callers align)."""
     lim = 1 << 31
     return (1 <= g.nseg <= 2 and g.K % QW_BK == 0 and g.kseg % QW_BK == 0 and g.a_rows * g.lda < lim
             and g.N * g.ldb < lim and g.N % 8 == 0 and g.ldc % 8 == 0 and g.c_group_col % 8 == 0)
 
 
-def qw_tile(rec: Recorder, g: Gemm, swiglu: bool, grp: int, row0: int, rows: int, n_tile: int, what: str):
+def qp_lists(gr: Gemm, gd: Optional[Gemm], bm: int, bn: int, grid: int):
+    """qp_list / qp_tile: per workgroup b, its tiles (which, grp, row0, rows, n_tile) in order."""
+    ntr = cdiv(gr.N, bn)
+    mr = len(gr.sched) if gr.sched is not None else cdiv(gr.dense_rows, bm) * gr.groups
+    tr = mr * ntr
+    per_r = cdiv(tr, 8)
+    ntd, td, per_d = 1, 0, 0
+    if gd is not None:
+        ntd = cdiv(gd.N, bn)
+        td = cdiv(gd.dense_rows, bm) * gd.groups * ntd
+        per_d = cdiv(td, 8)
+    nb = grid >> 3
+    out = []
+    for b in range(grid):
+        x, j = b & 7, b >> 3
+        r_base = x * per_r
+        r_cnt = max(0, min(per_r, tr - r_base))
+        d_base = x * per_d
+        d_cnt = max(0, min(per_d, td - d_base)) if gd is not None else 0
+        tot = d_cnt + r_cnt
+        ntiles = cdiv(tot - j, nb) if tot > j else 0
+        tiles = []
+        for i in range(ntiles):
+            li = j + i * nb
+            assert li < tot
+            if li < d_cnt:
+                lin, nt, g, which = d_base + li, ntd, gd, 1
+            else:
+                lin, nt, g, which = r_base + (li - d_cnt), ntr, gr, 0
+            m_tile, n_tile = divmod(lin, nt)
+            grp, row0, rows = _sched_tile(g, m_tile, bm)
+            tiles.append((which, grp, row0, rows, n_tile))
+        out.append(tiles)
+    return out
+
+
+def qp_loads(rec: Recorder, g: Gemm, swiglu: bool, grp: int, row0: int, rows: int, n_tile: int, what: str):
+    """qpa_rows / qpa_step and qpb_set / qpb_step for one tile: slabs 0 .. nk - 1."""
     NB = 2 if swiglu else 1
     BN = 128 if swiglu else 256
     n0 = n_tile * BN
@@ -200,12 +239,12 @@ def qw_tile(rec: Recorder, g: Gemm, swiglu: bool, grp: int, row0: int, rows: int
         arow = rec.index(g.a_map, row0 + ra, what + " a_map")
     else:
         arow = row0 + ra
-    offa = 2 * (arow * g.lda + c * 8)
+    offa = arow * (2 * g.lda) + c * 16
+    if np.any(offa >= 1 << 32):
+        raise Violation(f"{what}: A byte offset past 32 bits")
     bn = n0 + (r & 127) if NB == 2 else n0 + r
     offb = 2 * (np.minimum(bn, g.N - 1) * g.ldb + c * 8)
-    # slabs loaded: 0 .. nk + 1 (the main loop refills slab kb + 2), clamped to nk - 1
-    k0s = sorted({min(ka, nk - 1) * QW_BK for ka in (0, nk - 1, nk, nk + 1)})
-    for k0 in k0s:
+    for k0 in sorted({0, (nk - 1) * QW_BK}):
         rec.touch(g.A, offa + 2 * k0, offa + 2 * k0 + 16, what + " A")
         hi = k0 >= (g.kseg if g.nseg > 1 else 1 << 62)
         seg = g.nseg - 1 if hi else 0
@@ -214,44 +253,107 @@ def qw_tile(rec: Recorder, g: Gemm, swiglu: bool, grp: int, row0: int, rows: int
             tab = g.B1 if (NB == 2 and w >= 2) else g.B0
             blk = rec.index(np.array(tab, dtype=object), grp * g.nseg + seg, what + " B table")
             rec.touch(blk, offb[w] + 2 * kin, offb[w] + 2 * kin + 16, what + " B")
-            # a slab never reads past its K segment within a row
             seg_len = (g.K - g.kseg if hi else g.kseg) if g.nseg > 1 else g.K
             if kin + 64 > seg_len:
                 raise Violation(f"{what}: K slab {kin} past the segment")
-    # epilogue: rows r < rows, 16-byte chunks of BN columns
-    LPR = BN * 2 // 16
+
+
+def _qp_swz(r, WB):
+    return (((r >> 2) & 3) << 1) if WB == 64 else (((r >> 1) & 7) << 1)
+
+
+_QP_STAGE_CHECKED = set()
+
+
+def _qp_stage_check(swiglu: bool, rows: int):
+    """The wave -> output-row mapping and the LDS staging of one tile height:
+    staging stays inside the wave's own 8 KB, and the stored rows are exactly
+    0 .. rows - 1, each once per column group (checked once per height)."""
+    key = (swiglu, rows)
+    if key in _QP_STAGE_CHECKED:
+        return
+    TN = 1 if swiglu else 2
+    WB = 64 * TN
+    LPR = WB // 16
+    RPI = 64 // LPR
+    passes = [(0, 4)] if swiglu else [(0, 2), (2, 2)]
+    lane = np.arange(64)
+    for G in (0, 1):
+        for s in range(4):
+            wm = s >> 1
+            nmi = max(0, min(4, (cdiv(rows, 32) - wm + 1) >> 1))
+            stored = []
+            for j0, nj in passes:
+                for j in range(j0, min(j0 + nj, nmi)):
+                    r = (j - j0) * 32 + (lane & 31)
+                    for ni in range(TN):
+                        for q in range(4):
+                            u = ni * 8 + 2 * q + (lane >> 5)
+                            a = r * WB + ((u ^ _qp_swz(r, WB)) << 3)
+                            if a.min() < 0 or (a + 8).max() > QP_STAGE:
+                                raise Violation("staging write outside the wave's 8 KB")
+                for it in range(nj * 32 // RPI):
+                    j = j0 + (it * RPI) // 32
+                    if j >= nmi:
+                        break
+                    r = it * RPI + lane // LPR
+                    cc = lane % LPR
+                    a = r * WB + (((2 * cc) ^ _qp_swz(r, WB)) << 3)
+                    if a.min() < 0 or (a + 16).max() > QP_STAGE:
+                        raise Violation("staging read outside the wave's 8 KB")
+                    lr = (it * RPI) % 32 + lane // LPR
+                    m = (2 * j + wm) * 32 + lr
+                    stored += [int(v) for v, c in zip(m, cc) if v < rows and c == 0]
+            want = [m for m in range(rows) if (m // 32) % 2 == wm]
+            if sorted(stored) != want:
+                raise Violation(f"wave (G{G}, s{s}) stores rows {sorted(set(stored))[:8]}.. not its {want[:8]}..")
+    _QP_STAGE_CHECKED.add(key)
+
+
+def qp_epilogue(rec: Recorder, g: Gemm, swiglu: bool, grp: int, row0: int, rows: int, n_tile: int, what: str):
+    """qp_epilogue / qp_out_pass of every wave: rows 0 .. rows - 1 of the tile
+    (mapping and LDS staging checked by _qp_stage_check), each row's 16-byte
+    chunks of the tile's columns below N."""
+    _qp_stage_check(swiglu, rows)
+    BN = 128 if swiglu else 256
+    n0 = n_tile * BN
     rr = np.arange(rows)
-    if g.c_map is not None:
-        crow = rec.index(g.c_map, row0 + rr, what + " c_map")
-    else:
-        crow = row0 + rr
-    ccol = grp * g.c_group_col
-    n = n0 + np.arange(LPR) * 8
+    crow = rec.index(g.c_map, row0 + rr, what + " c_map") if g.c_map is not None else row0 + rr
+    n = n0 + np.arange(BN // 8) * 8
     n = n[n < g.N]
-    off = 2 * ((crow[:, None] * g.ldc + ccol + n[None, :]))
+    off = 2 * (crow[:, None] * g.ldc + grp * g.c_group_col + n[None, :])
     rec.touch(g.C, off, off + 16, what + " C")
     for sv in (g.Gs, g.Us):
         if swiglu and sv is not None:
             rec.touch(sv, off, off + 16, what + " G/U")
 
 
-def qw_launch(rec: Recorder, gr: Gemm, swiglu: bool, gd: Optional[Gemm] = None, what: str = "gemm_qw"):
-    """launch_gemm_qw / launch_gemm_qw_pair: grid from the host bounds, every block's tile."""
+def qp_launch(rec: Recorder, gr: Gemm, swiglu: bool, gd: Optional[Gemm] = None, what: str = "gemm_qp",
+              grid: int = 256):
+    """launch_gemm_qp / launch_gemm_qp_pair: one workgroup per CU, each through
+    its tile list; every tile of the problem(s) exactly once."""
     bn = 128 if swiglu else 256
-    mr = gr.m_tiles_bound if gr.sched is not None else cdiv(gr.dense_rows, QW_BM) * gr.groups
-    if gd is None:
-        grid = 8 * cdiv(mr * cdiv(gr.N, bn), 8)
-        tl = tiles_single(gr, QW_BM, bn, grid)
-    else:
-        md = cdiv(gd.dense_rows, QW_BM) * gd.groups
-        grid = 8 * (cdiv(md * cdiv(gd.N, bn), 8) + cdiv(mr * cdiv(gr.N, bn), 8))
-        tl = tiles_pair(gr, gd, QW_BM, bn, grid)
-    for which, grp, row0, rows, n_tile in tl:
-        g = gd if which else gr
-        if rows <= 0:
-            raise Violation(f"{what}: empty tile")
-        qw_tile(rec, g, swiglu, grp, row0, rows, n_tile, f"{what}[{'dense' if which else 'routed'} g{grp} r{row0}]")
-    return len(tl)
+    lists = qp_lists(gr, gd, QW_BM, bn, grid)
+    seen = set()
+    n = 0
+    for tiles in lists:
+        for which, grp, row0, rows, n_tile in tiles:
+            g = gd if which else gr
+            if rows <= 0:
+                raise Violation(f"{what}: empty tile")
+            key = (which, grp, row0, n_tile)
+            if key in seen:
+                raise Violation(f"{what}: tile {key} in two workgroups' lists")
+            seen.add(key)
+            tag = f"{what}[{'dense' if which else 'routed'} g{grp} r{row0}]"
+            qp_loads(rec, g, swiglu, grp, row0, rows, n_tile, tag)
+            qp_epilogue(rec, g, swiglu, grp, row0, rows, n_tile, tag)
+            n += 1
+    mr = len(gr.sched) if gr.sched is not None else cdiv(gr.dense_rows, QW_BM) * gr.groups
+    want = mr * cdiv(gr.N, bn) + (cdiv(gd.dense_rows, QW_BM) * gd.groups * cdiv(gd.N, bn) if gd is not None else 0)
+    if n != want:
+        raise Violation(f"{what}: {n} tiles covered of {want}")
+    return n
 
 
 # ---------------------------------------------------------------- gemm_sk (decode few-row kernel)

@@ -50,7 +50,7 @@ def _forward(rec, T, D, E, k, I, S, I_s, training, counts, sorted_token, sorted_
     gs_ = M.Buf("g", N * I * 2) if training else None
     us_ = M.Buf("u", N * I * 2) if training else None
     hs = M.Buf("hs", T * S * I_s * 2)
-    o_slots = M.Buf("o_slots", N * D * 2)
+    o_sorted = M.Buf("o_sorted", N * D * 2)
     shared_out = M.Buf("shared_out", T * D * 2)
     decode = not training and T <= M.SK_BM
     bm = M.SK_BM if decode else M.QW_BM
@@ -59,8 +59,8 @@ def _forward(rec, T, D, E, k, I, S, I_s, training, counts, sorted_token, sorted_
     assert len(sched) <= bound, "schedule longer than its workspace bound"
     g1 = M.Gemm(N=I, K=D, A=x, lda=D, a_rows=T, B0=w1, B1=w3, ldb=D, kseg=D, nseg=1, C=h, ldc=I, sched=sched,
                 a_map=sorted_token, Gs=gs_, Us=us_, m_tiles_bound=bound)
-    g2 = M.Gemm(N=D, K=I, A=h, lda=I, a_rows=N, B0=w2, B1=None, ldb=I, kseg=I, nseg=1, C=o_slots, ldc=D,
-                sched=sched, c_map=sorted_slot, m_tiles_bound=bound)
+    g2 = M.Gemm(N=D, K=I, A=h, lda=I, a_rows=N, B0=w2, B1=None, ldb=I, kseg=I, nseg=1, C=o_sorted, ldc=D,
+                sched=sched, m_tiles_bound=bound)
     d1 = d2 = None
     if S:
         d1 = M.Gemm(N=I_s, K=D, A=x, lda=D, a_rows=T, B0=s1, B1=s3, ldb=D, kseg=D, nseg=1, C=hs, ldc=S * I_s,
@@ -78,13 +78,13 @@ def _forward(rec, T, D, E, k, I, S, I_s, training, counts, sorted_token, sorted_
                 launched += M.sk_launch(rec, gr_, sw, gd)
             else:
                 launched += M.sk_launch(rec, gr_, sw)
-        elif M.qw_ok(gr):
-            if gd is not None and M.qw_ok(gd):
-                launched += M.qw_launch(rec, gr, sw, gd)
+        elif M.qp_ok(gr):
+            if gd is not None and M.qp_ok(gd):
+                launched += M.qp_launch(rec, gr, sw, gd)
             else:
-                launched += M.qw_launch(rec, gr, sw)
-                if gd is not None and M.qw_ok(gd):
-                    launched += M.qw_launch(rec, gd, sw)
+                launched += M.qp_launch(rec, gr, sw)
+                if gd is not None and M.qp_ok(gd):
+                    launched += M.qp_launch(rec, gd, sw)
     return launched
 
 
@@ -175,10 +175,10 @@ def test_forward_gemm_addresses_in_bounds(name, training):
     rec = M.Recorder()
     n = _forward(rec, T, D, E, k, I, S, I_s, training, counts, st, ss)
     assert n > 0
-    # the tiles cover the routed rows: h (gemm1) and o_slots (gemm2) are written up to their last row
+    # the tiles cover the routed rows: h (gemm1) and o_sorted (gemm2) are written up to their last row
     if not (not training and T <= M.SK_BM):
         assert rec.ext["h"][1] == T * k * I * 2
-    assert rec.ext["o_slots"][1] == T * k * D * 2
+    assert rec.ext["o_sorted"][1] == T * k * D * 2
 
 
 @pytest.mark.parametrize("name", ["c0_bf16", "c1", "c2_skew", "c3", "c4", "ragged_empty", "wide_e256", "one_token"])
