@@ -71,9 +71,9 @@ struct GPCfg {
 
 template <int NT, int SC>
 constexpr size_t gp_lds(bool route) {
-  return route && (size_t)4 * (GP_TOK * (NT * 32 + 1) + 2 * NT * 32) > (size_t)GPCfg<NT, SC>::LDS
-             ? (size_t)4 * (GP_TOK * (NT * 32 + 1) + 2 * NT * 32)
-             : (size_t)GPCfg<NT, SC>::LDS;
+  // routing: lg[GP_TOK][EP + 1] | bias[EP] | hist[EP] | scratch (64 ints per wave)
+  constexpr size_t r = (size_t)4 * (GP_TOK * (NT * 32 + 1) + 2 * NT * 32 + GP_THREADS);
+  return route && r > (size_t)GPCfg<NT, SC>::LDS ? r : (size_t)GPCfg<NT, SC>::LDS;
 }
 
 // Splits 4 fp32 weights into three bf16x4 words (hi, mid, lo) whose sum is
@@ -237,6 +237,7 @@ __global__ __launch_bounds__(GP_THREADS) void gate_mfma_kernel(const bf16_t* __r
     float* lg = reinterpret_cast<float*>(gsm);     // [GP_TOK][LDP]
     float* bias_s = lg + GP_TOK * LDP;
     int* hist = reinterpret_cast<int*>(bias_s + C::EP);
+    int32_t* scr = hist + C::EP;
     for (int e = tid; e < E; e += blockDim.x) {
       bias_s[e] = bias[e];
       hist[e] = 0;
@@ -258,7 +259,8 @@ __global__ __launch_bounds__(GP_THREADS) void gate_mfma_kernel(const bf16_t* __r
         const int tt = i / E, e = i - tt * E;
         out.logits[(int64_t)(t0 + tt) * E + e] = lg[tt * LDP + e];
       }
-    route_tokens(lg, LDP, ntok, t0, bias_s, E, k, route_scale, DSMOE_BF16, out, out.counts ? hist : nullptr);
+    route_tokens(lg, LDP, ntok, t0, bias_s, E, k, route_scale, DSMOE_BF16, out, out.counts ? hist : nullptr, nullptr,
+                 scr);
     __syncthreads();
     flush_hist(hist, E, out.counts);
   }
@@ -269,7 +271,8 @@ __global__ __launch_bounds__(GP_THREADS) void gate_mfma_kernel(const bf16_t* __r
 // RANK_TOKENS tokens (four tokens per wave).  With po.offsets set it also
 // ranks the block's slots (rank.h), and a call of one rank block finishes its
 // permute here.
-// LDS (4-byte words): lg[64][E + 1] | bias[E] | hist[E] | sel[64 k] | rank[64 k] | off[E + 1] | til[E + 1]
+// LDS (4-byte words): lg[64][E + 1] | bias[E] | hist[E] | sel[64 k] | rank[64 k] | off[E + 1] | til[E + 1] |
+// routing scratch[64 per wave]
 constexpr int RR_WAVES = RANK_TOKENS / 4;
 
 template <int KB>
@@ -286,6 +289,7 @@ __global__ __launch_bounds__(RR_WAVES * 64) void route_rank_kernel(const float* 
   int32_t* rank_lds = sel + RANK_TOKENS * k;
   int32_t* off = rank_lds + RANK_TOKENS * k;
   int32_t* til = off + E + 1;
+  int32_t* scr = til + E + 1;
   const int tid = threadIdx.x;
   const int b = blockIdx.x;
   const int t0 = b * RANK_TOKENS;
@@ -342,7 +346,7 @@ __global__ __launch_bounds__(RR_WAVES * 64) void route_rank_kernel(const float* 
   }
   __syncthreads();
   route_tokens(lg, ldl, ntok, t0, bias_s, E, k, route_scale, xdtype, out, (!rank && out.counts) ? hist : nullptr,
-               rank ? sel : nullptr);
+               rank ? sel : nullptr, scr);
   __syncthreads();
   if (!rank) {
     flush_hist(hist, E, out.counts);
@@ -355,6 +359,7 @@ __global__ __launch_bounds__(RR_WAVES * 64) void route_rank_kernel(const float* 
 
 // ------------------------------------------------------------------ SIMT logits (fp32 x, or D % 64 != 0)
 // LDS layout (floats): xs[KC][TB+4] | ws[KC][EC+4] | lg[TB][E+1] | bias[E] | hist[E] (int) | routing scratch
+// (64 ints per wave)
 template <typename XT, int EC>
 __global__ __launch_bounds__(GATE_THREADS) void gate_kernel(const XT* __restrict__ x, const float* __restrict__ gw,
                                                             const float* __restrict__ bias, int T, int D, int E, int k,
@@ -367,6 +372,7 @@ __global__ __launch_bounds__(GATE_THREADS) void gate_kernel(const XT* __restrict
   float* lg = ws + GATE_KC * (EC + 4);          // [TB][E+1]
   float* bias_s = lg + TB * (E + 1);            // [E]
   int* hist = reinterpret_cast<int*>(bias_s + E);  // [E]
+  int32_t* scr = hist + E;                      // [GATE_THREADS]
 
   const int tid = threadIdx.x;
   const int t0 = blockIdx.x * TB;
@@ -420,7 +426,7 @@ __global__ __launch_bounds__(GATE_THREADS) void gate_kernel(const XT* __restrict
       out.logits[(int64_t)(t0 + t) * E + e] = lg[t * ldl + e];
     }
   }
-  route_tokens(lg, ldl, ntok, t0, bias_s, E, k, route_scale, xdtype, out, out.counts ? hist : nullptr);
+  route_tokens(lg, ldl, ntok, t0, bias_s, E, k, route_scale, xdtype, out, out.counts ? hist : nullptr, nullptr, scr);
   __syncthreads();
   flush_hist(hist, E, out.counts);
 }
@@ -453,7 +459,7 @@ static int launch_gate_t(const void* x, const float* gw, const float* bias, cons
   constexpr int TX = EC / 4;
   constexpr int TB = (GATE_THREADS / TX) * 4;
   const size_t lds = sizeof(float) * (GATE_KC * (TB + 4) + GATE_KC * (EC + 4) + TB * (d.E + 1) + d.E) +
-                     sizeof(int) * d.E + 16;
+                     sizeof(int) * (d.E + GATE_THREADS) + 16;
   auto kern = gate_kernel<XT, EC>;
   int rc = set_lds((const void*)kern, lds);
   if (rc) return rc;
@@ -469,7 +475,8 @@ static int launch_route(const float* part, int ks, const float* bias, const dsmo
   PermuteOut none;
   std::memset(static_cast<void*>(&none), 0, sizeof(none));
   const int nb = (int)cdiv(d.T, RANK_TOKENS);
-  const size_t lds = sizeof(float) * (RANK_TOKENS * (d.E + 1) + 2 * d.E + 2 * RANK_TOKENS * d.k + 2 * (d.E + 1));
+  const size_t lds =
+      sizeof(float) * (RANK_TOKENS * (d.E + 1) + 2 * d.E + 2 * RANK_TOKENS * d.k + 2 * (d.E + 1) + RR_WAVES * 64);
   auto kern = d.k <= 8 ? route_rank_kernel<8> : route_rank_kernel<MAX_TOPK>;
   int rc = set_lds((const void*)kern, lds);
   if (rc) return rc;
