@@ -244,6 +244,89 @@ def decode_bench(dev, steps: int, warmup: int):
             "weight_bytes": nbytes, "GB/s": gbs, "frac_hbm": gbs / PEAK_HBM_GBS, "stage_ms": stage_ms}
 
 
+# MLA attention shape: configs/pretrain_a100_422m.yaml:20-45 (micro batch 8, full 2048 sequence, causal)
+MLA_SHAPE = {"B": 8, "H": 12, "S": 2048, "R": 192, "Dn": 48, "Dr": 24, "Dv": 64}
+
+
+def mla_bench(dev, steps: int, warmup: int, with_cpu: bool):
+    """Fused MLA attention forward (models/mla_triton.py:303-329) at the 422m
+    config's shape, causal: the two kernels of csrc/mla.hip (K, V
+    materialisation + flash attention) per call.  Algorithmic flops: 2 (Dn +
+    Dr + Dv) per visible (query, key) pair plus 2 R (Dn + Dv) per (batch,
+    head, key) for K and V.  Beside it, the reference's default SDPA path
+    (models/mla.py:155-172: K, V materialised with bmm, then
+    scaled_dot_product_attention) run by torch on the same GPU, when a fused
+    SDPA backend takes the shape."""
+    import torch
+    from dsmoe.mla import mla_attention_fwd
+    sh = MLA_SHAPE
+    B, H, S, R, Dn, Dr, Dv = (sh[k] for k in ("B", "H", "S", "R", "Dn", "Dr", "Dv"))
+    scale = (Dn + Dr) ** -0.5
+    g = torch.Generator(device=dev).manual_seed(0)
+    rn = lambda *s_: torch.randn(*s_, generator=g, device=dev, dtype=torch.float32)
+    ts = [t.to(torch.bfloat16) for t in (rn(B, H, S, Dn), rn(B, H, S, Dr), rn(B, S, R), rn(B, S, Dr),
+                                         rn(H, Dn, R) * 0.1, rn(H, Dv, R) * 0.1)]
+    log(f"[bench] mla: B={B} H={H} S={S} R={R} Dn={Dn} Dr={Dr} Dv={Dv} causal")
+
+    def step():
+        return mla_attention_fwd(*ts, scale, True, 0)
+
+    with torch.no_grad():
+        ms, _ = time_steps(step, steps, warmup)
+    vis = S * (S + 1) // 2
+    flop_attn = 2.0 * B * H * vis * (Dn + Dr + Dv)
+    flop_kv = 2.0 * B * H * S * R * (Dn + Dv)
+    tf = (flop_attn + flop_kv) / (ms * 1e-3) / 1e12
+    out = {"workload": f"MLA attention forward, B={B} H={H} S_q=S_kv={S} R={R} D_nope={Dn} D_rope={Dr} "
+                       f"D_v={Dv}, causal, bf16 (configs/pretrain_a100_422m.yaml shape)",
+           "ms_per_call": ms, "tokens_per_s": B * S / (ms * 1e-3), "flop": flop_attn + flop_kv,
+           "TFLOP/s": tf, "frac_mfma": tf / PEAK_BF16_TFLOPS,
+           # the reference kernel rebuilds K, V of every visible 64-key block
+           # for each 64-query block (models/mla_triton.py:135-147)
+           "reference_kernel_flop": 2.0 * B * H * vis * (Dn + Dr + Dv)
+           + 2.0 * B * H * sum(min(i + 1, (S + 63) // 64) for i in range((S + 63) // 64)) * 64 * R * (Dn + Dv)}
+    # the reference's SDPA path on this GPU (fused backends only: the math
+    # path's bf16 batched products are avoided on this pool)
+    try:
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        qn, qp, kv, pe, wk, wv = ts
+        wkv = torch.cat([wk, wv], dim=1).transpose(-1, -2).contiguous()          # (H, R, Dn + Dv)
+
+        def ref_step():
+            kvb = kv.reshape(B * S, R).unsqueeze(0).expand(H, -1, -1).contiguous()
+            kvh = torch.bmm(kvb, wkv)
+            k_n, v_h = kvh.split([Dn, Dv], dim=-1)
+            k_n = k_n.reshape(H, B, S, Dn).permute(1, 0, 2, 3)
+            v_h = v_h.reshape(H, B, S, Dv).permute(1, 0, 2, 3)
+            # V padded to the q/k head width (the fused SDPA backends take one width)
+            v_h = torch.nn.functional.pad(v_h, (0, Dn + Dr - Dv)).contiguous()
+            k = torch.cat([k_n, pe.unsqueeze(1).expand(-1, H, -1, -1)], dim=-1).contiguous()
+            q = torch.cat([qn, qp], dim=-1).contiguous()
+            return torch.nn.functional.scaled_dot_product_attention(q, k, v_h, is_causal=True, scale=scale)[..., :Dv]
+
+        with torch.no_grad(), sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            ref_ms, _ = time_steps(ref_step, max(3, steps // 2), max(2, warmup // 2))
+        out["reference_sdpa_ms"] = ref_ms
+        out["speedup_vs_reference_sdpa"] = ref_ms / ms
+    except Exception as e:  # no fused SDPA backend for this shape
+        out["reference_sdpa_ms"] = None
+        out["reference_sdpa_note"] = f"{type(e).__name__}: {str(e)[:160]}"
+    if with_cpu:
+        import time
+        from oracle.mla_ref import mla_attention_oracle
+        cpu = [t[:1, :1].cpu() if t.dim() == 4 else (t[:1].cpu() if t.size(0) == B else t[:1].cpu())
+               for t in ts]
+        t0 = time.perf_counter()
+        mla_attention_oracle(*cpu, scale, is_causal=True)
+        dt = time.perf_counter() - t0
+        out["cpu_baseline"] = {"value": S / dt, "unit": "queries/s of one (batch, head)", "cores": 1, "kind": "port",
+                               "sample": f"oracle/mla_ref.py float64 numpy, one (batch, head), S={S}, {dt:.2f} s"}
+        out["speedup_vs_cpu"] = (B * H * S / (ms * 1e-3)) / (S / dt)
+    log(f"[bench] mla: {ms:.4f} ms/call, {tf:.0f} TFLOP/s ({tf / PEAK_BF16_TFLOPS:.1%}), "
+        f"reference SDPA {out.get('reference_sdpa_ms')}")
+    return out
+
+
 def fwd_bench(name: str, dev, steps: int, warmup: int):
     """Forward of another BASELINE config (C1, C2 with its skewed bias): step
     time, routed tokens/s, the grouped GEMMs' rate, per-stage times and the
@@ -403,6 +486,7 @@ def main() -> int:
     ap.add_argument("--no-decode", action="store_true", help="skip the config-3 decode (T=64) measurement")
     ap.add_argument("--no-extra-configs", action="store_true", help="skip the C1 / C2 forward figures")
     ap.add_argument("--no-autocast", action="store_true", help="skip the module-under-autocast figures")
+    ap.add_argument("--no-mla", action="store_true", help="skip the MLA attention figures")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="instead of the layer, run --steps device copies of this many MiB (counter calibration)")
     ap.add_argument("--dma-mb", type=int, default=0,
@@ -502,6 +586,8 @@ def main() -> int:
     if not args.no_extra_configs and args.config == "c3":
         result["configs_fwd"] = {c: fwd_bench(c, dev, args.steps, args.warmup) for c in ("c1", "c2")}
         result["blas_dense_reference"] = blas_dense_reference(dev, cfg)
+    if not args.no_mla and args.config == "c3":
+        result["mla"] = mla_bench(dev, args.steps, args.warmup, not args.no_cpu_baseline)
     if not args.no_cpu_baseline:
         log("[bench] timing the CPU restatement of the reference path ...")
         result["cpu_baseline"] = cpu_baseline(cfg, x, gate_w, bias, weights)

@@ -34,6 +34,14 @@ class Dims(ctypes.Structure):
                 ("route_scale", ctypes.c_float)]
 
 
+class MlaDims(ctypes.Structure):
+    """dsmoe_mla_dims (include/dsmoe.h)."""
+    _fields_ = [("B", ctypes.c_int32), ("H", ctypes.c_int32), ("S_q", ctypes.c_int32), ("S_kv", ctypes.c_int32),
+                ("R", ctypes.c_int32), ("D_nope", ctypes.c_int32), ("D_rope", ctypes.c_int32),
+                ("D_v", ctypes.c_int32), ("dtype", ctypes.c_int32), ("is_causal", ctypes.c_int32),
+                ("q_start", ctypes.c_int32), ("softmax_scale", ctypes.c_float)]
+
+
 P = ctypes.c_void_p
 PP = ctypes.POINTER(ctypes.c_void_p)
 DIMS = ctypes.POINTER(Dims)
@@ -66,6 +74,8 @@ _SIGNATURES = {
     "dsmoe_timing_read": ([ctypes.POINTER(ctypes.c_double), I32, ctypes.POINTER(ctypes.c_int)], I32),
     "dsmoe_timing_stage_name": ([I32], ctypes.c_char_p),
     "dsmoe_probe_dma_read": ([P, SZ, P, P], I32),
+    "dsmoe_mla_attn_workspace_size": ([ctypes.POINTER(MlaDims)], SZ),
+    "dsmoe_mla_attn_fwd": ([P, P, P, P, P, P, ctypes.POINTER(MlaDims), P, P, SZ, P], I32),
 }
 
 _lib = None

@@ -28,7 +28,7 @@ CFLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{INCLUDE}", f"-I{CSRC}",
 ]
-SOURCES = ["api.hip", "gate.hip", "permute.hip", "gemm.hip", "gemm_qp.hip", "gemm_sk.hip", "gemm_x.hip", "gemm_xm.hip", "gemm_xq.hip", "bwd.hip", "combine.hip", "probe.hip"]
+SOURCES = ["api.hip", "gate.hip", "permute.hip", "gemm.hip", "gemm_qp.hip", "gemm_sk.hip", "gemm_x.hip", "gemm_xm.hip", "gemm_xq.hip", "bwd.hip", "combine.hip", "mla.hip", "probe.hip"]
 
 
 def _compile(src: Path) -> Path:

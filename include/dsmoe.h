@@ -242,6 +242,37 @@ const char* dsmoe_timing_stage_name(int stage);
  * workgroup per MiB, and writes one word per workgroup to sink. */
 int dsmoe_probe_dma_read(const void* src, size_t bytes, uint32_t* sink, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Multi-head latent attention forward (the fused MLA attention of
+ * models/mla_triton.py:73-183, entered through triton_mla_attention,
+ * models/mla_triton.py:303-329; dims as its argument shapes read them, :229-234).
+ * Tensors are contiguous bf16:
+ *   q_nope (B, H, S_q, D_nope)   q_pe (B, H, S_q, D_rope)   RoPE already applied
+ *   ctx_kv (B, S_kv, R)          ctx_pe (B, S_kv, D_rope)   latent cache
+ *   wkv_b_k (H, D_nope, R)       wkv_b_v (H, D_v, R)        per-head up-projections
+ *   out (B, S_q, H, D_v)
+ * out = softmax(softmax_scale * [q_nope | q_pe] [ctx_kv wkv_b_k^T | ctx_pe]^T) (ctx_kv wkv_b_v^T)
+ * per (batch, head), with the causal mask key <= query + q_start when
+ * is_causal (models/mla_triton.py:159-161) and no mask otherwise.  R, D_nope,
+ * D_rope, D_v <= 256 as the reference requires (:186-196: DSMOE_ERR_INVALID),
+ * and D_nope + D_rope <= 256 (DSMOE_ERR_UNSUPPORTED).  The workspace holds the
+ * materialised K and V of every (batch, head). */
+typedef struct dsmoe_mla_dims {
+  int32_t B, H, S_q, S_kv;
+  int32_t R;          /* kv_lora_rank        */
+  int32_t D_nope;     /* qk_nope_head_dim    */
+  int32_t D_rope;     /* qk_rope_head_dim    */
+  int32_t D_v;        /* v_head_dim          */
+  int32_t dtype;      /* DSMOE_BF16          */
+  int32_t is_causal;
+  int32_t q_start;
+  float softmax_scale;
+} dsmoe_mla_dims;
+size_t dsmoe_mla_attn_workspace_size(const dsmoe_mla_dims* dims);
+int dsmoe_mla_attn_fwd(const void* q_nope, const void* q_pe, const void* ctx_kv, const void* ctx_pe,
+                       const void* wkv_b_k, const void* wkv_b_v, const dsmoe_mla_dims* dims, void* out,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,108 @@
+"""CPU restatement of the reference MLA attention — TEST INFRASTRUCTURE ONLY.
+
+Parity oracle for ``dsmoe.mla`` (the HIP kernels in ``csrc/mla.hip``).  Only
+``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg
+may import it, and only as the checker / the timed CPU baseline.
+
+* ``mla_attention_oracle`` <- ``models/mla_triton.py:73-183`` (the fused
+  kernel ``_mla_flash_fwd_kernel`` as launched by ``triton_mla_attention``,
+  ``:303-329``): per (batch, head) K_nope = ctx_kv W_k^T, V = ctx_kv W_v^T
+  (``:146-147``), scores = scale ([q_nope | q_pe] . [K_nope | ctx_pe])
+  (``:154-155``), causal mask key <= query + q_start only when ``is_causal``
+  (``:157-160``), softmax over keys, output (B, S_q, H, D_v) (``:178-183``).
+  Evaluated in float64 from the given (bf16-representable) inputs.
+* ``square_mask=True`` adds what ``mla_attention_reference``
+  (``models/mla_triton.py:28-68``) also does: for ``is_causal=False`` with
+  ``S_q == S_kv`` it applies a triu(-inf) mask anyway (``:52-57``), which the
+  fused kernel it documents does not.  The HIP path follows the kernel; the
+  flag exists so the tests can state the difference.
+
+Pinned by (``tests/test_mla_oracle.py``): torch's
+``scaled_dot_product_attention`` in float64 on separately materialised K and
+V; the absorbed formulation (scores through q_nope W_k and the latent cache,
+output through the latent then W_v^T), which associates every product
+differently; closed forms (one key gives its V row, equal scores give the mean
+of the visible V rows); and the reference's own CPU test cases
+(``tests/test_mla_triton.py:68-110``: a last-position query attends every key,
+q_start offsets block future keys).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+
+def _f64(t) -> np.ndarray:
+    if hasattr(t, "detach"):
+        import torch
+        t = t.detach().cpu().to(torch.float64).numpy()
+    return np.asarray(t, dtype=np.float64)
+
+
+def mla_kv_oracle(ctx_kv, ctx_pe, wkv_b_k, wkv_b_v):
+    """Materialised K = [ctx_kv W_k^T | ctx_pe] (B, H, S_kv, Dn + Dr) and
+    V = ctx_kv W_v^T (B, H, S_kv, Dv) (models/mla_triton.py:146-152)."""
+    kv, pe, wk, wv = map(_f64, (ctx_kv, ctx_pe, wkv_b_k, wkv_b_v))
+    k_nope = np.einsum("bsr,hdr->bhsd", kv, wk)
+    v = np.einsum("bsr,hdr->bhsd", kv, wv)
+    B, H, S, _ = k_nope.shape
+    k = np.concatenate([k_nope, np.broadcast_to(pe[:, None], (B, H, S, pe.shape[-1]))], axis=-1)
+    return k, v
+
+
+def mla_mask_oracle(S_q: int, S_kv: int, is_causal: bool, q_start: int, square_mask: bool = False) -> np.ndarray:
+    """Boolean (S_q, S_kv): True where query i may attend key j."""
+    allow = np.ones((S_q, S_kv), dtype=bool)
+    if is_causal:
+        allow = (np.arange(S_q)[:, None] + q_start) >= np.arange(S_kv)[None, :]
+    elif square_mask and S_q == S_kv:
+        allow = np.arange(S_q)[:, None] >= np.arange(S_kv)[None, :]
+    return allow
+
+
+def mla_attention_oracle(q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v, softmax_scale: float,
+                         is_causal: bool = False, q_start: int = 0, square_mask: bool = False) -> np.ndarray:
+    """(B, S_q, H, D_v) float64 attention output (models/mla_triton.py:73-183)."""
+    qn, qp = _f64(q_nope), _f64(q_pe)
+    k, v = mla_kv_oracle(ctx_kv, ctx_pe, wkv_b_k, wkv_b_v)
+    q = np.concatenate([qn, qp], axis=-1)                      # (B, H, S_q, Dn + Dr)
+    s = np.einsum("bhqd,bhkd->bhqk", q, k) * float(softmax_scale)
+    allow = mla_mask_oracle(q.shape[2], k.shape[2], is_causal, q_start, square_mask)
+    s = np.where(allow[None, None], s, -np.inf)
+    s = s - s.max(axis=-1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(axis=-1, keepdims=True)
+    o = np.einsum("bhqk,bhkd->bhqd", p, v)
+    return np.ascontiguousarray(o.transpose(0, 2, 1, 3))
+
+
+def mla_attention_absorbed(q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v, softmax_scale: float,
+                           is_causal: bool = False, q_start: int = 0) -> np.ndarray:
+    """The same attention through the latent space (models/mla.py:149-152,
+    192-202 associate it this way): scores = (q_nope W_k) ctx_kv^T +
+    q_pe ctx_pe^T, output = (P ctx_kv) W_v^T.  A check of the oracle, not a
+    second oracle."""
+    qn, qp, kv, pe, wk, wv = map(_f64, (q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v))
+    q_abs = np.einsum("bhqd,hdr->bhqr", qn, wk)
+    s = (np.einsum("bhqr,bkr->bhqk", q_abs, kv) + np.einsum("bhqd,bkd->bhqk", qp, pe)) * float(softmax_scale)
+    allow = mla_mask_oracle(qn.shape[2], kv.shape[1], is_causal, q_start)
+    s = np.where(allow[None, None], s, -np.inf)
+    s = s - s.max(axis=-1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(axis=-1, keepdims=True)
+    lat = np.einsum("bhqk,bkr->bhqr", p, kv)
+    o = np.einsum("bhqr,hdr->bhqd", lat, wv)
+    return np.ascontiguousarray(o.transpose(0, 2, 1, 3))
+
+
+def mla_flops(B: int, H: int, S_q: int, S_kv: int, R: int, Dn: int, Dr: int, Dv: int, is_causal: bool,
+              q_start: int = 0) -> dict:
+    """Algorithmic flops: attention over the visible (query, key) pairs
+    (2 (Dn + Dr) + 2 Dv per pair) and the one-pass K, V materialisation
+    (2 R (Dn + Dv) per (batch, head, key))."""
+    if is_causal:
+        vis = int(np.clip(np.arange(S_q) + q_start + 1, 0, S_kv).sum())
+    else:
+        vis = S_q * S_kv
+    attn = 2.0 * B * H * vis * (Dn + Dr + Dv)
+    kv = 2.0 * B * H * S_kv * R * (Dn + Dv)
+    return {"attention": attn, "kv": kv, "total": attn + kv, "pairs": B * H * vis}

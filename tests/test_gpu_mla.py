@@ -1,0 +1,121 @@
+"""GPU parity of the MLA attention kernels (csrc/mla.hip) against the float64
+oracle (oracle/mla_ref.py) on the same bf16 inputs (MI355X only).
+
+Bar: the output is bf16 and the kernel rounds K, V and the probabilities to
+bf16 for the MFMAs (the reference kernel does the same with p,
+models/mla_triton.py:175), so the check is |gpu - oracle| <= 1e-2 + 1e-2 |oracle|
+elementwise, the tolerance of the reference's own GPU test
+(tests/test_mla_triton.py:136).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle.mla_ref import mla_attention_oracle
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+ATOL = RTOL = 1e-2
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _lib():
+    import dsmoe._lib as L
+    L.load()
+    assert torch.cuda.is_available()
+    yield
+
+
+def _inputs(B, H, S_q, S_kv, R, Dn, Dr, Dv, seed=0, wscale=0.1):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    rn = lambda *s: torch.randn(*s, generator=g, device=DEV, dtype=torch.float32)
+    t = (rn(B, H, S_q, Dn), rn(B, H, S_q, Dr), rn(B, S_kv, R), rn(B, S_kv, Dr), rn(H, Dn, R) * wscale,
+         rn(H, Dv, R) * wscale)
+    return tuple(x.to(torch.bfloat16) for x in t), (Dn + Dr) ** -0.5
+
+
+def _check(B, H, S_q, S_kv, R, Dn, Dr, Dv, causal, q_start, seed=0, wscale=0.1, scale=None):
+    from dsmoe.mla import mla_attention
+    print(f"[mla] B={B} H={H} S_q={S_q} S_kv={S_kv} R={R} Dn={Dn} Dr={Dr} Dv={Dv} causal={causal} "
+          f"q_start={q_start}", flush=True)
+    ts, sc = _inputs(B, H, S_q, S_kv, R, Dn, Dr, Dv, seed, wscale)
+    sc = sc if scale is None else scale
+    out = mla_attention(*ts, sc, is_causal=causal, q_start=q_start)
+    torch.cuda.synchronize()
+    assert out.shape == (B, S_q, H, Dv) and out.dtype == torch.bfloat16
+    ref = mla_attention_oracle(*[t.cpu() for t in ts], sc, is_causal=causal, q_start=q_start)
+    got = out.float().cpu().numpy().astype(np.float64)
+    err = np.abs(got - ref)
+    bound = ATOL + RTOL * np.abs(ref)
+    print(f"[mla]   max |err| {err.max():.3e}, max err/bound {(err / bound).max():.3f}", flush=True)
+    assert np.isfinite(got).all()
+    assert (err <= bound).all()
+    return out, ref
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_reference_gpu_test_shape(causal):
+    # tests/test_mla_triton.py:126-136
+    _check(1, 4, 16, 16, 32, 16, 8, 24, causal, 0)
+
+
+def test_pretrain_1650_2m_shape():
+    # configs/pretrain_1650_2m.yaml:14-26 (micro batch 2, full sequence, causal)
+    _check(2, 4, 128, 128, 16, 16, 16, 16, True, 0)
+
+
+def test_pretrain_a100_422m_shape():
+    # configs/pretrain_a100_422m.yaml:22-34 at one sequence of the micro batch
+    _check(1, 12, 2048, 2048, 192, 48, 24, 64, True, 0)
+
+
+@pytest.mark.parametrize("S_q,S_kv,q_start", [(100, 300, 200), (1, 777, 776), (65, 130, 0), (3, 5, 2)])
+def test_chunked_prefill_and_decode(S_q, S_kv, q_start):
+    _check(2, 3, S_q, S_kv, 64, 32, 16, 32, True, q_start, seed=1)
+
+
+@pytest.mark.parametrize("S_q,S_kv", [(130, 100), (16, 16), (1, 1), (200, 65)])
+def test_non_causal_ragged(S_q, S_kv):
+    # no mask without is_causal, square or not (the fused kernel's semantics)
+    _check(1, 2, S_q, S_kv, 48, 24, 8, 40, False, 0, seed=2)
+
+
+def test_wide_dims_and_odd_sizes():
+    _check(1, 2, 200, 200, 256, 128, 64, 128, True, 0, seed=3, wscale=0.05)
+    _check(2, 1, 70, 90, 8, 6, 4, 10, True, 5, seed=4, wscale=0.3)
+    _check(1, 1, 40, 40, 256, 192, 64, 256, False, 0, seed=5, wscale=0.05)
+
+
+def test_negative_and_large_scale():
+    _check(1, 2, 64, 64, 32, 16, 16, 32, True, 0, seed=6, scale=-0.2)
+    _check(1, 2, 64, 64, 32, 16, 16, 32, True, 0, seed=7, scale=2.0)
+
+
+def test_backward_matches_float64_attention():
+    from dsmoe.mla import mla_attention
+    ts, sc = _inputs(1, 2, 24, 24, 16, 8, 8, 16, seed=8, wscale=0.3)
+    ins = [t.clone().requires_grad_() for t in ts]
+    out = mla_attention(*ins, sc, is_causal=True)
+    dout = torch.randn_like(out)
+    out.backward(dout)
+    ref_in = [t.detach().cpu().double().requires_grad_() for t in ts]
+    qn, qp, kv, pe, wk, wv = ref_in
+    k = torch.cat([torch.einsum("bsr,hdr->bhsd", kv, wk), pe[:, None].expand(1, 2, 24, 8)], dim=-1)
+    v = torch.einsum("bsr,hdr->bhsd", kv, wv)
+    o = torch.nn.functional.scaled_dot_product_attention(torch.cat([qn, qp], -1), k, v, is_causal=True, scale=sc)
+    o.permute(0, 2, 1, 3).backward(dout.cpu().double())
+    for a, b in zip(ins, ref_in):
+        g, r = a.grad.float().cpu().double(), b.grad
+        assert (g - r).abs().max() <= 2e-2 + 2e-2 * r.abs().max(), float((g - r).abs().max())
+
+
+def test_rejects_what_the_reference_rejects():
+    from dsmoe.mla import mla_attention
+    ts, sc = _inputs(1, 1, 4, 4, 16, 8, 8, 8)
+    big = torch.zeros(1, 4, 300, dtype=torch.bfloat16, device=DEV)
+    wk = torch.zeros(1, 8, 300, dtype=torch.bfloat16, device=DEV)
+    wv = torch.zeros(1, 8, 300, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError, match="256"):
+        mla_attention(ts[0], ts[1], big, ts[3], wk, wv, sc)
+    with pytest.raises(ValueError, match="bf16"):
+        mla_attention(*[t.float() for t in ts], sc)
