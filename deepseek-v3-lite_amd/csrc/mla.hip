@@ -61,100 +61,192 @@ struct MlaArgs {
   int Rp, DQKp, DVp, S_kvp;
   int causal, q_start;
   int ksplit;             // K row = [k_hi | pe | k_lo] (else [k | pe])
-  float c;                // softmax_scale * log2(e)
+  int negq;               // softmax_scale < 0: q is negated on load and c = |scale| log2(e)
+  int qvec;               // 16-byte query loads (Dn, Dr % 8 == 0, q_nope / q_pe 16-byte aligned)
+  int kvvec;              // 16-byte latent / weight row loads (R % 8 == 0, aligned)
+  int pevec;              // 16-byte rope copies and K, V row pieces (Dn, Dr % 8 == 0, ctx_pe aligned)
+  int ovec;               // 8-byte output stores (Dv % 4 == 0, out 8-byte aligned)
+  float c;                // |softmax_scale| * log2(e) >= 0
 };
 
 // ---------------------------------------------------------------- K, V materialisation
-// Grid (B * S_kvp / 64, H).  A workgroup takes 64 latent rows of one batch
-// and one head and walks the head's Dn + Dv output columns in chunks of 64:
-// LDS holds the rows (64 x Rp) and the chunk's weight rows (64 x Rp), each
-// row padded by 16 bytes so the 16-byte fragment reads of 16 lanes hit 16
-// distinct bank groups.  Wave (wr, wc) computes rows 32 wr.., columns 32 wc..
-// with the latent rows as the first MFMA operand: a lane holds one output
-// column and 16 rows, so each store instruction writes 32 consecutive
-// columns of a row.  Rows past S_kv are loaded as zeros, so their K and V
-// rows come out zero; the rope and padding columns are written directly.
+// Grid (B * S_kvp / 64, H).  A workgroup computes 64 latent rows of one batch
+// against one head's Dn + Dv weight rows, in column passes of up to 128.
+// Wave (wr, wc) owns rows 32 wr.. and the pass's 32-column tiles wc, wc + 2;
+// it loads its MFMA fragments straight from global memory (16 bytes per lane
+// and K step, a row's 32 bytes per lane pair; every K step of the latent rows
+// and then of one weight tile in flight at once), with the latent rows as the
+// first operand, so a lane holds one output column and 16 rows.  The bf16
+// results (and the k_lo parts) are staged in LDS and leave as 16-byte row
+// pieces.  Rows past S_kv read as zeros, so their K and V rows come out
+// zero; the rope and padding columns are copied directly.
+// NKS = Rp / 16 K steps with 16-byte loads (R % 8 == 0, aligned rows): every
+// fragment load of a batch is issued unconditionally from a valid address
+// before any of them is used (a load under a branch, or one whose result is
+// used at once, makes the compiler wait for it there).  Dead latent rows read
+// row S_kv - 1 (finite values; their K and V rows then get probability 0 or
+// are never read), dead weight rows read the last one (never stored), and
+// with R % 16 == 8 the weight columns past R of the last K step are zeroed
+// after the batch.  NKS = 0: element loads, any R.
+constexpr int MLA_KVN = 128;   // output columns per pass
+constexpr int MLA_KS = 16;     // K steps of 16 at most (R <= 256)
+
+template <int NKS>
 __global__ __launch_bounds__(256) void mla_kv_kernel(const MlaArgs a) {
   extern __shared__ __attribute__((aligned(16))) char mla_kv_smem[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wr = wave >> 1, wc = wave & 1;
+  const int hi = lane >> 5, l32 = lane & 31;
   const int tiles_per_b = a.S_kvp / MLA_RB;
   const int b = blockIdx.x / tiles_per_b;
   const int s0 = (blockIdx.x - b * tiles_per_b) * MLA_RB;
   const int h = blockIdx.y;
-  const int rs = a.Rp * 2 + 16;            // LDS row stride (bytes)
-  char* sa = mla_kv_smem;                  // latent rows
-  char* sb = mla_kv_smem + MLA_RB * rs;    // weight rows of the chunk
-  const int cpr = a.Rp / 8;                // 16-byte chunks per row
-  // latent rows (zeros past S_kv and past R); 16-byte loads when rows are
-  // 16-byte aligned (R % 8 == 0)
-  const bool vec = (a.R & 7) == 0;
-  auto load_row8 = [&](const bf16_t* row, bool ok, int c) -> mla_u32x4 {
-    if (!ok) return mla_u32x4{0u, 0u, 0u, 0u};
-    if (vec) return *reinterpret_cast<const mla_u32x4*>(row + c * 8);
-    bf16_t v[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = c * 8 + e < a.R ? row[c * 8 + e] : bf16_t(0);
-    return *reinterpret_cast<const mla_u32x4*>(v);
-  };
-  for (int i = tid; i < MLA_RB * cpr; i += 256) {
-    const int r = i / cpr, c = i - r * cpr;
-    const int s = s0 + r;
-    *reinterpret_cast<mla_u32x4*>(sa + r * rs + c * 16) =
-        load_row8(a.ctx_kv + ((int64_t)b * a.S_kv + s) * a.R, s < a.S_kv && c * 8 < a.R, c);
-  }
+  const int nks = a.Rp / 16;
+  const int ncols = a.Dn + a.Dv;
+  const int lo_end = a.ksplit ? 2 * a.Dn + a.Dr : a.Dn + a.Dr;
+  const bool vout = a.pevec;   // 16-byte output pieces stay in one part
   const int64_t bh = (int64_t)b * a.H + h;
   bf16_t* krow0 = a.kbuf + (bh * a.S_kvp + s0) * a.DQKp;
   bf16_t* vrow0 = a.vbuf + (bh * a.S_kvp + s0) * a.DVp;
-  // rope columns and the zero padding of K (the k_lo columns come from the
-  // GEMM below), padding of V
-  const int lo_end = a.ksplit ? 2 * a.Dn + a.Dr : a.Dn + a.Dr;
-  for (int i = tid; i < MLA_RB * (a.DQKp - a.Dn); i += 256) {
-    const int r = i / (a.DQKp - a.Dn), j = a.Dn + (i - r * (a.DQKp - a.Dn));
-    const int s = s0 + r;
-    if (j >= a.Dn + a.Dr && j < lo_end) continue;
-    bf16_t v = bf16_t(0);
-    if (s < a.S_kv && j < a.Dn + a.Dr) v = a.ctx_pe[((int64_t)b * a.S_kv + s) * a.Dr + (j - a.Dn)];
-    krow0[(int64_t)r * a.DQKp + j] = v;
-  }
-  for (int i = tid; i < MLA_RB * (a.DVp - a.Dv); i += 256) {
-    const int r = i / (a.DVp - a.Dv), j = a.Dv + (i - r * (a.DVp - a.Dv));
-    vrow0[(int64_t)r * a.DVp + j] = bf16_t(0);
-  }
-  const int ncols = a.Dn + a.Dv;
-  for (int n0 = 0; n0 < ncols; n0 += 64) {
-    __syncthreads();   // the previous chunk's weight rows are read (first pass: the latent rows are written)
-    for (int i = tid; i < 64 * cpr; i += 256) {
-      const int r = i / cpr, c = i - r * cpr;
-      const int n = n0 + r;
-      const bf16_t* wrow = n < a.Dn ? a.w_k + ((int64_t)h * a.Dn + n) * a.R
-                                    : a.w_v + ((int64_t)h * a.Dv + (n - a.Dn)) * a.R;
-      *reinterpret_cast<mla_u32x4*>(sb + r * rs + c * 16) = load_row8(wrow, n < ncols && c * 8 < a.R, c);
-    }
-    __syncthreads();
-    mla_f32x16 acc;
+  constexpr int KS = NKS > 0 ? NKS : MLA_KS;
+  // 8 bf16 of a row at column c (zeros past R or for a dead row); row is a
+  // valid row address (clamped) on the vector path
+  auto frag = [&](const bf16_t* row, bool ok, int c) -> bf16x8_t {
+    mla_u32x4 v = {0u, 0u, 0u, 0u};
+    if (NKS > 0) {
+      v = *reinterpret_cast<const mla_u32x4*>(row + min(c, a.R - 8));
+    } else if (ok) {
+      bf16_t e8[8];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
-    const int rl = 32 * wr + (lane & 31), nl = 32 * wc + (lane & 31);
-    for (int k = 0; k < a.Rp; k += 16) {
-      const int cb = (k + 8 * (lane >> 5)) * 2;
-      const bf16x8_t fw = *reinterpret_cast<const bf16x8_t*>(sb + nl * rs + cb);
-      const bf16x8_t fx = *reinterpret_cast<const bf16x8_t*>(sa + rl * rs + cb);
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fx, fw, acc, 0, 0, 0);
+      for (int e = 0; e < 8; ++e) e8[e] = c + e < a.R ? row[c + e] : bf16_t(0);
+      v = *reinterpret_cast<const mla_u32x4*>(e8);
     }
-    // lane: column n = n0 + 32 wc + (lane & 31), latent rows
-    // 32 wr + 8 (i / 4) + 4 (lane >> 5) + i % 4
-    const int n = n0 + nl;
-    if (n < ncols) {
+    return __builtin_bit_cast(bf16x8_t, v);
+  };
+  // latent fragments of this wave's rows, every K step
+  const int srow = s0 + 32 * wr + l32;
+  const bf16_t* xrow = a.ctx_kv + ((int64_t)b * a.S_kv + min(srow, a.S_kv - 1)) * a.R;
+  bf16x8_t fx[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks)
+    if (NKS > 0 || ks < nks) fx[ks] = frag(xrow, srow < a.S_kv, 16 * ks + 8 * hi);
+  // rope columns [Dn, Dn + Dr) and zero columns [lo_end, DQKp) of K, [Dv, DVp) of V
+  {
+    const int r = tid >> 2, q = tid & 3;    // four threads per row
+    const int s = s0 + r;
+    const bool live = s < a.S_kv;
+    bf16_t* kr = krow0 + (int64_t)r * a.DQKp;
+    const bf16_t* pe = a.ctx_pe + ((int64_t)b * a.S_kv + (live ? s : 0)) * a.Dr;
+    if (vout) {
+      for (int j = 8 * q; j < a.Dr; j += 32)
+        *reinterpret_cast<mla_u32x4*>(kr + a.Dn + j) =
+            live ? *reinterpret_cast<const mla_u32x4*>(pe + j) : mla_u32x4{0u, 0u, 0u, 0u};
+    } else {
+      for (int j = q; j < a.Dr; j += 4) kr[a.Dn + j] = live ? pe[j] : bf16_t(0);
+    }
+    for (int j = lo_end + q; j < a.DQKp; j += 4) kr[j] = bf16_t(0);
+    for (int j = a.Dv + q; j < a.DVp; j += 4) vrow0[(int64_t)r * a.DVp + j] = bf16_t(0);
+  }
+  bf16_t* sho = reinterpret_cast<bf16_t*>(mla_kv_smem);   // staged outputs: hi [64][128], lo [64][128]
+  char* sw = mla_kv_smem;                                    // (first) the pass's weight rows, LDS rows rs
+  const int rs = a.Rp * 2 + 16;
+  const int cpr = a.Rp / 8;
+  for (int n0 = 0; n0 < ncols; n0 += MLA_KVN) {
+    const int np = min(MLA_KVN, ncols - n0);
+    if (n0 > 0) __syncthreads();              // the previous pass's staged outputs are stored
+    if (NKS > 0) {
+      // the pass's weight rows into LDS: one batch of loads per thread, all
+      // issued before the stores (row and chunk indices clamped, so every
+      // load reads valid memory; columns past R are zeroed afterwards)
+      constexpr int PER = NKS > 0 ? (MLA_KVN * NKS * 2 + 255) / 256 : 1;
+      const int tot = ((np + 31) / 32 * 32) * cpr;
+      mla_u32x4 wv[PER];
+#pragma unroll
+      for (int u = 0; u < PER; ++u) {
+        const int i = min(tid + 256 * u, tot - 1);
+        const int r = i / cpr, c = i - r * cpr;
+        const int nc = min(n0 + r, ncols - 1);
+        const bf16_t* wrow = nc < a.Dn ? a.w_k + ((int64_t)h * a.Dn + nc) * a.R
+                                       : a.w_v + ((int64_t)h * a.Dv + (nc - a.Dn)) * a.R;
+        wv[u] = *reinterpret_cast<const mla_u32x4*>(wrow + min(c * 8, a.R - 8));
+      }
+#pragma unroll
+      for (int u = 0; u < PER; ++u) {
+        const int i = tid + 256 * u;
+        if (i < tot) {
+          const int r = i / cpr, c = i - r * cpr;
+          *reinterpret_cast<mla_u32x4*>(sw + r * rs + c * 16) = c * 8 < a.R ? wv[u] : mla_u32x4{0u, 0u, 0u, 0u};
+        }
+      }
+      __syncthreads();
+    }
+    mla_f32x16 accs[MLA_KVN / 64];
+#pragma unroll
+    for (int j = 0; j < MLA_KVN / 64; ++j) {
+      const int t = wc + 2 * j;
+      if (32 * t >= np) continue;
+      const int n = n0 + 32 * t + l32;        // this lane's weight row (output column)
+      bf16x8_t fw[KS];
+      if (NKS > 0) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+          fw[ks] = *reinterpret_cast<const bf16x8_t*>(sw + (32 * t + l32) * rs + (16 * ks + 8 * hi) * 2);
+      } else {
+        const int nc = min(n, ncols - 1);
+        const bf16_t* wrow = nc < a.Dn ? a.w_k + ((int64_t)h * a.Dn + nc) * a.R
+                                       : a.w_v + ((int64_t)h * a.Dv + (nc - a.Dn)) * a.R;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+          if (ks < nks) fw[ks] = frag(wrow, n < ncols, 16 * ks + 8 * hi);
+      }
+      mla_f32x16& acc = accs[j];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        if (NKS > 0 || ks < nks) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fx[ks], fw[ks], acc, 0, 0, 0);
+    }
+    if (NKS > 0) __syncthreads();             // every wave is done with the weight rows
+#pragma unroll
+    for (int j = 0; j < MLA_KVN / 64; ++j) {
+      const int t = wc + 2 * j;
+      if (32 * t >= np) continue;
+      const mla_f32x16& acc = accs[j];
+      const int col = 32 * t + l32;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int r = 32 * wr + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+        const int r = 32 * wr + 8 * (i >> 2) + 4 * hi + (i & 3);
         const bf16_t v = f2bf(acc[i]);
+        sho[r * MLA_KVN + col] = v;
+        sho[MLA_RB * MLA_KVN + r * MLA_KVN + col] = f2bf(acc[i] - bf2f(v));
+      }
+    }
+    __syncthreads();
+    for (int i = tid; i < MLA_RB * (MLA_KVN / 8); i += 256) {
+      const int r = i / (MLA_KVN / 8), c8 = (i - r * (MLA_KVN / 8)) * 8;
+      if (c8 >= np) continue;
+      const int n = n0 + c8;
+      const bf16_t* hp = sho + r * MLA_KVN + c8;
+      const bf16_t* lp = sho + MLA_RB * MLA_KVN + r * MLA_KVN + c8;
+      if (vout && c8 + 8 <= np) {
+        const mla_u32x4 vh = *reinterpret_cast<const mla_u32x4*>(hp);
         if (n < a.Dn) {
-          krow0[(int64_t)r * a.DQKp + n] = v;
-          if (a.ksplit) krow0[(int64_t)r * a.DQKp + a.Dn + a.Dr + n] = f2bf(acc[i] - bf2f(v));
+          *reinterpret_cast<mla_u32x4*>(krow0 + (int64_t)r * a.DQKp + n) = vh;
+          if (a.ksplit)
+            *reinterpret_cast<mla_u32x4*>(krow0 + (int64_t)r * a.DQKp + a.Dn + a.Dr + n) =
+                *reinterpret_cast<const mla_u32x4*>(lp);
         } else {
-          vrow0[(int64_t)r * a.DVp + (n - a.Dn)] = v;
+          *reinterpret_cast<mla_u32x4*>(vrow0 + (int64_t)r * a.DVp + (n - a.Dn)) = vh;
+        }
+      } else {
+        for (int e = 0; e < 8 && c8 + e < np; ++e) {
+          const int ne = n + e;
+          if (ne < a.Dn) {
+            krow0[(int64_t)r * a.DQKp + ne] = hp[e];
+            if (a.ksplit) krow0[(int64_t)r * a.DQKp + a.Dn + a.Dr + ne] = lp[e];
+          } else {
+            vrow0[(int64_t)r * a.DVp + (ne - a.Dn)] = hp[e];
+          }
         }
       }
     }
@@ -218,9 +310,30 @@ __global__ __launch_bounds__(256) void mla_fa_kernel(const MlaArgs a) {
   // query fragments: step st holds columns 16 st + 8 hi .. +7 of
   // [q_nope | q_pe | q_nope (split K) | 0]
   bf16x8_t qf[NSTEP];
-  {
-    const bf16_t* qn = a.q_nope + (bh * a.S_q + qi) * a.Dn;
-    const bf16_t* qp = a.q_pe + (bh * a.S_q + qi) * a.Dr;
+  const bf16_t* qn = a.q_nope + (bh * a.S_q + qi) * a.Dn;
+  const bf16_t* qp = a.q_pe + (bh * a.S_q + qi) * a.Dr;
+  if (a.qvec) {
+    // each 8-column group lies in one part: one 16-byte load, issued
+    // unconditionally from a valid address (the row clamped to S_q - 1, a
+    // padding group reads q_nope) and zeroed by a select
+    const int qc = min(qi, a.S_q - 1);
+    const bf16_t* qnc = a.q_nope + (bh * a.S_q + qc) * a.Dn;
+    const bf16_t* qpc = a.q_pe + (bh * a.S_q + qc) * a.Dr;
+    const int qend = a.ksplit ? 2 * a.Dn + a.Dr : a.Dn + a.Dr;
+#pragma unroll
+    for (int st = 0; st < NSTEP; ++st) {
+      const int d = 16 * st + 8 * hi;
+      // padding groups read real q values: K is zero there; a dead query's
+      // row is finite and never stored
+      const bf16_t* src = d < a.Dn ? qnc + d : d < a.Dn + a.Dr ? qpc + (d - a.Dn) : d < qend ? qnc + (d - a.Dn - a.Dr) : qnc;
+      qf[st] = *reinterpret_cast<const bf16x8_t*>(src);
+    }
+    if (a.negq)
+#pragma unroll
+      for (int st = 0; st < NSTEP; ++st)
+        qf[st] = __builtin_bit_cast(bf16x8_t, __builtin_bit_cast(mla_u32x4, qf[st]) ^
+                                                   mla_u32x4{0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u});
+  } else {
 #pragma unroll
     for (int st = 0; st < NSTEP; ++st) {
       bf16_t v[8];
@@ -235,6 +348,7 @@ __global__ __launch_bounds__(256) void mla_fa_kernel(const MlaArgs a) {
             v[e] = qp[d - a.Dn];
           else if (a.ksplit && d < 2 * a.Dn + a.Dr)
             v[e] = qn[d - a.Dn - a.Dr];
+          if (a.negq) v[e] ^= 0x8000;   // exact: the scores change sign, c stays >= 0
         }
       }
       qf[st] = *reinterpret_cast<const bf16x8_t*>(v);
@@ -248,43 +362,44 @@ __global__ __launch_bounds__(256) void mla_fa_kernel(const MlaArgs a) {
   const bf16_t* kg = a.kbuf + bh * a.S_kvp * C::DQKp;
   const bf16_t* vg = a.vbuf + bh * a.S_kvp * C::DVp;
 
-  mla_u32x4 kst[C::NLK], vst[C::NLV];
-  auto gload = [&](int kb) {
+  // tiles are staged through registers two blocks ahead (two register sets)
+  mla_u32x4 kst[2][C::NLK], vst[2][C::NLV];
+  auto gload = [&](int kb, mla_u32x4(&ks)[C::NLK], mla_u32x4(&vs)[C::NLV]) {
     const int k0 = kb * MLA_KB;
 #pragma unroll
     for (int i = 0; i < C::NLK; ++i) {
       const int c = tid + 256 * i;
-      if (c < C::KCH) {
+      if (C::KCH % 256 == 0 || c < C::KCH) {
         const int r = c / (C::DQKp / 8), cc = c - r * (C::DQKp / 8);
-        kst[i] = *reinterpret_cast<const mla_u32x4*>(kg + (int64_t)(k0 + r) * C::DQKp + cc * 8);
+        ks[i] = *reinterpret_cast<const mla_u32x4*>(kg + (int64_t)(k0 + r) * C::DQKp + cc * 8);
       }
     }
 #pragma unroll
     for (int i = 0; i < C::NLV; ++i) {
       const int c = tid + 256 * i;
-      if (c < C::VCH) {
+      if (C::VCH % 256 == 0 || c < C::VCH) {
         const int r = c / (C::DVp / 8), cc = c - r * (C::DVp / 8);
-        vst[i] = *reinterpret_cast<const mla_u32x4*>(vg + (int64_t)(k0 + r) * C::DVp + cc * 8);
+        vs[i] = *reinterpret_cast<const mla_u32x4*>(vg + (int64_t)(k0 + r) * C::DVp + cc * 8);
       }
     }
   };
-  auto lstore = [&](int buf) {
+  auto lstore = [&](int buf, const mla_u32x4(&ks)[C::NLK], const mla_u32x4(&vs)[C::NLV]) {
     char* kt = mla_smem + buf * C::BUF;
     char* vt = kt + C::KT;
 #pragma unroll
     for (int i = 0; i < C::NLK; ++i) {
       const int c = tid + 256 * i;
-      if (c < C::KCH) {
+      if (C::KCH % 256 == 0 || c < C::KCH) {
         const int r = c / (C::DQKp / 8), cc = c - r * (C::DQKp / 8);
-        *reinterpret_cast<mla_u32x4*>(kt + r * C::KRS + cc * 16) = kst[i];
+        *reinterpret_cast<mla_u32x4*>(kt + r * C::KRS + cc * 16) = ks[i];
       }
     }
 #pragma unroll
     for (int i = 0; i < C::NLV; ++i) {
       const int c = tid + 256 * i;
-      if (c < C::VCH) {
+      if (C::VCH % 256 == 0 || c < C::VCH) {
         const int r = c / (C::DVp / 8), cc = c - r * (C::DVp / 8);
-        *reinterpret_cast<mla_u32x4*>(vt + r * (C::DVp * 2) + (((2 * cc) ^ mla_vswz<NV>(r)) << 3)) = vst[i];
+        *reinterpret_cast<mla_u32x4*>(vt + r * (C::DVp * 2) + (((2 * cc) ^ mla_vswz<NV>(r)) << 3)) = vs[i];
       }
     }
   };
@@ -297,14 +412,11 @@ __global__ __launch_bounds__(256) void mla_fa_kernel(const MlaArgs a) {
   float m = -INFINITY, l = 0.0f;
   const int qpos = qi + a.q_start;
 
-  if (nkb > 0) {
-    gload(0);
-    lstore(0);
-  }
-  __syncthreads();
-  for (int kb = 0; kb < nkb; ++kb) {
+  // block kb sits in LDS buffer kb & 1 and, before that, in register set kb & 1
+  auto block = [&](int kb, mla_u32x4(&ks_cur)[C::NLK], mla_u32x4(&vs_cur)[C::NLV], mla_u32x4(&ks_nxt)[C::NLK],
+                   mla_u32x4(&vs_nxt)[C::NLV]) {
     const int k0 = kb * MLA_KB;
-    if (kb + 1 < nkb) gload(kb + 1);
+    if (kb + 2 < nkb) gload(kb + 2, ks_cur, vs_cur);
     const char* kt = mla_smem + (kb & 1) * C::BUF;
     const char* vt = kt + C::KT;
     // scores: sub-tile t, register i -> key k0 + 32 t + 8 (i / 4) + 4 hi + i % 4
@@ -319,12 +431,8 @@ __global__ __launch_bounds__(256) void mla_fa_kernel(const MlaArgs a) {
         s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], s[t], 0, 0, 0);
       }
     }
-    // scores in log2 units (scale * log2 e); masks: keys past S_kv and, with
-    // the causal mask, keys past the query
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s[t][i] *= a.c;
+    // masks: keys past S_kv and, with the causal mask, keys past the query;
+    // p = exp2(c s - c m) with c >= 0, so the running max of s is the max
     const bool edge = k0 + MLA_KB > a.S_kv || (a.causal && k0 + MLA_KB - 1 > q0 + a.q_start);
     if (edge) {
 #pragma unroll
@@ -343,8 +451,9 @@ __global__ __launch_bounds__(256) void mla_fa_kernel(const MlaArgs a) {
     mb = mla_pair_max(mb);
     const float mn = fmaxf(m, mb);
     // a query whose keys so far are all masked keeps p = 0 (mn = -inf)
-    const float mc = mn == -INFINITY ? 0.0f : mn;
-    const float alpha = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mc);
+    const float mc = mn == -INFINITY ? 0.0f : mn * a.c;
+    const float alpha = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(fmaf(m, a.c, -mc));
+    const bool moved = m != mn;
     m = mn;
     float ls = 0.0f;
     bf16x8_t pf[4];
@@ -355,7 +464,7 @@ __global__ __launch_bounds__(256) void mla_fa_kernel(const MlaArgs a) {
         float p[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          p[e] = __builtin_amdgcn_exp2f(s[t][8 * half + e] - mc);
+          p[e] = __builtin_amdgcn_exp2f(fmaf(s[t][8 * half + e], a.c, -mc));
           ls += p[e];
         }
         bf16x2_t w[4];
@@ -367,10 +476,13 @@ __global__ __launch_bounds__(256) void mla_fa_kernel(const MlaArgs a) {
         pf[2 * t + half] = __builtin_bit_cast(bf16x8_t, w);
       }
     l = l * alpha + ls;
+    // the accumulators are rescaled only when some lane's maximum moved
+    if (__builtin_amdgcn_ballot_w64(moved)) {
 #pragma unroll
-    for (int v = 0; v < NV; ++v)
+      for (int v = 0; v < NV; ++v)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) o[v][i] *= alpha;
+        for (int i = 0; i < 16; ++i) o[v][i] *= alpha;
+    }
     // PV: step ps covers keys k0 + 16 ps .. +15 in the order above; the V
     // operand of lane l is column 32 v + (l & 31) at the same keys
     {
@@ -392,8 +504,16 @@ __global__ __launch_bounds__(256) void mla_fa_kernel(const MlaArgs a) {
         }
       }
     }
-    if (kb + 1 < nkb) lstore((kb + 1) & 1);
+    if (kb + 1 < nkb) lstore((kb + 1) & 1, ks_nxt, vs_nxt);
     __syncthreads();
+  };
+  gload(0, kst[0], vst[0]);
+  if (nkb > 1) gload(1, kst[1], vst[1]);
+  lstore(0, kst[0], vst[0]);
+  __syncthreads();
+  for (int kb = 0; kb < nkb; kb += 2) {
+    block(kb, kst[0], vst[0], kst[1], vst[1]);
+    if (kb + 1 < nkb) block(kb + 1, kst[1], vst[1], kst[0], vst[0]);
   }
 
   // out[b, qi, h, dv]: lane holds dv = 32 v + 8 (i / 4) + 4 hi + i % 4
@@ -406,7 +526,7 @@ __global__ __launch_bounds__(256) void mla_fa_kernel(const MlaArgs a) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int dv = 32 * v + 8 * g + 4 * hi;
-      if (dv + 3 < a.Dv && (a.Dv & 3) == 0) {
+      if (a.ovec && dv + 3 < a.Dv) {
         bf16x2_t w0, w1;
         w0[0] = (__bf16)(o[v][4 * g] * inv);
         w0[1] = (__bf16)(o[v][4 * g + 1] * inv);
@@ -470,7 +590,8 @@ static MlaArgs mla_args(const dsmoe_mla_dims* d) {
   a.S_kvp = mla_pad(d->S_kv, MLA_KB);
   a.causal = d->is_causal ? 1 : 0;
   a.q_start = d->q_start;
-  a.c = d->softmax_scale * MLA_LOG2E;
+  a.negq = d->softmax_scale < 0.0f ? 1 : 0;
+  a.c = (d->softmax_scale < 0.0f ? -d->softmax_scale : d->softmax_scale) * MLA_LOG2E;
   return a;
 }
 
@@ -528,15 +649,26 @@ extern "C" int dsmoe_mla_attn_fwd(const void* q_nope, const void* q_pe, const vo
   a.w_k = static_cast<const bf16_t*>(wkv_b_k);
   a.w_v = static_cast<const bf16_t*>(wkv_b_v);
   a.out = static_cast<bf16_t*>(out);
+  auto al = [](const void* p, uintptr_t m) { return (reinterpret_cast<uintptr_t>(p) & (m - 1)) == 0; };
+  a.qvec = (a.Dn % 8 == 0 && a.Dr % 8 == 0 && al(q_nope, 16) && al(q_pe, 16)) ? 1 : 0;
+  a.kvvec = (a.R % 8 == 0 && al(ctx_kv, 16) && al(wkv_b_k, 16) && al(wkv_b_v, 16)) ? 1 : 0;
+  a.pevec = (a.Dn % 8 == 0 && a.Dr % 8 == 0 && al(ctx_pe, 16)) ? 1 : 0;
+  a.ovec = (a.Dv % 4 == 0 && al(out, 8)) ? 1 : 0;
   a.kbuf = static_cast<bf16_t*>(workspace);
   a.vbuf = a.kbuf + (size_t)a.B * a.H * a.S_kvp * a.DQKp;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const size_t kv_lds = 2 * (size_t)MLA_RB * (a.Rp * 2 + 16);
-  static const hipError_t kv_attr = hipFuncSetAttribute((const void*)mla_kv_kernel,
-                                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-  if (kv_attr != hipSuccess) return fail(DSMOE_ERR_HIP, "mla: cannot raise LDS limit");
-  hipLaunchKernelGGL(mla_kv_kernel, dim3((unsigned)(a.B * (a.S_kvp / MLA_RB)), (unsigned)a.H), dim3(256), kv_lds,
-                     st, a);
+  // the pass's weight rows, then the staged outputs (hi and lo [64][128] bf16)
+  const size_t kv_lds = std::max((size_t)MLA_KVN * (a.Rp * 2 + 16), (size_t)2 * MLA_RB * MLA_KVN * sizeof(bf16_t));
+  const dim3 kv_grid((unsigned)(a.B * (a.S_kvp / MLA_RB)), (unsigned)a.H);
+  switch (a.kvvec ? a.Rp / 16 : 0) {
+#define MLA_KV_CASE(n) \
+  case n: hipLaunchKernelGGL(mla_kv_kernel<n>, kv_grid, dim3(256), kv_lds, st, a); break;
+    MLA_KV_CASE(1) MLA_KV_CASE(2) MLA_KV_CASE(3) MLA_KV_CASE(4) MLA_KV_CASE(5) MLA_KV_CASE(6) MLA_KV_CASE(7)
+    MLA_KV_CASE(8) MLA_KV_CASE(9) MLA_KV_CASE(10) MLA_KV_CASE(11) MLA_KV_CASE(12) MLA_KV_CASE(13) MLA_KV_CASE(14)
+    MLA_KV_CASE(15) MLA_KV_CASE(16)
+#undef MLA_KV_CASE
+    default: hipLaunchKernelGGL(mla_kv_kernel<0>, kv_grid, dim3(256), kv_lds, st, a); break;
+  }
   rc = check_launch("mla_kv");
   if (rc) return rc;
   switch (a.DQKp / 16) {

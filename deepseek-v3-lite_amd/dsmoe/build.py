@@ -28,12 +28,15 @@ CFLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{INCLUDE}", f"-I{CSRC}",
 ]
+# Per-source flags: the attention kernels keep MFMA accumulators in VGPRs (their
+# online-softmax rescaling reads and writes them every key block).
+EXTRA_FLAGS = {"mla.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 SOURCES = ["api.hip", "gate.hip", "permute.hip", "gemm.hip", "gemm_qp.hip", "gemm_sk.hip", "gemm_x.hip", "gemm_xm.hip", "gemm_xq.hip", "bwd.hip", "combine.hip", "mla.hip", "probe.hip"]
 
 
 def _compile(src: Path) -> Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [HIPCC, *CFLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *CFLAGS, *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{r.stdout}\n{r.stderr}")

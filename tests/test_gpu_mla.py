@@ -86,6 +86,23 @@ def test_wide_dims_and_odd_sizes():
     _check(1, 1, 40, 40, 256, 192, 64, 256, False, 0, seed=5, wscale=0.05)
 
 
+def test_unaligned_views_take_the_element_paths():
+    # contiguous views at odd element offsets: the kernels fall back to element loads and stores
+    from dsmoe.mla import mla_attention
+    B, H, S, R, Dn, Dr, Dv = 1, 2, 70, 32, 16, 8, 32
+    ts, sc = _inputs(B, H, S, S, R, Dn, Dr, Dv, seed=9)
+    shifted = []
+    for t in ts:
+        buf = torch.empty(t.numel() + 1, dtype=t.dtype, device=DEV)
+        v = buf[1:].view(t.shape)
+        v.copy_(t)
+        shifted.append(v)
+    out = mla_attention(*shifted, sc, is_causal=True)
+    ref = mla_attention_oracle(*[t.cpu() for t in ts], sc, is_causal=True)
+    got = out.float().cpu().numpy().astype(np.float64)
+    assert (np.abs(got - ref) <= ATOL + RTOL * np.abs(ref)).all()
+
+
 def test_negative_and_large_scale():
     _check(1, 2, 64, 64, 32, 16, 16, 32, True, 0, seed=6, scale=-0.2)
     _check(1, 2, 64, 64, 32, 16, 16, 32, True, 0, seed=7, scale=2.0)
