@@ -136,11 +136,14 @@ struct Vec16<float> {
 // Threads j < k put slot j at its ascending-expert position q in LDS (with
 // its expert and dlogit); the k slot rows of a column chunk are loaded
 // together before the fp32 sums.
-template <typename T, int KB>
+// KE > 0: k == KE at compile time (k <= 8): every load and sum is
+// unconditional, so the loads stay in flight together.
+template <typename T, int KB, int KE>
 __global__ __launch_bounds__(256) void dx_final_vec_kernel(const T* __restrict__ dx_slots, const T* __restrict__ dx_shared,
                                                            const float* __restrict__ dlog, const int32_t* __restrict__ idx,
-                                                           const float* __restrict__ gw, int D, int k,
+                                                           const float* __restrict__ gw, int D, int k_,
                                                            T* __restrict__ dx) {
+  const int k = KE > 0 ? KE : k_;
   constexpr int V = Vec16<T>::N;
   __shared__ int ord_s[KB], ev_s[KB];
   __shared__ float dl_s[KB];
@@ -165,7 +168,7 @@ __global__ __launch_bounds__(256) void dx_final_vec_kernel(const T* __restrict__
     for (int i = 0; i < V; ++i) acc[i] = 0.0f;
 #pragma unroll
     for (int q = 0; q < KB; ++q)
-      if (q < k) Vec16<T>::load(dx_slots + (t * k + ord_s[q]) * (int64_t)D + d, v[q]);
+      if (KE > 0 || q < k) Vec16<T>::load(dx_slots + (t * k + ord_s[q]) * (int64_t)D + d, v[q]);
 #pragma unroll
     for (int q = 0; q < KB; ++q) {
       if (q >= k) break;
@@ -302,11 +305,14 @@ __global__ __launch_bounds__(256) void dw_dot_tok_kernel(const bf16_t* __restric
 // once; for each slot j of the token, dw[t k + j] = <dY_t, o_slot> (the
 // dw_dot_tok_kernel sums, in the same order) and dy_w[slot_pos[t k + j]] =
 // bf16(w[t k + j] * dY_t) (scale_gather_kernel's rounding).
-template <int KB>
+// KE > 0: k == KE at compile time (k <= 8): every load is unconditional, so
+// the loads stay in flight together.
+template <int KB, int KE>
 __global__ __launch_bounds__(256) void prep_tok_kernel(const bf16_t* __restrict__ dy, const bf16_t* __restrict__ o_slots,
                                                        const int32_t* __restrict__ row_of, const float* __restrict__ w,
-                                                       const int32_t* __restrict__ slot_pos, int T, int k, int D,
+                                                       const int32_t* __restrict__ slot_pos, int T, int k_, int D,
                                                        float* __restrict__ dw, bf16_t* __restrict__ dy_w) {
+  const int k = KE > 0 ? KE : k_;
   const int lane = threadIdx.x & 63;
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
@@ -318,7 +324,7 @@ __global__ __launch_bounds__(256) void prep_tok_kernel(const bf16_t* __restrict_
     ws[j] = 0.0f;
     pos[j] = 0;
     orow[j] = 0;
-    if (j < k) {
+    if (KE > 0 || j < k) {
       ws[j] = w[t * k + j];
       pos[j] = slot_pos[t * k + j];
       orow[j] = row_of ? (int64_t)row_of[t * k + j] : t * k + j;
@@ -333,7 +339,7 @@ __global__ __launch_bounds__(256) void prep_tok_kernel(const bf16_t* __restrict_
     float bv[KB][8];
 #pragma unroll
     for (int j = 0; j < KB; ++j)
-      if (j < k) Vec16<bf16_t>::load(o_slots + orow[j] * D + c * 8, bv[j]);
+      if (KE > 0 || j < k) Vec16<bf16_t>::load(o_slots + orow[j] * D + c * 8, bv[j]);
 #pragma unroll
     for (int j = 0; j < KB; ++j) {
       if (j >= k) break;
@@ -362,9 +368,20 @@ int launch_prep_tok(const void* dy, const void* o_slots, const int32_t* row_of, 
   if (!(dtype == DSMOE_BF16 && D % 8 == 0 && k <= 8 && dy_w && al16p(dy) && al16p(o_slots) && al16p(dy_w)))
     return DSMOE_ERR_UNSUPPORTED;
   if (T == 0) return DSMOE_OK;
-  hipLaunchKernelGGL(prep_tok_kernel<8>, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, st, static_cast<const bf16_t*>(dy),
-                     static_cast<const bf16_t*>(o_slots), row_of, w, slot_pos, T, k, D, dw,
-                     static_cast<bf16_t*>(dy_w));
+  switch (k) {
+#define PREP_K(n)                                                                                                   \
+  case n:                                                                                                           \
+    hipLaunchKernelGGL((prep_tok_kernel<n, n>), dim3((unsigned)cdiv(T, 4)), dim3(256), 0, st,                       \
+                       static_cast<const bf16_t*>(dy), static_cast<const bf16_t*>(o_slots), row_of, w, slot_pos, T, \
+                       k, D, dw, static_cast<bf16_t*>(dy_w));                                                       \
+    break;
+    PREP_K(1) PREP_K(2) PREP_K(3) PREP_K(4) PREP_K(5) PREP_K(6) PREP_K(7) PREP_K(8)
+#undef PREP_K
+    default:
+      hipLaunchKernelGGL((prep_tok_kernel<8, 0>), dim3((unsigned)cdiv(T, 4)), dim3(256), 0, st,
+                         static_cast<const bf16_t*>(dy), static_cast<const bf16_t*>(o_slots), row_of, w, slot_pos, T, k,
+                         D, dw, static_cast<bf16_t*>(dy_w));
+  }
   return check_launch("prep_tok");
 }
 
@@ -456,25 +473,28 @@ int launch_dx_final(const void* dx_slots, const void* dx_shared, const float* dl
   const int V = dtype == DSMOE_BF16 ? 8 : 4;
   if (D % V == 0 && al16p(dx_slots) && al16p(dx) && al16p(gw) && (!dx_shared || al16p(dx_shared))) {
     const unsigned threads = (unsigned)std::min<int64_t>(256, cdiv(cdiv(D, V), 64) * 64);
-    if (dtype == DSMOE_BF16) {
-      if (k <= 8)
-        hipLaunchKernelGGL((dx_final_vec_kernel<bf16_t, 8>), dim3((unsigned)T), dim3(threads), 0, st,
-                           static_cast<const bf16_t*>(dx_slots), static_cast<const bf16_t*>(dx_shared), dlog, idx, gw,
-                           D, k, static_cast<bf16_t*>(dx));
-      else
-        hipLaunchKernelGGL((dx_final_vec_kernel<bf16_t, MAX_TOPK>), dim3((unsigned)T), dim3(threads), 0, st,
-                           static_cast<const bf16_t*>(dx_slots), static_cast<const bf16_t*>(dx_shared), dlog, idx, gw,
-                           D, k, static_cast<bf16_t*>(dx));
-    } else {
-      if (k <= 8)
-        hipLaunchKernelGGL((dx_final_vec_kernel<float, 8>), dim3((unsigned)T), dim3(threads), 0, st,
-                           static_cast<const float*>(dx_slots), static_cast<const float*>(dx_shared), dlog, idx, gw, D,
-                           k, static_cast<float*>(dx));
-      else
-        hipLaunchKernelGGL((dx_final_vec_kernel<float, MAX_TOPK>), dim3((unsigned)T), dim3(threads), 0, st,
-                           static_cast<const float*>(dx_slots), static_cast<const float*>(dx_shared), dlog, idx, gw, D,
-                           k, static_cast<float*>(dx));
-    }
+    auto go = [&](auto tag) {
+      using TT = decltype(tag);
+      const TT* s = static_cast<const TT*>(dx_slots);
+      const TT* sh = static_cast<const TT*>(dx_shared);
+      TT* o = static_cast<TT*>(dx);
+      switch (k) {
+#define DXF_K(n)                                                                                                   \
+  case n:                                                                                                          \
+    hipLaunchKernelGGL((dx_final_vec_kernel<TT, n, n>), dim3((unsigned)T), dim3(threads), 0, st, s, sh, dlog, idx, \
+                       gw, D, k, o);                                                                               \
+    break;
+        DXF_K(1) DXF_K(2) DXF_K(3) DXF_K(4) DXF_K(5) DXF_K(6) DXF_K(7) DXF_K(8)
+#undef DXF_K
+        default:
+          hipLaunchKernelGGL((dx_final_vec_kernel<TT, MAX_TOPK, 0>), dim3((unsigned)T), dim3(threads), 0, st, s, sh,
+                             dlog, idx, gw, D, k, o);
+      }
+    };
+    if (dtype == DSMOE_BF16)
+      go(bf16_t{});
+    else
+      go(float{});
     return check_launch("dx_final_vec");
   }
   const unsigned grid = (unsigned)cdiv((int64_t)T * D, 256);

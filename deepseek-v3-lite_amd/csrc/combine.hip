@@ -63,11 +63,15 @@ __device__ __forceinline__ void order_by_expert(const int32_t* idx_row, int k, i
 // c + blockDim, ... and issues the loads of the token's k rows before the fp32
 // accumulation in q order.  Slot s's output is row row_of[s] of o (the layer
 // keeps them in expert-sorted order, row_of = slot_pos) or row s (row_of null).
-template <typename T, int VEC, int KB>
+// KE > 0: k == KE at compile time (k <= 8), so every load and sum is
+// unconditional and the loads stay in flight together (a load the compiler
+// can sink into a k-guarded use is waited for there, one at a time).
+template <typename T, int VEC, int KB, int KE>
 __global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ o_slots, const int32_t* __restrict__ row_of,
                                                       const float* __restrict__ w, const int32_t* __restrict__ idx,
-                                                      const T* __restrict__ shared, int T_, int D, int k,
+                                                      const T* __restrict__ shared, int T_, int D, int k_,
                                                       T* __restrict__ y) {
+  const int k = KE > 0 ? KE : k_;
   using V = Vec<T, VEC>;
   using VT = typename V::type;
   __shared__ int row_s[KB];
@@ -87,12 +91,13 @@ __global__ __launch_bounds__(256) void combine_kernel(const T* __restrict__ o_sl
   __syncthreads();
   const int cpr = D / VEC;
   for (int c = threadIdx.x; c < cpr; c += blockDim.x) {
+    // every load unconditional (slots past k re-read slot k - 1, a missing
+    // shared row reads slot 0; neither is added): a guarded load would make
+    // the compiler wait for each in turn
     VT ov[KB];
 #pragma unroll
-    for (int q = 0; q < KB; ++q)
-      if (q < k) ov[q] = reinterpret_cast<const VT*>(o_slots + (int64_t)row_s[q] * D)[c];
-    VT sv;
-    if (shared) sv = reinterpret_cast<const VT*>(shared + t * (int64_t)D)[c];
+    for (int q = 0; q < KB; ++q) ov[q] = reinterpret_cast<const VT*>(o_slots + (int64_t)row_s[min(q, k - 1)] * D)[c];
+    const VT sv = reinterpret_cast<const VT*>(shared ? shared + t * (int64_t)D : o_slots + (int64_t)row_s[0] * D)[c];
     float acc[VEC];
 #pragma unroll
     for (int v = 0; v < VEC; ++v) acc[v] = 0.0f;
@@ -123,12 +128,18 @@ static void launch_combine_vec(const void* o_slots, const int32_t* row_of, const
   auto o = static_cast<const T*>(o_slots);
   auto sh = static_cast<const T*>(shared);
   auto yy = static_cast<T*>(y);
-  if (d.k <= 8)
-    hipLaunchKernelGGL((combine_kernel<T, VEC, 8>), dim3((unsigned)d.T), dim3(threads), 0, st, o, row_of, w, idx, sh,
-                       d.T, d.D, d.k, yy);
-  else
-    hipLaunchKernelGGL((combine_kernel<T, VEC, CMB_MAX_K>), dim3((unsigned)d.T), dim3(threads), 0, st, o, row_of, w,
-                       idx, sh, d.T, d.D, d.k, yy);
+  switch (d.k) {
+#define CMB_K(n)                                                                                                    \
+  case n:                                                                                                           \
+    hipLaunchKernelGGL((combine_kernel<T, VEC, n, n>), dim3((unsigned)d.T), dim3(threads), 0, st, o, row_of, w, idx, \
+                       sh, d.T, d.D, d.k, yy);                                                                      \
+    break;
+    CMB_K(1) CMB_K(2) CMB_K(3) CMB_K(4) CMB_K(5) CMB_K(6) CMB_K(7) CMB_K(8)
+#undef CMB_K
+    default:
+      hipLaunchKernelGGL((combine_kernel<T, VEC, CMB_MAX_K, 0>), dim3((unsigned)d.T), dim3(threads), 0, st, o, row_of,
+                         w, idx, sh, d.T, d.D, d.k, yy);
+  }
 }
 
 template <typename T>
