@@ -22,6 +22,7 @@
 // ranks their slots for the permute (rank.h).
 #include <cstdlib>
 #include <cstring>
+#include <type_traits>
 #include <mutex>
 #include <vector>
 
@@ -275,12 +276,15 @@ __global__ __launch_bounds__(GP_THREADS) void gate_mfma_kernel(const bf16_t* __r
 // routing scratch[64 per wave]
 constexpr int RR_WAVES = RANK_TOKENS / 4;
 
-template <int KB>
-__global__ __launch_bounds__(RR_WAVES * 64) void route_rank_kernel(const float* __restrict__ part, int ks,
+// KS > 0: ks == KS at compile time, so the split loads are unconditional and
+// stay in flight together (a guarded load is waited for at its guard).
+template <int KB, int KS>
+__global__ __launch_bounds__(RR_WAVES * 64) void route_rank_kernel(const float* __restrict__ part, int ks_,
                                                                   const float* __restrict__ bias, int T, int E, int k,
                                                                   float route_scale, int xdtype, GateOut out,
                                                                   PermuteOut po, int nb) {
   extern __shared__ __attribute__((aligned(16))) float rsm[];
+  const int ks = KS > 0 ? KS : ks_;
   const int ldl = E + 1;
   float* lg = rsm;
   float* bias_s = lg + RANK_TOKENS * ldl;
@@ -312,7 +316,7 @@ __global__ __launch_bounds__(RR_WAVES * 64) void route_rank_kernel(const float* 
       g_f32x4_t pv[GATE_KS_MAX];
 #pragma unroll
       for (int sp = 0; sp < GATE_KS_MAX; ++sp)
-        if (sp < ks) pv[sp] = *reinterpret_cast<const g_f32x4_t*>(p + sp * split_stride);
+        if (KS > 0 ? sp < KS : sp < ks) pv[sp] = *reinterpret_cast<const g_f32x4_t*>(p + sp * split_stride);
       g_f32x4_t v = pv[0];
 #pragma unroll
       for (int sp = 1; sp < GATE_KS_MAX; ++sp)
@@ -335,7 +339,7 @@ __global__ __launch_bounds__(RR_WAVES * 64) void route_rank_kernel(const float* 
       float pv[GATE_KS_MAX];
 #pragma unroll
       for (int sp = 0; sp < GATE_KS_MAX; ++sp)
-        if (sp < ks) pv[sp] = p[sp * split_stride];
+        if (KS > 0 ? sp < KS : sp < ks) pv[sp] = p[sp * split_stride];
       float v = pv[0];
 #pragma unroll
       for (int sp = 1; sp < GATE_KS_MAX; ++sp)
@@ -477,7 +481,19 @@ static int launch_route(const float* part, int ks, const float* bias, const dsmo
   const int nb = (int)cdiv(d.T, RANK_TOKENS);
   const size_t lds =
       sizeof(float) * (RANK_TOKENS * (d.E + 1) + 2 * d.E + 2 * RANK_TOKENS * d.k + 2 * (d.E + 1) + RR_WAVES * 64);
-  auto kern = d.k <= 8 ? route_rank_kernel<8> : route_rank_kernel<MAX_TOPK>;
+  // split counts are powers of two up to GATE_KS_MAX (gate_k_splits); given
+  // logits (ks = 1) take the KS = 1 instantiation too
+  auto pick = [&](auto kb) -> decltype(&route_rank_kernel<8, 0>) {
+    constexpr int KB = decltype(kb)::value;
+    switch (ks) {
+      case 1: return route_rank_kernel<KB, 1>;
+      case 2: return route_rank_kernel<KB, 2>;
+      case 4: return route_rank_kernel<KB, 4>;
+      case 8: return route_rank_kernel<KB, 8>;
+      default: return route_rank_kernel<KB, 0>;
+    }
+  };
+  auto kern = d.k <= 8 ? pick(std::integral_constant<int, 8>{}) : pick(std::integral_constant<int, MAX_TOPK>{});
   int rc = set_lds((const void*)kern, lds);
   if (rc) return rc;
   hipLaunchKernelGGL(kern, dim3((unsigned)max(nb, 1)), dim3(RR_WAVES * 64), lds, st, part, ks, bias, d.T, d.E, d.k,
