@@ -199,50 +199,70 @@ __global__ __launch_bounds__(256) void dx_final_vec_kernel(const T* __restrict__
   }
 }
 
-// dW_gate[e, cols] for one expert and 64 * VEC columns: 4 row groups of 64
-// threads take rows p0 + g, p0 + g + 4, ... of the expert's sorted rows; the
-// 4 partial sums are then added in group order (deterministic).
-template <typename T>
-__global__ __launch_bounds__(256) void dwgate_vec_kernel(const T* __restrict__ x, const float* __restrict__ dlog,
-                                                         const int32_t* __restrict__ sorted_slot,
-                                                         const int32_t* __restrict__ sorted_token,
-                                                         const int32_t* __restrict__ offsets, int D,
-                                                         float* __restrict__ dgw) {
+// dW_gate[e, cols] for one expert and 64 * VEC columns.
+// NW waves per (expert, 64 V columns); wave w takes the expert's rows
+// p0 + w, p0 + w + NW, ... in ascending order, U at a time: the x rows and
+// dlogits of a batch are loaded together while the sorted indices of the next
+// batch are already in flight (a batch waits for one round trip, not two), and
+// every load of a full batch is unconditional (clamped columns; a guarded load
+// is waited for at its branch).  The last, partial batch goes one row at a
+// time.  The waves' sums are added in wave order: a fixed order, so the result
+// does not depend on scheduling.
+template <typename T, int NW>
+__global__ __launch_bounds__(NW * 64) void dwgate_vec_kernel(const T* __restrict__ x, const float* __restrict__ dlog,
+                                                             const int32_t* __restrict__ sorted_slot,
+                                                             const int32_t* __restrict__ sorted_token,
+                                                             const int32_t* __restrict__ offsets, int D,
+                                                             float* __restrict__ dgw) {
   constexpr int V = Vec16<T>::N;
-  __shared__ float red[3][64 * V];
+  constexpr int U = 8;
+  __shared__ float red[NW - 1][64 * V];
   const int e = blockIdx.y;
   const int grp = threadIdx.x >> 6, l = threadIdx.x & 63;
-  const int d = (blockIdx.x * 64 + l) * V;
-  const bool live = d < D;
+  const int dl = (blockIdx.x * 64 + l) * V;
+  const bool live = dl < D;
+  const int d = min(dl, D - V);
   const int p0 = offsets[e], p1 = offsets[e + 1];
   float acc[V];
 #pragma unroll
   for (int i = 0; i < V; ++i) acc[i] = 0.0f;
-  if (live) {
-    // rows p0 + grp, p0 + grp + 4, ... in ascending order; the loads of U rows
-    // are issued before their FMAs so the index -> value round trips overlap
-    constexpr int U = 8;
-    for (int p = p0 + grp; p < p1; p += 4 * U) {
-      int slot[U], tok[U];
+  int p = p0 + grp;
+  if (p + NW * (U - 1) < p1) {
+    int slot[U], tok[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int pp = p + 4 * u;
-        slot[u] = pp < p1 ? sorted_slot[pp] : -1;
-        tok[u] = pp < p1 ? sorted_token[pp] : 0;
-      }
+    for (int u = 0; u < U; ++u) {
+      slot[u] = sorted_slot[p + NW * u];
+      tok[u] = sorted_token[p + NW * u];
+    }
+    for (;;) {
       float wv[U], xv[U][V];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        wv[u] = slot[u] >= 0 ? dlog[slot[u]] : 0.0f;
+        wv[u] = dlog[slot[u]];
         Vec16<T>::load(x + (int64_t)tok[u] * D + d, xv[u]);
       }
+      const int pn = p + NW * U;
+      const bool more = pn + NW * (U - 1) < p1;
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        if (slot[u] < 0) break;
+        const int q = min(pn + NW * u, p1 - 1);  // in the expert's range
+        slot[u] = sorted_slot[q];
+        tok[u] = sorted_token[q];
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
 #pragma unroll
         for (int i = 0; i < V; ++i) acc[i] = fmaf(wv[u], xv[u][i], acc[i]);
-      }
+      p = pn;
+      if (!more) break;
     }
+  }
+  for (; p < p1; p += NW) {
+    float xv[V];
+    const float wv = dlog[sorted_slot[p]];
+    Vec16<T>::load(x + (int64_t)sorted_token[p] * D + d, xv);
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = fmaf(wv, xv[i], acc[i]);
   }
   if (grp > 0) {
 #pragma unroll
@@ -251,7 +271,7 @@ __global__ __launch_bounds__(256) void dwgate_vec_kernel(const T* __restrict__ x
   __syncthreads();
   if (grp == 0 && live) {
 #pragma unroll
-    for (int gi = 0; gi < 3; ++gi)
+    for (int gi = 0; gi < NW - 1; ++gi)
 #pragma unroll
       for (int i = 0; i < V; ++i) acc[i] += red[gi][l * V + i];
     float* o = dgw + (int64_t)e * D + d;
@@ -444,16 +464,20 @@ int launch_gate_bwd(const float* dw, const float* sel, int T, int k, float rs, f
   return check_launch("gate_bwd");
 }
 
+constexpr int DWG_WAVES = 16;
+
 int launch_dwgate(const void* x, const float* dlog, const int32_t* sorted_slot, const int32_t* sorted_token,
                   const int32_t* offsets, int E, int D, int dtype, float* dgw, hipStream_t st) {
   const int V = dtype == DSMOE_BF16 ? 8 : 4;
   if (D % V == 0 && al16p(x) && al16p(dgw)) {
     const dim3 gv((unsigned)cdiv(D, 64 * V), (unsigned)E);
     if (dtype == DSMOE_BF16)
-      hipLaunchKernelGGL(dwgate_vec_kernel<bf16_t>, gv, dim3(256), 0, st, static_cast<const bf16_t*>(x), dlog,
+      hipLaunchKernelGGL((dwgate_vec_kernel<bf16_t, DWG_WAVES>), gv, dim3(DWG_WAVES * 64), 0, st,
+                         static_cast<const bf16_t*>(x), dlog,
                          sorted_slot, sorted_token, offsets, D, dgw);
     else
-      hipLaunchKernelGGL(dwgate_vec_kernel<float>, gv, dim3(256), 0, st, static_cast<const float*>(x), dlog,
+      hipLaunchKernelGGL((dwgate_vec_kernel<float, DWG_WAVES>), gv, dim3(DWG_WAVES * 64), 0, st,
+                         static_cast<const float*>(x), dlog,
                          sorted_slot, sorted_token, offsets, D, dgw);
     return check_launch("dwgate_vec");
   }
