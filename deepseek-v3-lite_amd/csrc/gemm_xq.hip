@@ -48,8 +48,13 @@ constexpr int XQ_LD = XQ_REG / 1024 / 4;              // direct loads per wave, 
 
 // A block of zeros: the source of weight-gradient A rows past the K range.
 __device__ __attribute__((aligned(16))) uint4 g_xq_zero[4];
+// 1.0: the row weight of an unweighted SwiGLU-backward epilogue.
+__device__ float g_xq_one[1] = {1.0f};
+// Where the SwiGLU-backward epilogue stores elements outside its tile (never read).
+__device__ __attribute__((aligned(16))) uint4 g_xq_sink[1];
 
 typedef short xq_v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) u32x4_t xq_gv4u;  // a global-memory u32x4_t
 
 // K-contiguous ("NT") slab: [256 rows][64 k], 128-byte rows, 16-byte chunk c
 // of row r at chunk c ^ ((r >> 1) & 7).
@@ -471,58 +476,76 @@ __global__ __launch_bounds__(256) void xgemm_q_kernel(const XGemm g) {
     }
     return;
   }
-  // SwiGLU backward: dh stays fp32 until dg and du are formed, so each column
-  // half (128 columns, owned by the waves with wn == half) is staged as fp32
-  // in turn; 16-byte unit u of row m at unit u ^ (m & 31).  Thread tid serves
-  // rows (tid >> 4) + 16 i and columns n0 + 128 half + 8 (tid & 15) + {0..7};
-  // the g, u and row weights of all its rows in the half are loaded before
-  // the staging, so their HBM latency overlaps it.
+  // SwiGLU backward: dh stays fp32 until dg and du are formed, so the tile is
+  // staged as fp32 one column quarter (64 columns, owned by the waves with
+  // wn == quarter / 2) at a time; 16-byte unit u of row m at unit u ^ (m & 15).
+  // Thread tid serves rows (tid >> 3) + 32 i and columns n0 + 64 quarter +
+  // 8 (tid & 7) + {0..7}.  The g and u of quarter q + 1 are loaded while
+  // quarter q is staged, formed and stored, so only the first quarter waits
+  // for its loads.  All four quarters run, and the body has no branches:
+  // loads read a clamped row and column, and an element outside the tile is
+  // stored to g_xq_sink.  The compiler then knows how many memory operations
+  // follow each load and waits for that load alone (a load or store under a
+  // lane guard makes it wait for all of them).
   const bf16_t* Gs = static_cast<const bf16_t*>(g.Gs);
   const bf16_t* Us = static_cast<const bf16_t*>(g.Us);
   rowp[tid] = my_rowp;
-  const int cc = tid & 15, rq = tid >> 4;
-  for (int half = 0; half < 2; ++half) {
-    const int n = n0 + half * 128 + cc * 8;
-    const bool col_ok = n < g.N;
-    u32x4_t gp[16], up[16];
-    float rwv[16];
+  const int cc = tid & 7, rq = tid >> 3;
+  // row weights, or a stride-0 read of 1.0 when there are none
+  const float* rw_base = g.row_w ? g.row_w : g_xq_one;
+  const int rw_step = g.row_w ? 1 : 0;
+  float rwv[8];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int r = rq + 16 * i;
-      gp[i] = up[i] = u32x4_t{0u, 0u, 0u, 0u};
-      rwv[i] = 0.0f;
-      if (r < rows && col_ok) {
-        const int64_t ogu = (int64_t)(row0 + r) * g.ld_gu + (int64_t)grp * g.gu_group_col + n;
-        gp[i] = *reinterpret_cast<const u32x4_t*>(Gs + ogu);
-        up[i] = *reinterpret_cast<const u32x4_t*>(Us + ogu);
-        rwv[i] = g.row_w ? g.row_w[row0 + r] : 1.0f;
-      }
+  for (int i = 0; i < 8; ++i) rwv[i] = rw_base[(row0 + min(rq + 32 * i, rows - 1)) * rw_step];
+  u32x4_t gp[2][8], up[2][8];
+  int64_t rpv[8];  // output row addresses of the thread's rows
+  auto issue = [&](int qt, u32x4_t (&gq)[8], u32x4_t (&uq)[8]) {
+    const int nc = min(n0 + qt * 64 + cc * 8, g.N - 8);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = min(rq + 32 * i, rows - 1);
+      const int64_t ogu = (int64_t)(row0 + r) * g.ld_gu + (int64_t)grp * g.gu_group_col + nc;
+      gq[i] = *reinterpret_cast<const u32x4_t*>(Gs + ogu);
+      uq[i] = *reinterpret_cast<const u32x4_t*>(Us + ogu);
     }
-    if (half) xq_sync();  // the first half's reads are done
-    if (wn == half) {
+  };
+  issue(0, gp[0], up[0]);
+#pragma unroll
+  for (int qt = 0; qt < 4; ++qt) {
+    if (qt + 1 < 4) issue(qt + 1, gp[(qt + 1) & 1], up[(qt + 1) & 1]);
+    if (qt) xq_sync();  // the previous quarter's reads are done
+    if (wn == (qt >> 1)) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int m = (2 * j + wm) * 32 + (lane & 31);
 #pragma unroll
-        for (int ni = 0; ni < 4; ++ni)
+        for (int nl = 0; nl < 2; ++nl)
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            const int u = (ni * 32 + q * 8 + (lane >> 5) * 4) >> 2;
-            *reinterpret_cast<float4*>(sm + m * 512 + ((u ^ (m & 31)) << 4)) =
+            const int ni = 2 * (qt & 1) + nl;
+            const int u = nl * 8 + q * 2 + (lane >> 5);
+            *reinterpret_cast<float4*>(sm + m * 256 + ((u ^ (m & 15)) << 4)) =
                 make_float4(acc[j][ni][q * 4], acc[j][ni][q * 4 + 1], acc[j][ni][q * 4 + 2], acc[j][ni][q * 4 + 3]);
           }
       }
     }
     xq_sync();
+    if (qt == 0)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int r = rq + 16 * i;
-      if (r >= rows || !col_ok) continue;
-      const float4 d0 = *reinterpret_cast<const float4*>(sm + r * 512 + (((2 * cc) ^ (r & 31)) << 4));
-      const float4 d1 = *reinterpret_cast<const float4*>(sm + r * 512 + (((2 * cc + 1) ^ (r & 31)) << 4));
+      for (int i = 0; i < 8; ++i) rpv[i] = rowp[rq + 32 * i];
+    const int n = n0 + qt * 64 + cc * 8;
+    const bool col_ok = n < g.N;
+    const u32x4_t(&gq)[8] = gp[qt & 1];
+    const u32x4_t(&uq)[8] = up[qt & 1];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = rq + 32 * i;
+      const bool ok = r < rows && col_ok;
+      const float4 d0 = *reinterpret_cast<const float4*>(sm + r * 256 + (((2 * cc) ^ (r & 15)) << 4));
+      const float4 d1 = *reinterpret_cast<const float4*>(sm + r * 256 + (((2 * cc + 1) ^ (r & 15)) << 4));
       const float dhv[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
-      const uint32_t gw[4] = {gp[i].x, gp[i].y, gp[i].z, gp[i].w};
-      const uint32_t uw[4] = {up[i].x, up[i].y, up[i].z, up[i].w};
+      const uint32_t gw[4] = {gq[i].x, gq[i].y, gq[i].z, gq[i].w};
+      const uint32_t uw[4] = {uq[i].x, uq[i].y, uq[i].z, uq[i].w};
       uint32_t dgw[4], duw[4];
 #pragma unroll
       for (int e2 = 0; e2 < 4; ++e2) {
@@ -539,9 +562,11 @@ __global__ __launch_bounds__(256) void xgemm_q_kernel(const XGemm g) {
         dgw[e2] = pack_bf16x2(dg[0], dg[1]);
         duw[e2] = pack_bf16x2(du[0], du[1]);
       }
-      bf16_t* out = reinterpret_cast<bf16_t*>(rowp[r]);
-      *reinterpret_cast<u32x4_t*>(out + n) = u32x4_t{dgw[0], dgw[1], dgw[2], dgw[3]};
-      *reinterpret_cast<u32x4_t*>(out + g.du_off + n) = u32x4_t{duw[0], duw[1], duw[2], duw[3]};
+      // global (not flat) stores: a flat store also counts as an LDS access
+      const int64_t dst = ok ? rpv[i] + 2 * (int64_t)n : reinterpret_cast<int64_t>(g_xq_sink);
+      const int64_t du_bytes = ok ? 2 * g.du_off : 0;
+      *reinterpret_cast<xq_gv4u*>(dst) = u32x4_t{dgw[0], dgw[1], dgw[2], dgw[3]};
+      *reinterpret_cast<xq_gv4u*>(dst + du_bytes) = u32x4_t{duw[0], duw[1], duw[2], duw[3]};
     }
   }
 }
