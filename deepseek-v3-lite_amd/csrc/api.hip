@@ -471,7 +471,7 @@ int dsmoe_moe_fwd(const void* x, const float* gate_w, const float* gate_bias, co
     // the routed rows of x in sorted order, for the backward's weight
     // gradient (a K-major operand read without a row gather); gemm1 keeps
     // gathering from x, which stays cache-resident
-    rc = launch_gather_rows(x, d.T, L.sorted_token, N, d.D, elem_size(d.dtype), L.x_sorted, st);
+    rc = launch_scatter_rows(x, d.T, d.k, L.slot_pos, L.sorted_token, d.D, elem_size(d.dtype), L.x_sorted, st);
   }
   tm.end();
   if (rc) return rc;

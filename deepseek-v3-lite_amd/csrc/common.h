@@ -197,6 +197,11 @@ size_t permute_scratch_carve(Carver& c, const dsmoe_dims& d, int bm, PermuteScra
 int launch_permute(const int32_t* idx, const dsmoe_dims& d, const PermuteOut& po, bool ranked, hipStream_t st);
 // dst[p] = x[rows[p]] for p < nrows (rows of D elements); rows outside
 // [0, src_rows) give zero rows.
+// x_sorted[slot_pos[t k + j]] = x[t]: the gather of the sorted rows from the
+// token side (falls back to the row gather through sorted_token when rows are
+// not 16-byte vectors).
+int launch_scatter_rows(const void* x, int64_t T, int k, const int32_t* slot_pos, const int32_t* sorted_token,
+                        int D, int elem, void* dst, hipStream_t st);
 int launch_gather_rows(const void* x, int64_t src_rows, const int32_t* rows, int64_t nrows, int D, int elem, void* dst,
                        hipStream_t st);
 int launch_sched_from_offsets(const int64_t* offsets64, int E, int bm, int64_t rows, int32_t* offsets32, MTile* sched,

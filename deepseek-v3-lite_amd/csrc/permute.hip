@@ -19,6 +19,8 @@
 //   A call of one rank block (T <= 64) is finished by its ranking workgroup:
 //   one launch.
 //   gather_rows  x_sorted[p] = x[sorted_token[p]] with 16-byte accesses.
+//   scatter_rows the same copy from the token side: x_sorted[slot_pos[t k + j]]
+//                = x[t], each row of x read once.
 #include "rank.h"
 
 namespace dsmoe {
@@ -107,6 +109,25 @@ __global__ void gather_rows_kernel(const uint4* __restrict__ src, const int32_t*
   const int c = (int)(i - r * vec_per_row);
   const int32_t sr = rows[r];
   dst[i] = (sr >= 0 && sr < src_rows) ? src[(int64_t)sr * vec_per_row + c] : make_uint4(0, 0, 0, 0);
+}
+
+// Token-major copy of a permutation's rows, 16-byte vectors: workgroup t
+// reads row t of src once and writes it to the k sorted rows slot_pos[t k + j]
+// (uniform per workgroup: scalar loads, issued with the row's loads).  A slot
+// position outside [0, nrows) (left unset by an invalid routing) is not
+// written.
+__global__ __launch_bounds__(256) void scatter_rows_kernel(const uint4* __restrict__ src,
+                                                           const int32_t* __restrict__ slot_pos, int k, int vec_per_row,
+                                                           int64_t nrows, uint4* __restrict__ dst) {
+  const int64_t t = blockIdx.x;
+  const int32_t* sp = slot_pos + t * k;
+  for (int c = threadIdx.x; c < vec_per_row; c += blockDim.x) {
+    const uint4 v = src[t * vec_per_row + c];
+    for (int j = 0; j < k; ++j) {
+      const int32_t p = sp[j];
+      if (p >= 0 && p < nrows) dst[(int64_t)p * vec_per_row + c] = v;
+    }
+  }
 }
 
 template <typename T>
@@ -231,6 +252,20 @@ int launch_gather_rows(const void* x, int64_t src_rows, const int32_t* rows, int
                        static_cast<const float*>(x), rows, nrows, D, src_rows, static_cast<float*>(dst));
   }
   return check_launch("gather_rows");
+}
+
+int launch_scatter_rows(const void* x, int64_t T, int k, const int32_t* slot_pos, const int32_t* sorted_token,
+                        int D, int elem, void* dst, hipStream_t st) {
+  const int64_t nrows = T * k;
+  if (nrows == 0) return DSMOE_OK;
+  const int64_t row_bytes = (int64_t)D * elem;
+  if (row_bytes % 16 || (uintptr_t)x % 16 || (uintptr_t)dst % 16)
+    return launch_gather_rows(x, T, sorted_token, nrows, D, elem, dst, st);
+  const int vpr = (int)(row_bytes / 16);
+  const unsigned threads = (unsigned)std::min<int64_t>(256, cdiv(vpr, 64) * 64);
+  hipLaunchKernelGGL(scatter_rows_kernel, dim3((unsigned)T), dim3(threads), 0, st, static_cast<const uint4*>(x),
+                     slot_pos, k, vpr, nrows, static_cast<uint4*>(dst));
+  return check_launch("scatter_rows");
 }
 
 int launch_sched_from_offsets(const int64_t* offsets64, int E, int bm, int64_t rows, int32_t* offsets32, MTile* sched,
