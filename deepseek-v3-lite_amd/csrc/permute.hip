@@ -64,11 +64,20 @@ __global__ __launch_bounds__(256) void prefix_scatter_kernel(const int32_t* __re
     const int e = e0 + lane;
     int32_t tot = 0, pre = 0;
     if (e < E) {
-#pragma unroll 8
-      for (int b = wave; b < nb; b += 4) {
-        const int32_t v = po.blockhist[(int64_t)b * E + e];
-        tot += v;
-        pre += b < b0 ? v : 0;
+      // 16 loads in flight per lane: unconditional, from a clamped block
+      // index, and those past nb are not added
+      constexpr int U = 16;
+      for (int b = wave; b < nb; b += 4 * U) {
+        int32_t v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = po.blockhist[(int64_t)min(b + 4 * u, nb - 1) * E + e];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int bb = b + 4 * u;
+          const int32_t w = bb < nb ? v[u] : 0;
+          tot += w;
+          pre += bb < b0 ? w : 0;
+        }
       }
     }
     red[wave * 64 + lane] = tot;
