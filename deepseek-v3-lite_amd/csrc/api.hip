@@ -504,7 +504,9 @@ int dsmoe_moe_fwd(const void* x, const float* gate_w, const float* gate_bias, co
                 : launch_grouped_gemm(g1, EPI_SWIGLU, d.dtype, nullptr, mfr, st);
   tm.end();
   if (rc) return rc;
-  // down projections: routed rows written back in slot order (t*k + j)
+  // down projections: routed rows written in expert-sorted order (row r of
+  // o_sorted is sorted position r); the combine and the backward read slot s
+  // at row slot_pos[s]
   tm.begin(ST_GEMM2);
   rc = sk ? launch_sk_pair(g2, s2, d.S > 0, EPI_STORE, d.dtype, mf, st)
           : d.S ? launch_grouped_gemm_pair(g2, s2, EPI_STORE, d.dtype, nullptr, mfr, mf, st)

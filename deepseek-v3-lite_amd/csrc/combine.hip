@@ -194,17 +194,28 @@ int launch_combine(const void* o_slots, const int32_t* row_of, const float* w, c
 
 // f1: models/moe.py:21-27 on device.  One block; counts (E) int32 (the gate
 // histogram) or fp32 (any caller-provided counts, fractional ones included).
-// The mean sums the fp32 counts in ascending expert order; integer counts far
-// below 2^24 make every partial sum exact, so any summation order gives the
-// same mean.
+// The reference's mean is counts.float().mean().  Integer counts (int32, or
+// fp32 holding integers below 2^24) make every fp32 partial sum exact, so any
+// summation order gives the same sum, and the fp32 division is the reference's.
+// For fractional counts torch's fp32 reduction order is its own; here the sum
+// is taken in fp64 and the mean rounded to fp32 once (the correctly rounded
+// mean), which can differ from torch's by an ulp and so flip a decision only
+// for a count within an ulp of a band edge.
 template <typename C>
 __global__ void update_bias_kernel(const C* __restrict__ counts, float* __restrict__ bias, int E, float speed,
                                    float upper, float lower) {
   __shared__ float s_avg;
   if (threadIdx.x == 0) {
-    float s = 0.0f;
-    for (int e = 0; e < E; ++e) s += (float)counts[e];
-    s_avg = s / (float)E;
+    double s = 0.0;
+    bool integral = true;
+    for (int e = 0; e < E; ++e) {
+      const float c = (float)counts[e];
+      s += (double)c;
+      integral = integral && c == truncf(c) && fabsf(c) < 16777216.0f;
+    }
+    // integral: the fp64 sum is the exact fp32 sum (below 2^24 per term, and
+    // E terms stay exact in fp64), and fp32 division of it is the reference's
+    s_avg = integral && fabs(s) < 16777216.0 ? (float)s / (float)E : (float)(s / (double)E);
   }
   __syncthreads();
   const float avg = s_avg;

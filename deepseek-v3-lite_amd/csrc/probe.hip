@@ -1,7 +1,9 @@
-// Measurement probe (no counterpart in the reference): reads an exact byte
+// Measurement probe (no counterpart in the reference), built into its own
+// library (libdsmoe_probe.so, declared in dsmoe_probe.h): reads an exact byte
 // count from global memory with the direct global -> LDS loads the grouped
 // GEMMs issue (global_load_lds_dwordx4), so the per-dispatch reading of a
 // traffic counter (FETCH_SIZE) can be set against the bytes actually read.
+#include "dsmoe_probe.h"
 #include "common.h"
 #include "mfma.h"
 
@@ -27,17 +29,12 @@ __global__ __launch_bounds__(256) void probe_dma_kernel(const char* __restrict__
   if (threadIdx.x == 0) sink[blockIdx.x] = *reinterpret_cast<const uint32_t*>(ring);
 }
 
-int launch_probe_dma(const void* src, size_t bytes, uint32_t* sink, hipStream_t st) {
-  DSMOE_REQUIRE(src && sink, DSMOE_ERR_INVALID, "probe: NULL pointer");
-  DSMOE_REQUIRE(bytes > 0 && bytes % PROBE_CHUNK == 0, DSMOE_ERR_INVALID, "probe: bytes must be a multiple of 1 MiB");
-  DSMOE_REQUIRE((reinterpret_cast<uintptr_t>(src) & 15) == 0, DSMOE_ERR_INVALID, "probe: src must be 16-byte aligned");
-  hipLaunchKernelGGL(probe_dma_kernel, dim3((unsigned)(bytes / PROBE_CHUNK)), dim3(256), 0, st,
-                     static_cast<const char*>(src), sink);
-  return check_launch("probe_dma");
-}
-
 }  // namespace dsmoe
 
 extern "C" int dsmoe_probe_dma_read(const void* src, size_t bytes, uint32_t* sink, void* stream) {
-  return dsmoe::launch_probe_dma(src, bytes, sink, static_cast<hipStream_t>(stream));
+  if (!src || !sink || bytes == 0 || bytes % dsmoe::PROBE_CHUNK != 0 || (reinterpret_cast<uintptr_t>(src) & 15) != 0)
+    return -1;
+  hipLaunchKernelGGL(dsmoe::probe_dma_kernel, dim3((unsigned)(bytes / dsmoe::PROBE_CHUNK)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const char*>(src), sink);
+  return hipGetLastError() == hipSuccess ? 0 : -4;
 }

@@ -73,7 +73,6 @@ _SIGNATURES = {
     "dsmoe_timing_enable": ([I32], I32),
     "dsmoe_timing_read": ([ctypes.POINTER(ctypes.c_double), I32, ctypes.POINTER(ctypes.c_int)], I32),
     "dsmoe_timing_stage_name": ([I32], ctypes.c_char_p),
-    "dsmoe_probe_dma_read": ([P, SZ, P, P], I32),
     "dsmoe_mla_attn_workspace_size": ([ctypes.POINTER(MlaDims)], SZ),
     "dsmoe_mla_attn_fwd": ([P, P, P, P, P, P, ctypes.POINTER(MlaDims), P, P, SZ, P], I32),
 }

@@ -19,6 +19,7 @@ CSRC = ROOT / "csrc"
 INCLUDE = REPO / "include"
 BUILD = ROOT / "_build"
 LIB = PKG / "libdsmoe.so"
+PROBE_LIB = PKG / "libdsmoe_probe.so"     # measurement tooling (bench.py --dma-mb), not the layer
 
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
@@ -31,7 +32,8 @@ CFLAGS = [
 # Per-source flags: the attention kernels keep MFMA accumulators in VGPRs (their
 # online-softmax rescaling reads and writes them every key block).
 EXTRA_FLAGS = {"mla.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
-SOURCES = ["api.hip", "gate.hip", "permute.hip", "gemm.hip", "gemm_qp.hip", "gemm_sk.hip", "gemm_x.hip", "gemm_xm.hip", "gemm_xq.hip", "bwd.hip", "combine.hip", "mla.hip", "probe.hip"]
+SOURCES = ["api.hip", "gate.hip", "permute.hip", "gemm.hip", "gemm_qp.hip", "gemm_sk.hip", "gemm_x.hip", "gemm_xm.hip", "gemm_xq.hip", "bwd.hip", "combine.hip", "mla.hip"]
+PROBE_SOURCES = ["probe.hip"]
 
 
 def _compile(src: Path) -> Path:
@@ -46,20 +48,26 @@ def _compile(src: Path) -> Path:
     return obj
 
 
-def build(verbose: bool = True) -> Path:
-    """Compile every source and link libdsmoe.so (always rebuilds)."""
-    BUILD.mkdir(exist_ok=True)
-    srcs = [CSRC / s for s in SOURCES]
-    with ThreadPoolExecutor(max_workers=min(len(srcs), 8)) as ex:
-        objs = list(ex.map(_compile, srcs))
-    tmp = LIB.with_suffix(".so.tmp")
+def _link(objs, out: Path) -> None:
+    tmp = out.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
-        raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
-    tmp.replace(LIB)
+        raise RuntimeError(f"link of {out.name} failed:\n{r.stdout}\n{r.stderr}")
+    tmp.replace(out)
+
+
+def build(verbose: bool = True) -> Path:
+    """Compile every source and link libdsmoe.so and the measurement probe
+    library libdsmoe_probe.so (always rebuilds)."""
+    BUILD.mkdir(exist_ok=True)
+    srcs = [CSRC / s for s in SOURCES + PROBE_SOURCES]
+    with ThreadPoolExecutor(max_workers=min(len(srcs), 8)) as ex:
+        objs = list(ex.map(_compile, srcs))
+    _link(objs[:len(SOURCES)], LIB)
+    _link(objs[len(SOURCES):], PROBE_LIB)
     if verbose:
-        print(f"[dsmoe.build] built {LIB} ({LIB.stat().st_size} bytes)")
+        print(f"[dsmoe.build] built {LIB} ({LIB.stat().st_size} bytes) and {PROBE_LIB.name}")
     return LIB
 
 

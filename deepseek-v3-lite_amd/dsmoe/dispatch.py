@@ -1,26 +1,30 @@
 """Config compatibility for the reference's backend-selection keys.
 
-The reference rewrites ``moe_dispatch='triton_grouped'`` to ``'stacked'``
-unless ``ENABLE_TRITON_KERNELS=1`` (models/_triton_dispatch.py:13-35).  Here
-there is one backend: ``DeepSeekMoE`` accepts any ``moe_dispatch`` value and
-always runs the HIP kernels, so this helper keeps the reference's config
-rewriting (callers that construct a model through it see the same config) but
-selects nothing.
+The reference rewrites ``moe_dispatch='triton_grouped'`` to ``'stacked'`` and
+``attn_impl='triton'`` to ``'sdpa'`` unless ``ENABLE_TRITON_KERNELS=1``
+(models/_triton_dispatch.py:13-35), at ``Transformer`` construction
+(models/transformer.py:48).  Here the MoE layer has one backend:
+``DeepSeekMoE`` accepts any ``moe_dispatch`` value and always runs the HIP
+kernels.  The attention key still selects in the reference's layer
+(models/mla.py:136-172): only ``attn_impl='triton'`` calls the fused operator,
+which ``dsmoe.mla.triton_mla_attention`` replaces, so a model that should run
+the HIP attention kernels is built with ``ENABLE_TRITON_KERNELS=1``.  This
+helper keeps the reference's rewriting so callers see the same config.
 """
 from __future__ import annotations
 
 import os
 from typing import Callable
 
-# The MoE layer's key only; the attention key the reference rewrites too
-# belongs to MLA attention, which this package does not provide.
-_REWRITES = {("moe_dispatch", "triton_grouped"): "stacked"}
+# Each Triton selection and the portable default it is reset to.
+_REWRITES = {("attn_impl", "triton"): "sdpa", ("moe_dispatch", "triton_grouped"): "stacked"}
 
 
 def enforce_triton_env_var(model_cfg: dict, log: Callable[[str], None]) -> None:
-    """Config rewrite of models/_triton_dispatch.py:19-35 for the MoE key:
-    without ENABLE_TRITON_KERNELS=1 a 'triton_grouped' dispatch becomes
-    'stacked', announced by one log call per rewritten config."""
+    """Config rewrite of models/_triton_dispatch.py:19-35: without
+    ENABLE_TRITON_KERNELS=1 a 'triton_grouped' MoE dispatch becomes 'stacked'
+    and a 'triton' attention becomes 'sdpa', announced by one log call per
+    rewritten config."""
     if os.environ.get("ENABLE_TRITON_KERNELS", "0") == "1":
         return
     changed = []
@@ -30,7 +34,8 @@ def enforce_triton_env_var(model_cfg: dict, log: Callable[[str], None]) -> None:
             changed.append(f"{key}: {value!r} becomes {replacement!r}")
     if changed:
         log("[warn] ENABLE_TRITON_KERNELS is not 1, so the config's Triton selections are reset ("
-            + "; ".join(changed) + "). The dsmoe layer runs its HIP kernels under either value.")
+            + "; ".join(changed) + "). The dsmoe MoE layer runs its HIP kernels under either value; the "
+            "attention reaches the fused operator only with ENABLE_TRITON_KERNELS=1.")
 
 
 def next_pow2(n: int) -> int:

@@ -8,6 +8,18 @@ forward runs the HIP kernels of csrc/mla.hip (bf16).  The backward, as in the
 reference (models/mla_triton.py:257-296), recomputes the attention with torch
 ops and differentiates that; it follows the forward's masking (causal only when
 ``is_causal``).
+
+Dtypes: the kernels compute in bf16.  Under bf16 autocast the reference's
+layer hands the operator a mix (models/mla.py:127-129,209-220 with
+training/pretrain.py:154,212-213): bf16 queries, fp32 views of the fp32
+``wkv_b.weight``, and fp32 or bf16 latent rows depending on the KV cache's
+dtype.  Each tensor is rounded to bf16 once per call (the weight views are
+H (D_nope + D_v) R elements, a few MB) and the output takes ``q_nope``'s dtype,
+as the reference's ``out`` does (models/mla_triton.py:218).  The backward
+returns each input's gradient in that input's dtype.  fp32 queries outside a
+bf16 autocast region raise ``ValueError`` (the reference layer then uses its
+SDPA path), since rounding them to bf16 would be a precision loss the caller
+did not ask for.
 """
 from __future__ import annotations
 
@@ -35,16 +47,38 @@ def _dims(q_nope, q_pe, ctx_kv, wkv_b_v, softmax_scale, is_causal, q_start) -> "
     return d
 
 
-def mla_attention_fwd(q_nope: torch.Tensor, q_pe: torch.Tensor, ctx_kv: torch.Tensor, ctx_pe: torch.Tensor,
-                      wkv_b_k: torch.Tensor, wkv_b_v: torch.Tensor, softmax_scale: float, is_causal: bool = False,
-                      q_start: int = 0) -> torch.Tensor:
-    """dsmoe_mla_attn_fwd: (B, S_q, H, D_v) bf16, no autograd."""
-    ts = (q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v)
+_ROWS_PER_CALL = 1 << 22
+
+# Successful launches of the HIP kernels (a caller can check that the fused
+# path ran rather than a fallback of its own).
+hip_calls = 0
+
+
+def _bf16_inputs(ts):
+    """The six inputs in bf16 for the kernels, or ValueError when the call is
+    not a bf16 one: q_nope in bf16, or a bf16 autocast region on its device."""
+    q = ts[0]
     for t in ts:
         if not t.is_cuda:
             raise RuntimeError("mla_attention: tensors must be on a ROCm GPU (no CPU implementation)")
-        if t.dtype != torch.bfloat16:
-            raise ValueError("mla_attention: bf16 tensors only")
+        if t.dtype not in (torch.bfloat16, torch.float32):
+            raise ValueError(f"mla_attention: bf16 or fp32 tensors only (got {t.dtype})")
+    dt = q.device.type
+    bf16_call = q.dtype == torch.bfloat16 or (torch.is_autocast_enabled(dt)
+                                               and torch.get_autocast_dtype(dt) == torch.bfloat16)
+    if not bf16_call:
+        raise ValueError("mla_attention: the kernels compute in bf16; fp32 queries need a bf16 autocast region")
+    return tuple(t if t.dtype == torch.bfloat16 else t.to(torch.bfloat16) for t in ts)
+
+
+def mla_attention_fwd(q_nope: torch.Tensor, q_pe: torch.Tensor, ctx_kv: torch.Tensor, ctx_pe: torch.Tensor,
+                      wkv_b_k: torch.Tensor, wkv_b_v: torch.Tensor, softmax_scale: float, is_causal: bool = False,
+                      q_start: int = 0) -> torch.Tensor:
+    """dsmoe_mla_attn_fwd: (B, S_q, H, D_v) in q_nope's dtype, no autograd."""
+    global hip_calls
+    out_dtype = q_nope.dtype
+    ts = _bf16_inputs((q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v))
+    q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v = ts
     B, H, S_q, D_nope = q_nope.shape
     R, D_rope, D_v = ctx_kv.size(-1), q_pe.shape[-1], wkv_b_v.size(1)
     _check_mla_dim_limits(R, D_nope, D_rope, D_v)
@@ -54,18 +88,31 @@ def mla_attention_fwd(q_nope: torch.Tensor, q_pe: torch.Tensor, ctx_kv: torch.Te
         raise ValueError("mla_attention: inconsistent shapes")
     dev = q_nope.device
     q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v = (t.contiguous() for t in ts)
-    d = _dims(q_nope, q_pe, ctx_kv, wkv_b_v, softmax_scale, is_causal, q_start)
+    # the kernels index rows with 32-bit offsets: B H pad64(S_kv) and B H S_q
+    # below 2^22 per call, so larger calls run in batch chunks
+    S_kv = ctx_kv.size(1)
+    per_batch = H * max(-(-S_kv // 64) * 64, S_q)
+    if per_batch >= _ROWS_PER_CALL:
+        raise ValueError(f"mla_attention: H * S_kv = {H * S_kv} (H * S_q = {H * S_q}) reaches 2^22, the limit of "
+                         "one batch row of the kernels' 32-bit row offsets")
+    bc = min(B, (_ROWS_PER_CALL - 1) // per_batch)
     lib = L.load()
+    d = _dims(q_nope[:bc], q_pe[:bc], ctx_kv[:bc], wkv_b_v, softmax_scale, is_causal, q_start)
     nbytes = int(lib.dsmoe_mla_attn_workspace_size(d))
     if nbytes == 0:
         L.check(lib.dsmoe_mla_attn_fwd(None, None, None, None, None, None, d, None, None, 0, None),
                 "dsmoe_mla_attn_fwd")
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     out = torch.empty(B, S_q, H, D_v, dtype=torch.bfloat16, device=dev)
-    rc = lib.dsmoe_mla_attn_fwd(L.ptr(q_nope), L.ptr(q_pe), L.ptr(ctx_kv), L.ptr(ctx_pe), L.ptr(wkv_b_k),
-                                L.ptr(wkv_b_v), d, L.ptr(out), L.ptr(ws), nbytes, L.stream_ptr(dev))
-    L.check(rc, "dsmoe_mla_attn_fwd")
-    return out
+    for b0 in range(0, B, bc):
+        b1 = min(B, b0 + bc)
+        d = _dims(q_nope[b0:b1], q_pe[b0:b1], ctx_kv[b0:b1], wkv_b_v, softmax_scale, is_causal, q_start)
+        rc = lib.dsmoe_mla_attn_fwd(L.ptr(q_nope[b0:b1]), L.ptr(q_pe[b0:b1]), L.ptr(ctx_kv[b0:b1]),
+                                    L.ptr(ctx_pe[b0:b1]), L.ptr(wkv_b_k), L.ptr(wkv_b_v), d, L.ptr(out[b0:b1]),
+                                    L.ptr(ws), nbytes, L.stream_ptr(dev))
+        L.check(rc, "dsmoe_mla_attn_fwd")
+    hip_calls += 1
+    return out if out_dtype == torch.bfloat16 else out.to(out_dtype)
 
 
 def _attention_torch(q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v, softmax_scale, is_causal, q_start):
@@ -96,7 +143,8 @@ class _MlaAttentionFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout):
         saved = ctx.saved_tensors
-        with torch.enable_grad():
+        # fp32 recompute whatever autocast state the backward runs under
+        with torch.enable_grad(), torch.autocast(saved[0].device.type, enabled=False):
             ins = [t.detach().float().requires_grad_() for t in saved]
             ref = _attention_torch(*ins, *ctx.args)
             grads = torch.autograd.grad(ref, ins, grad_outputs=dout.float(), allow_unused=True)

@@ -24,12 +24,39 @@ from typing import Optional, Tuple
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
+from torch.optim.optimizer import register_optimizer_step_post_hook
 
 from . import ops
 
 
 def _flt(t: torch.Tensor) -> torch.Tensor:
     return t if t.dtype == torch.float32 else t.float()
+
+
+# Parameter generation for the cast copies of fp32 expert weights.  A fused
+# optimizer step (torch.optim.AdamW(fused=True), the reference trainer's choice
+# on GPU, training/pretrain.py:197) rewrites the parameters in place without
+# moving their version counters, so a copy keyed on (_version, data_ptr) alone
+# would go stale.  Every torch.optim optimizer runs the global step post-hooks,
+# whichever implementation (fused, foreach, for-loop) it takes, so the
+# generation moves on every optimizer step of any optimizer.  Writes through
+# ``p.data`` outside an optimizer move neither counter: callers that do that
+# call ``invalidate_weight_casts()``.
+_weight_generation = [0]
+
+
+def invalidate_weight_casts() -> None:
+    """Marks every cached cast copy of an expert weight as stale (each is made
+    again on its next use).  Optimizer steps and in-place updates through the
+    parameter itself do this on their own; writes through ``param.data`` do not."""
+    _weight_generation[0] += 1
+
+
+def _after_optimizer_step(_optimizer, _args, _kwargs) -> None:
+    _weight_generation[0] += 1
+
+
+_optimizer_hook = register_optimizer_step_post_hook(_after_optimizer_step)
 
 
 def _compute_dtype(x: torch.Tensor) -> torch.dtype:
@@ -133,17 +160,18 @@ class DeepSeekMoE(nn.Module):
         self._last_counts: Optional[torch.Tensor] = None
         self._counts_of: Optional[torch.Tensor] = None  # the _last_indices _last_counts was computed from
         self._stack_dtype: Optional[torch.dtype] = None
-        # id(parameter) -> ((version, data_ptr, dtype), cast copy); see _cast
+        # id(parameter) -> ((generation, version, data_ptr, dtype), cast copy); see _cast
         self._cast_cache: dict = {}
 
     # -------------------------------------------------------------- forward
     def _cast(self, w: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
         """w in ``dtype`` for the expert GEMMs.  Under autocast the weights
         are fp32 parameters and the GEMMs read bf16: the cast copy is cached
-        and made again only when the parameter changes (its version counter
-        moves on every in-place update, e.g. an optimizer step), so a forward
-        does not re-cast all expert weights.  The gradient flows back to the
-        parameter in its own dtype, as through autocast's cast."""
+        and made again only when the parameter may have changed (an optimizer
+        step of any torch.optim optimizer, an in-place update that moves its
+        version counter, new storage), so a forward does not re-cast all
+        expert weights.  The gradient flows back to the parameter in its own
+        dtype, as through autocast's cast."""
         if w.dtype == dtype:
             return w
         if torch.compiler.is_compiling():
@@ -154,8 +182,11 @@ class DeepSeekMoE(nn.Module):
         return _CachedCast.apply(w, copy)
 
     def _cached_copy(self, w: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
-        """The detached cast copy of w, made again only when w changes."""
-        key = (w._version, w.data_ptr(), dtype)
+        """The detached cast copy of w, made again when w may have changed: the
+        optimizer-step generation, w's version counter or its storage moved.
+        Between a forward and its checkpoint recompute none of them moves, so
+        the recompute reads the same copy."""
+        key = (_weight_generation[0], w._version, w.data_ptr(), dtype)
         ent = self._cast_cache.get(id(w))
         if ent is None or ent[0] != key:
             with torch.no_grad():

@@ -201,7 +201,11 @@ int dsmoe_update_bias(const int32_t* counts, float* gate_bias, int E, float spee
 
 /* The same update from fp32 counts (E), for callers whose counts are not the
  * gate histogram (averaged or accumulated counts may be fractional); the
- * reference casts any counts with counts.float() (models/moe.py:24). */
+ * reference casts any counts with counts.float() (models/moe.py:24).  Integer
+ * counts give the reference's fp32 mean exactly.  For fractional counts the
+ * mean is the fp64 sum divided by E and rounded once; torch's fp32 reduction
+ * may differ from it by an ulp, which matters only for a count within an ulp
+ * of a band edge. */
 int dsmoe_update_bias_f32(const float* counts, float* gate_bias, int E, float speed, float upper, float lower,
                           void* stream);
 
@@ -236,12 +240,6 @@ int dsmoe_timing_enable(int on);
 int dsmoe_timing_read(double* stage_ms, int max_stages, int* n_calls);
 const char* dsmoe_timing_stage_name(int stage);
 
-/* Traffic-counter calibration for measurement tools (no counterpart in the
- * reference): reads exactly `bytes` (a multiple of 1 MiB, 16-byte aligned
- * src) with the direct global -> LDS loads of the grouped GEMMs, one
- * workgroup per MiB, and writes one word per workgroup to sink. */
-int dsmoe_probe_dma_read(const void* src, size_t bytes, uint32_t* sink, void* stream);
-
 /* ---------------------------------------------------------------------------
  * Multi-head latent attention forward (the fused MLA attention of
  * models/mla_triton.py:73-183, entered through triton_mla_attention,
@@ -256,7 +254,14 @@ int dsmoe_probe_dma_read(const void* src, size_t bytes, uint32_t* sink, void* st
  * is_causal (models/mla_triton.py:159-161) and no mask otherwise.  R, D_nope,
  * D_rope, D_v <= 256 as the reference requires (:186-196: DSMOE_ERR_INVALID),
  * and D_nope + D_rope <= 256 (DSMOE_ERR_UNSUPPORTED).  The workspace holds the
- * materialised K and V of every (batch, head). */
+ * materialised K and V of every (batch, head): B * H * pad64(S_kv) *
+ * (DQKp + DVp) * 2 + 256 bytes, DQKp = 2 D_nope + D_rope (D_nope + D_rope when
+ * that exceeds 256) and DVp = D_v, each rounded up to a multiple of 16 and 32
+ * (dsmoe_mla_attn_workspace_size gives the figure; about 2.7 GB at B 1,
+ * H 128, S_kv 32768, D_nope 128, D_rope 64, D_v 128).  Row indices are 32-bit:
+ * a call needs B * H * pad64(S_kv) and B * H * S_q below 2^22
+ * (DSMOE_ERR_UNSUPPORTED otherwise); dsmoe.mla splits larger calls by batch,
+ * so one batch's H * S_kv and H * S_q must stay below 2^22. */
 typedef struct dsmoe_mla_dims {
   int32_t B, H, S_q, S_kv;
   int32_t R;          /* kv_lora_rank        */

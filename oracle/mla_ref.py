@@ -11,6 +11,9 @@ may import it, and only as the checker / the timed CPU baseline.
   (``:154-155``), causal mask key <= query + q_start only when ``is_causal``
   (``:157-160``), softmax over keys, output (B, S_q, H, D_v) (``:178-183``).
   Evaluated in float64 from the given (bf16-representable) inputs.
+* ``mla_attention_sdpa_torch`` restates the reference layer's default SDPA
+  path (``models/mla.py:155-172``) with torch ops: the attention's CPU
+  baseline in bench.py (pinned against ``mla_attention_oracle``).
 * ``square_mask=True`` adds what ``mla_attention_reference``
   (``models/mla_triton.py:28-68``) also does: for ``is_causal=False`` with
   ``S_q == S_kv`` it applies a triu(-inf) mask anyway (``:52-57``), which the
@@ -92,6 +95,31 @@ def mla_attention_absorbed(q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v, softm
     lat = np.einsum("bhqk,bkr->bhqr", p, kv)
     o = np.einsum("bhqr,hdr->bhqd", lat, wv)
     return np.ascontiguousarray(o.transpose(0, 2, 1, 3))
+
+
+def mla_attention_sdpa_torch(q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v, softmax_scale: float,
+                             is_causal: bool = False):
+    """The reference layer's default attention path, restated with the same
+    torch ops (models/mla.py:155-172): K_nope and V of every head in one bmm
+    of the latent rows with [W_k; W_v], then scaled_dot_product_attention over
+    [q_nope | q_pe] and [K_nope | ctx_pe] (the layer's causal mask as
+    ``is_causal``).  Runs on the tensors' device in their dtype; bench.py times
+    it on the host cores as the attention's CPU baseline.  Returns
+    (B, S_q, H, D_v)."""
+    import torch
+    B, H, S_q, Dn = q_nope.shape
+    S_kv, R = ctx_kv.shape[1], ctx_kv.shape[2]
+    Dv = wkv_b_v.shape[1]
+    kv_rows = ctx_kv.reshape(B * S_kv, R).unsqueeze(0).expand(H, -1, -1)
+    w_kv = torch.cat([wkv_b_k, wkv_b_v], dim=1)
+    kv = torch.bmm(kv_rows, w_kv.transpose(-1, -2))
+    k_nope, v = kv.split([Dn, Dv], dim=-1)
+    k_nope = k_nope.reshape(H, B, S_kv, Dn).permute(1, 0, 2, 3)
+    v = v.reshape(H, B, S_kv, Dv).permute(1, 0, 2, 3).contiguous()
+    k = torch.cat([k_nope, ctx_pe.unsqueeze(1).expand(-1, H, -1, -1)], dim=-1)
+    q = torch.cat([q_nope, q_pe], dim=-1)
+    o = torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=is_causal, scale=softmax_scale)
+    return o.transpose(1, 2)
 
 
 def mla_flops(B: int, H: int, S_q: int, S_kv: int, R: int, Dn: int, Dr: int, Dv: int, is_causal: bool,

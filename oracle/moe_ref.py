@@ -94,22 +94,30 @@ def gate_logits_ref(x: torch.Tensor, gate_w: torch.Tensor) -> torch.Tensor:
     return F.linear(x.float(), gate_w.float())
 
 
-def route_from_logits_ref(logits: torch.Tensor, bias: torch.Tensor, k: int, route_scale: float = 1.0):
+def route_from_logits_ref(logits: torch.Tensor, bias: torch.Tensor, k: int, route_scale: float = 1.0,
+                          indices: Optional[torch.Tensor] = None):
     """models/moe.py:32-36 from given fp32 logits, with torch's own sigmoid/topk.
+    ``indices`` (T,k), when given, replaces the top-k selection (a routing
+    fixed elsewhere, e.g. the layer's own at a near-tie); the weights are still
+    gathered from these scores and renormalised.
 
     Returns (weights fp32 (T,k), indices int64 (T,k), scores fp32 (T,E))."""
     scores = logits.sigmoid()
     biased = scores + bias.to(scores.dtype)
-    indices = biased.topk(k, dim=-1)[1]
+    if indices is None:
+        indices = biased.topk(k, dim=-1)[1]
+    else:
+        indices = indices.to(torch.int64)
     weights = scores.gather(1, indices)
     weights = weights / weights.sum(dim=-1, keepdim=True).clamp(min=1e-10) * route_scale
     return weights, indices, scores
 
 
-def gate_ref(x: torch.Tensor, gate_w: torch.Tensor, bias: torch.Tensor, k: int, route_scale: float = 1.0):
+def gate_ref(x: torch.Tensor, gate_w: torch.Tensor, bias: torch.Tensor, k: int, route_scale: float = 1.0,
+             indices: Optional[torch.Tensor] = None):
     """AuxLossFreeGate.forward (models/moe.py:29-37) on x.float() with an fp32
     gate weight; weights are cast to ``x.dtype`` as in models/moe.py:36."""
-    w, idx, _ = route_from_logits_ref(gate_logits_ref(x, gate_w), bias, k, route_scale)
+    w, idx, _ = route_from_logits_ref(gate_logits_ref(x, gate_w), bias, k, route_scale, indices)
     return w.to(x.dtype), idx
 
 
@@ -175,12 +183,14 @@ def shared_ref(flat: torch.Tensor, sw1: List[torch.Tensor], sw2: List[torch.Tens
     return out.sum(dim=0)
 
 
-def moe_forward_ref(x: torch.Tensor, p: MoEParams, k: int, route_scale: float = 1.0, return_routing: bool = False):
-    """DeepSeekMoE.forward (models/moe.py:74-103): gate -> stacked routed -> + shared."""
+def moe_forward_ref(x: torch.Tensor, p: MoEParams, k: int, route_scale: float = 1.0, return_routing: bool = False,
+                    indices: Optional[torch.Tensor] = None):
+    """DeepSeekMoE.forward (models/moe.py:74-103): gate -> stacked routed -> + shared.
+    ``indices``: see route_from_logits_ref."""
     D = p.gate_w.shape[1]
     shape = x.shape
     flat = x.reshape(-1, D)
-    weights, indices = gate_ref(flat, p.gate_w, p.gate_bias, k, route_scale)
+    weights, indices = gate_ref(flat, p.gate_w, p.gate_bias, k, route_scale, indices)
     y = routed_stacked_ref(flat, indices, weights, p.w1, p.w2, p.w3)
     if p.sw1:
         y = y + shared_ref(flat, p.sw1, p.sw2, p.sw3)
@@ -261,10 +271,11 @@ def expert_grad_slice_ref(x_rows: torch.Tensor, dy_rows: torch.Tensor, w_rows: t
 # Autograd convenience: forward + backward of the restatement.
 # ----------------------------------------------------------------------------
 def moe_forward_backward_ref(x: torch.Tensor, p: MoEParams, k: int, dy: torch.Tensor,
-                             route_scale: float = 1.0) -> Dict[str, object]:
+                             route_scale: float = 1.0, indices: Optional[torch.Tensor] = None) -> Dict[str, object]:
     """Runs moe_forward_ref under autograd and returns y and all gradients.
 
-    Leaves: x, gate_w and every expert weight.  ``dy`` has x's shape."""
+    Leaves: x, gate_w and every expert weight.  ``dy`` has x's shape.
+    ``indices``: see route_from_logits_ref."""
     xl = x.detach().clone().requires_grad_(True)
     leaves = [t.detach().clone().requires_grad_(True) for t in p.tensors()]
     E, S = len(p.w1), len(p.sw1)
@@ -277,7 +288,7 @@ def moe_forward_backward_ref(x: torch.Tensor, p: MoEParams, k: int, dy: torch.Te
     sw2 = [next(it) for _ in range(S)]
     sw3 = [next(it) for _ in range(S)]
     q = MoEParams(gw, p.gate_bias, w1, w2, w3, sw1, sw2, sw3)
-    y, weights, indices = moe_forward_ref(xl, q, k, route_scale, return_routing=True)
+    y, weights, indices = moe_forward_ref(xl, q, k, route_scale, return_routing=True, indices=indices)
     y.backward(dy)
     z = lambda t: t.grad if t.grad is not None else torch.zeros_like(t)
     return {

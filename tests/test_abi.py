@@ -113,3 +113,14 @@ def test_permute_noalloc_rejects_calls_beyond_its_static_scratch(lib):
     assert str(L.PERMUTE_NOALLOC_BYTES).encode() in lib.dsmoe_last_error()
     small = L.Dims(8192, 2048, 64, 6, 1408, 2, 1408, L.DSMOE_BF16, 1.0)
     assert lib.dsmoe_permute_workspace_size(ctypes.byref(small)) <= L.PERMUTE_NOALLOC_BYTES
+
+
+def test_probe_is_measurement_tooling_outside_the_layer_abi(lib):
+    """The traffic-counter probe (include/dsmoe_probe.h) lives in its own
+    library; libdsmoe.so does not export it."""
+    import dsmoe._lib as L
+    assert not hasattr(lib, "dsmoe_probe_dma_read")
+    probe = ctypes.CDLL(str(L.LIB_PATH.with_name("libdsmoe_probe.so")))
+    text = re.sub(r"/\*.*?\*/", "", (ROOT / "include" / "dsmoe_probe.h").read_text(), flags=re.S)
+    for name in set(re.findall(r"\b(dsmoe_[a-z0-9_]+)\s*\(", text)):
+        assert hasattr(probe, name), name

@@ -181,6 +181,24 @@ def _slice_close(a, b, what):
     assert torch.allclose(a, b, rtol=2e-2, atol=2e-2 * b.abs().max().item()), f"{what}: max |diff| {err:.3e}"
 
 
+def _rows_close_or_fp32(a, b, what, x, p, dy, idx, k):
+    """Token-separable outputs (y, dx) over many rows: elementwise within
+    rtol = atol = 2e-2 of the bf16 oracle; a row where some element misses
+    that bar (over tens of millions of elements the two bf16 computations'
+    rounding differences reach past it) is checked against the fp32 oracle on
+    the same bf16 inputs and routing, and must be within the bar of it."""
+    a, b = a.float(), b.float()
+    miss = ~torch.isclose(a, b, rtol=2e-2, atol=2e-2)
+    rows = torch.nonzero(miss.any(-1)).flatten()
+    print(f"  {what}: {int(miss.sum())} of {miss.numel()} elements in {rows.numel()} rows miss the bar against "
+          f"the bf16 oracle (max |diff| {(a - b).abs().max().item():.3e})", flush=True)
+    assert rows.numel() <= max(16, a.shape[0] // 1000), rows.numel()
+    if rows.numel() == 0:
+        return
+    f32 = R.moe_forward_backward_ref(x[rows].float(), p.to(torch.float32), k, dy[rows].float(), indices=idx[rows])
+    _close(a[rows], f32[what], 2e-2, 2e-2, f"{what} rows against the fp32 oracle")
+
+
 def test_c4_full_size_gradients():
     """C4 (T=16384) at full size.  dx is token-separable: the oracle on a token
     sample is exact for those rows.  Weight gradients are sums over each
@@ -188,7 +206,8 @@ def test_c4_full_size_gradients():
     shared experts (all 16,384 rows) a slice of 64 inter columns of dW1, dW2
     and dW3 is compared with the fp32 oracle on exactly those rows
     (expert_grad_slice_ref), with the layer's routing and its fp32 weights.
-    Every gradient is finite; unrouted experts get exact zeros."""
+    Every gradient is finite; unrouted experts get exact zeros.  Then the
+    whole layer against the bf16 oracle's autograd at full size."""
     case = CS.C4
     x, p, dy = CS.make_inputs(case, with_dy=True)
     print(f"[c4] fwd+bwd T={case.T}", flush=True)
@@ -221,6 +240,34 @@ def test_c4_full_size_gradients():
         _slice_close(out["dsw1"][si][i0:i1], a, f"dsw1[{si}]")
         _slice_close(out["dsw2"][si][:, i0:i1], b, f"dsw2[{si}]")
         _slice_close(out["dsw3"][si][i0:i1], c, f"dsw3[{si}]")
+    # the whole layer under the oracle's autograd at full size (about 20 s of
+    # host time): routing, every row of dx, the full dW_gate (64 x 2048, each
+    # element a sum over about 1,500 rows) and every expert's dW, with the bf16
+    # bars of test_backward_bf16_vs_oracle
+    print("[c4] oracle autograd at full size", flush=True)
+    # Routing is bit-exact given the kernel's own fp32 logits (the layer
+    # routing tests); torch's CPU logits differ from them in accumulation
+    # order, so at 16,384 tokens a few tokens whose k-th and (k+1)-th biased
+    # scores are closer than that difference may pick the other expert.  The
+    # gradients are compared under the layer's routing, and each token whose
+    # set differs must be such a near-tie.
+    lg = R.gate_logits_ref(x, p.gate_w)
+    _, own, _ = R.route_from_logits_ref(lg, p.gate_bias, case.k)
+    differ = torch.nonzero((own.sort(-1)[0] != idx.sort(-1)[0]).any(-1)).flatten()
+    biased = (lg.sigmoid() + p.gate_bias).sort(-1, descending=True)[0]
+    gaps = (biased[differ, case.k - 1] - biased[differ, case.k]).abs()
+    print(f"[c4] tokens whose oracle top-k set differs: {differ.numel()}, gaps {gaps.tolist()}", flush=True)
+    assert differ.numel() <= 8 and (gaps < 1e-5).all()
+    ref = R.moe_forward_backward_ref(x, p, case.k, dy, indices=idx)
+    assert torch.equal(idx, ref["indices"])
+    _rows_close_or_fp32(out["y"], ref["y"], "y", x, p, dy, idx, case.k)
+    _rows_close_or_fp32(out["dx"], ref["dx"], "dx", x, p, dy, idx, case.k)
+    _sum_close(out["dgate_w"], ref["dgate_w"], "dgate_w")
+    rel = _relerr(out["dgate_w"], ref["dgate_w"])
+    print(f"[c4] dgate_w rel L2 vs the bf16 oracle {rel:.2e}", flush=True)
+    assert rel <= 2e-2, rel
+    for nm in ("dw1", "dw2", "dw3", "dsw1", "dsw2", "dsw3"):
+        _sum_close(torch.stack(out[nm]), torch.stack(ref[nm]), nm)
 
 
 def test_module_training_step_all_params_get_grads():

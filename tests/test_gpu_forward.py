@@ -352,6 +352,49 @@ def test_module_drop_in_forward_and_side_state():
     assert torch.equal(m._stacked_w1[3].cpu(), p.w1[3]) and torch.equal(m._shared_w1[0].cpu(), p.sw1[0])
 
 
+@pytest.mark.parametrize("training", [False, True])
+def test_dispatch_key_triton_grouped_equals_stacked(training):
+    """models/_triton_dispatch.py:13-35 and models/moe.py:61,87-99: a layer
+    built with moe_dispatch='triton_grouped' and one built with 'stacked' from
+    the same state_dict give the same result (the reference's own check,
+    tests/test_moe_triton.py:162-180, at atol 1e-5).  Here both keys run the
+    same HIP kernels, so outputs, routing and gradients are bitwise equal, and
+    both match the oracle; the config rewrite of enforce_triton_env_var leaves
+    the layer's results unchanged either way."""
+    from dsmoe import DeepSeekMoE, enforce_triton_env_var
+    case = CS.C1.with_tokens(768)
+    x, p, dy = CS.make_inputs(case, with_dy=True)
+    stacked = CS.load_module(case, p, DEV, lambda cfg: DeepSeekMoE(dict(cfg, moe_dispatch="stacked")))
+    triton = DeepSeekMoE(dict(case.config(), moe_dispatch="triton_grouped")).to(DEV, case.dtype)
+    triton.gate.float()
+    triton.load_state_dict(stacked.state_dict())
+    mods = {"stacked": stacked, "triton_grouped": triton}
+    for key, m in mods.items():
+        assert m.moe_dispatch == key
+    rewritten = dict(case.config(), moe_dispatch="triton_grouped")
+    enforce_triton_env_var(rewritten, lambda _msg: None)
+    outs = {}
+    for key, m in mods.items():
+        xin = x.clone().to(DEV).requires_grad_(training)
+        with torch.set_grad_enabled(training):
+            y = m(xin)
+            if training:
+                (y.float() * dy.to(DEV).float()).sum().backward()
+        torch.cuda.synchronize()
+        outs[key] = (y.detach(), m._last_indices.clone(), xin.grad if training else None,
+                     {n: q.grad.clone() for n, q in m.named_parameters() if training})
+    (ys, is_, gs, ps), (yt, it, gt, pt) = outs["stacked"], outs["triton_grouped"]
+    assert torch.equal(ys.view(torch.int16), yt.view(torch.int16)) and torch.equal(is_, it)
+    if training:
+        assert torch.equal(gs, gt)
+        for n in ps:
+            assert torch.equal(ps[n], pt[n]), n
+    y_ref, _, i_ref = R.moe_forward_ref(x, p, case.k, return_routing=True)
+    assert torch.equal(is_.cpu(), i_ref)
+    torch.testing.assert_close(ys.float().cpu(), y_ref.float(), rtol=2e-2, atol=2e-2)
+    assert rewritten["moe_dispatch"] in ("stacked", "triton_grouped")
+
+
 def test_module_update_bias_kats_on_device():
     """tests/test_models.py:325-345 and :760-777 on the device kernel."""
     from dsmoe import AuxLossFreeGate

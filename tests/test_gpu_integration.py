@@ -115,14 +115,23 @@ def test_torch_compile_inductor_backend():
         assert torch.equal(g0[n], g1[n]), n
 
 
-def test_autocast_weight_copies_follow_optimizer_steps():
+@pytest.mark.parametrize("optimizer", ["sgd", "adamw_fused", "adamw_foreach"])
+def test_autocast_weight_copies_follow_optimizer_steps(optimizer):
     """Under bf16 autocast the fp32 expert weights are cast once per
-    parameter version: two training steps with an SGD update between them give
-    the explicit bf16 layer's results on the updated (bf16-rounded) weights."""
+    parameter change: two training steps with an optimizer update between
+    them give the explicit bf16 layer's results on the updated (bf16-rounded)
+    weights.  The fused AdamW of the reference trainer (training/pretrain.py:197)
+    rewrites the parameters without moving their version counters; the cast
+    copies follow it through the optimizer step hook."""
     from dsmoe import DeepSeekMoE
     x, p, dy = CS.make_inputs(CASE32, with_dy=True)
     m32 = CS.load_module(CASE32, p, DEV, DeepSeekMoE)
-    opt = torch.optim.SGD(m32.parameters(), lr=0.5)
+    if optimizer == "sgd":
+        opt = torch.optim.SGD(m32.parameters(), lr=0.5)
+    else:
+        # a large rate so every weight moves by more than a bf16 ulp
+        opt = torch.optim.AdamW(m32.parameters(), lr=1e-2, weight_decay=0.1,
+                                fused=optimizer == "adamw_fused", foreach=optimizer == "adamw_foreach")
     for step in range(2):
         opt.zero_grad(set_to_none=True)
         xin = x.clone().to(DEV).requires_grad_(True)
@@ -139,4 +148,7 @@ def test_autocast_weight_copies_follow_optimizer_steps():
         assert torch.equal(xin.grad, dx16.float()), step
         for n, prm in m32.named_parameters():
             _same_gradient(f"{n} (step {step})" if not n.startswith("gate.") else n, prm.grad, g16[n])
+        before = m32.experts[0].w1.weight.detach().to(torch.bfloat16)
         opt.step()
+        # the update is visible at bf16 precision, so a stale copy would fail above
+        assert not torch.equal(before, m32.experts[0].w1.weight.detach().to(torch.bfloat16)), step

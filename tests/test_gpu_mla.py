@@ -136,3 +136,101 @@ def test_rejects_what_the_reference_rejects():
         mla_attention(ts[0], ts[1], big, ts[3], wk, wv, sc)
     with pytest.raises(ValueError, match="bf16"):
         mla_attention(*[t.float() for t in ts], sc)
+
+
+def test_bench_shape_all_batches_sampled_heads():
+    """The shape bench.py times (configs/pretrain_a100_422m.yaml: micro batch
+    8, 12 heads, S 2048, causal): 1536 work items over the XCD-chunked,
+    longest-first grid of mla_fa_kernel (block i runs item (i % 8) * 192 +
+    i / 8).  The (batch, head) pairs checked against the float64 oracle hold
+    the first item (0, 0), the last item of the first XCD chunk (0, 11) and
+    the first of the second (1, 0), a middle pair and the last item (7, 11)."""
+    from dsmoe.mla import mla_attention
+    B, H, S, R, Dn, Dr, Dv = 8, 12, 2048, 192, 48, 24, 64
+    print(f"[mla] bench shape B={B} H={H} S={S}", flush=True)
+    ts, sc = _inputs(B, H, S, S, R, Dn, Dr, Dv, seed=12)
+    out = mla_attention(*ts, sc, is_causal=True)
+    torch.cuda.synchronize()
+    assert out.shape == (B, S, H, Dv)
+    assert torch.isfinite(out.float()).all()
+    qn, qp, kv, pe, wk, wv = (t.cpu() for t in ts)
+    for b, h in ((0, 0), (0, 11), (1, 0), (4, 7), (7, 11)):
+        ref = mla_attention_oracle(qn[b:b + 1, h:h + 1], qp[b:b + 1, h:h + 1], kv[b:b + 1], pe[b:b + 1],
+                                   wk[h:h + 1], wv[h:h + 1], sc, is_causal=True)
+        got = out[b:b + 1, :, h:h + 1].float().cpu().numpy().astype(np.float64)
+        err = np.abs(got - ref)
+        bound = ATOL + RTOL * np.abs(ref)
+        print(f"[mla]   (b={b}, h={h}) max |err| {err.max():.3e}, max err/bound {(err / bound).max():.3f}", flush=True)
+        assert (err <= bound).all(), (b, h)
+
+
+def test_autocast_mixed_dtypes_from_the_reference_layer():
+    """Under bf16 autocast the reference's layer (models/mla.py:127-129,
+    209-220; trained as training/pretrain.py:154,212-213) hands the fused
+    operator bf16 queries, fp32 views of the fp32 wkv_b weight and fp32 latent
+    rows (an fp32 KV cache).  The HIP kernels run (no ValueError, so no SDPA
+    fallback in the layer), the output is bf16 (q_nope's dtype) within the
+    tolerance of the float64 oracle, and the backward gives the fp32 weight
+    and latent rows fp32 gradients close to float64 autograd."""
+    import dsmoe.mla as M
+    B, H, S, R, Dn, Dr, Dv = 2, 4, 96, 64, 32, 16, 32
+    g = torch.Generator().manual_seed(11)
+    wkv_b = torch.nn.Linear(R, H * (Dn + Dv), bias=False)
+    with torch.no_grad():
+        wkv_b.weight.copy_(torch.randn(wkv_b.weight.shape, generator=g) * 0.1)
+    wkv_b = wkv_b.to(DEV)
+    q = torch.randn(B, S, H, Dn + Dr, generator=g).to(DEV, torch.bfloat16)
+    q_nope = q[..., :Dn].permute(0, 2, 1, 3).contiguous()
+    q_pe = q[..., Dn:].permute(0, 2, 1, 3).contiguous()
+    ctx_kv = torch.randn(B, S, R, generator=g).to(DEV).requires_grad_(True)       # fp32
+    ctx_pe = torch.randn(B, S, Dr, generator=g).to(DEV)                           # fp32
+    full = wkv_b.weight.view(H, Dn + Dv, R)
+    wk, wv = full[:, :Dn], full[:, Dn:]
+    sc = (Dn + Dr) ** -0.5
+    calls = M.hip_calls
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        out = M.triton_mla_attention(q_nope, q_pe, ctx_kv, ctx_pe, wk, wv, sc, is_causal=True)
+    assert M.hip_calls == calls + 1
+    assert out.dtype == torch.bfloat16 and out.shape == (B, S, H, Dv)
+    r16 = lambda t: t.detach().to(torch.bfloat16).cpu()
+    ref = mla_attention_oracle(r16(q_nope), r16(q_pe), r16(ctx_kv), r16(ctx_pe), r16(wk), r16(wv), sc,
+                               is_causal=True)
+    got = out.detach().float().cpu().numpy().astype(np.float64)
+    assert (np.abs(got - ref) <= ATOL + RTOL * np.abs(ref)).all()
+    dout = torch.randn(out.shape, generator=g).to(DEV, torch.bfloat16)
+    out.backward(dout)
+    assert wkv_b.weight.grad.dtype == torch.float32 and ctx_kv.grad.dtype == torch.float32
+    f64 = lambda t: t.detach().cpu().double().requires_grad_()
+    qn, qp, kv, pe, w = f64(q_nope), f64(q_pe), f64(ctx_kv), f64(ctx_pe), f64(wkv_b.weight)
+    fv = w.view(H, Dn + Dv, R)
+    k = torch.cat([torch.einsum("bsr,hdr->bhsd", kv, fv[:, :Dn]), pe[:, None].expand(B, H, S, Dr)], dim=-1)
+    v = torch.einsum("bsr,hdr->bhsd", kv, fv[:, Dn:])
+    o = torch.nn.functional.scaled_dot_product_attention(torch.cat([qn, qp], -1), k, v, is_causal=True, scale=sc)
+    o.permute(0, 2, 1, 3).backward(dout.cpu().double())
+    for got_g, ref_g in ((wkv_b.weight.grad, w.grad), (ctx_kv.grad, kv.grad)):
+        d = (got_g.cpu().double() - ref_g).abs().max().item()
+        assert d <= 2e-2 + 2e-2 * ref_g.abs().max().item(), d
+
+
+def test_call_beyond_the_row_index_limit_runs_in_batch_chunks():
+    """B H S_kv = 2^22 exceeds the kernels' 32-bit row offsets for one call:
+    the operator splits it by batch (one batch per launch here) and every
+    batch's output matches the oracle (checked on a head of each chunk)."""
+    from dsmoe.mla import mla_attention
+    B, H, S, R, Dn, Dr, Dv = 2, 256, 8192, 16, 8, 8, 8
+    print(f"[mla] B={B} H={H} S={S}: B H S = 2^22", flush=True)
+    ts, sc = _inputs(B, H, S, S, R, Dn, Dr, Dv, seed=13, wscale=0.3)
+    out = mla_attention(*ts, sc, is_causal=True)
+    torch.cuda.synchronize()
+    qn, qp, kv, pe, wk, wv = (t.cpu() for t in ts)
+    for b, h in ((0, 0), (1, 255)):
+        ref = mla_attention_oracle(qn[b:b + 1, h:h + 1], qp[b:b + 1, h:h + 1], kv[b:b + 1], pe[b:b + 1],
+                                   wk[h:h + 1], wv[h:h + 1], sc, is_causal=True)
+        got = out[b:b + 1, :, h:h + 1].float().cpu().numpy().astype(np.float64)
+        assert (np.abs(got - ref) <= ATOL + RTOL * np.abs(ref)).all(), (b, h)
+    with pytest.raises(ValueError, match="2\\^22"):
+        big = torch.zeros(1, 512, 8192, 8, dtype=torch.bfloat16, device=DEV)
+        mla_attention(big, big, torch.zeros(1, 8192, R, dtype=torch.bfloat16, device=DEV),
+                      torch.zeros(1, 8192, 8, dtype=torch.bfloat16, device=DEV),
+                      torch.zeros(512, 8, R, dtype=torch.bfloat16, device=DEV),
+                      torch.zeros(512, 8, R, dtype=torch.bfloat16, device=DEV), sc, is_causal=True)

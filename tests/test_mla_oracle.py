@@ -100,3 +100,20 @@ def test_flop_count_pairs():
     f = mla_flops(1, 1, 4, 4, 8, 2, 2, 2, True)
     assert f["pairs"] == 10
     assert mla_flops(1, 1, 2, 6, 8, 2, 2, 2, True, q_start=4)["pairs"] == 5 + 6
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_sdpa_restatement_matches_the_oracle(causal):
+    """The torch restatement of the reference's SDPA path (bench.py's CPU
+    baseline for the attention) computes the oracle's attention: float64
+    inputs, within 1e-10."""
+    from oracle.mla_ref import mla_attention_sdpa_torch
+    g = torch.Generator().manual_seed(4)
+    B, H, S, R, Dn, Dr, Dv = 2, 3, 40, 24, 16, 8, 20
+    ts = [torch.randn(*s, generator=g, dtype=torch.float64) for s in
+          ((B, H, S, Dn), (B, H, S, Dr), (B, S, R), (B, S, Dr), (H, Dn, R), (H, Dv, R))]
+    sc = (Dn + Dr) ** -0.5
+    got = mla_attention_sdpa_torch(*ts, sc, is_causal=causal).numpy()
+    ref = mla_attention_oracle(*ts, sc, is_causal=causal)
+    assert got.shape == ref.shape == (B, S, H, Dv)
+    assert np.abs(got - ref).max() < 1e-10

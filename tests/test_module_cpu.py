@@ -107,6 +107,23 @@ def test_enforce_triton_env_var_compat(monkeypatch, env, cfg, expect, warned):
     assert bool(log) == warned
 
 
+@pytest.mark.parametrize("env", [None, "0", "1"])
+def test_enforce_triton_env_var_attention_key(monkeypatch, env):
+    """Both of the reference's keys (models/_triton_dispatch.py:13-16): the
+    attention selection is reset to 'sdpa' with the MoE one, in one log call."""
+    if env is None:
+        monkeypatch.delenv("ENABLE_TRITON_KERNELS", raising=False)
+    else:
+        monkeypatch.setenv("ENABLE_TRITON_KERNELS", env)
+    cfg = {"attn_impl": "triton", "moe_dispatch": "triton_grouped", "dim": 64}
+    log = []
+    enforce_triton_env_var(cfg, log.append)
+    if env == "1":
+        assert cfg == {"attn_impl": "triton", "moe_dispatch": "triton_grouped", "dim": 64} and not log
+    else:
+        assert cfg == {"attn_impl": "sdpa", "moe_dispatch": "stacked", "dim": 64} and len(log) == 1
+
+
 def test_next_pow2():
     assert [next_pow2(n) for n in (0, 1, 2, 3, 64, 65, 384)] == [1, 1, 2, 4, 64, 128, 512]
 
@@ -253,3 +270,30 @@ def test_autocast_cast_cache_follows_parameter_updates(small_cfg):
     assert moe._cast(w, torch.float32) is w
     moe.to(torch.float64)
     assert not moe._cast_cache
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_cast_cache_follows_adamw_steps(small_cfg, fused):
+    """A fused AdamW step (the reference trainer's optimizer on GPU,
+    training/pretrain.py:197) rewrites the parameters without moving their
+    version counters or storage; the cached bf16 copy must still follow it.
+    Writes through ``param.data`` move nothing: ``invalidate_weight_casts``
+    covers those."""
+    from dsmoe import invalidate_weight_casts
+    moe = DeepSeekMoE(small_cfg)
+    w = moe.experts[0].w1.weight
+    opt = torch.optim.AdamW(moe.parameters(), lr=1e-2, fused=fused, foreach=False if fused else None)
+    stale = moe._cached_copy(w, torch.bfloat16)
+    for p in moe.parameters():
+        p.grad = torch.ones_like(p)
+    version, ptr = w._version, w.data_ptr()
+    opt.step()
+    if fused:
+        assert (w._version, w.data_ptr()) == (version, ptr)   # nothing on the tensor shows the update
+    fresh = moe._cached_copy(w, torch.bfloat16)
+    assert not torch.equal(fresh, stale)
+    assert torch.equal(fresh, w.detach().to(torch.bfloat16))
+    with torch.no_grad():
+        w.data.add_(1.0)
+    invalidate_weight_casts()
+    assert torch.equal(moe._cached_copy(w, torch.bfloat16), w.detach().to(torch.bfloat16))

@@ -307,3 +307,25 @@ def test_expert_grad_slice_matches_full_layer_autograd():
     torch.testing.assert_close(a.double(), full["dsw1"][0], rtol=1e-5, atol=1e-6)
     torch.testing.assert_close(b.double(), full["dsw2"][0], rtol=1e-5, atol=1e-6)
     torch.testing.assert_close(c.double(), full["dsw3"][0], rtol=1e-5, atol=1e-6)
+
+
+def test_fixed_routing_option_reproduces_the_oracle_and_follows_a_given_set():
+    """moe_forward_backward_ref(indices=...) with the oracle's own routing gives
+    its results bit for bit; with one token's set changed, that token's
+    weights are the gathered, renormalised scores of the given experts."""
+    g = torch.Generator().manual_seed(9)
+    T, D, E, I, k = 40, 32, 8, 16, 2
+    x = torch.randn(T, D, generator=g)
+    dy = torch.randn(T, D, generator=g)
+    p = R.make_params(D, E, I, 1, seed=10)
+    a = R.moe_forward_backward_ref(x, p, k, dy)
+    b = R.moe_forward_backward_ref(x, p, k, dy, indices=a["indices"])
+    for key in ("y", "dx", "dgate_w"):
+        assert torch.equal(a[key], b[key]), key
+    forced = a["indices"].clone()
+    forced[3] = torch.tensor([e for e in range(E) if e not in forced[3].tolist()][:k])
+    c = R.moe_forward_backward_ref(x, p, k, dy, indices=forced)
+    assert torch.equal(c["indices"], forced)
+    s = R.gate_logits_ref(x, p.gate_w).sigmoid()[3, forced[3]]
+    assert torch.allclose(c["weights"][3], s / s.sum(), rtol=0, atol=1e-7)
+    assert not torch.equal(c["y"][3], a["y"][3]) and torch.equal(c["y"][4], a["y"][4])
