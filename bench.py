@@ -24,10 +24,11 @@ Printed as one JSON line, with
 
 Order: the headline workload's W + K steps first, in a process that has not
 used the GPU yet (``cold_start``: the clock is still ramping into its loaded
-state for the first ~25 steps), then the other workloads (decode, C1, C2, the
-vendor library's dense GEMMs, MLA attention), then the headline's W + K steps
-again on the loaded GPU (``value``, ``ms_per_step``, the stage times and the
-roofline), then the training step and the autocast figures.
+state for the first ~30 steps), then the other workloads (decode, C1, C2, MLA
+attention, the vendor library's dense GEMMs, the training step), then the
+headline's W + K steps again on the loaded GPU (``value``, ``ms_per_step``,
+the stage times and the roofline), then the autocast figures, and the
+host-side CPU baselines last.
 """
 from __future__ import annotations
 
@@ -572,14 +573,20 @@ def main() -> int:
         # headline, which is timed on the loaded GPU
         cold_ms, _ = time_steps(step, args.steps, args.warmup)
         log(f"[bench] cold start ({args.warmup} warm-up steps in a fresh process): {cold_ms:.3f} ms/step")
-    # the other workloads, then the headline on the loaded GPU
+    # the other workloads, then the headline on the loaded GPU: the MFMA-heavy
+    # ones (the vendor library's dense GEMMs, the training step) run last
+    # before it, since lighter work (attention, decode) leaves the clock below
+    # its loaded state
     if not args.no_decode and args.config == "c3":
         extra["decode"] = decode_bench(dev, max(10, args.steps), max(3, args.warmup))
     if not args.no_extra_configs and args.config == "c3":
         extra["configs_fwd"] = {c: fwd_bench(c, dev, args.steps, args.warmup) for c in ("c1", "c2")}
-        extra["blas_dense_reference"] = blas_dense_reference(dev, cfg)
     if not args.no_mla and args.config == "c3":
         extra["mla"] = mla_bench(dev, args.steps, args.warmup)
+    if not args.no_extra_configs and args.config == "c3":
+        extra["blas_dense_reference"] = blas_dense_reference(dev, cfg)
+    if not args.no_fwd_bwd:
+        extra["fwd_bwd"] = fwd_bwd_bench(args.fwd_bwd_config, dev, max(3, args.steps // 4), max(1, args.warmup // 2))
     with torch.no_grad():
         ms, wall = time_steps(step, args.steps, args.warmup)
         log(f"[bench] timed {args.steps} steps: {ms:.3f} ms/step (host wall {wall:.3f} ms/step)")
@@ -635,8 +642,6 @@ def main() -> int:
         "note": f"the same {args.warmup} warm-up + {args.steps} timed steps as the first GPU work of the process; "
                 "the headline is timed after the other workloads, on the loaded GPU"}
     result.update(extra)
-    if not args.no_fwd_bwd:
-        result["fwd_bwd"] = fwd_bwd_bench(args.fwd_bwd_config, dev, max(3, args.steps // 4), max(1, args.warmup // 2))
     if not args.no_autocast and args.config == "c3":
         fb = result.get("fwd_bwd")
         result["autocast"] = autocast_bench(dev, args.steps, args.warmup, ms,

@@ -185,6 +185,7 @@ struct QPA {
   uint32_t off[QW_LD];   // byte offsets; after a tile switch the A row indices until converted
   int lt, lk, nk, ls;    // load tile, its next slab, its slab count, global index of the next load
   int pend;              // off[] holds row indices
+  int nld;               // loads of this wave that hold rows of the tile (the rest are skipped)
 };
 
 __device__ __forceinline__ void qpa_rows(QPA& A, const QPTile& t, int s, int lane_) {
@@ -200,6 +201,12 @@ __device__ __forceinline__ void qpa_rows(QPA& A, const QPTile& t, int s, int lan
   }
   A.base = qp_uniform(g.A);
   A.lda2 = (uint32_t)(2 * g.lda);
+  // Load i of wave s covers rows (s QW_LD + i) 8 .. + 7; loads wholly past
+  // the tile's rows are skipped.  The LDS rows they would fill feed only
+  // output rows that are never stored (an output row depends on its A row
+  // alone), so a partial tile moves only the A bytes it uses (C3: the last
+  // M tile of 30 of the 64 experts holds 3 to 94 rows).
+  A.nld = __builtin_amdgcn_readfirstlane(min(QW_LD, max(0, (t.rows + 7) / 8 - s * QW_LD)));
   A.nk = t.nk;
   A.lk = 0;
   A.pend = 1;
@@ -219,8 +226,14 @@ __device__ __forceinline__ void qpa_step(QPA& A, const QPList& L, int bn, int s,
   }
   const uint32_t d = lds_a + (A.ls & 1) * QW_REG;
   const char* src = A.base + A.lk * (QW_BK * 2);
+  if (A.nld == QW_LD) {
 #pragma unroll
-  for (int i = 0; i < QW_LD; ++i) dma16s(src, A.off[i], d + i * 1024);
+    for (int i = 0; i < QW_LD; ++i) dma16s(src, A.off[i], d + i * 1024);
+  } else {
+#pragma unroll
+    for (int i = 0; i < QW_LD; ++i)
+      if (i < A.nld) dma16s(src, A.off[i], d + i * 1024);
+  }
   ++A.ls;
   if (++A.lk == A.nk) {
     if (++A.lt < L.ntiles) qpa_rows(A, qp_tile(L, bn, A.lt), s, lane);
@@ -451,11 +464,15 @@ __device__ __forceinline__ void qp_tile0(const QPTile& t, QPA& A, const QPList& 
     // (waited for with this phase's loads)
     if (k == t.nk - 1) qp_rowmap<NMI>(t, wm, crow);
     __builtin_amdgcn_sched_barrier(0);
+    // the MFMA wave takes issue precedence over the loading wave on its SIMD
+    // (measured on MI355X: about 1 % on both forward GEMMs at C3)
+    __builtin_amdgcn_s_setprio(3);
     if (k == 0)
       qw_mma_first<EPI, NMI>(F, acc);
     else
       qw_mma<EPI, NMI>(F, acc);
     __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(0);
     wait_vm<0>();  // this wave's part of A(s + k + 1) has landed
     qw_sync();
     if (k + 1 < t.nk) {
@@ -510,11 +527,13 @@ __device__ __forceinline__ void qp_tile1(const QPTile& t, QPB& B, const QPList& 
     // second-to-last slab (the next even phase's vmcnt wait covers it)
     if (k == t.nk - 2) qp_rowmap<NMI>(t, wm, crow);
     __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(3);
     if (k == 0)
       qw_mma_first<EPI, NMI>(F, acc);
     else
       qw_mma<EPI, NMI>(F, acc);
     __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(0);
     qw_sync();
   }
   // start of the even phase of slab S + 1 (S = the tile's last slab): the
