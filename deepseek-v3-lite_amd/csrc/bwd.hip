@@ -551,7 +551,7 @@ __global__ __launch_bounds__(256) void sched32_kernel(const int32_t* __restrict_
       m.group = e;
       m.row0 = o + i * bm;
       m.rows = min(bm, c - i * bm);
-      m.pad = 0;
+      m.seq = mtile_seq(i, (c + bm - 1) / bm);
       sched[til32[e] + i] = m;
     }
   }

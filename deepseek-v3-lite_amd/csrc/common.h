@@ -88,8 +88,12 @@ struct MTile {  // one M tile of the routed schedule
   int32_t group;
   int32_t row0;   // first row (sorted position)
   int32_t rows;   // valid rows in this tile (<= BM)
-  int32_t pad;
+  int32_t seq;    // mtile_seq(): this tile's index among its group's tiles and their count
 };
+
+// MTile::seq of tile i of a group of n M tiles: i << 16 | n, or 0 when the
+// group has more than 65535 tiles (consumers then keep the schedule order).
+__host__ __device__ inline int32_t mtile_seq(int32_t i, int32_t n) { return n < 65536 ? (i << 16) | n : 0; }
 
 struct GemmDesc {
   // schedule

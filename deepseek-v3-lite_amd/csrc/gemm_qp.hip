@@ -152,11 +152,27 @@ __device__ __forceinline__ QPTile qp_tile(const QPList& L, int bn, int i) {
   }
   t.which = __builtin_amdgcn_readfirstlane(t.which);
   const GemmDesc __attribute__((address_space(4)))& g = P->g[t.which];
-  const int mt = (int)((uint32_t)lin / (uint32_t)nt);
-  t.n0 = (lin - mt * nt) * bn;
+  int mt = (int)((uint32_t)lin / (uint32_t)nt);
+  int nb_i = lin - mt * nt;
   if (g.sched) {
     static_assert(sizeof(MTile) == sizeof(u32x4_t), "MTile is four 32-bit fields");
-    const u32x4_t m = ld_scalar(reinterpret_cast<const u32x4_t*>(g.sched + mt));
+    const u32x4_t* sch = reinterpret_cast<const u32x4_t*>(g.sched);
+    u32x4_t m = ld_scalar(sch + mt);
+    // Item order inside a group (expert) of n M tiles: every item reads 256
+    // weight rows and 256 activation rows per slab, so with more N blocks
+    // than M tiles (nt > n) the group's weights are the larger operand and
+    // its items run N block by N block (item q = nb_i * n + i of the group's
+    // range): the workgroups on consecutive items read the same weight rows
+    // at about the same time, and each weight block comes from HBM about
+    // once.  Otherwise M tile by M tile (the activation rows read once).
+    const uint32_t n = m.w & 0xffffu;  // MTile::seq: tiles of the group
+    if (n > 1 && (uint32_t)nt > n) {
+      const int t0 = mt - (int)(m.w >> 16);
+      const uint32_t q = (uint32_t)(lin - t0 * nt);
+      const int mt2 = t0 + (int)(q % n);
+      nb_i = (int)(q / n);
+      if (mt2 != mt) m = ld_scalar(sch + mt2);
+    }
     t.grp = (int)m.x;    // MTile::group
     t.row0 = (int)m.y;   // MTile::row0
     t.rows = (int)m.z;   // MTile::rows
@@ -166,6 +182,7 @@ __device__ __forceinline__ QPTile qp_tile(const QPList& L, int bn, int i) {
     t.row0 = (mt - t.grp * tpg) * QW_BM;
     t.rows = min(QW_BM, g.dense_rows - t.row0);
   }
+  t.n0 = nb_i * bn;
   t.nk = g.K / QW_BK;
   t.grp = __builtin_amdgcn_readfirstlane(t.grp);
   t.row0 = __builtin_amdgcn_readfirstlane(t.row0);

@@ -187,7 +187,7 @@ __global__ __launch_bounds__(256) void sched_from_offsets_kernel(const int64_t* 
       m.group = e;
       m.row0 = o + i * bm;
       m.rows = min(bm, c - i * bm);
-      m.pad = 0;
+      m.seq = mtile_seq(i, (c + bm - 1) / bm);
       sched[til[e] + i] = m;
     }
   }

@@ -119,7 +119,7 @@ __device__ __forceinline__ void write_offsets(const int32_t* cnt, const int32_t*
       m.group = e;
       m.row0 = off[e] + i * po.bm;
       m.rows = min(po.bm, c - i * po.bm);
-      m.pad = 0;
+      m.seq = mtile_seq(i, (c + po.bm - 1) / po.bm);
       po.sched[t0 + i] = m;
     }
   }
