@@ -50,8 +50,11 @@ constexpr int XQ_LD = XQ_REG / 1024 / 4;              // direct loads per wave, 
 __device__ __attribute__((aligned(16))) uint4 g_xq_zero[4];
 // 1.0: the row weight of an unweighted SwiGLU-backward epilogue.
 __device__ float g_xq_one[1] = {1.0f};
-// Where the SwiGLU-backward epilogue stores elements outside its tile (never read).
-__device__ __attribute__((aligned(16))) uint4 g_xq_sink[1];
+// Where the SwiGLU-backward epilogue stores elements outside its tile (never
+// read): 16 bytes per thread of 64 workgroup slots, so the out-of-tile stores
+// of a ragged tile spread over 256 KB instead of meeting in one cache line.
+constexpr int XQ_SINK_SLOTS = 64;
+__device__ __attribute__((aligned(16))) uint4 g_xq_sink[XQ_SINK_SLOTS * 256];
 
 typedef short xq_v4s __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(1))) u32x4_t xq_gv4u;  // a global-memory u32x4_t
@@ -489,6 +492,7 @@ __global__ __launch_bounds__(256) void xgemm_q_kernel(const XGemm g) {
   // lane guard makes it wait for all of them).
   const bf16_t* Gs = static_cast<const bf16_t*>(g.Gs);
   const bf16_t* Us = static_cast<const bf16_t*>(g.Us);
+  const uint4* sink = g_xq_sink + (blockIdx.x % XQ_SINK_SLOTS) * 256 + tid;
   rowp[tid] = my_rowp;
   const int cc = tid & 7, rq = tid >> 3;
   // row weights, or a stride-0 read of 1.0 when there are none
@@ -563,7 +567,7 @@ __global__ __launch_bounds__(256) void xgemm_q_kernel(const XGemm g) {
         duw[e2] = pack_bf16x2(du[0], du[1]);
       }
       // global (not flat) stores: a flat store also counts as an LDS access
-      const int64_t dst = ok ? rpv[i] + 2 * (int64_t)n : reinterpret_cast<int64_t>(g_xq_sink);
+      const int64_t dst = ok ? rpv[i] + 2 * (int64_t)n : reinterpret_cast<int64_t>(sink);
       const int64_t du_bytes = ok ? 2 * g.du_off : 0;
       *reinterpret_cast<xq_gv4u*>(dst) = u32x4_t{dgw[0], dgw[1], dgw[2], dgw[3]};
       *reinterpret_cast<xq_gv4u*>(dst + du_bytes) = u32x4_t{duw[0], duw[1], duw[2], duw[3]};
