@@ -168,6 +168,37 @@ def routed_schedule(counts, bm: int):
     return sched
 
 
+def sched_seq(sched):
+    """MTile::seq of each entry (mtile_seq): its index among its group's M tiles and their count."""
+    out, i = [], 0
+    while i < len(sched):
+        j = i
+        while j < len(sched) and sched[j][0] == sched[i][0]:
+            j += 1
+        out += [(k, j - i) for k in range(j - i)]
+        i = j
+    return out
+
+
+_SEQ_CACHE = {}
+
+
+def routed_item(sched, lin: int, nt: int):
+    """Item lin of a routed tile list (qp_tile): (M tile, N tile).  Inside a
+    group of n M tiles with nt > n the items run N tile by N tile."""
+    key = (id(sched), len(sched))
+    if key not in _SEQ_CACHE:
+        _SEQ_CACHE.clear()
+        _SEQ_CACHE[key] = sched_seq(sched)
+    mt, nb = divmod(lin, nt)
+    i, n = _SEQ_CACHE[key][mt]
+    if 1 < n < 65536 and nt > n:
+        t0 = mt - i
+        q = lin - t0 * nt
+        mt, nb = t0 + q % n, q // n
+    return mt, nb
+
+
 def sched_bound(rows: int, groups: int, bm: int) -> int:
     return rows // bm + groups + 1
 
@@ -216,7 +247,10 @@ def qp_lists(gr: Gemm, gd: Optional[Gemm], bm: int, bn: int, grid: int):
                 lin, nt, g, which = d_base + li, ntd, gd, 1
             else:
                 lin, nt, g, which = r_base + (li - d_cnt), ntr, gr, 0
-            m_tile, n_tile = divmod(lin, nt)
+            if which == 0 and g.sched is not None:
+                m_tile, n_tile = routed_item(g.sched, lin, nt)
+            else:
+                m_tile, n_tile = divmod(lin, nt)
             grp, row0, rows = _sched_tile(g, m_tile, bm)
             tiles.append((which, grp, row0, rows, n_tile))
         out.append(tiles)
@@ -640,6 +674,9 @@ def xq_ok(g: XGemm) -> bool:
 
 def xq_launch(rec: Recorder, g: XGemm, what: str):
     tl = xtiles(g)
+    keys = {(grp, row0, n_tile, split) for grp, row0, rows, n_tile, kbeg, kend, split in tl}
+    if len(keys) != len(tl):
+        raise Violation(f"{what}: a tile in two blocks")
     for grp, row0, rows, n_tile, kbeg, kend, split in tl:
         xq_tile(rec, g, grp, row0, rows, n_tile, kbeg, kend, split, f"{what}[g{grp} r{row0} n{n_tile} s{split}]")
     return len(tl)

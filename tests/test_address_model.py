@@ -218,3 +218,18 @@ def test_model_catches_a_slab_overrun():
             _backward(M.Recorder(), T, D, E, k, I, S, I_s, counts, st, ss, off)
     finally:
         M.xq_tile = orig
+
+
+def test_routed_item_order_is_a_permutation():
+    """qp_tile's item order inside an expert's M tiles: every (M tile,
+    N tile) once, N tile by N tile when the expert has fewer M tiles than
+    there are N tiles, M tile by M tile otherwise."""
+    sched = M.routed_schedule([600, 0, 40, 1300, 256], 256)  # 3, 0, 1, 6, 1 M tiles
+    nt = 4
+    items = [M.routed_item(sched, lin, nt) for lin in range(len(sched) * nt)]
+    assert sorted(items) == [(m, n) for m in range(len(sched)) for n in range(nt)]
+    # expert 0 (3 M tiles < 4 N tiles): N-major inside its item range
+    assert items[:6] == [(0, 0), (1, 0), (2, 0), (0, 1), (1, 1), (2, 1)]
+    # expert 3 (6 M tiles >= 4 N tiles): M-major, as enumerated
+    first3 = 4 * 4  # items before expert 3: 3 + 1 M tiles
+    assert items[first3:first3 + 5] == [(4, 0), (4, 1), (4, 2), (4, 3), (5, 0)]
