@@ -19,8 +19,9 @@ Printed as one JSON line, with
 * ``cpu_baseline``: the CPU restatement of the reference stacked path
   (oracle/moe_ref.py) timed on this host on a bounded token sample;
 * ``fwd_bwd``: the training step of BASELINE config 4 (the config-3 layer at
-  T=16384: forward, then backward to dx, dW_gate and every expert's dW) with
-  its own per-stage times and CPU baseline (the oracle under autograd).
+  T=16384: forward, then backward to dx, dW_gate and every expert's dW),
+  timed over K / 2 steps after W warm-up steps, with its own per-stage
+  times and CPU baseline (the oracle under autograd).
 
 Order: the headline workload's W + K steps first, in a process that has not
 used the GPU yet (``cold_start``: the clock is still ramping into its loaded
@@ -586,7 +587,7 @@ def main() -> int:
     if not args.no_extra_configs and args.config == "c3":
         extra["blas_dense_reference"] = blas_dense_reference(dev, cfg)
     if not args.no_fwd_bwd:
-        extra["fwd_bwd"] = fwd_bwd_bench(args.fwd_bwd_config, dev, max(3, args.steps // 4), max(1, args.warmup // 2))
+        extra["fwd_bwd"] = fwd_bwd_bench(args.fwd_bwd_config, dev, max(3, args.steps // 2), max(1, args.warmup))
     with torch.no_grad():
         ms, wall = time_steps(step, args.steps, args.warmup)
         log(f"[bench] timed {args.steps} steps: {ms:.3f} ms/step (host wall {wall:.3f} ms/step)")
