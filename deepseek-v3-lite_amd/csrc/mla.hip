@@ -55,6 +55,17 @@ struct MlaArgs {
   const bf16_t* w_k;      // (H, Dn, R)
   const bf16_t* w_v;      // (H, Dv, R)
   bf16_t* out;            // (B, S_q, H, Dv)
+  float* lse;             // (B, H, S_q): c m + log2(sum of p), the base-2 log-sum-exp of the scaled scores, or null
+  // backward
+  const bf16_t* dout;     // (B, S_q, H, Dv)
+  float* delta;           // (B, H, S_q) rowsum(dO * O)
+  float* dq_nope;         // (B, H, S_q, Dn) fp32
+  float* dq_pe;           // (B, H, S_q, Dr)
+  float* dk_nope;         // (B, S_kv, H, Dn): rows of the latent positions, heads side by side
+  float* dk_pe;           // (B, S_kv, H, Dr)
+  float* dv;              // (B, S_kv, H, Dv)
+  int dovec;              // 16-byte dO row loads (Dv % 8 == 0, dout 16-byte aligned)
+  float scale;            // softmax_scale
   bf16_t* kbuf;           // (B, H, S_kvp, DQKp)
   bf16_t* vbuf;           // (B, H, S_kvp, DVp)
   int B, H, S_q, S_kv, R, Dn, Dr, Dv;
@@ -520,6 +531,9 @@ __global__ __launch_bounds__(256) void mla_fa_kernel(const MlaArgs a) {
   const float lt = mla_pair_sum(l);
   const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
   if (qi >= a.S_q) return;
+  // the backward's probabilities are exp2(c s - lse); a query without a
+  // visible key gets +inf (probability 0)
+  if (a.lse && hi == 0) a.lse[bh * a.S_q + qi] = lt > 0.0f ? m * a.c + log2f(lt) : INFINITY;
   bf16_t* orow = a.out + (((int64_t)b * a.S_q + qi) * a.H + h) * a.Dv;
 #pragma unroll
   for (int v = 0; v < NV; ++v)
@@ -542,6 +556,502 @@ __global__ __launch_bounds__(256) void mla_fa_kernel(const MlaArgs a) {
           if (dv + e < a.Dv) orow[dv + e] = f2bf(o[v][4 * g + e] * inv);
       }
     }
+}
+
+// ---------------------------------------------------------------- backward
+// The attention's backward in two deterministic kernels (no atomics), with
+// P = exp2(c s - lse) (the forward's probabilities, rebuilt from its
+// per-query base-2 log-sum-exp), D = rowsum(dO * O) and z = scale q.k:
+//   dV = P^T dO,  dZ = P (dO V^T - D),  dK = scale dZ^T Q,  dQ = scale dZ K.
+// mla_bwd_kv_kernel owns 128 keys (four waves of 32) and walks the query
+// tiles that see them, accumulating dV and dK in registers;
+// mla_bwd_q_kernel owns 128 queries and walks their keys, accumulating dQ.
+// Both rebuild s with the forward's operands (K rows [k_hi | pe | k_lo] from
+// mla_kv_kernel, query rows [q_nope | q_pe | q_nope], q negated when the
+// scale is negative), so dK comes out as |scale| dZ^T q_eff and dQ over the
+// K columns, k_hi and k_lo parts added at the end.  The probabilities and dZ
+// enter the MFMAs as bf16.
+//
+// Staged tiles are read both as MFMA fragments (ds_read_b128: eight columns
+// of a row per lane) and transposed (ds_read_b64_tr_b16: four consecutive
+// rows of a column per lane), so 16-byte chunk c of row r sits at
+// c ^ mlb_g(r) inside each group of 16 chunks; sixteen consecutive rows at one
+// chunk, and four consecutive rows (r = 0 mod 4) at four consecutive chunks
+// (c = 0 mod 4), then fall on distinct banks.
+constexpr int MLB_KW = 128;   // keys per workgroup of the dK, dV kernel
+constexpr int MLB_QT = 32;    // queries per staged tile of the dK, dV kernel
+constexpr int MLB_KT = 64;    // keys per staged tile of the dQ kernel
+
+__device__ __forceinline__ int mlb_off(int r, int c, int rb) {
+  const int g = ((r & 3) << 2) | ((r >> 2) & 3);
+  return r * rb + (((c & ~15) | ((c & 15) ^ g)) << 4);
+}
+
+// MFMA fragment of a staged tile: row `row`, 16-byte chunk `chunk`.
+__device__ __forceinline__ bf16x8_t mlb_frag(const char* t, int rb, int row, int chunk) {
+  return *reinterpret_cast<const bf16x8_t*>(t + mlb_off(row, chunk, rb));
+}
+
+// Transposed fragment: columns c0 .. c0 + 31 (c0 = 0 mod 32) over rows
+// r0 .. r0 + 15 (r0 = 0 mod 8) of a staged tile, the rows in the order the
+// score MFMA leaves in a lane's registers (lanes 0-31: r0 + {0-3, 8-11},
+// lanes 32-63: r0 + {4-7, 12-15}); lane l gets column c0 + (l & 31).
+__device__ __forceinline__ bf16x8_t mlb_tfrag(const char* t, int rb, int r0, int c0, int lane) {
+  const int gq = lane >> 4, sl = lane & 15;
+  const int r = r0 + 4 * (gq >> 1) + (sl >> 2);
+  const int u = (c0 >> 2) + 4 * (gq & 1) + (sl & 3);   // 8-byte unit: columns 4u .. 4u + 3
+  const mla_v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) mla_v4s*)(t + mlb_off(r, u >> 1, rb) + ((u & 1) << 3)));
+  const mla_v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) mla_v4s*)(t + mlb_off(r + 8, u >> 1, rb) + ((u & 1) << 3)));
+  typedef short v8s __attribute__((ext_vector_type(8)));
+  const v8s v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+
+// 16 bf16 probabilities (or dZ values) of a lane's registers as the two
+// 16-key (16-query) K-steps of the next MFMAs.
+__device__ __forceinline__ void mlb_pack(const float (&p)[16], bf16x8_t (&f)[2]) {
+#pragma unroll
+  for (int ps = 0; ps < 2; ++ps) {
+    bf16x2_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      w[e][0] = (__bf16)p[8 * ps + 2 * e];
+      w[e][1] = (__bf16)p[8 * ps + 2 * e + 1];
+    }
+    f[ps] = __builtin_bit_cast(bf16x8_t, w);
+  }
+}
+
+// 8 columns d .. d + 7 of query row q (B H S_q layout) in the forward's
+// query layout [q_nope | q_pe | q_nope (split K) | 0], negated for a negative
+// scale; zeros past S_q.
+__device__ __forceinline__ mla_u32x4 mlb_qchunk(const MlaArgs& a, int64_t bh, int q, int d) {
+  mla_u32x4 v = {0u, 0u, 0u, 0u};
+  if (q >= a.S_q) return v;
+  const int qend = a.ksplit ? 2 * a.Dn + a.Dr : a.Dn + a.Dr;
+  const bf16_t* qn = a.q_nope + (bh * a.S_q + q) * a.Dn;
+  const bf16_t* qp = a.q_pe + (bh * a.S_q + q) * a.Dr;
+  if (a.qvec) {
+    // each 8-column group lies in one part (D_nope, D_rope multiples of 8)
+    if (d < a.Dn) v = *reinterpret_cast<const mla_u32x4*>(qn + d);
+    else if (d < a.Dn + a.Dr) v = *reinterpret_cast<const mla_u32x4*>(qp + (d - a.Dn));
+    else if (d < qend) v = *reinterpret_cast<const mla_u32x4*>(qn + (d - a.Dn - a.Dr));
+  } else {
+    bf16_t e8[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int c = d + e;
+      e8[e] = c < a.Dn ? qn[c] : c < a.Dn + a.Dr ? qp[c - a.Dn] : c < qend ? qn[c - a.Dn - a.Dr] : bf16_t(0);
+    }
+    v = *reinterpret_cast<const mla_u32x4*>(e8);
+  }
+  if (a.negq) v ^= mla_u32x4{0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
+  return v;
+}
+
+// 8 dO values d .. d + 7 of query q ((B, S_q, H, D_v) layout); zeros past
+// S_q or D_v.
+__device__ __forceinline__ mla_u32x4 mlb_dochunk(const MlaArgs& a, int b, int h, int q, int d) {
+  mla_u32x4 v = {0u, 0u, 0u, 0u};
+  if (q >= a.S_q || d >= a.Dv) return v;
+  const bf16_t* row = a.dout + (((int64_t)b * a.S_q + q) * a.H + h) * a.Dv;
+  if (a.dovec) return *reinterpret_cast<const mla_u32x4*>(row + d);
+  bf16_t e8[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) e8[e] = d + e < a.Dv ? row[d + e] : bf16_t(0);
+  return *reinterpret_cast<const mla_u32x4*>(e8);
+}
+
+template <int NSTEP, int NV>
+struct MlbKvCfg {
+  static constexpr int DQKp = NSTEP * 16;
+  static constexpr int DVp = NV * 32;
+  static constexpr int QRB = (DQKp + 127) / 128 * 256;   // Q tile row bytes
+  static constexpr int ORB = (DVp + 127) / 128 * 256;    // dO tile row bytes
+  static constexpr int QT = MLB_QT * QRB;
+  static constexpr int OT = MLB_QT * ORB;
+  static constexpr int BUF = QT + OT + 2 * MLB_QT * 4;   // Q, dO, lse, D
+  static constexpr int QCH = MLB_QT * DQKp / 8;          // 16-byte chunks of a tile with data
+  static constexpr int OCH = MLB_QT * DVp / 8;
+  static constexpr int NLQ = (QCH + 255) / 256;
+  static constexpr int NLO = (OCH + 255) / 256;
+};
+
+// Work items (batch, head, 128-key block), block i on XCD i % 8 taking
+// contiguous eighths (a head's key blocks share their XCD's L2 copy of its
+// queries and dO).  Wave w owns keys k0 + 32 w ..; a lane one key, with its
+// K and V rows (the B operands of the score and dP MFMAs) in registers.
+template <int NSTEP, int NV>
+__global__ __launch_bounds__(256) void mla_bwd_kv_kernel(const MlaArgs a) {
+  using C = MlbKvCfg<NSTEP, NV>;
+  extern __shared__ __attribute__((aligned(16))) char mlb_smem[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hi = lane >> 5, l32 = lane & 31;
+  const int nkb = (a.S_kv + MLB_KW - 1) / MLB_KW;
+  const int total = nkb * a.H * a.B;
+  const int per = (total + 7) / 8;
+  const int item = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+  if (item >= total) return;
+  const int hb = item / nkb;
+  const int h = hb % a.H, b = hb / a.H;
+  const int k0 = (item - hb * nkb) * MLB_KW;
+  const int kw0 = k0 + 32 * wave;
+  const int key = kw0 + l32;
+  const int64_t bh = (int64_t)b * a.H + h;
+  const int nc = (a.Dn + a.Dr + 31) / 32;   // 32-column tiles of dK
+
+  bf16x8_t kf[NSTEP], vf[2 * NV];
+  {
+    const int kr = min(key, a.S_kvp - 1);   // rows past S_kv are zero and masked below
+    const bf16_t* krow = a.kbuf + (bh * a.S_kvp + kr) * C::DQKp;
+    const bf16_t* vrow = a.vbuf + (bh * a.S_kvp + kr) * C::DVp;
+#pragma unroll
+    for (int st = 0; st < NSTEP; ++st) kf[st] = *reinterpret_cast<const bf16x8_t*>(krow + 16 * st + 8 * hi);
+#pragma unroll
+    for (int st = 0; st < 2 * NV; ++st) vf[st] = *reinterpret_cast<const bf16x8_t*>(vrow + 16 * st + 8 * hi);
+  }
+  mla_f32x16 dva[NV], dka[NSTEP / 2];
+#pragma unroll
+  for (int v = 0; v < NV; ++v)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) dva[v][i] = 0.0f;
+#pragma unroll
+  for (int t = 0; t < NSTEP / 2; ++t)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) dka[t][i] = 0.0f;
+
+  // query tiles that see a key of this block: q >= k0 - q_start when causal
+  const int qb = a.causal ? max(0, k0 - a.q_start) / MLB_QT * MLB_QT : 0;
+  const int nqt = a.S_q > qb ? (a.S_q - qb + MLB_QT - 1) / MLB_QT : 0;
+
+  mla_u32x4 qst[C::NLQ], ost[C::NLO];
+  float lst = 0.0f;
+  auto gload = [&](int i) {
+    const int qt = qb + i * MLB_QT;
+#pragma unroll
+    for (int u = 0; u < C::NLQ; ++u) {
+      const int ch = tid + 256 * u;
+      if (C::QCH % 256 == 0 || ch < C::QCH) {
+        const int r = ch / (C::DQKp / 8), cc = ch - r * (C::DQKp / 8);
+        qst[u] = mlb_qchunk(a, bh, qt + r, 8 * cc);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < C::NLO; ++u) {
+      const int ch = tid + 256 * u;
+      if (C::OCH % 256 == 0 || ch < C::OCH) {
+        const int r = ch / (C::DVp / 8), cc = ch - r * (C::DVp / 8);
+        ost[u] = mlb_dochunk(a, b, h, qt + r, 8 * cc);
+      }
+    }
+    if (tid < 2 * MLB_QT) {
+      const int q = qt + (tid & (MLB_QT - 1));
+      lst = tid < MLB_QT ? (q < a.S_q ? a.lse[bh * a.S_q + q] : INFINITY)
+                         : (q < a.S_q ? a.delta[bh * a.S_q + q] : 0.0f);
+    }
+  };
+  auto lstore = [&](int buf) {
+    char* tq = mlb_smem + buf * C::BUF;
+    char* to = tq + C::QT;
+    float* tl = reinterpret_cast<float*>(to + C::OT);
+#pragma unroll
+    for (int u = 0; u < C::NLQ; ++u) {
+      const int ch = tid + 256 * u;
+      if (C::QCH % 256 == 0 || ch < C::QCH) {
+        const int r = ch / (C::DQKp / 8), cc = ch - r * (C::DQKp / 8);
+        *reinterpret_cast<mla_u32x4*>(tq + mlb_off(r, cc, C::QRB)) = qst[u];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < C::NLO; ++u) {
+      const int ch = tid + 256 * u;
+      if (C::OCH % 256 == 0 || ch < C::OCH) {
+        const int r = ch / (C::DVp / 8), cc = ch - r * (C::DVp / 8);
+        *reinterpret_cast<mla_u32x4*>(to + mlb_off(r, cc, C::ORB)) = ost[u];
+      }
+    }
+    if (tid < 2 * MLB_QT) tl[tid] = lst;   // lse[0 .. 31], then D[0 .. 31]
+  };
+
+  if (nqt > 0) {
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    if (nqt > 1) gload(1);
+  }
+  for (int i = 0; i < nqt; ++i) {
+    const int qt = qb + i * MLB_QT;
+    const char* tq = mlb_smem + (i & 1) * C::BUF;
+    const char* to = tq + C::QT;
+    const float* tl = reinterpret_cast<const float*>(to + C::OT);
+    // a wave whose keys the whole tile cannot see skips it
+    const bool live = kw0 < a.S_kv && !(a.causal && qt + MLB_QT - 1 + a.q_start < kw0);
+    if (live) {
+      // s, dP: lane = key, register r = query qt + 8 (r / 4) + 4 hi + r % 4
+      mla_f32x16 sc, dp;
+#pragma unroll
+      for (int i2 = 0; i2 < 16; ++i2) {
+        sc[i2] = 0.0f;
+        dp[i2] = 0.0f;
+      }
+#pragma unroll
+      for (int st = 0; st < NSTEP; ++st)
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mlb_frag(tq, C::QRB, l32, 2 * st + hi), kf[st], sc, 0, 0, 0);
+#pragma unroll
+      for (int st = 0; st < 2 * NV; ++st)
+        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mlb_frag(to, C::ORB, l32, 2 * st + hi), vf[st], dp, 0, 0, 0);
+      float p[16], dz[16];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 l4 = *reinterpret_cast<const float4*>(tl + 8 * g + 4 * hi);
+        const float4 d4 = *reinterpret_cast<const float4*>(tl + MLB_QT + 8 * g + 4 * hi);
+        const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+        const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * g + e;
+          const int q = qt + 8 * g + 4 * hi + e;
+          const bool ok = q < a.S_q && key < a.S_kv && (!a.causal || key <= q + a.q_start);
+          p[r] = ok ? __builtin_amdgcn_exp2f(fmaf(sc[r], a.c, -lv[e])) : 0.0f;
+          dz[r] = p[r] * (dp[r] - dv[e]);
+        }
+      }
+      bf16x8_t pf[2], zf[2];
+      mlb_pack(p, pf);
+      mlb_pack(dz, zf);
+#pragma unroll
+      for (int ps = 0; ps < 2; ++ps) {
+#pragma unroll
+        for (int v = 0; v < NV; ++v)
+          dva[v] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mlb_tfrag(to, C::ORB, 16 * ps, 32 * v, lane), pf[ps],
+                                                           dva[v], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < NSTEP / 2; ++t)
+          if (t < nc)
+            dka[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mlb_tfrag(tq, C::QRB, 16 * ps, 32 * t, lane), zf[ps],
+                                                             dka[t], 0, 0, 0);
+      }
+    }
+    if (i + 1 < nqt) lstore((i + 1) & 1);
+    __syncthreads();
+    if (i + 2 < nqt) gload(i + 2);
+  }
+
+  // dK = |scale| dZ^T q_eff (lane = key, register r: column 32 t + 8 (r / 4)
+  // + 4 hi + r % 4), dV = P^T dO (dv likewise)
+  if (key >= a.S_kv) return;
+  const float sk = a.c * (1.0f / MLA_LOG2E);
+  const int64_t kh = ((int64_t)b * a.S_kv + key) * a.H + h;
+  float* dkn = a.dk_nope + kh * a.Dn;
+  float* dkp = a.dk_pe + kh * a.Dr;
+  float* dvo = a.dv + kh * a.Dv;
+#pragma unroll
+  for (int t = 0; t < NSTEP / 2; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int c = 32 * t + 8 * (r >> 2) + 4 * hi + (r & 3);
+      if (t < nc) {
+        if (c < a.Dn)
+          dkn[c] = sk * dka[t][r];
+        else if (c < a.Dn + a.Dr)
+          dkp[c - a.Dn] = sk * dka[t][r];
+      }
+    }
+#pragma unroll
+  for (int v = 0; v < NV; ++v)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int c = 32 * v + 8 * (r >> 2) + 4 * hi + (r & 3);
+      if (c < a.Dv) dvo[c] = dva[v][r];
+    }
+}
+
+template <int NSTEP, int NV>
+struct MlbQCfg {
+  static constexpr int DQKp = NSTEP * 16;
+  static constexpr int DVp = NV * 32;
+  static constexpr int KRB = (DQKp + 127) / 128 * 256;
+  static constexpr int VRB = (DVp + 127) / 128 * 256;
+  static constexpr int KT = MLB_KT * KRB;
+  static constexpr int BUF = KT + MLB_KT * VRB;
+  static constexpr int KCH = MLB_KT * DQKp / 8;
+  static constexpr int VCH = MLB_KT * DVp / 8;
+  static constexpr int NLK = (KCH + 255) / 256;
+  static constexpr int NLV = (VCH + 255) / 256;
+  static constexpr int SRS = DQKp + 4;                     // fp32 dQ staging row (floats)
+  static constexpr int STG = 4 * 32 * SRS * 4;
+  static constexpr int LDS = 2 * BUF > STG ? 2 * BUF : STG;
+};
+
+// Work items as the forward's: (batch, head, 128-query block), a head's
+// blocks longest first.  Lane: one query, its query fragments and dO row (the
+// B operands of the score and dP MFMAs) in registers.
+template <int NSTEP, int NV>
+__global__ __launch_bounds__(256) void mla_bwd_q_kernel(const MlaArgs a) {
+  using C = MlbQCfg<NSTEP, NV>;
+  extern __shared__ __attribute__((aligned(16))) char mlb_smem[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hi = lane >> 5, l32 = lane & 31;
+  const int nq = (a.S_q + MLA_QB - 1) / MLA_QB;
+  const int total = nq * a.H * a.B;
+  const int per = (total + 7) / 8;
+  const int item = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+  if (item >= total) return;
+  const int hb = item / nq;
+  const int h = hb % a.H, b = hb / a.H;
+  const int q0 = (nq - 1 - (item - hb * nq)) * MLA_QB;
+  const int qi = q0 + 32 * wave + l32;
+  const int64_t bh = (int64_t)b * a.H + h;
+
+  bf16x8_t qf[NSTEP], of[2 * NV];
+#pragma unroll
+  for (int st = 0; st < NSTEP; ++st) qf[st] = __builtin_bit_cast(bf16x8_t, mlb_qchunk(a, bh, qi, 16 * st + 8 * hi));
+#pragma unroll
+  for (int st = 0; st < 2 * NV; ++st) of[st] = __builtin_bit_cast(bf16x8_t, mlb_dochunk(a, b, h, qi, 16 * st + 8 * hi));
+  const float lq = qi < a.S_q ? a.lse[bh * a.S_q + qi] : INFINITY;
+  const float dq = qi < a.S_q ? a.delta[bh * a.S_q + qi] : 0.0f;
+  const int qpos = qi + a.q_start;
+  mla_f32x16 dqa[NSTEP / 2];
+#pragma unroll
+  for (int t = 0; t < NSTEP / 2; ++t)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) dqa[t][i] = 0.0f;
+
+  int kend = a.S_kv;
+  if (a.causal) kend = min(kend, min(q0 + MLA_QB, a.S_q) - 1 + a.q_start + 1);
+  const int nkb = (kend + MLB_KT - 1) / MLB_KT;
+  const bf16_t* kg = a.kbuf + bh * a.S_kvp * C::DQKp;
+  const bf16_t* vg = a.vbuf + bh * a.S_kvp * C::DVp;
+
+  mla_u32x4 kst[C::NLK], vst[C::NLV];
+  auto gload = [&](int kb) {
+    const int kk = kb * MLB_KT;
+#pragma unroll
+    for (int u = 0; u < C::NLK; ++u) {
+      const int ch = tid + 256 * u;
+      if (C::KCH % 256 == 0 || ch < C::KCH) {
+        const int r = ch / (C::DQKp / 8), cc = ch - r * (C::DQKp / 8);
+        kst[u] = *reinterpret_cast<const mla_u32x4*>(kg + (int64_t)(kk + r) * C::DQKp + cc * 8);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < C::NLV; ++u) {
+      const int ch = tid + 256 * u;
+      if (C::VCH % 256 == 0 || ch < C::VCH) {
+        const int r = ch / (C::DVp / 8), cc = ch - r * (C::DVp / 8);
+        vst[u] = *reinterpret_cast<const mla_u32x4*>(vg + (int64_t)(kk + r) * C::DVp + cc * 8);
+      }
+    }
+  };
+  auto lstore = [&](int buf) {
+    char* tk = mlb_smem + buf * C::BUF;
+    char* tv = tk + C::KT;
+#pragma unroll
+    for (int u = 0; u < C::NLK; ++u) {
+      const int ch = tid + 256 * u;
+      if (C::KCH % 256 == 0 || ch < C::KCH) {
+        const int r = ch / (C::DQKp / 8), cc = ch - r * (C::DQKp / 8);
+        *reinterpret_cast<mla_u32x4*>(tk + mlb_off(r, cc, C::KRB)) = kst[u];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < C::NLV; ++u) {
+      const int ch = tid + 256 * u;
+      if (C::VCH % 256 == 0 || ch < C::VCH) {
+        const int r = ch / (C::DVp / 8), cc = ch - r * (C::DVp / 8);
+        *reinterpret_cast<mla_u32x4*>(tv + mlb_off(r, cc, C::VRB)) = vst[u];
+      }
+    }
+  };
+
+  if (nkb > 0) {
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    if (nkb > 1) gload(1);
+  }
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int kk = kb * MLB_KT;
+    const char* tk = mlb_smem + (kb & 1) * C::BUF;
+    const char* tv = tk + C::KT;
+#pragma unroll
+    for (int t = 0; t < MLB_KT / 32; ++t) {
+      // s, dP: lane = query, register r = key kk + 32 t + 8 (r / 4) + 4 hi + r % 4
+      mla_f32x16 sc, dp;
+#pragma unroll
+      for (int i2 = 0; i2 < 16; ++i2) {
+        sc[i2] = 0.0f;
+        dp[i2] = 0.0f;
+      }
+#pragma unroll
+      for (int st = 0; st < NSTEP; ++st)
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mlb_frag(tk, C::KRB, 32 * t + l32, 2 * st + hi), qf[st], sc, 0,
+                                                     0, 0);
+#pragma unroll
+      for (int st = 0; st < 2 * NV; ++st)
+        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mlb_frag(tv, C::VRB, 32 * t + l32, 2 * st + hi), of[st], dp, 0,
+                                                     0, 0);
+      float dz[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int k = kk + 32 * t + 8 * (r >> 2) + 4 * hi + (r & 3);
+        const bool ok = qi < a.S_q && k < a.S_kv && (!a.causal || k <= qpos);
+        const float p = ok ? __builtin_amdgcn_exp2f(fmaf(sc[r], a.c, -lq)) : 0.0f;
+        dz[r] = p * (dp[r] - dq);
+      }
+      bf16x8_t zf[2];
+      mlb_pack(dz, zf);
+#pragma unroll
+      for (int ps = 0; ps < 2; ++ps)
+#pragma unroll
+        for (int ct = 0; ct < NSTEP / 2; ++ct)
+          dqa[ct] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mlb_tfrag(tk, C::KRB, 32 * t + 16 * ps, 32 * ct, lane),
+                                                            zf[ps], dqa[ct], 0, 0, 0);
+    }
+    if (kb + 1 < nkb) lstore((kb + 1) & 1);
+    __syncthreads();
+    if (kb + 2 < nkb) gload(kb + 2);
+  }
+
+  // dQ over the K columns (lane = query, register r: column 32 ct + 8 (r / 4)
+  // + 4 hi + r % 4), staged per wave as fp32 rows, then dq_nope = scale
+  // (k_hi part + k_lo part), dq_pe = scale pe part, written row by row
+  float* stg = reinterpret_cast<float*>(mlb_smem) + wave * 32 * C::SRS;
+#pragma unroll
+  for (int ct = 0; ct < NSTEP / 2; ++ct)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      *reinterpret_cast<float4*>(stg + l32 * C::SRS + 32 * ct + 8 * g + 4 * hi) =
+          make_float4(dqa[ct][4 * g], dqa[ct][4 * g + 1], dqa[ct][4 * g + 2], dqa[ct][4 * g + 3]);
+  __syncthreads();
+  const int qw = q0 + 32 * wave;
+  const float sq = a.scale;
+  for (int i = lane; i < 32 * a.Dn; i += 64) {
+    const int r = i / a.Dn, d = i - r * a.Dn;
+    if (qw + r < a.S_q)
+      a.dq_nope[(bh * a.S_q + qw + r) * a.Dn + d] =
+          sq * (stg[r * C::SRS + d] + (a.ksplit ? stg[r * C::SRS + a.Dn + a.Dr + d] : 0.0f));
+  }
+  for (int i = lane; i < 32 * a.Dr; i += 64) {
+    const int r = i / a.Dr, d = i - r * a.Dr;
+    if (qw + r < a.S_q) a.dq_pe[(bh * a.S_q + qw + r) * a.Dr + d] = sq * stg[r * C::SRS + a.Dn + d];
+  }
+}
+
+// D = rowsum(dO * O) per (batch, head, query) in fp32: thread per (b, q, h) row.
+__global__ __launch_bounds__(256) void mla_bwd_delta_kernel(const MlaArgs a) {
+  const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;   // (b, q, h)
+  if (row >= (int64_t)a.B * a.S_q * a.H) return;
+  const int h = (int)(row % a.H);
+  const int64_t bq = row / a.H;
+  const int q = (int)(bq % a.S_q), b = (int)(bq / a.S_q);
+  const bf16_t* o = a.out + row * a.Dv;
+  const bf16_t* g = a.dout + row * a.Dv;
+  float s = 0.0f;
+  for (int d = 0; d < a.Dv; ++d) s = fmaf(bf2f(o[d]), bf2f(g[d]), s);
+  a.delta[((int64_t)b * a.H + h) * a.S_q + q] = s;
 }
 
 // ---------------------------------------------------------------- host side
@@ -592,6 +1102,7 @@ static MlaArgs mla_args(const dsmoe_mla_dims* d) {
   a.q_start = d->q_start;
   a.negq = d->softmax_scale < 0.0f ? 1 : 0;
   a.c = (d->softmax_scale < 0.0f ? -d->softmax_scale : d->softmax_scale) * MLA_LOG2E;
+  a.scale = d->softmax_scale;
   return a;
 }
 
@@ -620,43 +1131,47 @@ static int mla_launch_fa_nv(const MlaArgs& a, hipStream_t st) {
   }
 }
 
-}  // namespace dsmoe
-
-using namespace dsmoe;
-
-extern "C" size_t dsmoe_mla_attn_workspace_size(const dsmoe_mla_dims* dims) {
-  if (mla_validate(dims) != DSMOE_OK) return 0;
-  const MlaArgs a = mla_args(dims);
-  return (size_t)a.B * a.H * a.S_kvp * (a.DQKp + a.DVp) * sizeof(bf16_t) + 256;
+template <int NSTEP, int NV>
+static int mla_launch_bwd(const MlaArgs& a, hipStream_t st) {
+  {
+    using C = MlbKvCfg<NSTEP, NV>;
+    constexpr size_t lds = 2 * (size_t)C::BUF;
+    auto kern = mla_bwd_kv_kernel<NSTEP, NV>;
+    if (lds > 64 * 1024) {
+      static const hipError_t attr =
+          hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (attr != hipSuccess) return fail(DSMOE_ERR_HIP, "mla: cannot raise LDS limit");
+    }
+    const int64_t total = cdiv(a.S_kv, MLB_KW) * a.H * a.B;
+    hipLaunchKernelGGL(kern, dim3((unsigned)(8 * cdiv(total, 8))), dim3(256), lds, st, a);
+    const int rc = check_launch("mla_bwd_kv");
+    if (rc) return rc;
+  }
+  using C = MlbQCfg<NSTEP, NV>;
+  constexpr size_t lds = (size_t)C::LDS;
+  auto kern = mla_bwd_q_kernel<NSTEP, NV>;
+  if (lds > 64 * 1024) {
+    static const hipError_t attr =
+        hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr != hipSuccess) return fail(DSMOE_ERR_HIP, "mla: cannot raise LDS limit");
+  }
+  const int64_t total = cdiv(a.S_q, MLA_QB) * a.H * a.B;
+  hipLaunchKernelGGL(kern, dim3((unsigned)(8 * cdiv(total, 8))), dim3(256), lds, st, a);
+  return check_launch("mla_bwd_q");
 }
 
-extern "C" int dsmoe_mla_attn_fwd(const void* q_nope, const void* q_pe, const void* ctx_kv, const void* ctx_pe,
-                                  const void* wkv_b_k, const void* wkv_b_v, const dsmoe_mla_dims* dims, void* out,
-                                  void* workspace, size_t workspace_bytes, void* stream) {
-  int rc = mla_validate(dims);
-  if (rc) return rc;
-  DSMOE_REQUIRE(q_nope && q_pe && ctx_kv && ctx_pe && wkv_b_k && wkv_b_v && out, DSMOE_ERR_INVALID,
-                "mla: NULL tensor pointer");
-  const size_t need = dsmoe_mla_attn_workspace_size(dims);
-  DSMOE_REQUIRE(workspace && workspace_bytes >= need, DSMOE_ERR_WORKSPACE, "mla: workspace too small");
-  DSMOE_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15) == 0, DSMOE_ERR_INVALID,
-                "mla: workspace must be 16-byte aligned");
-  MlaArgs a = mla_args(dims);
-  a.q_nope = static_cast<const bf16_t*>(q_nope);
-  a.q_pe = static_cast<const bf16_t*>(q_pe);
-  a.ctx_kv = static_cast<const bf16_t*>(ctx_kv);
-  a.ctx_pe = static_cast<const bf16_t*>(ctx_pe);
-  a.w_k = static_cast<const bf16_t*>(wkv_b_k);
-  a.w_v = static_cast<const bf16_t*>(wkv_b_v);
-  a.out = static_cast<bf16_t*>(out);
-  auto al = [](const void* p, uintptr_t m) { return (reinterpret_cast<uintptr_t>(p) & (m - 1)) == 0; };
-  a.qvec = (a.Dn % 8 == 0 && a.Dr % 8 == 0 && al(q_nope, 16) && al(q_pe, 16)) ? 1 : 0;
-  a.kvvec = (a.R % 8 == 0 && al(ctx_kv, 16) && al(wkv_b_k, 16) && al(wkv_b_v, 16)) ? 1 : 0;
-  a.pevec = (a.Dn % 8 == 0 && a.Dr % 8 == 0 && al(ctx_pe, 16)) ? 1 : 0;
-  a.ovec = (a.Dv % 4 == 0 && al(out, 8)) ? 1 : 0;
-  a.kbuf = static_cast<bf16_t*>(workspace);
-  a.vbuf = a.kbuf + (size_t)a.B * a.H * a.S_kvp * a.DQKp;
-  hipStream_t st = static_cast<hipStream_t>(stream);
+template <int NSTEP>
+static int mla_launch_bwd_nv(const MlaArgs& a, hipStream_t st) {
+  switch (a.DVp / 32) {
+    case 1: return mla_launch_bwd<NSTEP, 1>(a, st);
+    case 2: return mla_launch_bwd<NSTEP, 2>(a, st);
+    case 4: return mla_launch_bwd<NSTEP, 4>(a, st);
+    default: return mla_launch_bwd<NSTEP, 8>(a, st);
+  }
+}
+
+// K and V rows of every (batch, head) into the workspace (mla_kv_kernel).
+static int mla_launch_kv(const MlaArgs& a, hipStream_t st) {
   // the pass's weight rows, then the staged outputs (hi and lo [64][128] bf16)
   const size_t kv_lds = std::max((size_t)MLA_KVN * (a.Rp * 2 + 16), (size_t)2 * MLA_RB * MLA_KVN * sizeof(bf16_t));
   const dim3 kv_grid((unsigned)(a.B * (a.S_kvp / MLA_RB)), (unsigned)a.H);
@@ -669,7 +1184,55 @@ extern "C" int dsmoe_mla_attn_fwd(const void* q_nope, const void* q_pe, const vo
 #undef MLA_KV_CASE
     default: hipLaunchKernelGGL(mla_kv_kernel<0>, kv_grid, dim3(256), kv_lds, st, a); break;
   }
-  rc = check_launch("mla_kv");
+  return check_launch("mla_kv");
+}
+
+// The forward's operands, vector-load flags and K, V buffers of a call.
+static MlaArgs mla_bind(const void* q_nope, const void* q_pe, const void* ctx_kv, const void* ctx_pe,
+                        const void* wkv_b_k, const void* wkv_b_v, const dsmoe_mla_dims* dims, void* workspace) {
+  MlaArgs a = mla_args(dims);
+  a.q_nope = static_cast<const bf16_t*>(q_nope);
+  a.q_pe = static_cast<const bf16_t*>(q_pe);
+  a.ctx_kv = static_cast<const bf16_t*>(ctx_kv);
+  a.ctx_pe = static_cast<const bf16_t*>(ctx_pe);
+  a.w_k = static_cast<const bf16_t*>(wkv_b_k);
+  a.w_v = static_cast<const bf16_t*>(wkv_b_v);
+  auto al = [](const void* p, uintptr_t m) { return (reinterpret_cast<uintptr_t>(p) & (m - 1)) == 0; };
+  a.qvec = (a.Dn % 8 == 0 && a.Dr % 8 == 0 && al(q_nope, 16) && al(q_pe, 16)) ? 1 : 0;
+  a.kvvec = (a.R % 8 == 0 && al(ctx_kv, 16) && al(wkv_b_k, 16) && al(wkv_b_v, 16)) ? 1 : 0;
+  a.pevec = (a.Dn % 8 == 0 && a.Dr % 8 == 0 && al(ctx_pe, 16)) ? 1 : 0;
+  a.kbuf = static_cast<bf16_t*>(workspace);
+  a.vbuf = a.kbuf + (size_t)a.B * a.H * a.S_kvp * a.DQKp;
+  return a;
+}
+
+}  // namespace dsmoe
+
+using namespace dsmoe;
+
+extern "C" size_t dsmoe_mla_attn_workspace_size(const dsmoe_mla_dims* dims) {
+  if (mla_validate(dims) != DSMOE_OK) return 0;
+  const MlaArgs a = mla_args(dims);
+  return (size_t)a.B * a.H * a.S_kvp * (a.DQKp + a.DVp) * sizeof(bf16_t) + 256;
+}
+
+static int mla_fwd(const void* q_nope, const void* q_pe, const void* ctx_kv, const void* ctx_pe, const void* wkv_b_k,
+                   const void* wkv_b_v, const dsmoe_mla_dims* dims, void* out, float* lse, void* workspace,
+                   size_t workspace_bytes, void* stream) {
+  int rc = mla_validate(dims);
+  if (rc) return rc;
+  DSMOE_REQUIRE(q_nope && q_pe && ctx_kv && ctx_pe && wkv_b_k && wkv_b_v && out, DSMOE_ERR_INVALID,
+                "mla: NULL tensor pointer");
+  const size_t need = dsmoe_mla_attn_workspace_size(dims);
+  DSMOE_REQUIRE(workspace && workspace_bytes >= need, DSMOE_ERR_WORKSPACE, "mla: workspace too small");
+  DSMOE_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15) == 0, DSMOE_ERR_INVALID,
+                "mla: workspace must be 16-byte aligned");
+  MlaArgs a = mla_bind(q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v, dims, workspace);
+  a.out = static_cast<bf16_t*>(out);
+  a.lse = lse;
+  a.ovec = (a.Dv % 4 == 0 && (reinterpret_cast<uintptr_t>(out) & 7) == 0) ? 1 : 0;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  rc = mla_launch_kv(a, st);
   if (rc) return rc;
   switch (a.DQKp / 16) {
     case 2: return mla_launch_fa_nv<2>(a, st);
@@ -678,5 +1241,70 @@ extern "C" int dsmoe_mla_attn_fwd(const void* q_nope, const void* q_pe, const vo
     case 8: return mla_launch_fa_nv<8>(a, st);
     case 12: return mla_launch_fa_nv<12>(a, st);
     default: return mla_launch_fa_nv<16>(a, st);
+  }
+}
+
+extern "C" int dsmoe_mla_attn_fwd(const void* q_nope, const void* q_pe, const void* ctx_kv, const void* ctx_pe,
+                                  const void* wkv_b_k, const void* wkv_b_v, const dsmoe_mla_dims* dims, void* out,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  return mla_fwd(q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v, dims, out, nullptr, workspace, workspace_bytes,
+                 stream);
+}
+
+extern "C" int dsmoe_mla_attn_fwd_lse(const void* q_nope, const void* q_pe, const void* ctx_kv, const void* ctx_pe,
+                                      const void* wkv_b_k, const void* wkv_b_v, const dsmoe_mla_dims* dims, void* out,
+                                      float* lse, void* workspace, size_t workspace_bytes, void* stream) {
+  DSMOE_REQUIRE(lse, DSMOE_ERR_INVALID, "mla: NULL lse pointer");
+  return mla_fwd(q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v, dims, out, lse, workspace, workspace_bytes, stream);
+}
+
+// Workspace of dsmoe_mla_attn_bwd: the forward's K, V buffers, then D.
+extern "C" size_t dsmoe_mla_attn_bwd_workspace_size(const dsmoe_mla_dims* dims) {
+  const size_t kv = dsmoe_mla_attn_workspace_size(dims);
+  if (kv == 0) return 0;
+  return kv + (size_t)dims->B * dims->H * dims->S_q * sizeof(float) + 256;
+}
+
+extern "C" int dsmoe_mla_attn_bwd(const void* q_nope, const void* q_pe, const void* ctx_kv, const void* ctx_pe,
+                                  const void* wkv_b_k, const void* wkv_b_v, const dsmoe_mla_dims* dims,
+                                  const void* out, const void* dout, const float* lse, float* dq_nope, float* dq_pe,
+                                  float* dk_nope, float* dk_pe, float* dv, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  int rc = mla_validate(dims);
+  if (rc) return rc;
+  DSMOE_REQUIRE(q_nope && q_pe && ctx_kv && ctx_pe && wkv_b_k && wkv_b_v && out && dout && lse, DSMOE_ERR_INVALID,
+                "mla: NULL tensor pointer");
+  DSMOE_REQUIRE(dq_nope && dq_pe && dk_nope && dk_pe && dv, DSMOE_ERR_INVALID, "mla: NULL gradient pointer");
+  const size_t need = dsmoe_mla_attn_bwd_workspace_size(dims);
+  DSMOE_REQUIRE(workspace && workspace_bytes >= need, DSMOE_ERR_WORKSPACE, "mla: workspace too small");
+  DSMOE_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15) == 0, DSMOE_ERR_INVALID,
+                "mla: workspace must be 16-byte aligned");
+  MlaArgs a = mla_bind(q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v, dims, workspace);
+  a.out = static_cast<bf16_t*>(const_cast<void*>(out));   // read only (delta)
+  a.dout = static_cast<const bf16_t*>(dout);
+  a.lse = const_cast<float*>(lse);                          // read only
+  a.dovec = (a.Dv % 8 == 0 && (reinterpret_cast<uintptr_t>(dout) & 15) == 0) ? 1 : 0;
+  // D after the K, V buffers (their size is a multiple of 64 rows x 16 columns x 2 bytes)
+  a.delta = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                     (size_t)a.B * a.H * a.S_kvp * (a.DQKp + a.DVp) * sizeof(bf16_t));
+  a.dq_nope = dq_nope;
+  a.dq_pe = dq_pe;
+  a.dk_nope = dk_nope;
+  a.dk_pe = dk_pe;
+  a.dv = dv;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  rc = mla_launch_kv(a, st);
+  if (rc) return rc;
+  const int64_t rows = (int64_t)a.B * a.S_q * a.H;
+  hipLaunchKernelGGL(mla_bwd_delta_kernel, dim3((unsigned)cdiv(rows, 256)), dim3(256), 0, st, a);
+  rc = check_launch("mla_bwd_delta");
+  if (rc) return rc;
+  switch (a.DQKp / 16) {
+    case 2: return mla_launch_bwd_nv<2>(a, st);
+    case 4: return mla_launch_bwd_nv<4>(a, st);
+    case 6: return mla_launch_bwd_nv<6>(a, st);
+    case 8: return mla_launch_bwd_nv<8>(a, st);
+    case 12: return mla_launch_bwd_nv<12>(a, st);
+    default: return mla_launch_bwd_nv<16>(a, st);
   }
 }

@@ -3,11 +3,18 @@
 ``mla_attention`` mirrors ``triton_mla_attention`` of models/mla_triton.py:303-329
 (same arguments, output (B, S_q, H, D_v), the same ValueError for a dimension
 above 256, models/mla_triton.py:186-196); ``triton_mla_attention`` is the same
-function under the reference's name, so a caller can swap the import.  The
-forward runs the HIP kernels of csrc/mla.hip (bf16).  The backward, as in the
-reference (models/mla_triton.py:257-296), recomputes the attention with torch
-ops and differentiates that; it follows the forward's masking (causal only when
-``is_causal``).
+function under the reference's name, so a caller can swap the import.  Both
+directions run the HIP kernels of csrc/mla.hip (bf16 operands, fp32
+accumulation).  The reference's backward (models/mla_triton.py:269-296)
+differentiates a torch recompute of the attention; here the training forward
+also keeps each query's log-sum-exp, and the backward rebuilds the
+probabilities from it in two flash-attention kernels (dsmoe_mla_attn_bwd:
+dq per query block, dk and dv per key block) and maps the per-head key
+gradients onto ctx_kv, wkv_b_k and wkv_b_v with fp32 GEMMs.  The gradient is
+that of the function the forward computes: its masking (causal only when
+``is_causal``; the reference's recompute, mla_attention_reference, also masks
+a square non-causal call, models/mla_triton.py:52-57, which its forward
+kernel does not).
 
 Dtypes: the kernels compute in bf16.  Under bf16 autocast the reference's
 layer hands the operator a mix (models/mla.py:127-129,209-220 with
@@ -71,12 +78,9 @@ def _bf16_inputs(ts):
     return tuple(t if t.dtype == torch.bfloat16 else t.to(torch.bfloat16) for t in ts)
 
 
-def mla_attention_fwd(q_nope: torch.Tensor, q_pe: torch.Tensor, ctx_kv: torch.Tensor, ctx_pe: torch.Tensor,
-                      wkv_b_k: torch.Tensor, wkv_b_v: torch.Tensor, softmax_scale: float, is_causal: bool = False,
-                      q_start: int = 0) -> torch.Tensor:
-    """dsmoe_mla_attn_fwd: (B, S_q, H, D_v) in q_nope's dtype, no autograd."""
-    global hip_calls
-    out_dtype = q_nope.dtype
+def _prepare(q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v):
+    """The six inputs as contiguous bf16 tensors (shapes checked) and the
+    batch chunk of one launch."""
     ts = _bf16_inputs((q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v))
     q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v = ts
     B, H, S_q, D_nope = q_nope.shape
@@ -86,8 +90,6 @@ def mla_attention_fwd(q_nope: torch.Tensor, q_pe: torch.Tensor, ctx_kv: torch.Te
             or tuple(ctx_pe.shape) != (B, ctx_kv.size(1), D_rope) or tuple(wkv_b_k.shape) != (H, D_nope, R)
             or wkv_b_v.dim() != 3 or wkv_b_v.size(0) != H or wkv_b_v.size(2) != R):
         raise ValueError("mla_attention: inconsistent shapes")
-    dev = q_nope.device
-    q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v = (t.contiguous() for t in ts)
     # the kernels index rows with 32-bit offsets: B H pad64(S_kv) and B H S_q
     # below 2^22 per call, so larger calls run in batch chunks
     S_kv = ctx_kv.size(1)
@@ -96,6 +98,16 @@ def mla_attention_fwd(q_nope: torch.Tensor, q_pe: torch.Tensor, ctx_kv: torch.Te
         raise ValueError(f"mla_attention: H * S_kv = {H * S_kv} (H * S_q = {H * S_q}) reaches 2^22, the limit of "
                          "one batch row of the kernels' 32-bit row offsets")
     bc = min(B, (_ROWS_PER_CALL - 1) // per_batch)
+    return tuple(t.contiguous() for t in ts), bc
+
+
+def _forward(ts, bc: int, softmax_scale: float, is_causal: bool, q_start: int, want_lse: bool):
+    """dsmoe_mla_attn_fwd (or _fwd_lse) over the batch chunks: bf16 out and
+    the fp32 lse (None unless asked for)."""
+    q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v = ts
+    B, H, S_q, _ = q_nope.shape
+    D_v = wkv_b_v.size(1)
+    dev = q_nope.device
     lib = L.load()
     d = _dims(q_nope[:bc], q_pe[:bc], ctx_kv[:bc], wkv_b_v, softmax_scale, is_causal, q_start)
     nbytes = int(lib.dsmoe_mla_attn_workspace_size(d))
@@ -104,52 +116,104 @@ def mla_attention_fwd(q_nope: torch.Tensor, q_pe: torch.Tensor, ctx_kv: torch.Te
                 "dsmoe_mla_attn_fwd")
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     out = torch.empty(B, S_q, H, D_v, dtype=torch.bfloat16, device=dev)
+    lse = torch.empty(B, H, S_q, dtype=torch.float32, device=dev) if want_lse else None
     for b0 in range(0, B, bc):
         b1 = min(B, b0 + bc)
         d = _dims(q_nope[b0:b1], q_pe[b0:b1], ctx_kv[b0:b1], wkv_b_v, softmax_scale, is_causal, q_start)
-        rc = lib.dsmoe_mla_attn_fwd(L.ptr(q_nope[b0:b1]), L.ptr(q_pe[b0:b1]), L.ptr(ctx_kv[b0:b1]),
-                                    L.ptr(ctx_pe[b0:b1]), L.ptr(wkv_b_k), L.ptr(wkv_b_v), d, L.ptr(out[b0:b1]),
-                                    L.ptr(ws), nbytes, L.stream_ptr(dev))
-        L.check(rc, "dsmoe_mla_attn_fwd")
+        ins = (L.ptr(q_nope[b0:b1]), L.ptr(q_pe[b0:b1]), L.ptr(ctx_kv[b0:b1]), L.ptr(ctx_pe[b0:b1]),
+               L.ptr(wkv_b_k), L.ptr(wkv_b_v), d, L.ptr(out[b0:b1]))
+        if want_lse:
+            L.check(lib.dsmoe_mla_attn_fwd_lse(*ins, L.ptr(lse[b0:b1]), L.ptr(ws), nbytes, L.stream_ptr(dev)),
+                    "dsmoe_mla_attn_fwd_lse")
+        else:
+            L.check(lib.dsmoe_mla_attn_fwd(*ins, L.ptr(ws), nbytes, L.stream_ptr(dev)), "dsmoe_mla_attn_fwd")
+    return out, lse
+
+
+def mla_attention_fwd(q_nope: torch.Tensor, q_pe: torch.Tensor, ctx_kv: torch.Tensor, ctx_pe: torch.Tensor,
+                      wkv_b_k: torch.Tensor, wkv_b_v: torch.Tensor, softmax_scale: float, is_causal: bool = False,
+                      q_start: int = 0) -> torch.Tensor:
+    """dsmoe_mla_attn_fwd: (B, S_q, H, D_v) in q_nope's dtype, no autograd."""
+    global hip_calls
+    out_dtype = q_nope.dtype
+    ts, bc = _prepare(q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v)
+    out, _ = _forward(ts, bc, softmax_scale, is_causal, q_start, want_lse=False)
     hip_calls += 1
     return out if out_dtype == torch.bfloat16 else out.to(out_dtype)
 
 
-def _attention_torch(q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v, softmax_scale, is_causal, q_start):
-    """The forward's math in float32 torch ops, for the recompute backward."""
-    k_nope = torch.einsum("bsr,hdr->bhsd", ctx_kv, wkv_b_k)
-    v = torch.einsum("bsr,hdr->bhsd", ctx_kv, wkv_b_v)
-    B, H, S_kv, _ = k_nope.shape
-    k = torch.cat([k_nope, ctx_pe.unsqueeze(1).expand(B, H, S_kv, ctx_pe.size(-1))], dim=-1)
-    q = torch.cat([q_nope, q_pe], dim=-1)
-    s = torch.einsum("bhqd,bhkd->bhqk", q, k) * softmax_scale
-    if is_causal:
-        qi = torch.arange(q.size(2), device=s.device)[:, None] + q_start
-        ki = torch.arange(S_kv, device=s.device)[None, :]
-        s = s.masked_fill(qi < ki, float("-inf"))
-    o = torch.einsum("bhqk,bhkd->bhqd", s.softmax(dim=-1), v)
-    return o.permute(0, 2, 1, 3).contiguous()
+def mla_attention_bwd_heads(ts, bc: int, out: torch.Tensor, lse: torch.Tensor, dout: torch.Tensor,
+                            softmax_scale: float, is_causal: bool, q_start: int):
+    """dsmoe_mla_attn_bwd over the batch chunks: fp32 dq_nope (B, H, S_q, Dn),
+    dq_pe (B, H, S_q, Dr) and the per-head key-side gradients dk_nope
+    (B, S_kv, H, Dn), dk_pe (B, S_kv, H, Dr), dv (B, S_kv, H, Dv).  ``ts`` and
+    ``bc`` as ``_prepare`` returns them; out, lse from the training forward."""
+    q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v = ts
+    B, H, S_q, Dn = q_nope.shape
+    S_kv, Dr, Dv = ctx_kv.size(1), q_pe.size(-1), wkv_b_v.size(1)
+    dev = q_nope.device
+    dout = dout.to(torch.bfloat16).contiguous()
+    lib = L.load()
+    d = _dims(q_nope[:bc], q_pe[:bc], ctx_kv[:bc], wkv_b_v, softmax_scale, is_causal, q_start)
+    nbytes = int(lib.dsmoe_mla_attn_bwd_workspace_size(d))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    f32 = dict(dtype=torch.float32, device=dev)
+    dq_nope, dq_pe = torch.empty(B, H, S_q, Dn, **f32), torch.empty(B, H, S_q, Dr, **f32)
+    dk_nope, dk_pe, dv = (torch.empty(B, S_kv, H, Dn, **f32), torch.empty(B, S_kv, H, Dr, **f32),
+                          torch.empty(B, S_kv, H, Dv, **f32))
+    for b0 in range(0, B, bc):
+        b1 = min(B, b0 + bc)
+        d = _dims(q_nope[b0:b1], q_pe[b0:b1], ctx_kv[b0:b1], wkv_b_v, softmax_scale, is_causal, q_start)
+        rc = lib.dsmoe_mla_attn_bwd(
+            L.ptr(q_nope[b0:b1]), L.ptr(q_pe[b0:b1]), L.ptr(ctx_kv[b0:b1]), L.ptr(ctx_pe[b0:b1]), L.ptr(wkv_b_k),
+            L.ptr(wkv_b_v), d, L.ptr(out[b0:b1]), L.ptr(dout[b0:b1]), L.ptr(lse[b0:b1]), L.ptr(dq_nope[b0:b1]),
+            L.ptr(dq_pe[b0:b1]), L.ptr(dk_nope[b0:b1]), L.ptr(dk_pe[b0:b1]), L.ptr(dv[b0:b1]), L.ptr(ws), nbytes,
+            L.stream_ptr(dev))
+        L.check(rc, "dsmoe_mla_attn_bwd")
+    return dq_nope, dq_pe, dk_nope, dk_pe, dv
+
+
+def _project_kv_grads(ctx_kv, wkv_b_k, wkv_b_v, dk_nope, dk_pe, dv):
+    """Key-side gradients onto the latent rows and the up-projections (fp32
+    GEMMs): k_nope = ctx_kv W_k^T and v = ctx_kv W_v^T per head, so
+    d ctx_kv = dk_nope W_k + dv W_v (summed over heads), dW_k = dk_nope^T
+    ctx_kv, dW_v = dv^T ctx_kv (summed over batch and positions), and
+    d ctx_pe = dk_pe summed over heads."""
+    B, S_kv, H, Dn = dk_nope.shape
+    R, Dv = ctx_kv.size(-1), dv.size(-1)
+    kv = ctx_kv.float().view(B * S_kv, R)
+    dkn, dvv = dk_nope.view(B * S_kv, H * Dn), dv.view(B * S_kv, H * Dv)
+    dctx_kv = torch.addmm(dkn @ wkv_b_k.float().reshape(H * Dn, R), dvv, wkv_b_v.float().reshape(H * Dv, R))
+    dwk = (dkn.t() @ kv).view(H, Dn, R)
+    dwv = (dvv.t() @ kv).view(H, Dv, R)
+    return dctx_kv.view(B, S_kv, R), dk_pe.sum(2), dwk, dwv
 
 
 class _MlaAttentionFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v, softmax_scale, is_causal, q_start):
-        out = mla_attention_fwd(q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v, softmax_scale, is_causal, q_start)
-        ctx.save_for_backward(q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v)
-        ctx.args = (softmax_scale, is_causal, q_start)
-        return out
+        global hip_calls
+        out_dtype = q_nope.dtype
+        ctx.dtypes = tuple(t.dtype for t in (q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v))
+        ts, bc = _prepare(q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v)
+        out, lse = _forward(ts, bc, softmax_scale, is_causal, q_start, want_lse=True)
+        hip_calls += 1
+        # the backward runs on the bf16 operands the kernels saw
+        ctx.save_for_backward(*ts, out, lse)
+        ctx.args = (bc, softmax_scale, is_causal, q_start)
+        return out if out_dtype == torch.bfloat16 else out.to(out_dtype)
 
     @staticmethod
     def backward(ctx, dout):
-        saved = ctx.saved_tensors
-        # fp32 recompute whatever autocast state the backward runs under
-        with torch.enable_grad(), torch.autocast(saved[0].device.type, enabled=False):
-            ins = [t.detach().float().requires_grad_() for t in saved]
-            ref = _attention_torch(*ins, *ctx.args)
-            grads = torch.autograd.grad(ref, ins, grad_outputs=dout.float(), allow_unused=True)
-        return tuple(g.to(t.dtype) if g is not None else torch.zeros_like(t) for g, t in zip(grads, saved)) + (
-            None, None, None)
+        *ts, out, lse = ctx.saved_tensors
+        bc, softmax_scale, is_causal, q_start = ctx.args
+        with torch.autocast(dout.device.type, enabled=False):
+            dq_nope, dq_pe, dk_nope, dk_pe, dv = mla_attention_bwd_heads(ts, bc, out, lse, dout, softmax_scale,
+                                                                         is_causal, q_start)
+            dctx_kv, dctx_pe, dwk, dwv = _project_kv_grads(ts[2], ts[4], ts[5], dk_nope, dk_pe, dv)
+        grads = (dq_nope, dq_pe, dctx_kv, dctx_pe, dwk, dwv)
+        return tuple(g.to(dt) for g, dt in zip(grads, ctx.dtypes)) + (None, None, None)
 
 
 def mla_attention(q_nope: torch.Tensor, q_pe: torch.Tensor, ctx_kv: torch.Tensor, ctx_pe: torch.Tensor,

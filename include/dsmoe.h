@@ -277,6 +277,36 @@ size_t dsmoe_mla_attn_workspace_size(const dsmoe_mla_dims* dims);
 int dsmoe_mla_attn_fwd(const void* q_nope, const void* q_pe, const void* ctx_kv, const void* ctx_pe,
                        const void* wkv_b_k, const void* wkv_b_v, const dsmoe_mla_dims* dims, void* out,
                        void* workspace, size_t workspace_bytes, void* stream);
+/* dsmoe_mla_attn_fwd that also writes lse (B, H, S_q) fp32, each query's
+ * base-2 log-sum-exp of its scaled scores: log2(sum over visible keys of
+ * exp(softmax_scale q.k)), +inf for a query without a visible key.  The
+ * training forward of models/mla_triton.py:200-267 (_TritonMlaAttentionFunction.forward),
+ * whose backward needs the probabilities again. */
+int dsmoe_mla_attn_fwd_lse(const void* q_nope, const void* q_pe, const void* ctx_kv, const void* ctx_pe,
+                           const void* wkv_b_k, const void* wkv_b_v, const dsmoe_mla_dims* dims, void* out,
+                           float* lse, void* workspace, size_t workspace_bytes, void* stream);
+/* Backward of the attention (models/mla_triton.py:269-296,
+ * _TritonMlaAttentionFunction.backward, which differentiates a torch recompute of
+ * the same function), for the per-head operands: given the forward's inputs,
+ * its out and lse, and dout (B, S_q, H, D_v) bf16, writes fp32
+ *   dq_nope (B, H, S_q, D_nope)   dq_pe (B, H, S_q, D_rope)
+ *   dk_nope (B, S_kv, H, D_nope)  dk_pe (B, S_kv, H, D_rope)  dv (B, S_kv, H, D_v)
+ * the gradients of k_nope = ctx_kv wkv_b_k^T, k_pe = ctx_pe (per head) and
+ * v = ctx_kv wkv_b_v^T, laid out so that (B S_kv, H D) views are the left
+ * operands of the GEMMs that map them onto ctx_kv (dk_nope wkv_b_k + dv
+ * wkv_b_v as (H D, R) matrices), wkv_b_k and wkv_b_v (their transposes times
+ * ctx_kv); ctx_pe's gradient is dk_pe summed over heads.  The gradient is
+ * that of the function the forward computes (for is_causal = 0 no mask,
+ * square or not).  Every element
+ * of the five outputs is written (zeros where no probability reaches it).
+ * The probabilities and dZ enter their MFMAs in bf16 with fp32 accumulation.
+ * Workspace: dsmoe_mla_attn_bwd_workspace_size bytes (the forward's K, V
+ * buffers and B * H * S_q floats); dims and limits as dsmoe_mla_attn_fwd. */
+size_t dsmoe_mla_attn_bwd_workspace_size(const dsmoe_mla_dims* dims);
+int dsmoe_mla_attn_bwd(const void* q_nope, const void* q_pe, const void* ctx_kv, const void* ctx_pe,
+                       const void* wkv_b_k, const void* wkv_b_v, const dsmoe_mla_dims* dims, const void* out,
+                       const void* dout, const float* lse, float* dq_nope, float* dq_pe, float* dk_nope,
+                       float* dk_pe, float* dv, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -11,6 +11,9 @@ may import it, and only as the checker / the timed CPU baseline.
   (``:154-155``), causal mask key <= query + q_start only when ``is_causal``
   (``:157-160``), softmax over keys, output (B, S_q, H, D_v) (``:178-183``).
   Evaluated in float64 from the given (bf16-representable) inputs.
+* ``mla_attention_bwd_oracle`` <- ``models/mla_triton.py:269-296`` (the
+  backward: autograd of a recompute of the same function): the gradients of
+  ``mla_attention_oracle`` in closed form, float64.
 * ``mla_attention_sdpa_torch`` restates the reference layer's default SDPA
   path (``models/mla.py:155-172``) with torch ops: the attention's CPU
   baseline in bench.py (pinned against ``mla_attention_oracle``).
@@ -27,7 +30,12 @@ output through the latent then W_v^T), which associates every product
 differently; closed forms (one key gives its V row, equal scores give the mean
 of the visible V rows); and the reference's own CPU test cases
 (``tests/test_mla_triton.py:68-110``: a last-position query attends every key,
-q_start offsets block future keys).
+q_start offsets block future keys).  The backward is pinned against torch
+float64 autograd of scaled_dot_product_attention on the materialised K and V
+(a different evaluation of the chain rule), against central finite
+differences of ``mla_attention_oracle``, and by the invariants that the
+probabilities' gradient rows sum to zero (so the logits' gradient does too)
+and that dV sums, over keys, to dO summed over queries.
 """
 from __future__ import annotations
 
@@ -76,6 +84,51 @@ def mla_attention_oracle(q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v, softmax
     p /= p.sum(axis=-1, keepdims=True)
     o = np.einsum("bhqk,bhkd->bhqd", p, v)
     return np.ascontiguousarray(o.transpose(0, 2, 1, 3))
+
+
+def mla_attention_bwd_oracle(q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v, dout, softmax_scale: float,
+                             is_causal: bool = False, q_start: int = 0) -> dict:
+    """float64 gradients of ``mla_attention_oracle`` for dout (B, S_q, H, D_v).
+
+    The reference's backward (models/mla_triton.py:269-296) is torch autograd
+    of a recompute of the same function; this states the chain rule in
+    closed form: with P the probabilities, z = scale q.k the logits and
+    O = P V, per (batch, head)
+      dV = P^T dO,  dP = dO V^T,  dz = P (dP - rowsum(dO O)),
+      dq = scale dz K,  dK = scale dz^T q,
+    then through K_nope = ctx_kv W_k^T, V = ctx_kv W_v^T, K_pe = ctx_pe:
+      d ctx_kv = sum_h (dK_nope W_k + dV W_v),  dW_k = sum_{b,s} dK_nope^T ctx_kv,
+      dW_v likewise,  d ctx_pe = sum_h dK_pe.
+    Returns the six input gradients (keys q_nope .. wkv_b_v) and the per-head
+    ones (dk_nope, dk_pe, dv in (B, H, S_kv, D) order)."""
+    qn, qp = _f64(q_nope), _f64(q_pe)
+    kv, pe, wk, wv = map(_f64, (ctx_kv, ctx_pe, wkv_b_k, wkv_b_v))
+    do = _f64(dout).transpose(0, 2, 1, 3)                     # (B, H, S_q, Dv)
+    Dn = qn.shape[-1]
+    k, v = mla_kv_oracle(kv, pe, wk, wv)
+    q = np.concatenate([qn, qp], axis=-1)
+    sc = float(softmax_scale)
+    z = np.einsum("bhqd,bhkd->bhqk", q, k) * sc
+    allow = mla_mask_oracle(q.shape[2], k.shape[2], is_causal, q_start)
+    z = np.where(allow[None, None], z, -np.inf)
+    zmax = z.max(axis=-1, keepdims=True)
+    p = np.exp(z - np.where(np.isfinite(zmax), zmax, 0.0))
+    tot = p.sum(axis=-1, keepdims=True)
+    p = np.divide(p, tot, out=np.zeros_like(p), where=tot > 0)
+    o = np.einsum("bhqk,bhkd->bhqd", p, v)
+    dv = np.einsum("bhqk,bhqd->bhkd", p, do)
+    dp = np.einsum("bhqd,bhkd->bhqk", do, v)
+    dz = p * (dp - (do * o).sum(axis=-1, keepdims=True))
+    dq = np.einsum("bhqk,bhkd->bhqd", dz, k) * sc
+    dk = np.einsum("bhqk,bhqd->bhkd", dz, q) * sc
+    dk_nope, dk_pe = dk[..., :Dn], dk[..., Dn:]
+    return {
+        "q_nope": dq[..., :Dn], "q_pe": dq[..., Dn:],
+        "ctx_kv": np.einsum("bhsd,hdr->bsr", dk_nope, wk) + np.einsum("bhsd,hdr->bsr", dv, wv),
+        "ctx_pe": dk_pe.sum(axis=1),
+        "wkv_b_k": np.einsum("bhsd,bsr->hdr", dk_nope, kv), "wkv_b_v": np.einsum("bhsd,bsr->hdr", dv, kv),
+        "dk_nope": dk_nope, "dk_pe": dk_pe, "dv": dv,
+    }
 
 
 def mla_attention_absorbed(q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v, softmax_scale: float,

@@ -234,3 +234,148 @@ def test_call_beyond_the_row_index_limit_runs_in_batch_chunks():
                       torch.zeros(1, 8192, 8, dtype=torch.bfloat16, device=DEV),
                       torch.zeros(512, 8, R, dtype=torch.bfloat16, device=DEV),
                       torch.zeros(512, 8, R, dtype=torch.bfloat16, device=DEV), sc, is_causal=True)
+
+
+# ---------------------------------------------------------------- backward
+# Bar for the backward kernels (dsmoe_mla_attn_bwd): they rebuild the
+# probabilities from the forward's lse with the forward's operands (K_nope
+# as an exact bf16 pair, V in bf16) and feed P and dZ to their MFMAs in bf16
+# (fp32 accumulation), as the forward feeds P (models/mla_triton.py:175).
+# Each gradient is compared with the float64 closed form of
+# oracle/mla_ref.py on the same bf16 inputs and bf16 dout: relative L2
+# error <= 1e-2 and max |err| <= 2e-2 max |oracle| (the reference's GPU test
+# holds the forward to 1e-2, tests/test_mla_triton.py:136).
+BWD_RL2 = 1e-2
+BWD_MAX = 2e-2
+
+
+def _bwd_compare(name, got, ref):
+    got = got.detach().float().cpu().numpy().astype(np.float64)
+    assert got.shape == ref.shape, (name, got.shape, ref.shape)
+    assert np.isfinite(got).all(), name
+    scale = max(np.abs(ref).max(), 1e-30)
+    rl2 = np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30)
+    mx = np.abs(got - ref).max() / scale
+    print(f"[mla-bwd]   {name:8s} rel-L2 {rl2:.2e}  max|err|/max|ref| {mx:.2e}", flush=True)
+    assert rl2 <= BWD_RL2 and mx <= BWD_MAX, name
+
+
+def _bwd_heads(ts, sc, causal, q_start, dout):
+    """The training forward (out, lse) and dsmoe_mla_attn_bwd through the
+    package's C-ABI wrappers."""
+    import dsmoe.mla as M
+    ts2, bc = M._prepare(*ts)
+    out, lse = M._forward(ts2, bc, sc, causal, q_start, want_lse=True)
+    grads = M.mla_attention_bwd_heads(ts2, bc, out, lse, dout, sc, causal, q_start)
+    torch.cuda.synchronize()
+    return out, lse, grads
+
+
+def _check_bwd(B, H, S_q, S_kv, R, Dn, Dr, Dv, causal, q_start, seed=0, wscale=0.1, scale=None, heads=None):
+    from oracle.mla_ref import mla_attention_bwd_oracle
+    print(f"[mla-bwd] B={B} H={H} S_q={S_q} S_kv={S_kv} R={R} Dn={Dn} Dr={Dr} Dv={Dv} causal={causal} "
+          f"q_start={q_start} scale={scale}", flush=True)
+    ts, sc = _inputs(B, H, S_q, S_kv, R, Dn, Dr, Dv, seed, wscale)
+    sc = sc if scale is None else scale
+    g = torch.Generator(device=DEV).manual_seed(seed + 100)
+    dout = torch.randn(B, S_q, H, Dv, generator=g, device=DEV).to(torch.bfloat16)
+    out, lse, (dqn, dqp, dkn, dkp, dv) = _bwd_heads(ts, sc, causal, q_start, dout)
+    cpu = [t.cpu() for t in ts]
+    for b, h in (heads or [(b, h) for b in range(B) for h in range(H)]):
+        sl = (cpu[0][b:b + 1, h:h + 1], cpu[1][b:b + 1, h:h + 1], cpu[2][b:b + 1], cpu[3][b:b + 1],
+              cpu[4][h:h + 1], cpu[5][h:h + 1])
+        ref = mla_attention_bwd_oracle(*sl, dout[b:b + 1, :, h:h + 1].cpu(), sc, is_causal=causal, q_start=q_start)
+        print(f"[mla-bwd]  (b={b}, h={h})", flush=True)
+        _bwd_compare("dq_nope", dqn[b:b + 1, h:h + 1], ref["q_nope"])
+        _bwd_compare("dq_pe", dqp[b:b + 1, h:h + 1], ref["q_pe"])
+        _bwd_compare("dk_nope", dkn[b:b + 1, :, h:h + 1].permute(0, 2, 1, 3), ref["dk_nope"])
+        _bwd_compare("dk_pe", dkp[b:b + 1, :, h:h + 1].permute(0, 2, 1, 3), ref["dk_pe"])
+        _bwd_compare("dv", dv[b:b + 1, :, h:h + 1].permute(0, 2, 1, 3), ref["dv"])
+        # lse: log2 of the sum of exp(scale q.k) over the visible keys
+        qh = np.concatenate([sl[0].double().numpy(), sl[1].double().numpy()], -1)[0, 0]
+        from oracle.mla_ref import mla_kv_oracle, mla_mask_oracle
+        k, _ = mla_kv_oracle(*sl[2:])
+        z = qh @ k[0, 0].T * sc
+        allow = mla_mask_oracle(S_q, S_kv, causal, q_start)
+        zm = np.where(allow, z, -np.inf)
+        mx = zm.max(-1)
+        with np.errstate(divide="ignore"):
+            lse_ref = (mx + np.log(np.where(allow, np.exp(zm - np.where(np.isfinite(mx), mx, 0)[:, None]), 0).sum(-1))) / np.log(2)
+        got = lse[b, h].cpu().numpy().astype(np.float64)
+        fin = np.isfinite(lse_ref)
+        assert np.array_equal(np.isfinite(got), fin)
+        assert np.abs(got[fin] - lse_ref[fin]).max() <= 2e-3 * max(1.0, np.abs(lse_ref[fin]).max())
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_backward_reference_gpu_test_shape(causal):
+    # tests/test_mla_triton.py:126-136 shape
+    _check_bwd(1, 4, 16, 16, 32, 16, 8, 24, causal, 0)
+
+
+def test_backward_pretrain_1650_2m_shape():
+    _check_bwd(2, 4, 128, 128, 16, 16, 16, 16, True, 0, seed=1)
+
+
+def test_backward_pretrain_a100_422m_shape():
+    # configs/pretrain_a100_422m.yaml:22-34, one sequence; heads sampled
+    _check_bwd(1, 12, 2048, 2048, 192, 48, 24, 64, True, 0, seed=2, heads=[(0, 0), (0, 5), (0, 11)])
+
+
+@pytest.mark.parametrize("S_q,S_kv,q_start", [(100, 300, 200), (1, 777, 776), (65, 130, 0), (3, 5, 2), (40, 300, 0)])
+def test_backward_chunked_prefill_and_decode(S_q, S_kv, q_start):
+    # (40, 300, 0): keys past the last query's position get no gradient
+    _check_bwd(2, 3, S_q, S_kv, 64, 32, 16, 32, True, q_start, seed=3)
+
+
+@pytest.mark.parametrize("S_q,S_kv", [(130, 100), (16, 16), (1, 1), (200, 65)])
+def test_backward_non_causal_ragged(S_q, S_kv):
+    _check_bwd(1, 2, S_q, S_kv, 48, 24, 8, 40, False, 0, seed=4)
+
+
+def test_backward_wide_dims_and_odd_sizes():
+    # D_nope + D_rope = 192 (split K), 256 (no split: 2 D_nope + D_rope > 256),
+    # and sizes off every vector width (element loads)
+    _check_bwd(1, 2, 200, 200, 256, 128, 64, 128, True, 0, seed=5, wscale=0.05)
+    _check_bwd(1, 1, 96, 96, 64, 192, 64, 256, False, 0, seed=6, wscale=0.05)
+    _check_bwd(2, 1, 70, 90, 8, 6, 4, 10, True, 5, seed=7, wscale=0.3)
+
+
+def test_backward_negative_and_large_scale():
+    _check_bwd(1, 2, 64, 64, 32, 16, 16, 32, True, 0, seed=8, scale=-0.2)
+    _check_bwd(1, 2, 64, 64, 32, 16, 16, 32, True, 0, seed=9, scale=2.0)
+
+
+def test_backward_input_gradients_and_batch_chunks(monkeypatch):
+    """mla_attention(...).backward: the six input gradients (the per-head
+    key gradients mapped onto ctx_kv, wkv_b_k, wkv_b_v, ctx_pe by fp32 GEMMs)
+    against the float64 oracle, once in one launch and once split into one
+    launch per batch (the path of calls beyond the 32-bit row limit)."""
+    import dsmoe.mla as M
+    from oracle.mla_ref import mla_attention_bwd_oracle
+    B, H, S, R, Dn, Dr, Dv = 3, 4, 130, 64, 32, 16, 32
+    ts, sc = _inputs(B, H, S, S, R, Dn, Dr, Dv, seed=10, wscale=0.2)
+    g = torch.Generator(device=DEV).manual_seed(11)
+    dout = torch.randn(B, S, H, Dv, generator=g, device=DEV).to(torch.bfloat16)
+    ref = mla_attention_bwd_oracle(*[t.cpu() for t in ts], dout.cpu(), sc, is_causal=True)
+    keys = ("q_nope", "q_pe", "ctx_kv", "ctx_pe", "wkv_b_k", "wkv_b_v")
+    for rows in (None, H * 192 + 1):
+        if rows is not None:
+            monkeypatch.setattr(M, "_ROWS_PER_CALL", rows)     # one batch per launch
+            assert M._prepare(*ts)[1] == 1
+        ins = [t.clone().requires_grad_() for t in ts]
+        out = M.mla_attention(*ins, sc, is_causal=True)
+        out.backward(dout)
+        for k, t in zip(keys, ins):
+            assert t.grad.dtype == torch.bfloat16
+            _bwd_compare(k, t.grad, ref[k])
+
+
+def test_backward_is_deterministic():
+    ts, sc = _inputs(2, 3, 300, 300, 64, 32, 16, 32, seed=12)
+    g = torch.Generator(device=DEV).manual_seed(13)
+    dout = torch.randn(2, 300, 3, 32, generator=g, device=DEV).to(torch.bfloat16)
+    a = _bwd_heads(ts, sc, True, 0, dout)[2]
+    b = _bwd_heads(ts, sc, True, 0, dout)[2]
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)

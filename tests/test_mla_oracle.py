@@ -117,3 +117,61 @@ def test_sdpa_restatement_matches_the_oracle(causal):
     ref = mla_attention_oracle(*ts, sc, is_causal=causal)
     assert got.shape == ref.shape == (B, S, H, Dv)
     assert np.abs(got - ref).max() < 1e-10
+
+
+_GRAD_KEYS = ("q_nope", "q_pe", "ctx_kv", "ctx_pe", "wkv_b_k", "wkv_b_v")
+
+
+@pytest.mark.parametrize("causal,q_start,S_q,S_kv", [(False, 0, 7, 9), (True, 0, 9, 9), (True, 2, 7, 9),
+                                                    (True, 8, 1, 9), (False, 0, 9, 9)])
+def test_backward_oracle_matches_float64_autograd(causal, q_start, S_q, S_kv):
+    # the closed-form chain rule against torch autograd of SDPA on materialised K, V
+    from oracle.mla_ref import mla_attention_bwd_oracle
+    qn, qp, kv, pe, wk, wv, sc = _tensors(S_q=S_q, S_kv=S_kv, seed=3)
+    g = torch.Generator().manual_seed(4)
+    dout = torch.randn(2, S_q, 3, 5, generator=g, dtype=torch.float64)
+    ins = [t.clone().requires_grad_() for t in (qn, qp, kv, pe, wk, wv)]
+    a_qn, a_qp, a_kv, a_pe, a_wk, a_wv = ins
+    k = torch.cat([torch.einsum("bsr,hdr->bhsd", a_kv, a_wk), a_pe[:, None].expand(2, 3, S_kv, 4)], dim=-1)
+    v = torch.einsum("bsr,hdr->bhsd", a_kv, a_wv)
+    mask = torch.from_numpy(mla_mask_oracle(S_q, S_kv, causal, q_start))
+    o = torch.nn.functional.scaled_dot_product_attention(torch.cat([a_qn, a_qp], -1), k, v, attn_mask=mask, scale=sc)
+    o.permute(0, 2, 1, 3).backward(dout)
+    got = mla_attention_bwd_oracle(qn, qp, kv, pe, wk, wv, dout, sc, is_causal=causal, q_start=q_start)
+    for key, t in zip(_GRAD_KEYS, ins):
+        np.testing.assert_allclose(got[key], t.grad.numpy(), rtol=1e-10, atol=1e-11, err_msg=key)
+
+
+def test_backward_oracle_matches_finite_differences():
+    from oracle.mla_ref import mla_attention_bwd_oracle
+    qn, qp, kv, pe, wk, wv, sc = _tensors(B=1, H=2, S_q=4, S_kv=5, R=3, Dn=2, Dr=2, Dv=3, seed=5)
+    ins = [t.numpy().copy() for t in (qn, qp, kv, pe, wk, wv)]
+    dout = np.random.default_rng(6).standard_normal((1, 4, 2, 3))
+    got = mla_attention_bwd_oracle(*ins, dout, sc, is_causal=True, q_start=1)
+    f = lambda xs: float((mla_attention_oracle(*xs, sc, is_causal=True, q_start=1) * dout).sum())
+    h = 1e-6
+    for key, x in zip(_GRAD_KEYS, range(6)):
+        flat = ins[x].reshape(-1)
+        num = np.empty(flat.size)
+        for i in range(flat.size):
+            keep = flat[i]
+            flat[i] = keep + h
+            up = f(ins)
+            flat[i] = keep - h
+            dn = f(ins)
+            flat[i] = keep
+            num[i] = (up - dn) / (2 * h)
+        np.testing.assert_allclose(got[key].reshape(-1), num, rtol=1e-6, atol=1e-8, err_msg=key)
+
+
+def test_backward_oracle_invariants():
+    # each query's probabilities sum to one, so dV = P^T dO summed over keys
+    # equals dO summed over queries
+    from oracle.mla_ref import mla_attention_bwd_oracle
+    qn, qp, kv, pe, wk, wv, sc = _tensors(S_q=6, S_kv=8, seed=7)
+    dout = np.random.default_rng(8).standard_normal((2, 6, 3, 5))
+    got = mla_attention_bwd_oracle(qn, qp, kv, pe, wk, wv, dout, sc, is_causal=True, q_start=2)
+    np.testing.assert_allclose(got["dv"].sum(axis=2), dout.sum(axis=1), rtol=1e-12, atol=1e-12)
+    # a key no query sees (causal, key > last query + q_start) gets no gradient
+    got = mla_attention_bwd_oracle(qn, qp, kv, pe, wk, wv, dout, sc, is_causal=True, q_start=0)
+    assert np.all(got["dk_nope"][:, :, 6:] == 0) and np.all(got["dv"][:, :, 6:] == 0)
