@@ -58,7 +58,11 @@ struct MlaArgs {
   float* lse;             // (B, H, S_q): c m + log2(sum of p), the base-2 log-sum-exp of the scaled scores, or null
   // backward
   const bf16_t* dout;     // (B, S_q, H, Dv)
-  float* delta;           // (B, H, S_q) rowsum(dO * O)
+  bf16_t* qpk;            // (B, H, S_qp, DQKp) packed query rows as the score MFMA takes them (q_eff)
+  bf16_t* dopk;           // (B, H, S_qp, DVp) packed dO rows (zeros past D_v and S_q)
+  float* lsep;            // (B, H, S_qp) lse (+inf past S_q)
+  float* deltap;          // (B, H, S_qp) D = rowsum(dO * O) (0 past S_q)
+  int S_qp;               // S_q rounded up to a multiple of 64
   float* dq_nope;         // (B, H, S_q, Dn) fp32
   float* dq_pe;           // (B, H, S_q, Dr)
   float* dk_nope;         // (B, S_kv, H, Dn): rows of the latent positions, heads side by side
@@ -563,9 +567,11 @@ __global__ __launch_bounds__(256) void mla_fa_kernel(const MlaArgs a) {
 // P = exp2(c s - lse) (the forward's probabilities, rebuilt from its
 // per-query base-2 log-sum-exp), D = rowsum(dO * O) and z = scale q.k:
 //   dV = P^T dO,  dZ = P (dO V^T - D),  dK = scale dZ^T Q,  dQ = scale dZ K.
-// mla_bwd_kv_kernel owns 128 keys (four waves of 32) and walks the query
-// tiles that see them, accumulating dV and dK in registers;
-// mla_bwd_q_kernel owns 128 queries and walks their keys, accumulating dQ.
+// mla_bwd_q_kernel runs first: it owns 128 queries, computes their D, walks
+// their keys accumulating dQ, and leaves the query rows as the score MFMA
+// takes them, the dO rows, lse and D packed in the workspace;
+// mla_bwd_kv_kernel then owns 128 keys (four waves of 32) and walks the
+// query tiles that see them, accumulating dV and dK in registers.
 // Both rebuild s with the forward's operands (K rows [k_hi | pe | k_lo] from
 // mla_kv_kernel, query rows [q_nope | q_pe | q_nope], q negated when the
 // scale is negative), so dK comes out as |scale| dZ^T q_eff and dQ over the
@@ -579,7 +585,7 @@ __global__ __launch_bounds__(256) void mla_fa_kernel(const MlaArgs a) {
 // chunk, and four consecutive rows (r = 0 mod 4) at four consecutive chunks
 // (c = 0 mod 4), then fall on distinct banks.
 constexpr int MLB_KW = 128;   // keys per workgroup of the dK, dV kernel
-constexpr int MLB_QT = 32;    // queries per staged tile of the dK, dV kernel
+constexpr int MLB_QI = 64;    // queries per staged tile of the dK, dV kernel (two halves of 32)
 constexpr int MLB_KT = 64;    // keys per staged tile of the dQ kernel
 
 __device__ __forceinline__ int mlb_off(int r, int c, int rb) {
@@ -651,12 +657,12 @@ __device__ __forceinline__ mla_u32x4 mlb_qchunk(const MlaArgs& a, int64_t bh, in
   return v;
 }
 
-// 8 dO values d .. d + 7 of query q ((B, S_q, H, D_v) layout); zeros past
-// S_q or D_v.
-__device__ __forceinline__ mla_u32x4 mlb_dochunk(const MlaArgs& a, int b, int h, int q, int d) {
+// 8 values d .. d + 7 of query q of dO or O ((B, S_q, H, D_v) layout);
+// zeros past S_q or D_v.
+__device__ __forceinline__ mla_u32x4 mlb_dochunk(const MlaArgs& a, const bf16_t* t, int b, int h, int q, int d) {
   mla_u32x4 v = {0u, 0u, 0u, 0u};
   if (q >= a.S_q || d >= a.Dv) return v;
-  const bf16_t* row = a.dout + (((int64_t)b * a.S_q + q) * a.H + h) * a.Dv;
+  const bf16_t* row = t + (((int64_t)b * a.S_q + q) * a.H + h) * a.Dv;
   if (a.dovec) return *reinterpret_cast<const mla_u32x4*>(row + d);
   bf16_t e8[8];
 #pragma unroll
@@ -670,24 +676,27 @@ struct MlbKvCfg {
   static constexpr int DVp = NV * 32;
   static constexpr int QRB = (DQKp + 127) / 128 * 256;   // Q tile row bytes
   static constexpr int ORB = (DVp + 127) / 128 * 256;    // dO tile row bytes
-  static constexpr int QT = MLB_QT * QRB;
-  static constexpr int OT = MLB_QT * ORB;
-  static constexpr int BUF = QT + OT + 2 * MLB_QT * 4;   // Q, dO, lse, D
-  static constexpr int QCH = MLB_QT * DQKp / 8;          // 16-byte chunks of a tile with data
-  static constexpr int OCH = MLB_QT * DVp / 8;
-  static constexpr int NLQ = (QCH + 255) / 256;
-  static constexpr int NLO = (OCH + 255) / 256;
+  static constexpr int QT = MLB_QI * QRB;
+  static constexpr int OT = MLB_QI * ORB;
+  static constexpr int BUF = QT + OT + 2 * MLB_QI * 4;   // Q, dO, lse, D
+  static constexpr int NQI = QT / 4096;                  // 1 KB direct loads per wave and tile
+  static constexpr int NOI = OT / 4096;
 };
 
 // Work items (batch, head, 128-key block), block i on XCD i % 8 taking
 // contiguous eighths (a head's key blocks share their XCD's L2 copy of its
 // queries and dO).  Wave w owns keys k0 + 32 w ..; a lane one key, with its
-// K and V rows (the B operands of the score and dP MFMAs) in registers.
+// K and V rows (the B operands of the score and dP MFMAs) in registers.  The
+// query tiles (64 queries, two halves of 32) come from the packed rows
+// mla_bwd_q_kernel leaves in the workspace (q_eff, dO, lse and D padded to
+// S_qp rows), straight into LDS by direct loads (no staging registers), two
+// buffers: tile i + 1 loads while tile i is used.
 template <int NSTEP, int NV>
 __global__ __launch_bounds__(256) void mla_bwd_kv_kernel(const MlaArgs a) {
   using C = MlbKvCfg<NSTEP, NV>;
   extern __shared__ __attribute__((aligned(16))) char mlb_smem[];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hi = lane >> 5, l32 = lane & 31;
   const int nkb = (a.S_kv + MLB_KW - 1) / MLB_KW;
   const int total = nkb * a.H * a.B;
@@ -723,72 +732,58 @@ __global__ __launch_bounds__(256) void mla_bwd_kv_kernel(const MlaArgs a) {
     for (int i = 0; i < 16; ++i) dka[t][i] = 0.0f;
 
   // query tiles that see a key of this block: q >= k0 - q_start when causal
-  const int qb = a.causal ? max(0, k0 - a.q_start) / MLB_QT * MLB_QT : 0;
-  const int nqt = a.S_q > qb ? (a.S_q - qb + MLB_QT - 1) / MLB_QT : 0;
-
-  mla_u32x4 qst[C::NLQ], ost[C::NLO];
-  float lst = 0.0f;
-  auto gload = [&](int i) {
-    const int qt = qb + i * MLB_QT;
+  const int qb = a.causal ? max(0, k0 - a.q_start) / MLB_QI * MLB_QI : 0;
+  const int nqt = a.S_q > qb ? (a.S_q - qb + MLB_QI - 1) / MLB_QI : 0;
+  const char* qsrc = reinterpret_cast<const char*>(a.qpk + (bh * a.S_qp + qb) * C::DQKp);
+  const char* osrc = reinterpret_cast<const char*>(a.dopk + (bh * a.S_qp + qb) * C::DVp);
+  const char* lsrc = reinterpret_cast<const char*>((wave == 0 ? a.lsep : a.deltap) + bh * a.S_qp + qb);
+  // tile j into buffer j & 1: the wave's 1 KB blocks of the Q and dO tiles
+  // (lane: 16 bytes at LDS offset 16 lane, physical chunk pc of its row,
+  // which holds logical chunk pc ^ mlb_g(row)); chunks past the data width
+  // are never read and not loaded.  Waves 0 and 1: the tile's 64 lse and D.
+  auto issue = [&](int j) {
+    const uint32_t lds0 = lds_addr(mlb_smem + (j & 1) * C::BUF);
+    const int64_t q0 = (int64_t)j * MLB_QI;
 #pragma unroll
-    for (int u = 0; u < C::NLQ; ++u) {
-      const int ch = tid + 256 * u;
-      if (C::QCH % 256 == 0 || ch < C::QCH) {
-        const int r = ch / (C::DQKp / 8), cc = ch - r * (C::DQKp / 8);
-        qst[u] = mlb_qchunk(a, bh, qt + r, 8 * cc);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < C::NLO; ++u) {
-      const int ch = tid + 256 * u;
-      if (C::OCH % 256 == 0 || ch < C::OCH) {
-        const int r = ch / (C::DVp / 8), cc = ch - r * (C::DVp / 8);
-        ost[u] = mlb_dochunk(a, b, h, qt + r, 8 * cc);
-      }
-    }
-    if (tid < 2 * MLB_QT) {
-      const int q = qt + (tid & (MLB_QT - 1));
-      lst = tid < MLB_QT ? (q < a.S_q ? a.lse[bh * a.S_q + q] : INFINITY)
-                         : (q < a.S_q ? a.delta[bh * a.S_q + q] : 0.0f);
-    }
-  };
-  auto lstore = [&](int buf) {
-    char* tq = mlb_smem + buf * C::BUF;
-    char* to = tq + C::QT;
-    float* tl = reinterpret_cast<float*>(to + C::OT);
-#pragma unroll
-    for (int u = 0; u < C::NLQ; ++u) {
-      const int ch = tid + 256 * u;
-      if (C::QCH % 256 == 0 || ch < C::QCH) {
-        const int r = ch / (C::DQKp / 8), cc = ch - r * (C::DQKp / 8);
-        *reinterpret_cast<mla_u32x4*>(tq + mlb_off(r, cc, C::QRB)) = qst[u];
-      }
+    for (int u = 0; u < C::NQI; ++u) {
+      const int blk = wave * C::NQI + u;
+      const int ofs = blk * 1024 + 16 * lane;
+      const int row = ofs / C::QRB, pc = (ofs % C::QRB) >> 4;
+      const int g = ((row & 3) << 2) | ((row >> 2) & 3);
+      const int cl = (pc & ~15) | ((pc & 15) ^ g);
+      if (cl < C::DQKp / 8)
+        dma16s(qsrc + q0 * C::DQKp * 2, (uint32_t)(row * C::DQKp * 2 + 16 * cl), lds0 + blk * 1024);
     }
 #pragma unroll
-    for (int u = 0; u < C::NLO; ++u) {
-      const int ch = tid + 256 * u;
-      if (C::OCH % 256 == 0 || ch < C::OCH) {
-        const int r = ch / (C::DVp / 8), cc = ch - r * (C::DVp / 8);
-        *reinterpret_cast<mla_u32x4*>(to + mlb_off(r, cc, C::ORB)) = ost[u];
-      }
+    for (int u = 0; u < C::NOI; ++u) {
+      const int blk = wave * C::NOI + u;
+      const int ofs = blk * 1024 + 16 * lane;
+      const int row = ofs / C::ORB, pc = (ofs % C::ORB) >> 4;
+      const int g = ((row & 3) << 2) | ((row >> 2) & 3);
+      const int cl = (pc & ~15) | ((pc & 15) ^ g);
+      if (cl < C::DVp / 8)
+        dma16s(osrc + q0 * C::DVp * 2, (uint32_t)(row * C::DVp * 2 + 16 * cl), lds0 + C::QT + blk * 1024);
     }
-    if (tid < 2 * MLB_QT) tl[tid] = lst;   // lse[0 .. 31], then D[0 .. 31]
+    if (wave < 2 && lane < MLB_QI / 4) dma16s(lsrc + q0 * 4, 16u * lane, lds0 + C::QT + C::OT + wave * MLB_QI * 4);
   };
 
-  if (nqt > 0) {
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    if (nqt > 1) gload(1);
-  }
+  if (nqt > 0) issue(0);
   for (int i = 0; i < nqt; ++i) {
-    const int qt = qb + i * MLB_QT;
+    // tile i has landed for every wave, and every wave is done with tile i - 1
+    wait_vm<0>();
+    wait_lgkm0();
+    lds_barrier();
+    if (i + 1 < nqt) issue(i + 1);
     const char* tq = mlb_smem + (i & 1) * C::BUF;
     const char* to = tq + C::QT;
     const float* tl = reinterpret_cast<const float*>(to + C::OT);
-    // a wave whose keys the whole tile cannot see skips it
-    const bool live = kw0 < a.S_kv && !(a.causal && qt + MLB_QT - 1 + a.q_start < kw0);
-    if (live) {
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int qt = qb + i * MLB_QI + 32 * half;
+      const int r0 = 32 * half;
+      // a wave whose keys the half-tile cannot see skips it
+      const bool live = kw0 < a.S_kv && qt < a.S_q && !(a.causal && qt + 31 + a.q_start < kw0);
+      if (!live) continue;
       // s, dP: lane = key, register r = query qt + 8 (r / 4) + 4 hi + r % 4
       mla_f32x16 sc, dp;
 #pragma unroll
@@ -798,23 +793,28 @@ __global__ __launch_bounds__(256) void mla_bwd_kv_kernel(const MlaArgs a) {
       }
 #pragma unroll
       for (int st = 0; st < NSTEP; ++st)
-        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mlb_frag(tq, C::QRB, l32, 2 * st + hi), kf[st], sc, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mlb_frag(tq, C::QRB, r0 + l32, 2 * st + hi), kf[st], sc, 0, 0, 0);
 #pragma unroll
       for (int st = 0; st < 2 * NV; ++st)
-        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mlb_frag(to, C::ORB, l32, 2 * st + hi), vf[st], dp, 0, 0, 0);
+        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mlb_frag(to, C::ORB, r0 + l32, 2 * st + hi), vf[st], dp, 0, 0, 0);
+      // masks only where the half-tile crosses S_q, S_kv or the diagonal
+      const bool edge = qt + 32 > a.S_q || kw0 + 32 > a.S_kv || (a.causal && kw0 + 31 > qt + a.q_start);
       float p[16], dz[16];
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const float4 l4 = *reinterpret_cast<const float4*>(tl + 8 * g + 4 * hi);
-        const float4 d4 = *reinterpret_cast<const float4*>(tl + MLB_QT + 8 * g + 4 * hi);
+        const float4 l4 = *reinterpret_cast<const float4*>(tl + r0 + 8 * g + 4 * hi);
+        const float4 d4 = *reinterpret_cast<const float4*>(tl + MLB_QI + r0 + 8 * g + 4 * hi);
         const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
         const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int r = 4 * g + e;
-          const int q = qt + 8 * g + 4 * hi + e;
-          const bool ok = q < a.S_q && key < a.S_kv && (!a.causal || key <= q + a.q_start);
-          p[r] = ok ? __builtin_amdgcn_exp2f(fmaf(sc[r], a.c, -lv[e])) : 0.0f;
+          p[r] = __builtin_amdgcn_exp2f(fmaf(sc[r], a.c, -lv[e]));
+          if (edge) {
+            const int q = qt + 8 * g + 4 * hi + e;
+            const bool ok = q < a.S_q && key < a.S_kv && (!a.causal || key <= q + a.q_start);
+            p[r] = ok ? p[r] : 0.0f;
+          }
           dz[r] = p[r] * (dp[r] - dv[e]);
         }
       }
@@ -825,18 +825,15 @@ __global__ __launch_bounds__(256) void mla_bwd_kv_kernel(const MlaArgs a) {
       for (int ps = 0; ps < 2; ++ps) {
 #pragma unroll
         for (int v = 0; v < NV; ++v)
-          dva[v] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mlb_tfrag(to, C::ORB, 16 * ps, 32 * v, lane), pf[ps],
+          dva[v] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mlb_tfrag(to, C::ORB, r0 + 16 * ps, 32 * v, lane), pf[ps],
                                                            dva[v], 0, 0, 0);
 #pragma unroll
         for (int t = 0; t < NSTEP / 2; ++t)
           if (t < nc)
-            dka[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mlb_tfrag(tq, C::QRB, 16 * ps, 32 * t, lane), zf[ps],
-                                                             dka[t], 0, 0, 0);
+            dka[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mlb_tfrag(tq, C::QRB, r0 + 16 * ps, 32 * t, lane),
+                                                             zf[ps], dka[t], 0, 0, 0);
       }
     }
-    if (i + 1 < nqt) lstore((i + 1) & 1);
-    __syncthreads();
-    if (i + 2 < nqt) gload(i + 2);
   }
 
   // dK = |scale| dZ^T q_eff (lane = key, register r: column 32 t + 8 (r / 4)
@@ -909,9 +906,31 @@ __global__ __launch_bounds__(256) void mla_bwd_q_kernel(const MlaArgs a) {
 #pragma unroll
   for (int st = 0; st < NSTEP; ++st) qf[st] = __builtin_bit_cast(bf16x8_t, mlb_qchunk(a, bh, qi, 16 * st + 8 * hi));
 #pragma unroll
-  for (int st = 0; st < 2 * NV; ++st) of[st] = __builtin_bit_cast(bf16x8_t, mlb_dochunk(a, b, h, qi, 16 * st + 8 * hi));
+  for (int st = 0; st < 2 * NV; ++st)
+    of[st] = __builtin_bit_cast(bf16x8_t, mlb_dochunk(a, a.dout, b, h, qi, 16 * st + 8 * hi));
   const float lq = qi < a.S_q ? a.lse[bh * a.S_q + qi] : INFINITY;
-  const float dq = qi < a.S_q ? a.delta[bh * a.S_q + qi] : 0.0f;
+  // D = rowsum(dO * O): this lane's columns 16 st + 8 hi .., then the other half of the row
+  float dq = 0.0f;
+#pragma unroll
+  for (int st = 0; st < 2 * NV; ++st) {
+    const bf16x8_t o8 = __builtin_bit_cast(bf16x8_t, mlb_dochunk(a, a.out, b, h, qi, 16 * st + 8 * hi));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dq = fmaf((float)o8[e], (float)of[st][e], dq);
+  }
+  dq += __shfl_xor(dq, 32);
+  // the packed rows and padded lse, D the dK, dV kernel loads (rows up to S_qp)
+  if (qi < a.S_qp) {
+    bf16_t* qrow = a.qpk + (bh * a.S_qp + qi) * C::DQKp;
+    bf16_t* orow = a.dopk + (bh * a.S_qp + qi) * C::DVp;
+#pragma unroll
+    for (int st = 0; st < NSTEP; ++st) *reinterpret_cast<bf16x8_t*>(qrow + 16 * st + 8 * hi) = qf[st];
+#pragma unroll
+    for (int st = 0; st < 2 * NV; ++st) *reinterpret_cast<bf16x8_t*>(orow + 16 * st + 8 * hi) = of[st];
+    if (hi == 0) {
+      a.lsep[bh * a.S_qp + qi] = lq;
+      a.deltap[bh * a.S_qp + qi] = dq;
+    }
+  }
   const int qpos = qi + a.q_start;
   mla_f32x16 dqa[NSTEP / 2];
 #pragma unroll
@@ -1040,20 +1059,6 @@ __global__ __launch_bounds__(256) void mla_bwd_q_kernel(const MlaArgs a) {
   }
 }
 
-// D = rowsum(dO * O) per (batch, head, query) in fp32: thread per (b, q, h) row.
-__global__ __launch_bounds__(256) void mla_bwd_delta_kernel(const MlaArgs a) {
-  const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;   // (b, q, h)
-  if (row >= (int64_t)a.B * a.S_q * a.H) return;
-  const int h = (int)(row % a.H);
-  const int64_t bq = row / a.H;
-  const int q = (int)(bq % a.S_q), b = (int)(bq / a.S_q);
-  const bf16_t* o = a.out + row * a.Dv;
-  const bf16_t* g = a.dout + row * a.Dv;
-  float s = 0.0f;
-  for (int d = 0; d < a.Dv; ++d) s = fmaf(bf2f(o[d]), bf2f(g[d]), s);
-  a.delta[((int64_t)b * a.H + h) * a.S_q + q] = s;
-}
-
 // ---------------------------------------------------------------- host side
 static int mla_pad(int v, int m) { return (v + m - 1) / m * m; }
 // Supported K / V column buckets (16-column MFMA steps, 32-column V tiles).
@@ -1098,6 +1103,7 @@ static MlaArgs mla_args(const dsmoe_mla_dims* d) {
   a.DQKp = 16 * mla_nstep(a.ksplit ? 2 * d->D_nope + d->D_rope : d->D_nope + d->D_rope);
   a.DVp = 32 * mla_nv(d->D_v);
   a.S_kvp = mla_pad(d->S_kv, MLA_KB);
+  a.S_qp = mla_pad(d->S_q, MLB_QI);
   a.causal = d->is_causal ? 1 : 0;
   a.q_start = d->q_start;
   a.negq = d->softmax_scale < 0.0f ? 1 : 0;
@@ -1131,33 +1137,34 @@ static int mla_launch_fa_nv(const MlaArgs& a, hipStream_t st) {
   }
 }
 
+// mla_bwd_q_kernel (dQ; D and the packed rows), then mla_bwd_kv_kernel (dK, dV).
 template <int NSTEP, int NV>
 static int mla_launch_bwd(const MlaArgs& a, hipStream_t st) {
   {
-    using C = MlbKvCfg<NSTEP, NV>;
-    constexpr size_t lds = 2 * (size_t)C::BUF;
-    auto kern = mla_bwd_kv_kernel<NSTEP, NV>;
+    using C = MlbQCfg<NSTEP, NV>;
+    constexpr size_t lds = (size_t)C::LDS;
+    auto kern = mla_bwd_q_kernel<NSTEP, NV>;
     if (lds > 64 * 1024) {
       static const hipError_t attr =
           hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
       if (attr != hipSuccess) return fail(DSMOE_ERR_HIP, "mla: cannot raise LDS limit");
     }
-    const int64_t total = cdiv(a.S_kv, MLB_KW) * a.H * a.B;
+    const int64_t total = cdiv(a.S_q, MLA_QB) * a.H * a.B;
     hipLaunchKernelGGL(kern, dim3((unsigned)(8 * cdiv(total, 8))), dim3(256), lds, st, a);
-    const int rc = check_launch("mla_bwd_kv");
+    const int rc = check_launch("mla_bwd_q");
     if (rc) return rc;
   }
-  using C = MlbQCfg<NSTEP, NV>;
-  constexpr size_t lds = (size_t)C::LDS;
-  auto kern = mla_bwd_q_kernel<NSTEP, NV>;
+  using C = MlbKvCfg<NSTEP, NV>;
+  constexpr size_t lds = 2 * (size_t)C::BUF;
+  auto kern = mla_bwd_kv_kernel<NSTEP, NV>;
   if (lds > 64 * 1024) {
     static const hipError_t attr =
         hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (attr != hipSuccess) return fail(DSMOE_ERR_HIP, "mla: cannot raise LDS limit");
   }
-  const int64_t total = cdiv(a.S_q, MLA_QB) * a.H * a.B;
+  const int64_t total = cdiv(a.S_kv, MLB_KW) * a.H * a.B;
   hipLaunchKernelGGL(kern, dim3((unsigned)(8 * cdiv(total, 8))), dim3(256), lds, st, a);
-  return check_launch("mla_bwd_q");
+  return check_launch("mla_bwd_kv");
 }
 
 template <int NSTEP>
@@ -1258,11 +1265,23 @@ extern "C" int dsmoe_mla_attn_fwd_lse(const void* q_nope, const void* q_pe, cons
   return mla_fwd(q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v, dims, out, lse, workspace, workspace_bytes, stream);
 }
 
-// Workspace of dsmoe_mla_attn_bwd: the forward's K, V buffers, then D.
+// Workspace of dsmoe_mla_attn_bwd: the forward's K, V buffers, then the
+// packed query and dO rows and the padded lse and D (S_qp rows each), each
+// part a multiple of 256 bytes.
+static size_t mla_bwd_part(const MlaArgs& a, int part) {
+  const size_t rows = (size_t)a.B * a.H * a.S_qp;
+  switch (part) {
+    case 0: return (size_t)a.B * a.H * a.S_kvp * (a.DQKp + a.DVp) * sizeof(bf16_t);   // K, V
+    case 1: return rows * a.DQKp * sizeof(bf16_t);
+    case 2: return rows * a.DVp * sizeof(bf16_t);
+    default: return rows * sizeof(float);                                             // lse, D
+  }
+}
+
 extern "C" size_t dsmoe_mla_attn_bwd_workspace_size(const dsmoe_mla_dims* dims) {
-  const size_t kv = dsmoe_mla_attn_workspace_size(dims);
-  if (kv == 0) return 0;
-  return kv + (size_t)dims->B * dims->H * dims->S_q * sizeof(float) + 256;
+  if (mla_validate(dims) != DSMOE_OK) return 0;
+  const MlaArgs a = mla_args(dims);
+  return mla_bwd_part(a, 0) + mla_bwd_part(a, 1) + mla_bwd_part(a, 2) + 2 * mla_bwd_part(a, 3) + 256;
 }
 
 extern "C" int dsmoe_mla_attn_bwd(const void* q_nope, const void* q_pe, const void* ctx_kv, const void* ctx_pe,
@@ -1280,13 +1299,22 @@ extern "C" int dsmoe_mla_attn_bwd(const void* q_nope, const void* q_pe, const vo
   DSMOE_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15) == 0, DSMOE_ERR_INVALID,
                 "mla: workspace must be 16-byte aligned");
   MlaArgs a = mla_bind(q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v, dims, workspace);
-  a.out = static_cast<bf16_t*>(const_cast<void*>(out));   // read only (delta)
+  a.out = static_cast<bf16_t*>(const_cast<void*>(out));   // read only (D)
   a.dout = static_cast<const bf16_t*>(dout);
   a.lse = const_cast<float*>(lse);                          // read only
   a.dovec = (a.Dv % 8 == 0 && (reinterpret_cast<uintptr_t>(dout) & 15) == 0) ? 1 : 0;
-  // D after the K, V buffers (their size is a multiple of 64 rows x 16 columns x 2 bytes)
-  a.delta = reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                     (size_t)a.B * a.H * a.S_kvp * (a.DQKp + a.DVp) * sizeof(bf16_t));
+  // parts: K, V (64-row multiples x 16-column multiples x 2 bytes), packed
+  // query rows, packed dO rows, lse, D (S_qp = 64-row multiples): every part
+  // starts 256-byte aligned
+  char* ws = static_cast<char*>(workspace);
+  size_t off = mla_bwd_part(a, 0);
+  a.qpk = reinterpret_cast<bf16_t*>(ws + off);
+  off += mla_bwd_part(a, 1);
+  a.dopk = reinterpret_cast<bf16_t*>(ws + off);
+  off += mla_bwd_part(a, 2);
+  a.lsep = reinterpret_cast<float*>(ws + off);
+  off += mla_bwd_part(a, 3);
+  a.deltap = reinterpret_cast<float*>(ws + off);
   a.dq_nope = dq_nope;
   a.dq_pe = dq_pe;
   a.dk_nope = dk_nope;
@@ -1294,10 +1322,6 @@ extern "C" int dsmoe_mla_attn_bwd(const void* q_nope, const void* q_pe, const vo
   a.dv = dv;
   hipStream_t st = static_cast<hipStream_t>(stream);
   rc = mla_launch_kv(a, st);
-  if (rc) return rc;
-  const int64_t rows = (int64_t)a.B * a.S_q * a.H;
-  hipLaunchKernelGGL(mla_bwd_delta_kernel, dim3((unsigned)cdiv(rows, 256)), dim3(256), 0, st, a);
-  rc = check_launch("mla_bwd_delta");
   if (rc) return rc;
   switch (a.DQKp / 16) {
     case 2: return mla_launch_bwd_nv<2>(a, st);

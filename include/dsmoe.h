@@ -301,7 +301,8 @@ int dsmoe_mla_attn_fwd_lse(const void* q_nope, const void* q_pe, const void* ctx
  * of the five outputs is written (zeros where no probability reaches it).
  * The probabilities and dZ enter their MFMAs in bf16 with fp32 accumulation.
  * Workspace: dsmoe_mla_attn_bwd_workspace_size bytes (the forward's K, V
- * buffers and B * H * S_q floats); dims and limits as dsmoe_mla_attn_fwd. */
+ * buffers, then packed query and dO rows, lse and rowsum(dout * out) for
+ * S_q rounded up to 64 rows); dims and limits as dsmoe_mla_attn_fwd. */
 size_t dsmoe_mla_attn_bwd_workspace_size(const dsmoe_mla_dims* dims);
 int dsmoe_mla_attn_bwd(const void* q_nope, const void* q_pe, const void* ctx_kv, const void* ctx_pe,
                        const void* wkv_b_k, const void* wkv_b_v, const dsmoe_mla_dims* dims, const void* out,
