@@ -31,7 +31,9 @@
 //    each 16-key step; the V operand is read in the same order with
 //    transposing LDS reads).
 #include <algorithm>
+#include <climits>
 #include <cstring>
+#include <type_traits>
 
 #include "common.h"
 #include "mfma.h"
@@ -584,6 +586,10 @@ __global__ __launch_bounds__(256) void mla_fa_kernel(const MlaArgs a) {
 // c ^ mlb_g(r) inside each group of 16 chunks; sixteen consecutive rows at one
 // chunk, and four consecutive rows (r = 0 mod 4) at four consecutive chunks
 // (c = 0 mod 4), then fall on distinct banks.
+// The backward kernels' tile loops come in a masked and an unmasked copy
+// for the common widths; the widest take the masked one everywhere (two
+// copies of their bodies exceed what the register allocator handles).
+#define MLB_SPLIT_EDGE(NSTEP, NV) ((NSTEP) + 2 * (NV) <= 16)
 constexpr int MLB_KW = 128;   // keys per workgroup of the dK, dV kernel
 constexpr int MLB_QI = 64;    // queries per staged tile of the dK, dV kernel (two halves of 32)
 constexpr int MLB_KT = 64;    // keys per staged tile of the dQ kernel
@@ -593,27 +599,48 @@ __device__ __forceinline__ int mlb_off(int r, int c, int rb) {
   return r * rb + (((c & ~15) | ((c & 15) ^ g)) << 4);
 }
 
-// MFMA fragment of a staged tile: row `row`, 16-byte chunk `chunk`.
-__device__ __forceinline__ bf16x8_t mlb_frag(const char* t, int rb, int row, int chunk) {
-  return *reinterpret_cast<const bf16x8_t*>(t + mlb_off(row, chunk, rb));
-}
-
-// Transposed fragment: columns c0 .. c0 + 31 (c0 = 0 mod 32) over rows
-// r0 .. r0 + 15 (r0 = 0 mod 8) of a staged tile, the rows in the order the
-// score MFMA leaves in a lane's registers (lanes 0-31: r0 + {0-3, 8-11},
-// lanes 32-63: r0 + {4-7, 12-15}); lane l gets column c0 + (l & 31).
-__device__ __forceinline__ bf16x8_t mlb_tfrag(const char* t, int rb, int r0, int c0, int lane) {
-  const int gq = lane >> 4, sl = lane & 15;
-  const int r = r0 + 4 * (gq >> 1) + (sl >> 2);
-  const int u = (c0 >> 2) + 4 * (gq & 1) + (sl & 3);   // 8-byte unit: columns 4u .. 4u + 3
-  const mla_v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) mla_v4s*)(t + mlb_off(r, u >> 1, rb) + ((u & 1) << 3)));
-  const mla_v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) mla_v4s*)(t + mlb_off(r + 8, u >> 1, rb) + ((u & 1) << 3)));
-  typedef short v8s __attribute__((ext_vector_type(8)));
-  const v8s v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-  return __builtin_bit_cast(bf16x8_t, v);
-}
+// Reads of a staged tile with row bytes RB, the lane-dependent part of their
+// offsets computed once per kernel (the swizzle sees only a row's low four
+// bits and a chunk's low four, so rows R + .. with R = 0 mod 16 and chunk
+// group k add R RB + 256 k as immediates):
+//  * frag(t, R, st): the MFMA fragment of row R + (l & 31), 16-byte chunk
+//    2 st + hi (columns 16 st + 8 hi .. + 7);
+//  * tfrag(t, r0, ct): columns 32 ct .. + 31 over rows r0 .. r0 + 15
+//    (r0 = 0 mod 16) by two ds_read_b64_tr_b16, the rows in the order the
+//    score MFMA leaves in a lane's registers (lanes 0-31: r0 + {0-3, 8-11},
+//    lanes 32-63: r0 + {4-7, 12-15}); lane l gets column 32 ct + (l & 31).
+//    In a 16-lane group lane s addresses row s >> 2, columns 4 (s & 3) ..
+//    + 3 (8-byte unit u), and receives one column of the four rows.
+template <int RB>
+struct MlbLane {
+  int f[8], t0[4], t1[4];
+  __device__ __forceinline__ explicit MlbLane(int lane) {
+    const int hi = lane >> 5, l32 = lane & 31;
+#pragma unroll
+    for (int st = 0; st < 8; ++st) f[st] = mlb_off(l32, 2 * st + hi, RB);
+    const int gq = lane >> 4, sl = lane & 15;
+    const int r = 4 * (gq >> 1) + (sl >> 2);
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      const int u = 8 * ct + 4 * (gq & 1) + (sl & 3);
+      t0[ct] = mlb_off(r, u >> 1, RB) + ((u & 1) << 3);
+      t1[ct] = mlb_off(r + 8, u >> 1, RB) + ((u & 1) << 3);
+    }
+  }
+  __device__ __forceinline__ bf16x8_t frag(const char* t, int R, int st) const {
+    return *reinterpret_cast<const bf16x8_t*>(t + f[st & 7] + R * RB + 256 * (st >> 3));
+  }
+  __device__ __forceinline__ bf16x8_t tfrag(const char* t, int r0, int ct) const {
+    const int k = r0 * RB + 256 * (ct >> 2);
+    const mla_v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) mla_v4s*)(t + t0[ct & 3] + k));
+    const mla_v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) mla_v4s*)(t + t1[ct & 3] + k));
+    typedef short v8s __attribute__((ext_vector_type(8)));
+    const v8s v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(bf16x8_t, v);
+  }
+};
 
 // 16 bf16 probabilities (or dZ values) of a lane's registers as the two
 // 16-key (16-query) K-steps of the next MFMAs.
@@ -767,8 +794,11 @@ __global__ __launch_bounds__(256) void mla_bwd_kv_kernel(const MlaArgs a) {
     if (wave < 2 && lane < MLB_QI / 4) dma16s(lsrc + q0 * 4, 16u * lane, lds0 + C::QT + C::OT + wave * MLB_QI * 4);
   };
 
-  if (nqt > 0) issue(0);
-  for (int i = 0; i < nqt; ++i) {
+  const MlbLane<C::QRB> lq(lane);
+  const MlbLane<C::ORB> lo(lane);
+  // tile i: EDGE = with the masks (q < S_q, key < S_kv, causal key <= q + q_start)
+  auto tile = [&](int i, auto edge_c) {
+    constexpr bool EDGE = decltype(edge_c)::value;
     // tile i has landed for every wave, and every wave is done with tile i - 1
     wait_vm<0>();
     wait_lgkm0();
@@ -782,8 +812,7 @@ __global__ __launch_bounds__(256) void mla_bwd_kv_kernel(const MlaArgs a) {
       const int qt = qb + i * MLB_QI + 32 * half;
       const int r0 = 32 * half;
       // a wave whose keys the half-tile cannot see skips it
-      const bool live = kw0 < a.S_kv && qt < a.S_q && !(a.causal && qt + 31 + a.q_start < kw0);
-      if (!live) continue;
+      if (EDGE && (kw0 >= a.S_kv || qt >= a.S_q || (a.causal && qt + 31 + a.q_start < kw0))) continue;
       // s, dP: lane = key, register r = query qt + 8 (r / 4) + 4 hi + r % 4
       mla_f32x16 sc, dp;
 #pragma unroll
@@ -793,12 +822,13 @@ __global__ __launch_bounds__(256) void mla_bwd_kv_kernel(const MlaArgs a) {
       }
 #pragma unroll
       for (int st = 0; st < NSTEP; ++st)
-        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mlb_frag(tq, C::QRB, r0 + l32, 2 * st + hi), kf[st], sc, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lq.frag(tq, r0, st), kf[st], sc, 0, 0, 0);
 #pragma unroll
       for (int st = 0; st < 2 * NV; ++st)
-        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mlb_frag(to, C::ORB, r0 + l32, 2 * st + hi), vf[st], dp, 0, 0, 0);
-      // masks only where the half-tile crosses S_q, S_kv or the diagonal
-      const bool edge = qt + 32 > a.S_q || kw0 + 32 > a.S_kv || (a.causal && kw0 + 31 > qt + a.q_start);
+        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lo.frag(to, r0, st), vf[st], dp, 0, 0, 0);
+      // the pair is visible when q = qt + 4 hi + off(r) has qlo <= off(r) <= qhi
+      const int qlo = (key < a.S_kv ? (a.causal ? key - a.q_start : INT_MIN / 2) : INT_MAX / 2) - qt - 4 * hi;
+      const int qhi = a.S_q - 1 - qt - 4 * hi;
       float p[16], dz[16];
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
@@ -810,11 +840,7 @@ __global__ __launch_bounds__(256) void mla_bwd_kv_kernel(const MlaArgs a) {
         for (int e = 0; e < 4; ++e) {
           const int r = 4 * g + e;
           p[r] = __builtin_amdgcn_exp2f(fmaf(sc[r], a.c, -lv[e]));
-          if (edge) {
-            const int q = qt + 8 * g + 4 * hi + e;
-            const bool ok = q < a.S_q && key < a.S_kv && (!a.causal || key <= q + a.q_start);
-            p[r] = ok ? p[r] : 0.0f;
-          }
+          if (EDGE) p[r] = 8 * g + e >= qlo && 8 * g + e <= qhi ? p[r] : 0.0f;
           dz[r] = p[r] * (dp[r] - dv[e]);
         }
       }
@@ -825,16 +851,27 @@ __global__ __launch_bounds__(256) void mla_bwd_kv_kernel(const MlaArgs a) {
       for (int ps = 0; ps < 2; ++ps) {
 #pragma unroll
         for (int v = 0; v < NV; ++v)
-          dva[v] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mlb_tfrag(to, C::ORB, r0 + 16 * ps, 32 * v, lane), pf[ps],
-                                                           dva[v], 0, 0, 0);
+          dva[v] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lo.tfrag(to, r0 + 16 * ps, v), pf[ps], dva[v], 0, 0, 0);
 #pragma unroll
         for (int t = 0; t < NSTEP / 2; ++t)
           if (t < nc)
-            dka[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mlb_tfrag(tq, C::QRB, r0 + 16 * ps, 32 * t, lane),
-                                                             zf[ps], dka[t], 0, 0, 0);
+            dka[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lq.tfrag(tq, r0 + 16 * ps, t), zf[ps], dka[t], 0, 0, 0);
       }
     }
+  };
+  // tiles every pair of which is visible: queries qt .. qt + 63 < S_q, keys
+  // k0 .. k0 + 127 < S_kv and (causal) k0 + 127 <= qt + q_start; the others,
+  // the diagonal's before them and the S_q edge after, take the masks
+  int i_lo = 0, i_hi = 0;   // 0 <= i_lo <= i_hi <= nqt
+  if (k0 + MLB_KW <= a.S_kv) {
+    i_lo = a.causal ? min(nqt, max(0, (k0 + MLB_KW - 1 - a.q_start - qb + MLB_QI - 1) / MLB_QI)) : 0;
+    i_hi = max(i_lo, (a.S_q - qb) / MLB_QI);
   }
+  if (nqt > 0) issue(0);
+  int i = 0;
+  for (; i < i_lo; ++i) tile(i, std::true_type{});
+  for (; i < i_hi; ++i) tile(i, std::bool_constant<!MLB_SPLIT_EDGE(NSTEP, NV)>{});
+  for (; i < nqt; ++i) tile(i, std::true_type{});
 
   // dK = |scale| dZ^T q_eff (lane = key, register r: column 32 t + 8 (r / 4)
   // + 4 hi + r % 4), dV = P^T dO (dv likewise)
@@ -873,10 +910,8 @@ struct MlbQCfg {
   static constexpr int VRB = (DVp + 127) / 128 * 256;
   static constexpr int KT = MLB_KT * KRB;
   static constexpr int BUF = KT + MLB_KT * VRB;
-  static constexpr int KCH = MLB_KT * DQKp / 8;
-  static constexpr int VCH = MLB_KT * DVp / 8;
-  static constexpr int NLK = (KCH + 255) / 256;
-  static constexpr int NLV = (VCH + 255) / 256;
+  static constexpr int NLK = KT / 4096;                    // 1 KB direct loads per wave and tile
+  static constexpr int NLV = MLB_KT * VRB / 4096;
   static constexpr int SRS = DQKp + 4;                     // fp32 dQ staging row (floats)
   static constexpr int STG = 4 * 32 * SRS * 4;
   static constexpr int LDS = 2 * BUF > STG ? 2 * BUF : STG;
@@ -884,12 +919,15 @@ struct MlbQCfg {
 
 // Work items as the forward's: (batch, head, 128-query block), a head's
 // blocks longest first.  Lane: one query, its query fragments and dO row (the
-// B operands of the score and dP MFMAs) in registers.
+// B operands of the score and dP MFMAs) in registers.  The 64-key K and V
+// tiles go straight into LDS by direct loads, two buffers: tile i + 1 loads
+// while tile i is used.
 template <int NSTEP, int NV>
 __global__ __launch_bounds__(256) void mla_bwd_q_kernel(const MlaArgs a) {
   using C = MlbQCfg<NSTEP, NV>;
   extern __shared__ __attribute__((aligned(16))) char mlb_smem[];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hi = lane >> 5, l32 = lane & 31;
   const int nq = (a.S_q + MLA_QB - 1) / MLA_QB;
   const int total = nq * a.H * a.B;
@@ -941,63 +979,55 @@ __global__ __launch_bounds__(256) void mla_bwd_q_kernel(const MlaArgs a) {
   int kend = a.S_kv;
   if (a.causal) kend = min(kend, min(q0 + MLA_QB, a.S_q) - 1 + a.q_start + 1);
   const int nkb = (kend + MLB_KT - 1) / MLB_KT;
-  const bf16_t* kg = a.kbuf + bh * a.S_kvp * C::DQKp;
-  const bf16_t* vg = a.vbuf + bh * a.S_kvp * C::DVp;
-
-  mla_u32x4 kst[C::NLK], vst[C::NLV];
-  auto gload = [&](int kb) {
-    const int kk = kb * MLB_KT;
+  const char* kg = reinterpret_cast<const char*>(a.kbuf + bh * a.S_kvp * C::DQKp);
+  const char* vg = reinterpret_cast<const char*>(a.vbuf + bh * a.S_kvp * C::DVp);
+  // tile j into buffer j & 1 (the dK, dV kernel's scheme: lane 16 bytes at
+  // LDS offset 16 lane, physical chunk pc holding logical chunk pc ^ mlb_g)
+  auto issue = [&](int j) {
+    const uint32_t lds0 = lds_addr(mlb_smem + (j & 1) * C::BUF);
+    const int64_t k0 = (int64_t)j * MLB_KT;
 #pragma unroll
     for (int u = 0; u < C::NLK; ++u) {
-      const int ch = tid + 256 * u;
-      if (C::KCH % 256 == 0 || ch < C::KCH) {
-        const int r = ch / (C::DQKp / 8), cc = ch - r * (C::DQKp / 8);
-        kst[u] = *reinterpret_cast<const mla_u32x4*>(kg + (int64_t)(kk + r) * C::DQKp + cc * 8);
-      }
+      const int blk = wave * C::NLK + u;
+      const int ofs = blk * 1024 + 16 * lane;
+      const int row = ofs / C::KRB, pc = (ofs % C::KRB) >> 4;
+      const int g = ((row & 3) << 2) | ((row >> 2) & 3);
+      const int cl = (pc & ~15) | ((pc & 15) ^ g);
+      if (cl < C::DQKp / 8)
+        dma16s(kg + k0 * C::DQKp * 2, (uint32_t)(row * C::DQKp * 2 + 16 * cl), lds0 + blk * 1024);
     }
 #pragma unroll
     for (int u = 0; u < C::NLV; ++u) {
-      const int ch = tid + 256 * u;
-      if (C::VCH % 256 == 0 || ch < C::VCH) {
-        const int r = ch / (C::DVp / 8), cc = ch - r * (C::DVp / 8);
-        vst[u] = *reinterpret_cast<const mla_u32x4*>(vg + (int64_t)(kk + r) * C::DVp + cc * 8);
-      }
-    }
-  };
-  auto lstore = [&](int buf) {
-    char* tk = mlb_smem + buf * C::BUF;
-    char* tv = tk + C::KT;
-#pragma unroll
-    for (int u = 0; u < C::NLK; ++u) {
-      const int ch = tid + 256 * u;
-      if (C::KCH % 256 == 0 || ch < C::KCH) {
-        const int r = ch / (C::DQKp / 8), cc = ch - r * (C::DQKp / 8);
-        *reinterpret_cast<mla_u32x4*>(tk + mlb_off(r, cc, C::KRB)) = kst[u];
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < C::NLV; ++u) {
-      const int ch = tid + 256 * u;
-      if (C::VCH % 256 == 0 || ch < C::VCH) {
-        const int r = ch / (C::DVp / 8), cc = ch - r * (C::DVp / 8);
-        *reinterpret_cast<mla_u32x4*>(tv + mlb_off(r, cc, C::VRB)) = vst[u];
-      }
+      const int blk = wave * C::NLV + u;
+      const int ofs = blk * 1024 + 16 * lane;
+      const int row = ofs / C::VRB, pc = (ofs % C::VRB) >> 4;
+      const int g = ((row & 3) << 2) | ((row >> 2) & 3);
+      const int cl = (pc & ~15) | ((pc & 15) ^ g);
+      if (cl < C::DVp / 8)
+        dma16s(vg + k0 * C::DVp * 2, (uint32_t)(row * C::DVp * 2 + 16 * cl), lds0 + C::KT + blk * 1024);
     }
   };
 
-  if (nkb > 0) {
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    if (nkb > 1) gload(1);
-  }
-  for (int kb = 0; kb < nkb; ++kb) {
+  const int qw = q0 + 32 * wave;   // this wave's first query
+  const MlbLane<C::KRB> lk(lane);
+  const MlbLane<C::VRB> lv(lane);
+  // tile kb: EDGE = with the masks (q < S_q, key < S_kv, causal key <= q + q_start)
+  auto tile = [&](int kb, auto edge_c) {
+    constexpr bool EDGE = decltype(edge_c)::value;
+    // tile kb has landed for every wave, and every wave is done with tile kb - 1
+    wait_vm<0>();
+    wait_lgkm0();
+    lds_barrier();
+    if (kb + 1 < nkb) issue(kb + 1);
     const int kk = kb * MLB_KT;
     const char* tk = mlb_smem + (kb & 1) * C::BUF;
     const char* tv = tk + C::KT;
 #pragma unroll
     for (int t = 0; t < MLB_KT / 32; ++t) {
-      // s, dP: lane = query, register r = key kk + 32 t + 8 (r / 4) + 4 hi + r % 4
+      const int ks = kk + 32 * t;
+      // a wave whose queries see no key of the sub-tile skips it
+      if (EDGE && (qw >= a.S_q || ks >= a.S_kv || (a.causal && ks > qw + 31 + a.q_start))) continue;
+      // s, dP: lane = query, register r = key ks + 8 (r / 4) + 4 hi + r % 4
       mla_f32x16 sc, dp;
 #pragma unroll
       for (int i2 = 0; i2 < 16; ++i2) {
@@ -1006,18 +1036,17 @@ __global__ __launch_bounds__(256) void mla_bwd_q_kernel(const MlaArgs a) {
       }
 #pragma unroll
       for (int st = 0; st < NSTEP; ++st)
-        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mlb_frag(tk, C::KRB, 32 * t + l32, 2 * st + hi), qf[st], sc, 0,
-                                                     0, 0);
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lk.frag(tk, 32 * t, st), qf[st], sc, 0, 0, 0);
 #pragma unroll
       for (int st = 0; st < 2 * NV; ++st)
-        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mlb_frag(tv, C::VRB, 32 * t + l32, 2 * st + hi), of[st], dp, 0,
-                                                     0, 0);
+        dp = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lv.frag(tv, 32 * t, st), of[st], dp, 0, 0, 0);
+      // keys past min(S_kv - 1, the query's position) and queries past S_q get p = 0
+      const int klim = qi < a.S_q ? min(a.S_kv - 1, a.causal ? qpos : a.S_kv) - ks - 4 * hi : -1;
       float dz[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int k = kk + 32 * t + 8 * (r >> 2) + 4 * hi + (r & 3);
-        const bool ok = qi < a.S_q && k < a.S_kv && (!a.causal || k <= qpos);
-        const float p = ok ? __builtin_amdgcn_exp2f(fmaf(sc[r], a.c, -lq)) : 0.0f;
+        float p = __builtin_amdgcn_exp2f(fmaf(sc[r], a.c, -lq));
+        if (EDGE) p = 8 * (r >> 2) + (r & 3) <= klim ? p : 0.0f;
         dz[r] = p * (dp[r] - dq);
       }
       bf16x8_t zf[2];
@@ -1026,14 +1055,22 @@ __global__ __launch_bounds__(256) void mla_bwd_q_kernel(const MlaArgs a) {
       for (int ps = 0; ps < 2; ++ps)
 #pragma unroll
         for (int ct = 0; ct < NSTEP / 2; ++ct)
-          dqa[ct] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mlb_tfrag(tk, C::KRB, 32 * t + 16 * ps, 32 * ct, lane),
-                                                            zf[ps], dqa[ct], 0, 0, 0);
+          dqa[ct] =
+              __builtin_amdgcn_mfma_f32_32x32x16_bf16(lk.tfrag(tk, 32 * t + 16 * ps, ct), zf[ps], dqa[ct], 0, 0, 0);
     }
-    if (kb + 1 < nkb) lstore((kb + 1) & 1);
-    __syncthreads();
-    if (kb + 2 < nkb) gload(kb + 2);
-  }
+  };
+  // leading tiles every pair of which is visible: queries q0 .. q0 + 127 <
+  // S_q and keys kk .. kk + 63 below min(S_kv, q0 + q_start + 1 when causal)
+  int kfull = 0;
+  if (q0 + MLA_QB <= a.S_q) kfull = min(nkb, (a.causal ? min(a.S_kv, q0 + a.q_start + 1) : a.S_kv) / MLB_KT);
+  if (nkb > 0) issue(0);
+  int kb = 0;
+  for (; kb < kfull; ++kb) tile(kb, std::bool_constant<!MLB_SPLIT_EDGE(NSTEP, NV)>{});
+  for (; kb < nkb; ++kb) tile(kb, std::true_type{});
 
+  // every wave is done with the last tile before its buffer is reused
+  wait_lgkm0();
+  lds_barrier();
   // dQ over the K columns (lane = query, register r: column 32 ct + 8 (r / 4)
   // + 4 hi + r % 4), staged per wave as fp32 rows, then dq_nope = scale
   // (k_hi part + k_lo part), dq_pe = scale pe part, written row by row
@@ -1045,17 +1082,14 @@ __global__ __launch_bounds__(256) void mla_bwd_q_kernel(const MlaArgs a) {
       *reinterpret_cast<float4*>(stg + l32 * C::SRS + 32 * ct + 8 * g + 4 * hi) =
           make_float4(dqa[ct][4 * g], dqa[ct][4 * g + 1], dqa[ct][4 * g + 2], dqa[ct][4 * g + 3]);
   __syncthreads();
-  const int qw = q0 + 32 * wave;
   const float sq = a.scale;
-  for (int i = lane; i < 32 * a.Dn; i += 64) {
-    const int r = i / a.Dn, d = i - r * a.Dn;
-    if (qw + r < a.S_q)
-      a.dq_nope[(bh * a.S_q + qw + r) * a.Dn + d] =
-          sq * (stg[r * C::SRS + d] + (a.ksplit ? stg[r * C::SRS + a.Dn + a.Dr + d] : 0.0f));
-  }
-  for (int i = lane; i < 32 * a.Dr; i += 64) {
-    const int r = i / a.Dr, d = i - r * a.Dr;
-    if (qw + r < a.S_q) a.dq_pe[(bh * a.S_q + qw + r) * a.Dr + d] = sq * stg[r * C::SRS + a.Dn + d];
+  const int nr = min(32, a.S_q - qw);
+  for (int r = 0; r < nr; ++r) {
+    const float* srow = stg + r * C::SRS;
+    float* dn = a.dq_nope + (bh * a.S_q + qw + r) * a.Dn;
+    float* dp = a.dq_pe + (bh * a.S_q + qw + r) * a.Dr;
+    for (int d = lane; d < a.Dn; d += 64) dn[d] = sq * (srow[d] + (a.ksplit ? srow[a.Dn + a.Dr + d] : 0.0f));
+    for (int d = lane; d < a.Dr; d += 64) dp[d] = sq * srow[a.Dn + d];
   }
 }
 
