@@ -67,9 +67,9 @@ struct MlaArgs {
   int S_qp;               // S_q rounded up to a multiple of 64
   float* dq_nope;         // (B, H, S_q, Dn) fp32
   float* dq_pe;           // (B, H, S_q, Dr)
-  float* dk_nope;         // (B, S_kv, H, Dn): rows of the latent positions, heads side by side
+  bf16_t* dkv;            // (B, S_kv, H, Dn + Dv) bf16 rows [dk_nope | dv]: latent positions, heads side by side
   float* dk_pe;           // (B, S_kv, H, Dr)
-  float* dv;              // (B, S_kv, H, Dv)
+  int kvec;               // 8-byte dkv stores (Dn, Dv % 4 == 0, dkv 8-byte aligned)
   int dovec;              // 16-byte dO row loads (Dv % 8 == 0, dout 16-byte aligned)
   float scale;            // softmax_scale
   bf16_t* kbuf;           // (B, H, S_kvp, DQKp)
@@ -874,31 +874,50 @@ __global__ __launch_bounds__(256) void mla_bwd_kv_kernel(const MlaArgs a) {
   for (; i < nqt; ++i) tile(i, std::true_type{});
 
   // dK = |scale| dZ^T q_eff (lane = key, register r: column 32 t + 8 (r / 4)
-  // + 4 hi + r % 4), dV = P^T dO (dv likewise)
+  // + 4 hi + r % 4), dV = P^T dO (dv likewise): the bf16 row [dk_nope | dv]
+  // of (batch, key, head), four consecutive columns per 8-byte store when
+  // D_nope and D_v are multiples of 4; dk_pe in fp32
   if (key >= a.S_kv) return;
   const float sk = a.c * (1.0f / MLA_LOG2E);
   const int64_t kh = ((int64_t)b * a.S_kv + key) * a.H + h;
-  float* dkn = a.dk_nope + kh * a.Dn;
+  bf16_t* dkv = a.dkv + kh * (a.Dn + a.Dv);
   float* dkp = a.dk_pe + kh * a.Dr;
-  float* dvo = a.dv + kh * a.Dv;
+  auto put4 = [&](int c, float v0, float v1, float v2, float v3) {   // columns c .. c + 3 of the row
+    u32x2_t w;
+    w.x = pack_bf16x2(v0, v1);
+    w.y = pack_bf16x2(v2, v3);
+    *reinterpret_cast<u32x2_t*>(dkv + c) = w;
+  };
 #pragma unroll
   for (int t = 0; t < NSTEP / 2; ++t)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int c = 32 * t + 8 * (r >> 2) + 4 * hi + (r & 3);
-      if (t < nc) {
-        if (c < a.Dn)
-          dkn[c] = sk * dka[t][r];
-        else if (c < a.Dn + a.Dr)
-          dkp[c - a.Dn] = sk * dka[t][r];
+    for (int g = 0; g < 4; ++g) {
+      const int c = 32 * t + 8 * g + 4 * hi;
+      if (t >= nc) continue;
+      if (a.kvec && c + 3 < a.Dn) {
+        put4(c, sk * dka[t][4 * g], sk * dka[t][4 * g + 1], sk * dka[t][4 * g + 2], sk * dka[t][4 * g + 3]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (c + e < a.Dn)
+            dkv[c + e] = f2bf(sk * dka[t][4 * g + e]);
+          else if (c + e < a.Dn + a.Dr)
+            dkp[c + e - a.Dn] = sk * dka[t][4 * g + e];
+        }
       }
     }
 #pragma unroll
   for (int v = 0; v < NV; ++v)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int c = 32 * v + 8 * (r >> 2) + 4 * hi + (r & 3);
-      if (c < a.Dv) dvo[c] = dva[v][r];
+    for (int g = 0; g < 4; ++g) {
+      const int c = 32 * v + 8 * g + 4 * hi;
+      if (a.kvec && c + 3 < a.Dv) {
+        put4(a.Dn + c, dva[v][4 * g], dva[v][4 * g + 1], dva[v][4 * g + 2], dva[v][4 * g + 3]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (c + e < a.Dv) dkv[a.Dn + c + e] = f2bf(dva[v][4 * g + e]);
+      }
     }
 }
 
@@ -1321,13 +1340,12 @@ extern "C" size_t dsmoe_mla_attn_bwd_workspace_size(const dsmoe_mla_dims* dims) 
 extern "C" int dsmoe_mla_attn_bwd(const void* q_nope, const void* q_pe, const void* ctx_kv, const void* ctx_pe,
                                   const void* wkv_b_k, const void* wkv_b_v, const dsmoe_mla_dims* dims,
                                   const void* out, const void* dout, const float* lse, float* dq_nope, float* dq_pe,
-                                  float* dk_nope, float* dk_pe, float* dv, void* workspace, size_t workspace_bytes,
-                                  void* stream) {
+                                  void* dkv, float* dk_pe, void* workspace, size_t workspace_bytes, void* stream) {
   int rc = mla_validate(dims);
   if (rc) return rc;
   DSMOE_REQUIRE(q_nope && q_pe && ctx_kv && ctx_pe && wkv_b_k && wkv_b_v && out && dout && lse, DSMOE_ERR_INVALID,
                 "mla: NULL tensor pointer");
-  DSMOE_REQUIRE(dq_nope && dq_pe && dk_nope && dk_pe && dv, DSMOE_ERR_INVALID, "mla: NULL gradient pointer");
+  DSMOE_REQUIRE(dq_nope && dq_pe && dkv && dk_pe, DSMOE_ERR_INVALID, "mla: NULL gradient pointer");
   const size_t need = dsmoe_mla_attn_bwd_workspace_size(dims);
   DSMOE_REQUIRE(workspace && workspace_bytes >= need, DSMOE_ERR_WORKSPACE, "mla: workspace too small");
   DSMOE_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15) == 0, DSMOE_ERR_INVALID,
@@ -1351,9 +1369,9 @@ extern "C" int dsmoe_mla_attn_bwd(const void* q_nope, const void* q_pe, const vo
   a.deltap = reinterpret_cast<float*>(ws + off);
   a.dq_nope = dq_nope;
   a.dq_pe = dq_pe;
-  a.dk_nope = dk_nope;
+  a.dkv = static_cast<bf16_t*>(dkv);
   a.dk_pe = dk_pe;
-  a.dv = dv;
+  a.kvec = (a.Dn % 4 == 0 && a.Dv % 4 == 0 && (reinterpret_cast<uintptr_t>(dkv) & 7) == 0) ? 1 : 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
   rc = mla_launch_kv(a, st);
   if (rc) return rc;

@@ -10,7 +10,8 @@ differentiates a torch recompute of the attention; here the training forward
 also keeps each query's log-sum-exp, and the backward rebuilds the
 probabilities from it in two flash-attention kernels (dsmoe_mla_attn_bwd:
 dq per query block, dk and dv per key block) and maps the per-head key
-gradients onto ctx_kv, wkv_b_k and wkv_b_v with fp32 GEMMs.  The gradient is
+gradients onto ctx_kv, wkv_b_k and wkv_b_v with two GEMMs (bf16 operands,
+fp32 accumulation and results, as autocast computes weight gradients).  The gradient is
 that of the function the forward computes: its masking (causal only when
 ``is_causal``; the reference's recompute, mla_attention_reference, also masks
 a square non-causal call, models/mla_triton.py:52-57, which its forward
@@ -144,10 +145,10 @@ def mla_attention_fwd(q_nope: torch.Tensor, q_pe: torch.Tensor, ctx_kv: torch.Te
 
 def mla_attention_bwd_heads(ts, bc: int, out: torch.Tensor, lse: torch.Tensor, dout: torch.Tensor,
                             softmax_scale: float, is_causal: bool, q_start: int):
-    """dsmoe_mla_attn_bwd over the batch chunks: fp32 dq_nope (B, H, S_q, Dn),
-    dq_pe (B, H, S_q, Dr) and the per-head key-side gradients dk_nope
-    (B, S_kv, H, Dn), dk_pe (B, S_kv, H, Dr), dv (B, S_kv, H, Dv).  ``ts`` and
-    ``bc`` as ``_prepare`` returns them; out, lse from the training forward."""
+    """dsmoe_mla_attn_bwd over the batch chunks: fp32 dq_nope (B, H, S_q, Dn)
+    and dq_pe (B, H, S_q, Dr), the bf16 key-side rows dkv (B, S_kv, H, Dn + Dv)
+    = [dk_nope | dv] and fp32 dk_pe (B, S_kv, H, Dr).  ``ts`` and ``bc`` as
+    ``_prepare`` returns them; out, lse from the training forward."""
     q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v = ts
     B, H, S_q, Dn = q_nope.shape
     S_kv, Dr, Dv = ctx_kv.size(1), q_pe.size(-1), wkv_b_v.size(1)
@@ -159,34 +160,36 @@ def mla_attention_bwd_heads(ts, bc: int, out: torch.Tensor, lse: torch.Tensor, d
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     f32 = dict(dtype=torch.float32, device=dev)
     dq_nope, dq_pe = torch.empty(B, H, S_q, Dn, **f32), torch.empty(B, H, S_q, Dr, **f32)
-    dk_nope, dk_pe, dv = (torch.empty(B, S_kv, H, Dn, **f32), torch.empty(B, S_kv, H, Dr, **f32),
-                          torch.empty(B, S_kv, H, Dv, **f32))
+    dkv = torch.empty(B, S_kv, H, Dn + Dv, dtype=torch.bfloat16, device=dev)
+    dk_pe = torch.empty(B, S_kv, H, Dr, **f32)
     for b0 in range(0, B, bc):
         b1 = min(B, b0 + bc)
         d = _dims(q_nope[b0:b1], q_pe[b0:b1], ctx_kv[b0:b1], wkv_b_v, softmax_scale, is_causal, q_start)
         rc = lib.dsmoe_mla_attn_bwd(
             L.ptr(q_nope[b0:b1]), L.ptr(q_pe[b0:b1]), L.ptr(ctx_kv[b0:b1]), L.ptr(ctx_pe[b0:b1]), L.ptr(wkv_b_k),
             L.ptr(wkv_b_v), d, L.ptr(out[b0:b1]), L.ptr(dout[b0:b1]), L.ptr(lse[b0:b1]), L.ptr(dq_nope[b0:b1]),
-            L.ptr(dq_pe[b0:b1]), L.ptr(dk_nope[b0:b1]), L.ptr(dk_pe[b0:b1]), L.ptr(dv[b0:b1]), L.ptr(ws), nbytes,
-            L.stream_ptr(dev))
+            L.ptr(dq_pe[b0:b1]), L.ptr(dkv[b0:b1]), L.ptr(dk_pe[b0:b1]), L.ptr(ws), nbytes, L.stream_ptr(dev))
         L.check(rc, "dsmoe_mla_attn_bwd")
-    return dq_nope, dq_pe, dk_nope, dk_pe, dv
+    return dq_nope, dq_pe, dkv, dk_pe
 
 
-def _project_kv_grads(ctx_kv, wkv_b_k, wkv_b_v, dk_nope, dk_pe, dv):
-    """Key-side gradients onto the latent rows and the up-projections (fp32
-    GEMMs): k_nope = ctx_kv W_k^T and v = ctx_kv W_v^T per head, so
-    d ctx_kv = dk_nope W_k + dv W_v (summed over heads), dW_k = dk_nope^T
-    ctx_kv, dW_v = dv^T ctx_kv (summed over batch and positions), and
+def _project_kv_grads(ctx_kv, wkv_b_k, wkv_b_v, dkv, dk_pe):
+    """Key-side gradients onto the latent rows and the up-projections: with
+    W = [W_k; W_v] per head (wkv_b's layout, (H (Dn + Dv), R)), k_nope and v
+    are ctx_kv W^T split per head, so d ctx_kv = dkv W and [dW_k | dW_v] =
+    dkv^T ctx_kv (bf16 operands, fp32 accumulation and results; the second
+    product split over row slices whose fp32 partials are summed), and
     d ctx_pe = dk_pe summed over heads."""
-    B, S_kv, H, Dn = dk_nope.shape
-    R, Dv = ctx_kv.size(-1), dv.size(-1)
-    kv = ctx_kv.float().view(B * S_kv, R)
-    dkn, dvv = dk_nope.view(B * S_kv, H * Dn), dv.view(B * S_kv, H * Dv)
-    dctx_kv = torch.addmm(dkn @ wkv_b_k.float().reshape(H * Dn, R), dvv, wkv_b_v.float().reshape(H * Dv, R))
-    dwk = (dkn.t() @ kv).view(H, Dn, R)
-    dwv = (dvv.t() @ kv).view(H, Dv, R)
-    return dctx_kv.view(B, S_kv, R), dk_pe.sum(2), dwk, dwv
+    B, S_kv, H, Dkv = dkv.shape
+    Dn, R = wkv_b_k.size(1), ctx_kv.size(-1)
+    rows = B * S_kv
+    d2 = dkv.view(rows, H * Dkv)
+    w = torch.cat([wkv_b_k, wkv_b_v], dim=1).reshape(H * Dkv, R)
+    dctx_kv = torch.mm(d2, w, out_dtype=torch.float32)
+    n = next(k for k in (8, 4, 2, 1) if rows % k == 0 and rows // k >= 256 or k == 1)
+    dw = torch.bmm(d2.view(n, rows // n, H * Dkv).transpose(1, 2), ctx_kv.reshape(n, rows // n, R),
+                   out_dtype=torch.float32).sum(0).view(H, Dkv, R)
+    return dctx_kv.view(B, S_kv, R), dk_pe.sum(2), dw[:, :Dn], dw[:, Dn:]
 
 
 class _MlaAttentionFunction(torch.autograd.Function):
@@ -209,9 +212,9 @@ class _MlaAttentionFunction(torch.autograd.Function):
         *ts, out, lse = ctx.saved_tensors
         bc, softmax_scale, is_causal, q_start = ctx.args
         with torch.autocast(dout.device.type, enabled=False):
-            dq_nope, dq_pe, dk_nope, dk_pe, dv = mla_attention_bwd_heads(ts, bc, out, lse, dout, softmax_scale,
-                                                                         is_causal, q_start)
-            dctx_kv, dctx_pe, dwk, dwv = _project_kv_grads(ts[2], ts[4], ts[5], dk_nope, dk_pe, dv)
+            dq_nope, dq_pe, dkv, dk_pe = mla_attention_bwd_heads(ts, bc, out, lse, dout, softmax_scale, is_causal,
+                                                                 q_start)
+            dctx_kv, dctx_pe, dwk, dwv = _project_kv_grads(ts[2], ts[4], ts[5], dkv, dk_pe)
         grads = (dq_nope, dq_pe, dctx_kv, dctx_pe, dwk, dwv)
         return tuple(g.to(dt) for g, dt in zip(grads, ctx.dtypes)) + (None, None, None)
 

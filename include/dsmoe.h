@@ -288,26 +288,28 @@ int dsmoe_mla_attn_fwd_lse(const void* q_nope, const void* q_pe, const void* ctx
 /* Backward of the attention (models/mla_triton.py:269-296,
  * _TritonMlaAttentionFunction.backward, which differentiates a torch recompute of
  * the same function), for the per-head operands: given the forward's inputs,
- * its out and lse, and dout (B, S_q, H, D_v) bf16, writes fp32
- *   dq_nope (B, H, S_q, D_nope)   dq_pe (B, H, S_q, D_rope)
- *   dk_nope (B, S_kv, H, D_nope)  dk_pe (B, S_kv, H, D_rope)  dv (B, S_kv, H, D_v)
- * the gradients of k_nope = ctx_kv wkv_b_k^T, k_pe = ctx_pe (per head) and
- * v = ctx_kv wkv_b_v^T, laid out so that (B S_kv, H D) views are the left
- * operands of the GEMMs that map them onto ctx_kv (dk_nope wkv_b_k + dv
- * wkv_b_v as (H D, R) matrices), wkv_b_k and wkv_b_v (their transposes times
- * ctx_kv); ctx_pe's gradient is dk_pe summed over heads.  The gradient is
- * that of the function the forward computes (for is_causal = 0 no mask,
- * square or not).  Every element
- * of the five outputs is written (zeros where no probability reaches it).
- * The probabilities and dZ enter their MFMAs in bf16 with fp32 accumulation.
+ * its out and lse, and dout (B, S_q, H, D_v) bf16, writes
+ *   dq_nope (B, H, S_q, D_nope) fp32   dq_pe (B, H, S_q, D_rope) fp32
+ *   dkv (B, S_kv, H, D_nope + D_v) bf16: rows [dk_nope | dv]
+ *   dk_pe (B, S_kv, H, D_rope) fp32
+ * the gradients of q, of k_nope = ctx_kv wkv_b_k^T, v = ctx_kv wkv_b_v^T and
+ * k_pe = ctx_pe (per head).  A (B S_kv, H (D_nope + D_v)) view of dkv pairs
+ * with the weight in the wkv_b layout (per head the D_nope k rows, then the
+ * D_v v rows: an (H (D_nope + D_v), R) matrix W), so the caller finishes with
+ * two GEMMs: d ctx_kv = dkv W and [dW_k | dW_v] = dkv^T ctx_kv; ctx_pe's
+ * gradient is dk_pe summed over heads.  The gradient is that of the function
+ * the forward computes (for is_causal = 0 no mask, square or not).  Every
+ * element of the four outputs is written (zeros where no probability reaches
+ * it).  The probabilities and dZ enter their MFMAs in bf16 with fp32
+ * accumulation; dkv is rounded to bf16 once (the operand of those GEMMs).
  * Workspace: dsmoe_mla_attn_bwd_workspace_size bytes (the forward's K, V
  * buffers, then packed query and dO rows, lse and rowsum(dout * out) for
  * S_q rounded up to 64 rows); dims and limits as dsmoe_mla_attn_fwd. */
 size_t dsmoe_mla_attn_bwd_workspace_size(const dsmoe_mla_dims* dims);
 int dsmoe_mla_attn_bwd(const void* q_nope, const void* q_pe, const void* ctx_kv, const void* ctx_pe,
                        const void* wkv_b_k, const void* wkv_b_v, const dsmoe_mla_dims* dims, const void* out,
-                       const void* dout, const float* lse, float* dq_nope, float* dq_pe, float* dk_nope,
-                       float* dk_pe, float* dv, void* workspace, size_t workspace_bytes, void* stream);
+                       const void* dout, const float* lse, float* dq_nope, float* dq_pe, void* dkv,
+                       float* dk_pe, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -240,7 +240,8 @@ def test_call_beyond_the_row_index_limit_runs_in_batch_chunks():
 # Bar for the backward kernels (dsmoe_mla_attn_bwd): they rebuild the
 # probabilities from the forward's lse with the forward's operands (K_nope
 # as an exact bf16 pair, V in bf16) and feed P and dZ to their MFMAs in bf16
-# (fp32 accumulation), as the forward feeds P (models/mla_triton.py:175).
+# (fp32 accumulation), as the forward feeds P (models/mla_triton.py:175);
+# the key-side rows [dk_nope | dv] come out rounded to bf16.
 # Each gradient is compared with the float64 closed form of
 # oracle/mla_ref.py on the same bf16 inputs and bf16 dout: relative L2
 # error <= 1e-2 and max |err| <= 2e-2 max |oracle| (the reference's GPU test
@@ -279,7 +280,9 @@ def _check_bwd(B, H, S_q, S_kv, R, Dn, Dr, Dv, causal, q_start, seed=0, wscale=0
     sc = sc if scale is None else scale
     g = torch.Generator(device=DEV).manual_seed(seed + 100)
     dout = torch.randn(B, S_q, H, Dv, generator=g, device=DEV).to(torch.bfloat16)
-    out, lse, (dqn, dqp, dkn, dkp, dv) = _bwd_heads(ts, sc, causal, q_start, dout)
+    out, lse, (dqn, dqp, dkv, dkp) = _bwd_heads(ts, sc, causal, q_start, dout)
+    assert dkv.dtype == torch.bfloat16 and dkv.shape == (B, S_kv, H, Dn + Dv)
+    dkn, dv = dkv[..., :Dn], dkv[..., Dn:]
     cpu = [t.cpu() for t in ts]
     for b, h in (heads or [(b, h) for b in range(B) for h in range(H)]):
         sl = (cpu[0][b:b + 1, h:h + 1], cpu[1][b:b + 1, h:h + 1], cpu[2][b:b + 1], cpu[3][b:b + 1],
