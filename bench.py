@@ -299,7 +299,8 @@ def mla_cpu_baseline(dev, gpu_ms: float):
 def mla_bench(dev, steps: int, warmup: int):
     """Fused MLA attention forward (models/mla_triton.py:303-329) at the 422m
     config's shape, causal: the two kernels of csrc/mla.hip (K, V
-    materialisation + flash attention) per call.  Algorithmic flops: 2 (Dn +
+    materialisation + flash attention) per call; then the operator's
+    training step (forward and backward to every input) as "fwd_bwd".  Algorithmic flops: 2 (Dn +
     Dr + Dv) per visible (query, key) pair plus 2 R (Dn + Dv) per (batch,
     head, key) for K and V.  Beside it, the reference's default SDPA path
     (models/mla.py:155-172: K, V materialised with bmm, then
@@ -355,8 +356,28 @@ def mla_bench(dev, steps: int, warmup: int):
     except Exception as e:  # no fused SDPA backend for this shape
         out["reference_sdpa_ms"] = None
         out["reference_sdpa_note"] = f"{type(e).__name__}: {str(e)[:160]}"
+    # training step of the operator: forward (with the log-sum-exp) and the
+    # backward to all six inputs (csrc/mla.hip backward kernels + the two
+    # projection GEMMs); algorithmic flops: the forward's, then per visible
+    # pair dV, dP, dQ, dK (2 (2 (Dn + Dr) + 2 Dv)) and the projections
+    # d ctx_kv, dW (2 x 2 B S H (Dn + Dv) R); the backward's recompute of K, V
+    # and of the scores is not counted
+    from dsmoe.mla import mla_attention
+    ins = [t.clone().requires_grad_(True) for t in ts]
+    g = torch.Generator(device=dev).manual_seed(1)
+    dout = torch.randn(B, S, H, Dv, generator=g, device=dev).to(torch.bfloat16)
+
+    def train_step():
+        o = mla_attention(*ins, scale, True, 0)
+        return torch.autograd.grad(o, ins, dout)
+
+    ms_fb, _ = time_steps(train_step, max(3, steps // 2), max(2, warmup))
+    flop_fb = flop_attn + flop_kv + 2.0 * B * H * vis * (2 * (Dn + Dr) + 2 * Dv) + 4.0 * B * S * H * (Dn + Dv) * R
+    out["fwd_bwd"] = {"ms_per_step": ms_fb, "flop": flop_fb, "TFLOP/s": flop_fb / (ms_fb * 1e-3) / 1e12,
+                      "tokens_per_s": B * S / (ms_fb * 1e-3)}
     log(f"[bench] mla: {ms:.4f} ms/call, {tf:.0f} TFLOP/s ({tf / PEAK_BF16_TFLOPS:.1%}), "
-        f"reference SDPA {out.get('reference_sdpa_ms')}")
+        f"reference SDPA {out.get('reference_sdpa_ms')}; forward + backward {ms_fb:.4f} ms "
+        f"({out['fwd_bwd']['TFLOP/s']:.0f} TFLOP/s)")
     return out
 
 

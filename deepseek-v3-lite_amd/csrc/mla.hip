@@ -1318,48 +1318,69 @@ extern "C" int dsmoe_mla_attn_fwd_lse(const void* q_nope, const void* q_pe, cons
   return mla_fwd(q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v, dims, out, lse, workspace, workspace_bytes, stream);
 }
 
-// Workspace of dsmoe_mla_attn_bwd: the forward's K, V buffers, then the
-// packed query and dO rows and the padded lse and D (S_qp rows each), each
-// part a multiple of 256 bytes.
+// K and V alone: the forward's first launch, for a backward whose caller did
+// not keep the forward's workspace.
+extern "C" int dsmoe_mla_attn_kv(const void* ctx_kv, const void* ctx_pe, const void* wkv_b_k, const void* wkv_b_v,
+                                 const dsmoe_mla_dims* dims, void* kv_ws, size_t kv_bytes, void* stream) {
+  const int rc = mla_validate(dims);
+  if (rc) return rc;
+  DSMOE_REQUIRE(ctx_kv && ctx_pe && wkv_b_k && wkv_b_v, DSMOE_ERR_INVALID, "mla: NULL tensor pointer");
+  DSMOE_REQUIRE(kv_ws && kv_bytes >= dsmoe_mla_attn_workspace_size(dims), DSMOE_ERR_WORKSPACE,
+                "mla: workspace too small");
+  DSMOE_REQUIRE((reinterpret_cast<uintptr_t>(kv_ws) & 15) == 0, DSMOE_ERR_INVALID,
+                "mla: workspace must be 16-byte aligned");
+  // (no queries: the query-load flag, which K, V do not use, sees ctx_kv)
+  const MlaArgs a = mla_bind(ctx_kv, ctx_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v, dims, kv_ws);
+  return mla_launch_kv(a, static_cast<hipStream_t>(stream));
+}
+
+// Workspace of dsmoe_mla_attn_bwd: the packed query and dO rows and the
+// padded lse and D (S_qp rows each), each part a multiple of 256 bytes.
 static size_t mla_bwd_part(const MlaArgs& a, int part) {
   const size_t rows = (size_t)a.B * a.H * a.S_qp;
   switch (part) {
-    case 0: return (size_t)a.B * a.H * a.S_kvp * (a.DQKp + a.DVp) * sizeof(bf16_t);   // K, V
     case 1: return rows * a.DQKp * sizeof(bf16_t);
     case 2: return rows * a.DVp * sizeof(bf16_t);
-    default: return rows * sizeof(float);                                             // lse, D
+    default: return rows * sizeof(float);   // lse, D
   }
 }
 
 extern "C" size_t dsmoe_mla_attn_bwd_workspace_size(const dsmoe_mla_dims* dims) {
   if (mla_validate(dims) != DSMOE_OK) return 0;
   const MlaArgs a = mla_args(dims);
-  return mla_bwd_part(a, 0) + mla_bwd_part(a, 1) + mla_bwd_part(a, 2) + 2 * mla_bwd_part(a, 3) + 256;
+  return mla_bwd_part(a, 1) + mla_bwd_part(a, 2) + 2 * mla_bwd_part(a, 3) + 256;
 }
 
-extern "C" int dsmoe_mla_attn_bwd(const void* q_nope, const void* q_pe, const void* ctx_kv, const void* ctx_pe,
-                                  const void* wkv_b_k, const void* wkv_b_v, const dsmoe_mla_dims* dims,
-                                  const void* out, const void* dout, const float* lse, float* dq_nope, float* dq_pe,
-                                  void* dkv, float* dk_pe, void* workspace, size_t workspace_bytes, void* stream) {
+extern "C" int dsmoe_mla_attn_bwd(const void* q_nope, const void* q_pe, const dsmoe_mla_dims* dims,
+                                  const void* kv_ws, size_t kv_bytes, const void* out, const void* dout,
+                                  const float* lse, float* dq_nope, float* dq_pe, void* dkv, float* dk_pe,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
   int rc = mla_validate(dims);
   if (rc) return rc;
-  DSMOE_REQUIRE(q_nope && q_pe && ctx_kv && ctx_pe && wkv_b_k && wkv_b_v && out && dout && lse, DSMOE_ERR_INVALID,
-                "mla: NULL tensor pointer");
+  DSMOE_REQUIRE(q_nope && q_pe && out && dout && lse, DSMOE_ERR_INVALID, "mla: NULL tensor pointer");
   DSMOE_REQUIRE(dq_nope && dq_pe && dkv && dk_pe, DSMOE_ERR_INVALID, "mla: NULL gradient pointer");
+  DSMOE_REQUIRE(kv_ws && kv_bytes >= dsmoe_mla_attn_workspace_size(dims), DSMOE_ERR_WORKSPACE,
+                "mla: K, V workspace too small");
   const size_t need = dsmoe_mla_attn_bwd_workspace_size(dims);
   DSMOE_REQUIRE(workspace && workspace_bytes >= need, DSMOE_ERR_WORKSPACE, "mla: workspace too small");
-  DSMOE_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15) == 0, DSMOE_ERR_INVALID,
-                "mla: workspace must be 16-byte aligned");
-  MlaArgs a = mla_bind(q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v, dims, workspace);
+  DSMOE_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15) == 0 && (reinterpret_cast<uintptr_t>(kv_ws) & 15) == 0,
+                DSMOE_ERR_INVALID, "mla: workspaces must be 16-byte aligned");
+  // queries, and K, V as the forward left them
+  MlaArgs a = mla_args(dims);
+  a.q_nope = static_cast<const bf16_t*>(q_nope);
+  a.q_pe = static_cast<const bf16_t*>(q_pe);
+  a.qvec = (a.Dn % 8 == 0 && a.Dr % 8 == 0 && (reinterpret_cast<uintptr_t>(q_nope) & 15) == 0 &&
+            (reinterpret_cast<uintptr_t>(q_pe) & 15) == 0) ? 1 : 0;
+  a.kbuf = static_cast<bf16_t*>(const_cast<void*>(kv_ws));
+  a.vbuf = a.kbuf + (size_t)a.B * a.H * a.S_kvp * a.DQKp;
   a.out = static_cast<bf16_t*>(const_cast<void*>(out));   // read only (D)
   a.dout = static_cast<const bf16_t*>(dout);
   a.lse = const_cast<float*>(lse);                          // read only
   a.dovec = (a.Dv % 8 == 0 && (reinterpret_cast<uintptr_t>(dout) & 15) == 0) ? 1 : 0;
-  // parts: K, V (64-row multiples x 16-column multiples x 2 bytes), packed
-  // query rows, packed dO rows, lse, D (S_qp = 64-row multiples): every part
-  // starts 256-byte aligned
+  // parts: packed query rows, packed dO rows, lse, D (S_qp = 64-row
+  // multiples): every part starts 256-byte aligned
   char* ws = static_cast<char*>(workspace);
-  size_t off = mla_bwd_part(a, 0);
+  size_t off = 0;
   a.qpk = reinterpret_cast<bf16_t*>(ws + off);
   off += mla_bwd_part(a, 1);
   a.dopk = reinterpret_cast<bf16_t*>(ws + off);
@@ -1373,8 +1394,6 @@ extern "C" int dsmoe_mla_attn_bwd(const void* q_nope, const void* q_pe, const vo
   a.dk_pe = dk_pe;
   a.kvec = (a.Dn % 4 == 0 && a.Dv % 4 == 0 && (reinterpret_cast<uintptr_t>(dkv) & 7) == 0) ? 1 : 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  rc = mla_launch_kv(a, st);
-  if (rc) return rc;
   switch (a.DQKp / 16) {
     case 2: return mla_launch_bwd_nv<2>(a, st);
     case 4: return mla_launch_bwd_nv<4>(a, st);

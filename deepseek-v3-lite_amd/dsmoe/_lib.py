@@ -77,7 +77,8 @@ _SIGNATURES = {
     "dsmoe_mla_attn_fwd": ([P, P, P, P, P, P, ctypes.POINTER(MlaDims), P, P, SZ, P], I32),
     "dsmoe_mla_attn_fwd_lse": ([P, P, P, P, P, P, ctypes.POINTER(MlaDims), P, P, P, SZ, P], I32),
     "dsmoe_mla_attn_bwd_workspace_size": ([ctypes.POINTER(MlaDims)], SZ),
-    "dsmoe_mla_attn_bwd": ([P, P, P, P, P, P, ctypes.POINTER(MlaDims), P, P, P, P, P, P, P, P, SZ, P], I32),
+    "dsmoe_mla_attn_kv": ([P, P, P, P, ctypes.POINTER(MlaDims), P, SZ, P], I32),
+    "dsmoe_mla_attn_bwd": ([P, P, ctypes.POINTER(MlaDims), P, SZ, P, P, P, P, P, P, P, P, SZ, P], I32),
 }
 
 _lib = None

@@ -103,8 +103,9 @@ def _prepare(q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v):
 
 
 def _forward(ts, bc: int, softmax_scale: float, is_causal: bool, q_start: int, want_lse: bool):
-    """dsmoe_mla_attn_fwd (or _fwd_lse) over the batch chunks: bf16 out and
-    the fp32 lse (None unless asked for)."""
+    """dsmoe_mla_attn_fwd (or _fwd_lse) over the batch chunks: bf16 out, the
+    fp32 lse (None unless asked for) and the workspace, which holds the last
+    chunk's K and V."""
     q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v = ts
     B, H, S_q, _ = q_nope.shape
     D_v = wkv_b_v.size(1)
@@ -128,7 +129,7 @@ def _forward(ts, bc: int, softmax_scale: float, is_causal: bool, q_start: int, w
                     "dsmoe_mla_attn_fwd_lse")
         else:
             L.check(lib.dsmoe_mla_attn_fwd(*ins, L.ptr(ws), nbytes, L.stream_ptr(dev)), "dsmoe_mla_attn_fwd")
-    return out, lse
+    return out, lse, ws
 
 
 def mla_attention_fwd(q_nope: torch.Tensor, q_pe: torch.Tensor, ctx_kv: torch.Tensor, ctx_pe: torch.Tensor,
@@ -138,17 +139,19 @@ def mla_attention_fwd(q_nope: torch.Tensor, q_pe: torch.Tensor, ctx_kv: torch.Te
     global hip_calls
     out_dtype = q_nope.dtype
     ts, bc = _prepare(q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v)
-    out, _ = _forward(ts, bc, softmax_scale, is_causal, q_start, want_lse=False)
+    out, _, _ = _forward(ts, bc, softmax_scale, is_causal, q_start, want_lse=False)
     hip_calls += 1
     return out if out_dtype == torch.bfloat16 else out.to(out_dtype)
 
 
 def mla_attention_bwd_heads(ts, bc: int, out: torch.Tensor, lse: torch.Tensor, dout: torch.Tensor,
-                            softmax_scale: float, is_causal: bool, q_start: int):
+                            softmax_scale: float, is_causal: bool, q_start: int, kv_ws=None):
     """dsmoe_mla_attn_bwd over the batch chunks: fp32 dq_nope (B, H, S_q, Dn)
     and dq_pe (B, H, S_q, Dr), the bf16 key-side rows dkv (B, S_kv, H, Dn + Dv)
     = [dk_nope | dv] and fp32 dk_pe (B, S_kv, H, Dr).  ``ts`` and ``bc`` as
-    ``_prepare`` returns them; out, lse from the training forward."""
+    ``_prepare`` returns them; out, lse from the training forward; kv_ws the
+    forward's workspace when it ran in one chunk (its K and V are reused),
+    else None (K and V are rebuilt per chunk by dsmoe_mla_attn_kv)."""
     q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v = ts
     B, H, S_q, Dn = q_nope.shape
     S_kv, Dr, Dv = ctx_kv.size(1), q_pe.size(-1), wkv_b_v.size(1)
@@ -158,17 +161,28 @@ def mla_attention_bwd_heads(ts, bc: int, out: torch.Tensor, lse: torch.Tensor, d
     d = _dims(q_nope[:bc], q_pe[:bc], ctx_kv[:bc], wkv_b_v, softmax_scale, is_causal, q_start)
     nbytes = int(lib.dsmoe_mla_attn_bwd_workspace_size(d))
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    if kv_ws is not None and bc < B:
+        raise ValueError("mla_attention_bwd_heads: a forward workspace holds one chunk's K and V")
+    if kv_ws is None:
+        kv_ws = torch.empty(int(lib.dsmoe_mla_attn_workspace_size(d)), dtype=torch.uint8, device=dev)
+        rebuild = True
+    else:
+        rebuild = False
     f32 = dict(dtype=torch.float32, device=dev)
     dq_nope, dq_pe = torch.empty(B, H, S_q, Dn, **f32), torch.empty(B, H, S_q, Dr, **f32)
     dkv = torch.empty(B, S_kv, H, Dn + Dv, dtype=torch.bfloat16, device=dev)
     dk_pe = torch.empty(B, S_kv, H, Dr, **f32)
+    st = L.stream_ptr(dev)
     for b0 in range(0, B, bc):
         b1 = min(B, b0 + bc)
         d = _dims(q_nope[b0:b1], q_pe[b0:b1], ctx_kv[b0:b1], wkv_b_v, softmax_scale, is_causal, q_start)
+        if rebuild:
+            L.check(lib.dsmoe_mla_attn_kv(L.ptr(ctx_kv[b0:b1]), L.ptr(ctx_pe[b0:b1]), L.ptr(wkv_b_k), L.ptr(wkv_b_v),
+                                          d, L.ptr(kv_ws), kv_ws.numel(), st), "dsmoe_mla_attn_kv")
         rc = lib.dsmoe_mla_attn_bwd(
-            L.ptr(q_nope[b0:b1]), L.ptr(q_pe[b0:b1]), L.ptr(ctx_kv[b0:b1]), L.ptr(ctx_pe[b0:b1]), L.ptr(wkv_b_k),
-            L.ptr(wkv_b_v), d, L.ptr(out[b0:b1]), L.ptr(dout[b0:b1]), L.ptr(lse[b0:b1]), L.ptr(dq_nope[b0:b1]),
-            L.ptr(dq_pe[b0:b1]), L.ptr(dkv[b0:b1]), L.ptr(dk_pe[b0:b1]), L.ptr(ws), nbytes, L.stream_ptr(dev))
+            L.ptr(q_nope[b0:b1]), L.ptr(q_pe[b0:b1]), d, L.ptr(kv_ws), kv_ws.numel(), L.ptr(out[b0:b1]),
+            L.ptr(dout[b0:b1]), L.ptr(lse[b0:b1]), L.ptr(dq_nope[b0:b1]), L.ptr(dq_pe[b0:b1]), L.ptr(dkv[b0:b1]),
+            L.ptr(dk_pe[b0:b1]), L.ptr(ws), nbytes, st)
         L.check(rc, "dsmoe_mla_attn_bwd")
     return dq_nope, dq_pe, dkv, dk_pe
 
@@ -200,10 +214,13 @@ class _MlaAttentionFunction(torch.autograd.Function):
         out_dtype = q_nope.dtype
         ctx.dtypes = tuple(t.dtype for t in (q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v))
         ts, bc = _prepare(q_nope, q_pe, ctx_kv, ctx_pe, wkv_b_k, wkv_b_v)
-        out, lse = _forward(ts, bc, softmax_scale, is_causal, q_start, want_lse=True)
+        out, lse, kv_ws = _forward(ts, bc, softmax_scale, is_causal, q_start, want_lse=True)
         hip_calls += 1
-        # the backward runs on the bf16 operands the kernels saw
+        # the backward runs on the bf16 operands the kernels saw, and on the
+        # forward's K and V when one launch covered the batch (B H pad64(S_kv)
+        # (DQKp + DVp) bf16, held until the backward); otherwise it rebuilds them
         ctx.save_for_backward(*ts, out, lse)
+        ctx.kv_ws = kv_ws if bc >= ts[0].size(0) else None
         ctx.args = (bc, softmax_scale, is_causal, q_start)
         return out if out_dtype == torch.bfloat16 else out.to(out_dtype)
 
@@ -213,7 +230,8 @@ class _MlaAttentionFunction(torch.autograd.Function):
         bc, softmax_scale, is_causal, q_start = ctx.args
         with torch.autocast(dout.device.type, enabled=False):
             dq_nope, dq_pe, dkv, dk_pe = mla_attention_bwd_heads(ts, bc, out, lse, dout, softmax_scale, is_causal,
-                                                                 q_start)
+                                                                 q_start, ctx.kv_ws)
+            ctx.kv_ws = None
             dctx_kv, dctx_pe, dwk, dwv = _project_kv_grads(ts[2], ts[4], ts[5], dkv, dk_pe)
         grads = (dq_nope, dq_pe, dctx_kv, dctx_pe, dwk, dwv)
         return tuple(g.to(dt) for g, dt in zip(grads, ctx.dtypes)) + (None, None, None)

@@ -285,10 +285,18 @@ int dsmoe_mla_attn_fwd(const void* q_nope, const void* q_pe, const void* ctx_kv,
 int dsmoe_mla_attn_fwd_lse(const void* q_nope, const void* q_pe, const void* ctx_kv, const void* ctx_pe,
                            const void* wkv_b_k, const void* wkv_b_v, const dsmoe_mla_dims* dims, void* out,
                            float* lse, void* workspace, size_t workspace_bytes, void* stream);
+/* K and V of every (batch, head) into kv_ws (dsmoe_mla_attn_workspace_size
+ * bytes), the first launch of dsmoe_mla_attn_fwd on its own: for a backward
+ * whose caller did not keep the forward's workspace.  No counterpart in the
+ * reference (its backward recomputes everything, models/mla_triton.py:269-296). */
+int dsmoe_mla_attn_kv(const void* ctx_kv, const void* ctx_pe, const void* wkv_b_k, const void* wkv_b_v,
+                      const dsmoe_mla_dims* dims, void* kv_ws, size_t kv_bytes, void* stream);
 /* Backward of the attention (models/mla_triton.py:269-296,
  * _TritonMlaAttentionFunction.backward, which differentiates a torch recompute of
- * the same function), for the per-head operands: given the forward's inputs,
- * its out and lse, and dout (B, S_q, H, D_v) bf16, writes
+ * the same function), for the per-head operands.  Given the forward's queries,
+ * kv_ws as dsmoe_mla_attn_fwd(_lse) left it for the same inputs and dims
+ * (or as dsmoe_mla_attn_kv fills it), the forward's out and lse, and dout
+ * (B, S_q, H, D_v) bf16, writes
  *   dq_nope (B, H, S_q, D_nope) fp32   dq_pe (B, H, S_q, D_rope) fp32
  *   dkv (B, S_kv, H, D_nope + D_v) bf16: rows [dk_nope | dv]
  *   dk_pe (B, S_kv, H, D_rope) fp32
@@ -302,14 +310,14 @@ int dsmoe_mla_attn_fwd_lse(const void* q_nope, const void* q_pe, const void* ctx
  * element of the four outputs is written (zeros where no probability reaches
  * it).  The probabilities and dZ enter their MFMAs in bf16 with fp32
  * accumulation; dkv is rounded to bf16 once (the operand of those GEMMs).
- * Workspace: dsmoe_mla_attn_bwd_workspace_size bytes (the forward's K, V
- * buffers, then packed query and dO rows, lse and rowsum(dout * out) for
- * S_q rounded up to 64 rows); dims and limits as dsmoe_mla_attn_fwd. */
+ * Workspace: dsmoe_mla_attn_bwd_workspace_size bytes (packed query and dO
+ * rows, lse and rowsum(dout * out) for S_q rounded up to 64 rows); dims and
+ * limits as dsmoe_mla_attn_fwd. */
 size_t dsmoe_mla_attn_bwd_workspace_size(const dsmoe_mla_dims* dims);
-int dsmoe_mla_attn_bwd(const void* q_nope, const void* q_pe, const void* ctx_kv, const void* ctx_pe,
-                       const void* wkv_b_k, const void* wkv_b_v, const dsmoe_mla_dims* dims, const void* out,
-                       const void* dout, const float* lse, float* dq_nope, float* dq_pe, void* dkv,
-                       float* dk_pe, void* workspace, size_t workspace_bytes, void* stream);
+int dsmoe_mla_attn_bwd(const void* q_nope, const void* q_pe, const dsmoe_mla_dims* dims, const void* kv_ws,
+                       size_t kv_bytes, const void* out, const void* dout, const float* lse, float* dq_nope,
+                       float* dq_pe, void* dkv, float* dk_pe, void* workspace, size_t workspace_bytes,
+                       void* stream);
 
 #ifdef __cplusplus
 }

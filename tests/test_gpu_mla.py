@@ -266,8 +266,12 @@ def _bwd_heads(ts, sc, causal, q_start, dout):
     package's C-ABI wrappers."""
     import dsmoe.mla as M
     ts2, bc = M._prepare(*ts)
-    out, lse = M._forward(ts2, bc, sc, causal, q_start, want_lse=True)
-    grads = M.mla_attention_bwd_heads(ts2, bc, out, lse, dout, sc, causal, q_start)
+    out, lse, kv_ws = M._forward(ts2, bc, sc, causal, q_start, want_lse=True)
+    grads = M.mla_attention_bwd_heads(ts2, bc, out, lse, dout, sc, causal, q_start, kv_ws)
+    # the same with K and V rebuilt by dsmoe_mla_attn_kv: bit for bit
+    again = M.mla_attention_bwd_heads(ts2, bc, out, lse, dout, sc, causal, q_start)
+    for x, y in zip(grads, again):
+        assert torch.equal(x, y)
     torch.cuda.synchronize()
     return out, lse, grads
 

@@ -297,3 +297,18 @@ def test_cast_cache_follows_adamw_steps(small_cfg, fused):
         w.data.add_(1.0)
     invalidate_weight_casts()
     assert torch.equal(moe._cached_copy(w, torch.bfloat16), w.detach().to(torch.bfloat16))
+
+
+def test_mla_operator_rejects_host_tensors_and_bad_dims():
+    # the MLA drop-in has no CPU implementation: host tensors raise before any
+    # launch, and the reference's 256 cap per dimension raises ValueError
+    # (models/mla_triton.py:186-196)
+    import torch
+    from dsmoe.mla import _check_mla_dim_limits, mla_attention, triton_mla_attention
+    assert triton_mla_attention is mla_attention
+    t = torch.zeros(1, 1, 4, 8, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        mla_attention(t, t, torch.zeros(1, 4, 8, dtype=torch.bfloat16), torch.zeros(1, 4, 8, dtype=torch.bfloat16),
+                      torch.zeros(1, 8, 8, dtype=torch.bfloat16), torch.zeros(1, 8, 8, dtype=torch.bfloat16), 0.3)
+    with pytest.raises(ValueError, match="256"):
+        _check_mla_dim_limits(300, 8, 8, 8)
