@@ -270,11 +270,76 @@ __global__ __launch_bounds__(256) void mla_kv_kernel(const MlaArgs a) {
   }
 }
 
+// ---------------------------------------------------------------- staged tiles
+// Staged tiles are read both as MFMA fragments (ds_read_b128: eight columns
+// of a row per lane) and transposed (ds_read_b64_tr_b16: four consecutive
+// rows of a column per lane), so 16-byte chunk c of row r sits at
+// c ^ mlb_g(r) inside each group of 16 chunks; sixteen consecutive rows at one
+// chunk, and four consecutive rows (r = 0 mod 4) at four consecutive chunks
+// (c = 0 mod 4), then fall on distinct banks.
+// The backward kernels' tile loops come in a masked and an unmasked copy
+// for the common widths; the widest take the masked one everywhere (two
+// copies of their bodies exceed what the register allocator handles).
+#define MLB_SPLIT_EDGE(NSTEP, NV) ((NSTEP) + 2 * (NV) <= 16)
+constexpr int MLB_KW = 128;   // keys per workgroup of the dK, dV kernel
+constexpr int MLB_QI = 64;    // queries per staged tile of the dK, dV kernel (two halves of 32)
+constexpr int MLB_KT = 64;    // keys per staged tile of the dQ kernel
+
+__device__ __forceinline__ int mlb_off(int r, int c, int rb) {
+  const int g = ((r & 3) << 2) | ((r >> 2) & 3);
+  return r * rb + (((c & ~15) | ((c & 15) ^ g)) << 4);
+}
+
+// Reads of a staged tile with row bytes RB, the lane-dependent part of their
+// offsets computed once per kernel (the swizzle sees only a row's low four
+// bits and a chunk's low four, so rows R + .. with R = 0 mod 16 and chunk
+// group k add R RB + 256 k as immediates):
+//  * frag(t, R, st): the MFMA fragment of row R + (l & 31), 16-byte chunk
+//    2 st + hi (columns 16 st + 8 hi .. + 7);
+//  * tfrag(t, r0, ct): columns 32 ct .. + 31 over rows r0 .. r0 + 15
+//    (r0 = 0 mod 16) by two ds_read_b64_tr_b16, the rows in the order the
+//    score MFMA leaves in a lane's registers (lanes 0-31: r0 + {0-3, 8-11},
+//    lanes 32-63: r0 + {4-7, 12-15}); lane l gets column 32 ct + (l & 31).
+//    In a 16-lane group lane s addresses row s >> 2, columns 4 (s & 3) ..
+//    + 3 (8-byte unit u), and receives one column of the four rows.
+template <int RB>
+struct MlbLane {
+  int f[8], t0[4], t1[4];
+  __device__ __forceinline__ explicit MlbLane(int lane) {
+    const int hi = lane >> 5, l32 = lane & 31;
+#pragma unroll
+    for (int st = 0; st < 8; ++st) f[st] = mlb_off(l32, 2 * st + hi, RB);
+    const int gq = lane >> 4, sl = lane & 15;
+    const int r = 4 * (gq >> 1) + (sl >> 2);
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      const int u = 8 * ct + 4 * (gq & 1) + (sl & 3);
+      t0[ct] = mlb_off(r, u >> 1, RB) + ((u & 1) << 3);
+      t1[ct] = mlb_off(r + 8, u >> 1, RB) + ((u & 1) << 3);
+    }
+  }
+  __device__ __forceinline__ bf16x8_t frag(const char* t, int R, int st) const {
+    return *reinterpret_cast<const bf16x8_t*>(t + f[st & 7] + R * RB + 256 * (st >> 3));
+  }
+  __device__ __forceinline__ bf16x8_t tfrag(const char* t, int r0, int ct) const {
+    const int k = r0 * RB + 256 * (ct >> 2);
+    const mla_v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) mla_v4s*)(t + t0[ct & 3] + k));
+    const mla_v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) mla_v4s*)(t + t1[ct & 3] + k));
+    typedef short v8s __attribute__((ext_vector_type(8)));
+    const v8s v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(bf16x8_t, v);
+  }
+};
+
 // ---------------------------------------------------------------- attention
-// LDS per buffer: K tile 64 x (DQKp * 2 + 16) bytes, then V tile 64 x DVp * 2
-// bytes with 8-byte unit u of key row k stored at u ^ mla_vswz(k): the
-// transposing reads of 32 lanes cover four consecutive key rows and eight
-// units each, which this spreads over distinct banks.
+// LDS per buffer: K tile 64 x KRB bytes in the mlb_off layout, then V tile
+// 64 x DVp * 2 bytes with 8-byte unit u of key row k stored at
+// u ^ mla_vswz(k): the transposing reads of 32 lanes cover four consecutive
+// key rows and eight units each, which this spreads over distinct banks.  The
+// swizzle moves whole 16-byte chunks (it is a multiple of 8 units), so a tile
+// arrives by direct 16-byte loads.
 template <int NV>
 __device__ __forceinline__ int mla_vswz(int k) {
   return NV == 1 ? 0 : NV == 2 ? 8 * ((k >> 1) & 1) : 8 * (k & 3);
@@ -284,14 +349,12 @@ template <int NSTEP, int NV>
 struct MlaCfg {
   static constexpr int DQKp = NSTEP * 16;
   static constexpr int DVp = NV * 32;
-  static constexpr int KRS = DQKp * 2 + 16;            // K row stride (bytes)
-  static constexpr int KT = MLA_KB * KRS;              // K tile bytes
+  static constexpr int KRB = (DQKp + 127) / 128 * 256;   // K tile row bytes (mlb_off layout)
+  static constexpr int KT = MLA_KB * KRB;              // K tile bytes
   static constexpr int VT = MLA_KB * DVp * 2;          // V tile bytes
   static constexpr int BUF = KT + VT;
-  static constexpr int KCH = MLA_KB * DQKp / 8;        // 16-byte chunks of a K tile
-  static constexpr int VCH = MLA_KB * DVp / 8;
-  static constexpr int NLK = (KCH + 255) / 256;        // loads per thread
-  static constexpr int NLV = (VCH + 255) / 256;
+  static constexpr int NLK = KT / 4096;                // 1 KB direct loads per wave and tile
+  static constexpr int NLV = VT / 4096;
 };
 
 __device__ __forceinline__ float mla_pair_max(float x) {
@@ -376,50 +439,35 @@ __global__ __launch_bounds__(256) void mla_fa_kernel(const MlaArgs a) {
   int kend = a.S_kv;
   if (a.causal) kend = min(kend, min(q0 + MLA_QB, a.S_q) - 1 + a.q_start + 1);
   const int nkb = (kend + MLA_KB - 1) / MLA_KB;
-  const bf16_t* kg = a.kbuf + bh * a.S_kvp * C::DQKp;
-  const bf16_t* vg = a.vbuf + bh * a.S_kvp * C::DVp;
-
-  // tiles are staged through registers two blocks ahead (two register sets)
-  mla_u32x4 kst[2][C::NLK], vst[2][C::NLV];
-  auto gload = [&](int kb, mla_u32x4(&ks)[C::NLK], mla_u32x4(&vs)[C::NLV]) {
-    const int k0 = kb * MLA_KB;
+  const char* kg = reinterpret_cast<const char*>(a.kbuf + bh * a.S_kvp * C::DQKp);
+  const char* vg = reinterpret_cast<const char*>(a.vbuf + bh * a.S_kvp * C::DVp);
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  // block j straight into LDS buffer j & 1: the wave's 1 KB pieces of the K
+  // and V tiles (lane: 16 bytes at LDS offset 16 lane, which hold the chunk
+  // the tile's swizzle puts there)
+  auto issue = [&](int j) {
+    const uint32_t lds0 = lds_addr(mla_smem + (j & 1) * C::BUF);
+    const int64_t k0 = (int64_t)j * MLA_KB;
 #pragma unroll
-    for (int i = 0; i < C::NLK; ++i) {
-      const int c = tid + 256 * i;
-      if (C::KCH % 256 == 0 || c < C::KCH) {
-        const int r = c / (C::DQKp / 8), cc = c - r * (C::DQKp / 8);
-        ks[i] = *reinterpret_cast<const mla_u32x4*>(kg + (int64_t)(k0 + r) * C::DQKp + cc * 8);
-      }
+    for (int u = 0; u < C::NLK; ++u) {
+      const int blk = wv * C::NLK + u;
+      const int ofs = blk * 1024 + 16 * lane;
+      const int row = ofs / C::KRB, pc = (ofs % C::KRB) >> 4;
+      const int g = ((row & 3) << 2) | ((row >> 2) & 3);
+      const int cl = (pc & ~15) | ((pc & 15) ^ g);
+      if (cl < C::DQKp / 8)
+        dma16s(kg + k0 * C::DQKp * 2, (uint32_t)(row * C::DQKp * 2 + 16 * cl), lds0 + blk * 1024);
     }
 #pragma unroll
-    for (int i = 0; i < C::NLV; ++i) {
-      const int c = tid + 256 * i;
-      if (C::VCH % 256 == 0 || c < C::VCH) {
-        const int r = c / (C::DVp / 8), cc = c - r * (C::DVp / 8);
-        vs[i] = *reinterpret_cast<const mla_u32x4*>(vg + (int64_t)(k0 + r) * C::DVp + cc * 8);
-      }
-    }
-  };
-  auto lstore = [&](int buf, const mla_u32x4(&ks)[C::NLK], const mla_u32x4(&vs)[C::NLV]) {
-    char* kt = mla_smem + buf * C::BUF;
-    char* vt = kt + C::KT;
-#pragma unroll
-    for (int i = 0; i < C::NLK; ++i) {
-      const int c = tid + 256 * i;
-      if (C::KCH % 256 == 0 || c < C::KCH) {
-        const int r = c / (C::DQKp / 8), cc = c - r * (C::DQKp / 8);
-        *reinterpret_cast<mla_u32x4*>(kt + r * C::KRS + cc * 16) = ks[i];
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < C::NLV; ++i) {
-      const int c = tid + 256 * i;
-      if (C::VCH % 256 == 0 || c < C::VCH) {
-        const int r = c / (C::DVp / 8), cc = c - r * (C::DVp / 8);
-        *reinterpret_cast<mla_u32x4*>(vt + r * (C::DVp * 2) + (((2 * cc) ^ mla_vswz<NV>(r)) << 3)) = vs[i];
-      }
+    for (int u = 0; u < C::NLV; ++u) {
+      const int blk = wv * C::NLV + u;
+      const int ofs = blk * 1024 + 16 * lane;
+      const int row = ofs / (C::DVp * 2), pc = (ofs % (C::DVp * 2)) >> 4;
+      const int cl = pc ^ (mla_vswz<NV>(row) >> 1);
+      dma16s(vg + k0 * C::DVp * 2, (uint32_t)(row * C::DVp * 2 + 16 * cl), lds0 + C::KT + blk * 1024);
     }
   };
+  const MlbLane<C::KRB> lk(lane);
 
   mla_f32x16 o[NV];
 #pragma unroll
@@ -429,11 +477,14 @@ __global__ __launch_bounds__(256) void mla_fa_kernel(const MlaArgs a) {
   float m = -INFINITY, l = 0.0f;
   const int qpos = qi + a.q_start;
 
-  // block kb sits in LDS buffer kb & 1 and, before that, in register set kb & 1
-  auto block = [&](int kb, mla_u32x4(&ks_cur)[C::NLK], mla_u32x4(&vs_cur)[C::NLV], mla_u32x4(&ks_nxt)[C::NLK],
-                   mla_u32x4(&vs_nxt)[C::NLV]) {
+  if (nkb > 0) issue(0);
+  for (int kb = 0; kb < nkb; ++kb) {
+    // block kb has landed for every wave, and every wave is done with block kb - 1
+    wait_vm<0>();
+    wait_lgkm0();
+    lds_barrier();
+    if (kb + 1 < nkb) issue(kb + 1);
     const int k0 = kb * MLA_KB;
-    if (kb + 2 < nkb) gload(kb + 2, ks_cur, vs_cur);
     const char* kt = mla_smem + (kb & 1) * C::BUF;
     const char* vt = kt + C::KT;
     // scores: sub-tile t, register i -> key k0 + 32 t + 8 (i / 4) + 4 hi + i % 4
@@ -443,10 +494,8 @@ __global__ __launch_bounds__(256) void mla_fa_kernel(const MlaArgs a) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) s[t][i] = 0.0f;
 #pragma unroll
-      for (int st = 0; st < NSTEP; ++st) {
-        const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(kt + (32 * t + ql) * C::KRS + (2 * st + hi) * 16);
-        s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], s[t], 0, 0, 0);
-      }
+      for (int st = 0; st < NSTEP; ++st)
+        s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(lk.frag(kt, 32 * t, st), qf[st], s[t], 0, 0, 0);
     }
     // masks: keys past S_kv and, with the causal mask, keys past the query;
     // p = exp2(c s - c m) with c >= 0, so the running max of s is the max
@@ -521,16 +570,6 @@ __global__ __launch_bounds__(256) void mla_fa_kernel(const MlaArgs a) {
         }
       }
     }
-    if (kb + 1 < nkb) lstore((kb + 1) & 1, ks_nxt, vs_nxt);
-    __syncthreads();
-  };
-  gload(0, kst[0], vst[0]);
-  if (nkb > 1) gload(1, kst[1], vst[1]);
-  lstore(0, kst[0], vst[0]);
-  __syncthreads();
-  for (int kb = 0; kb < nkb; kb += 2) {
-    block(kb, kst[0], vst[0], kst[1], vst[1]);
-    if (kb + 1 < nkb) block(kb + 1, kst[1], vst[1], kst[0], vst[0]);
   }
 
   // out[b, qi, h, dv]: lane holds dv = 32 v + 8 (i / 4) + 4 hi + i % 4
@@ -580,68 +619,6 @@ __global__ __launch_bounds__(256) void mla_fa_kernel(const MlaArgs a) {
 // K columns, k_hi and k_lo parts added at the end.  The probabilities and dZ
 // enter the MFMAs as bf16.
 //
-// Staged tiles are read both as MFMA fragments (ds_read_b128: eight columns
-// of a row per lane) and transposed (ds_read_b64_tr_b16: four consecutive
-// rows of a column per lane), so 16-byte chunk c of row r sits at
-// c ^ mlb_g(r) inside each group of 16 chunks; sixteen consecutive rows at one
-// chunk, and four consecutive rows (r = 0 mod 4) at four consecutive chunks
-// (c = 0 mod 4), then fall on distinct banks.
-// The backward kernels' tile loops come in a masked and an unmasked copy
-// for the common widths; the widest take the masked one everywhere (two
-// copies of their bodies exceed what the register allocator handles).
-#define MLB_SPLIT_EDGE(NSTEP, NV) ((NSTEP) + 2 * (NV) <= 16)
-constexpr int MLB_KW = 128;   // keys per workgroup of the dK, dV kernel
-constexpr int MLB_QI = 64;    // queries per staged tile of the dK, dV kernel (two halves of 32)
-constexpr int MLB_KT = 64;    // keys per staged tile of the dQ kernel
-
-__device__ __forceinline__ int mlb_off(int r, int c, int rb) {
-  const int g = ((r & 3) << 2) | ((r >> 2) & 3);
-  return r * rb + (((c & ~15) | ((c & 15) ^ g)) << 4);
-}
-
-// Reads of a staged tile with row bytes RB, the lane-dependent part of their
-// offsets computed once per kernel (the swizzle sees only a row's low four
-// bits and a chunk's low four, so rows R + .. with R = 0 mod 16 and chunk
-// group k add R RB + 256 k as immediates):
-//  * frag(t, R, st): the MFMA fragment of row R + (l & 31), 16-byte chunk
-//    2 st + hi (columns 16 st + 8 hi .. + 7);
-//  * tfrag(t, r0, ct): columns 32 ct .. + 31 over rows r0 .. r0 + 15
-//    (r0 = 0 mod 16) by two ds_read_b64_tr_b16, the rows in the order the
-//    score MFMA leaves in a lane's registers (lanes 0-31: r0 + {0-3, 8-11},
-//    lanes 32-63: r0 + {4-7, 12-15}); lane l gets column 32 ct + (l & 31).
-//    In a 16-lane group lane s addresses row s >> 2, columns 4 (s & 3) ..
-//    + 3 (8-byte unit u), and receives one column of the four rows.
-template <int RB>
-struct MlbLane {
-  int f[8], t0[4], t1[4];
-  __device__ __forceinline__ explicit MlbLane(int lane) {
-    const int hi = lane >> 5, l32 = lane & 31;
-#pragma unroll
-    for (int st = 0; st < 8; ++st) f[st] = mlb_off(l32, 2 * st + hi, RB);
-    const int gq = lane >> 4, sl = lane & 15;
-    const int r = 4 * (gq >> 1) + (sl >> 2);
-#pragma unroll
-    for (int ct = 0; ct < 4; ++ct) {
-      const int u = 8 * ct + 4 * (gq & 1) + (sl & 3);
-      t0[ct] = mlb_off(r, u >> 1, RB) + ((u & 1) << 3);
-      t1[ct] = mlb_off(r + 8, u >> 1, RB) + ((u & 1) << 3);
-    }
-  }
-  __device__ __forceinline__ bf16x8_t frag(const char* t, int R, int st) const {
-    return *reinterpret_cast<const bf16x8_t*>(t + f[st & 7] + R * RB + 256 * (st >> 3));
-  }
-  __device__ __forceinline__ bf16x8_t tfrag(const char* t, int r0, int ct) const {
-    const int k = r0 * RB + 256 * (ct >> 2);
-    const mla_v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (__attribute__((address_space(3))) mla_v4s*)(t + t0[ct & 3] + k));
-    const mla_v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (__attribute__((address_space(3))) mla_v4s*)(t + t1[ct & 3] + k));
-    typedef short v8s __attribute__((ext_vector_type(8)));
-    const v8s v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-    return __builtin_bit_cast(bf16x8_t, v);
-  }
-};
-
 // 16 bf16 probabilities (or dZ values) of a lane's registers as the two
 // 16-key (16-query) K-steps of the next MFMAs.
 __device__ __forceinline__ void mlb_pack(const float (&p)[16], bf16x8_t (&f)[2]) {
