@@ -71,6 +71,8 @@ struct MlaArgs {
   float* dk_pe;           // (B, S_kv, H, Dr)
   int kvec;               // 8-byte dkv stores (Dn, Dv % 4 == 0, dkv 8-byte aligned)
   int dovec;              // 16-byte dO row loads (Dv % 8 == 0, dout 16-byte aligned)
+  int outvec;             // 16-byte O row loads in the backward (Dv % 8 == 0, out 16-byte aligned)
+  int dqvec;              // 16-byte dq stores (Dn, Dr % 8 == 0, dq_nope / dq_pe 16-byte aligned)
   float scale;            // softmax_scale
   bf16_t* kbuf;           // (B, H, S_kvp, DQKp)
   bf16_t* vbuf;           // (B, H, S_kvp, DVp)
@@ -936,21 +938,61 @@ __global__ __launch_bounds__(256) void mla_bwd_q_kernel(const MlaArgs a) {
   const int qi = q0 + 32 * wave + l32;
   const int64_t bh = (int64_t)b * a.H + h;
 
-  bf16x8_t qf[NSTEP], of[2 * NV];
+  // the lane's query fragments, dO and O row pieces: with 16-byte rows every
+  // load is issued unconditionally from a valid address (the row clamped to
+  // S_q - 1, padding columns reading the row's start) and zeroed by a select
+  // afterwards, so the batch stays in flight (a load under a runtime guard is
+  // waited for at the guard's end)
+  bf16x8_t qf[NSTEP], of[2 * NV], o8[2 * NV];
+  const int qc = min(qi, a.S_q - 1);
+  const bool qok = qi < a.S_q;
+  if (a.qvec) {
+    const int qend = a.ksplit ? 2 * a.Dn + a.Dr : a.Dn + a.Dr;
+    const bf16_t* qn = a.q_nope + (bh * a.S_q + qc) * a.Dn;
+    const bf16_t* qp = a.q_pe + (bh * a.S_q + qc) * a.Dr;
+    mla_u32x4 v[NSTEP];
 #pragma unroll
-  for (int st = 0; st < NSTEP; ++st) qf[st] = __builtin_bit_cast(bf16x8_t, mlb_qchunk(a, bh, qi, 16 * st + 8 * hi));
+    for (int st = 0; st < NSTEP; ++st) {
+      const int d = 16 * st + 8 * hi;
+      const bf16_t* src = d < a.Dn ? qn + d : d < a.Dn + a.Dr ? qp + (d - a.Dn) : d < qend ? qn + (d - a.Dn - a.Dr) : qn;
+      v[st] = *reinterpret_cast<const mla_u32x4*>(src);
+    }
+    const mla_u32x4 sgn = a.negq ? mla_u32x4{0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u}
+                                 : mla_u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
-  for (int st = 0; st < 2 * NV; ++st)
-    of[st] = __builtin_bit_cast(bf16x8_t, mlb_dochunk(a, a.dout, b, h, qi, 16 * st + 8 * hi));
-  const float lq = qi < a.S_q ? a.lse[bh * a.S_q + qi] : INFINITY;
+    for (int st = 0; st < NSTEP; ++st) {
+      const bool ok = qok && 16 * st + 8 * hi < qend;
+      qf[st] = __builtin_bit_cast(bf16x8_t, ok ? v[st] ^ sgn : mla_u32x4{0u, 0u, 0u, 0u});
+    }
+  } else {
+#pragma unroll
+    for (int st = 0; st < NSTEP; ++st) qf[st] = __builtin_bit_cast(bf16x8_t, mlb_qchunk(a, bh, qi, 16 * st + 8 * hi));
+  }
+  {
+    const int64_t orow = (((int64_t)b * a.S_q + qc) * a.H + h) * a.Dv;
+    mla_u32x4 vd[2 * NV], vo[2 * NV];
+#pragma unroll
+    for (int st = 0; st < 2 * NV; ++st) {
+      const int d = min(16 * st + 8 * hi, a.Dv - 8);
+      if (a.dovec) vd[st] = *reinterpret_cast<const mla_u32x4*>(a.dout + orow + d);
+      if (a.outvec) vo[st] = *reinterpret_cast<const mla_u32x4*>(a.out + orow + d);
+    }
+#pragma unroll
+    for (int st = 0; st < 2 * NV; ++st) {
+      const bool ok = qok && 16 * st + 8 * hi < a.Dv;
+      of[st] = __builtin_bit_cast(bf16x8_t, a.dovec ? (ok ? vd[st] : mla_u32x4{0u, 0u, 0u, 0u})
+                                                    : mlb_dochunk(a, a.dout, b, h, qi, 16 * st + 8 * hi));
+      o8[st] = __builtin_bit_cast(bf16x8_t, a.outvec ? (ok ? vo[st] : mla_u32x4{0u, 0u, 0u, 0u})
+                                                     : mlb_dochunk(a, a.out, b, h, qi, 16 * st + 8 * hi));
+    }
+  }
+  const float lq = qok ? a.lse[bh * a.S_q + qc] : INFINITY;
   // D = rowsum(dO * O): this lane's columns 16 st + 8 hi .., then the other half of the row
   float dq = 0.0f;
 #pragma unroll
-  for (int st = 0; st < 2 * NV; ++st) {
-    const bf16x8_t o8 = __builtin_bit_cast(bf16x8_t, mlb_dochunk(a, a.out, b, h, qi, 16 * st + 8 * hi));
+  for (int st = 0; st < 2 * NV; ++st)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) dq = fmaf((float)o8[e], (float)of[st][e], dq);
-  }
+    for (int e = 0; e < 8; ++e) dq = fmaf((float)o8[st][e], (float)of[st][e], dq);
   dq += __shfl_xor(dq, 32);
   // the packed rows and padded lse, D the dK, dV kernel loads (rows up to S_qp)
   if (qi < a.S_qp) {
@@ -1080,12 +1122,36 @@ __global__ __launch_bounds__(256) void mla_bwd_q_kernel(const MlaArgs a) {
   __syncthreads();
   const float sq = a.scale;
   const int nr = min(32, a.S_q - qw);
-  for (int r = 0; r < nr; ++r) {
-    const float* srow = stg + r * C::SRS;
-    float* dn = a.dq_nope + (bh * a.S_q + qw + r) * a.Dn;
-    float* dp = a.dq_pe + (bh * a.S_q + qw + r) * a.Dr;
-    for (int d = lane; d < a.Dn; d += 64) dn[d] = sq * (srow[d] + (a.ksplit ? srow[a.Dn + a.Dr + d] : 0.0f));
-    for (int d = lane; d < a.Dr; d += 64) dp[d] = sq * srow[a.Dn + d];
+  if (a.dqvec) {
+    // a lane pair per row, each lane every other 4-column group: 16-byte LDS
+    // reads and global stores, all of a lane's independent
+    const int r = lane >> 1, c0 = 4 * (lane & 1);
+    if (r < nr) {
+      const float* srow = stg + r * C::SRS;
+      float* dn = a.dq_nope + (bh * a.S_q + qw + r) * a.Dn;
+      float* dp = a.dq_pe + (bh * a.S_q + qw + r) * a.Dr;
+      const int lo = a.ksplit ? a.Dn + a.Dr : 0;
+      for (int d = c0; d < a.Dn; d += 8) {
+        float4 v = *reinterpret_cast<const float4*>(srow + d);
+        if (a.ksplit) {
+          const float4 w = *reinterpret_cast<const float4*>(srow + lo + d);
+          v.x += w.x; v.y += w.y; v.z += w.z; v.w += w.w;
+        }
+        *reinterpret_cast<float4*>(dn + d) = make_float4(sq * v.x, sq * v.y, sq * v.z, sq * v.w);
+      }
+      for (int d = c0; d < a.Dr; d += 8) {
+        const float4 v = *reinterpret_cast<const float4*>(srow + a.Dn + d);
+        *reinterpret_cast<float4*>(dp + d) = make_float4(sq * v.x, sq * v.y, sq * v.z, sq * v.w);
+      }
+    }
+  } else {
+    for (int r = 0; r < nr; ++r) {
+      const float* srow = stg + r * C::SRS;
+      float* dn = a.dq_nope + (bh * a.S_q + qw + r) * a.Dn;
+      float* dp = a.dq_pe + (bh * a.S_q + qw + r) * a.Dr;
+      for (int d = lane; d < a.Dn; d += 64) dn[d] = sq * (srow[d] + (a.ksplit ? srow[a.Dn + a.Dr + d] : 0.0f));
+      for (int d = lane; d < a.Dr; d += 64) dp[d] = sq * srow[a.Dn + d];
+    }
   }
 }
 
@@ -1354,6 +1420,9 @@ extern "C" int dsmoe_mla_attn_bwd(const void* q_nope, const void* q_pe, const ds
   a.dout = static_cast<const bf16_t*>(dout);
   a.lse = const_cast<float*>(lse);                          // read only
   a.dovec = (a.Dv % 8 == 0 && (reinterpret_cast<uintptr_t>(dout) & 15) == 0) ? 1 : 0;
+  a.outvec = (a.Dv % 8 == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0) ? 1 : 0;
+  a.dqvec = (a.Dn % 8 == 0 && a.Dr % 8 == 0 && (reinterpret_cast<uintptr_t>(dq_nope) & 15) == 0 &&
+             (reinterpret_cast<uintptr_t>(dq_pe) & 15) == 0) ? 1 : 0;
   // parts: packed query rows, packed dO rows, lse, D (S_qp = 64-row
   // multiples): every part starts 256-byte aligned
   char* ws = static_cast<char*>(workspace);
