@@ -335,6 +335,38 @@ struct MlbLane {
   }
 };
 
+// ---------------------------------------------------------------- work items
+// The attention kernels' work items are (batch-head pair hb, rank) with rank
+// r the r-th longest of a pair's items under the causal mask (the forward
+// and dQ kernels: query blocks from the last; the dK, dV kernel: key blocks
+// from the first).  Block i runs on XCD i % 8 (local index j = i / 8).  With
+// at least MLA_SPREAD pairs, XCD x owns the pairs x, x + 8, ... (their K, V
+// or query-side rows share its L2) and walks them rank-major, so the
+// dispatcher, which starts blocks in order as slots free up, runs every
+// pair's longest item first and the short ones fill the tail.  Fewer pairs:
+// the XCDs take contiguous eighths of the pair-major list (every XCD busy).
+// Grid: 8 * ceil(BH / 8) * nrank blocks; false for a block past the items.
+constexpr int MLA_SPREAD = 32;
+
+__device__ __forceinline__ bool mla_item(int blk, int BH, int nrank, int& hb, int& rank) {
+  const int x = blk & 7, j = blk >> 3;
+  if (BH >= MLA_SPREAD) {
+    const int nh = (BH - x + 7) >> 3;   // pairs on this XCD
+    if (j >= nh * nrank) return false;
+    rank = j / nh;
+    hb = x + 8 * (j - rank * nh);
+    return true;
+  }
+  const int total = BH * nrank, per = (total + 7) / 8;
+  const int item = x * per + j;
+  if (j >= per || item >= total) return false;
+  hb = item / nrank;
+  rank = item - hb * nrank;
+  return true;
+}
+
+__host__ __device__ inline int64_t mla_grid(int BH, int nrank) { return 8 * (int64_t)((BH + 7) / 8) * nrank; }
+
 // ---------------------------------------------------------------- attention
 // LDS per buffer: K tile 64 x KRB bytes in the mlb_off layout, then V tile
 // 64 x DVp * 2 bytes with 8-byte unit u of key row k stored at
@@ -368,10 +400,8 @@ __device__ __forceinline__ float mla_pair_sum(float x) {
   return __int_as_float(r[0]) + __int_as_float(r[1]);
 }
 
-// Work items (batch, head, query block) are numbered (batch, head)-major with
-// a head's query blocks last-first (causal: the longest first); block i runs
-// on XCD i % 8 and the XCDs take contiguous eighths of the items, so the
-// query blocks of a head share their XCD's L2 copy of its K and V.
+// Work items (batch, head, query block) as mla_item orders them, a pair's
+// query blocks last-first (causal: the longest first).
 template <int NSTEP, int NV>
 __global__ __launch_bounds__(256) void mla_fa_kernel(const MlaArgs a) {
   using C = MlaCfg<NSTEP, NV>;
@@ -379,13 +409,10 @@ __global__ __launch_bounds__(256) void mla_fa_kernel(const MlaArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hi = lane >> 5, ql = lane & 31;
   const int nq = (a.S_q + MLA_QB - 1) / MLA_QB;
-  const int total = nq * a.H * a.B;
-  const int per = (total + 7) / 8;
-  const int item = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
-  if (item >= total) return;
-  const int hb = item / nq;
+  int hb, rank;
+  if (!mla_item((int)blockIdx.x, a.B * a.H, nq, hb, rank)) return;
   const int h = hb % a.H, b = hb / a.H;
-  const int q0 = (nq - 1 - (item - hb * nq)) * MLA_QB;
+  const int q0 = (nq - 1 - rank) * MLA_QB;
   const int qi = q0 + 32 * wave + ql;          // this lane's query
   const int64_t bh = (int64_t)b * a.H + h;
 
@@ -689,9 +716,8 @@ struct MlbKvCfg {
   static constexpr int NOI = OT / 4096;
 };
 
-// Work items (batch, head, 128-key block), block i on XCD i % 8 taking
-// contiguous eighths (a head's key blocks share their XCD's L2 copy of its
-// queries and dO).  Wave w owns keys k0 + 32 w ..; a lane one key, with its
+// Work items (batch, head, 128-key block) as mla_item orders them, a pair's
+// key blocks first-first (causal: the longest first).  Wave w owns keys k0 + 32 w ..; a lane one key, with its
 // K and V rows (the B operands of the score and dP MFMAs) in registers.  The
 // query tiles (64 queries, two halves of 32) come from the packed rows
 // mla_bwd_q_kernel leaves in the workspace (q_eff, dO, lse and D padded to
@@ -705,13 +731,10 @@ __global__ __launch_bounds__(256) void mla_bwd_kv_kernel(const MlaArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hi = lane >> 5, l32 = lane & 31;
   const int nkb = (a.S_kv + MLB_KW - 1) / MLB_KW;
-  const int total = nkb * a.H * a.B;
-  const int per = (total + 7) / 8;
-  const int item = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
-  if (item >= total) return;
-  const int hb = item / nkb;
+  int hb, rank;
+  if (!mla_item((int)blockIdx.x, a.B * a.H, nkb, hb, rank)) return;
   const int h = hb % a.H, b = hb / a.H;
-  const int k0 = (item - hb * nkb) * MLB_KW;
+  const int k0 = rank * MLB_KW;
   const int kw0 = k0 + 32 * wave;
   const int key = kw0 + l32;
   const int64_t bh = (int64_t)b * a.H + h;
@@ -915,7 +938,7 @@ struct MlbQCfg {
   static constexpr int LDS = 2 * BUF > STG ? 2 * BUF : STG;
 };
 
-// Work items as the forward's: (batch, head, 128-query block), a head's
+// Work items as the forward's: (batch, head, 128-query block), a pair's
 // blocks longest first.  Lane: one query, its query fragments and dO row (the
 // B operands of the score and dP MFMAs) in registers.  The 64-key K and V
 // tiles go straight into LDS by direct loads, two buffers: tile i + 1 loads
@@ -928,13 +951,10 @@ __global__ __launch_bounds__(256) void mla_bwd_q_kernel(const MlaArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hi = lane >> 5, l32 = lane & 31;
   const int nq = (a.S_q + MLA_QB - 1) / MLA_QB;
-  const int total = nq * a.H * a.B;
-  const int per = (total + 7) / 8;
-  const int item = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
-  if (item >= total) return;
-  const int hb = item / nq;
+  int hb, rank;
+  if (!mla_item((int)blockIdx.x, a.B * a.H, nq, hb, rank)) return;
   const int h = hb % a.H, b = hb / a.H;
-  const int q0 = (nq - 1 - (item - hb * nq)) * MLA_QB;
+  const int q0 = (nq - 1 - rank) * MLA_QB;
   const int qi = q0 + 32 * wave + l32;
   const int64_t bh = (int64_t)b * a.H + h;
 
@@ -1218,8 +1238,7 @@ static int mla_launch_fa(const MlaArgs& a, hipStream_t st) {
         hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (attr != hipSuccess) return fail(DSMOE_ERR_HIP, "mla: cannot raise LDS limit");
   }
-  const int64_t total = cdiv(a.S_q, MLA_QB) * a.H * a.B;
-  hipLaunchKernelGGL(kern, dim3((unsigned)(8 * cdiv(total, 8))), dim3(256), lds, st, a);
+  hipLaunchKernelGGL(kern, dim3((unsigned)mla_grid(a.B * a.H, (int)cdiv(a.S_q, MLA_QB))), dim3(256), lds, st, a);
   return check_launch("mla_fa");
 }
 
@@ -1245,8 +1264,7 @@ static int mla_launch_bwd(const MlaArgs& a, hipStream_t st) {
           hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
       if (attr != hipSuccess) return fail(DSMOE_ERR_HIP, "mla: cannot raise LDS limit");
     }
-    const int64_t total = cdiv(a.S_q, MLA_QB) * a.H * a.B;
-    hipLaunchKernelGGL(kern, dim3((unsigned)(8 * cdiv(total, 8))), dim3(256), lds, st, a);
+    hipLaunchKernelGGL(kern, dim3((unsigned)mla_grid(a.B * a.H, (int)cdiv(a.S_q, MLA_QB))), dim3(256), lds, st, a);
     const int rc = check_launch("mla_bwd_q");
     if (rc) return rc;
   }
@@ -1258,8 +1276,7 @@ static int mla_launch_bwd(const MlaArgs& a, hipStream_t st) {
         hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (attr != hipSuccess) return fail(DSMOE_ERR_HIP, "mla: cannot raise LDS limit");
   }
-  const int64_t total = cdiv(a.S_kv, MLB_KW) * a.H * a.B;
-  hipLaunchKernelGGL(kern, dim3((unsigned)(8 * cdiv(total, 8))), dim3(256), lds, st, a);
+  hipLaunchKernelGGL(kern, dim3((unsigned)mla_grid(a.B * a.H, (int)cdiv(a.S_kv, MLB_KW))), dim3(256), lds, st, a);
   return check_launch("mla_bwd_kv");
 }
 
