@@ -234,10 +234,11 @@ __global__ __launch_bounds__(256) void mla_kv_kernel(const MlaArgs a) {
       const int col = 32 * t + l32;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
+        // hardware round-to-nearest-even conversions (v_cvt_pk_bf16_f32)
         const int r = 32 * wr + 8 * (i >> 2) + 4 * hi + (i & 3);
-        const bf16_t v = f2bf(acc[i]);
-        sho[r * MLA_KVN + col] = v;
-        sho[MLA_RB * MLA_KVN + r * MLA_KVN + col] = f2bf(acc[i] - bf2f(v));
+        const __bf16 v = (__bf16)acc[i];
+        sho[r * MLA_KVN + col] = __builtin_bit_cast(bf16_t, v);
+        sho[MLA_RB * MLA_KVN + r * MLA_KVN + col] = __builtin_bit_cast(bf16_t, (__bf16)(acc[i] - (float)v));
       }
     }
     __syncthreads();
