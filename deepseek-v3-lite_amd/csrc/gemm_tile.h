@@ -96,14 +96,15 @@ __device__ __forceinline__ bool tile_for_block_pair(const GemmDesc& gr, const Ge
 }
 
 // Backward GEMM tile lookup for the three XGemm schedules (same XCD-chunked
-// enumeration as tile_for_block).  Returns false for surplus blocks.
+// enumeration as tile_for_block) of block blk, which runs on XCD blk mod 8.
+// Returns false for surplus blocks.
 //   XS_ROUTED  schedule entries of height bm, split into bm / BMK sub-tiles;
 //   XS_DENSE   every group covers rows [0, dense_rows);
 //   XS_WGRAD   M = weight rows per group; K range = k_off[grp] .. k_off[grp+1],
 //              cut into ksplit parts of whole 64-row slabs (part index -> split).
 template <int BMK, int BNK>
-__device__ __forceinline__ bool xtile(const XGemm& g, int& grp, int& row0, int& rows, int& n_tile, int& kbeg, int& kend,
-                                      int& split) {
+__device__ __forceinline__ bool xtile_at(const XGemm& g, int64_t blk, int& grp, int& row0, int& rows, int& n_tile,
+                                         int& kbeg, int& kend, int& split) {
   const int n_tiles = (int)cdiv(g.N, BNK);
   int64_t m_total;
   int sub = 1, tpg = 0;
@@ -119,9 +120,9 @@ __device__ __forceinline__ bool xtile(const XGemm& g, int& grp, int& row0, int& 
   }
   const int64_t total = m_total * n_tiles;
   const int64_t per_xcd = cdiv(total, 8);
-  const int64_t j = blockIdx.x >> 3;
+  const int64_t j = blk >> 3;
   if (j >= per_xcd) return false;
-  const int64_t lin = (int64_t)(blockIdx.x & 7) * per_xcd + j;
+  const int64_t lin = (blk & 7) * per_xcd + j;
   if (lin >= total) return false;
   const int64_t mt = lin / n_tiles;
   n_tile = (int)(lin - mt * n_tiles);
@@ -156,6 +157,12 @@ __device__ __forceinline__ bool xtile(const XGemm& g, int& grp, int& row0, int& 
     }
   }
   return true;
+}
+
+template <int BMK, int BNK>
+__device__ __forceinline__ bool xtile(const XGemm& g, int& grp, int& row0, int& rows, int& n_tile, int& kbeg, int& kend,
+                                      int& split) {
+  return xtile_at<BMK, BNK>(g, blockIdx.x, grp, row0, rows, n_tile, kbeg, kend, split);
 }
 
 }  // namespace dsmoe

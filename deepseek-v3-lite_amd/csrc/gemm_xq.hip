@@ -32,6 +32,7 @@
 // shared-expert weight gradients are added in ascending part order by
 // wgrad_reduce_kernel.
 #include <algorithm>
+#include <atomic>
 
 #include "gemm_tile.h"
 #include "mfma.h"
@@ -97,6 +98,7 @@ struct XQLoad {
   uint32_t kmb[2];        // B: offset of load i = kmb[i & 1] + 2 i ldb  (= k_i * ldb + column)
   int kseg;               // K at which b1 takes over (0x7fffffff: one segment)
   int kbeg, kend, nk;
+  int g0;                 // persistent loop: ring index of the tile's first slab (ring index - g0 = K slab)
   int lds_off;            // byte offset of this wave's 8 KB inside an operand region
   int krow0;              // KM: first k row of this wave's loads (16 w)
 };
@@ -575,6 +577,301 @@ __global__ __launch_bounds__(256) void xgemm_q_kernel(const XGemm g) {
   }
 }
 
+// ------------------------------------------------- persistent weight gradients
+// Weight gradients without split-K (each routed expert's dW1 | dW3 and dW2)
+// as a persistent loop.  One workgroup per CU walks the tiles of virtual
+// blocks blockIdx.x, blockIdx.x + gridDim.x, ... (the XCD-chunked order of
+// one block per tile; gridDim.x is a multiple of 8, so every virtual block
+// stays on its block's XCD).  The ring index counts the slabs of all the
+// workgroup's tiles in a row: the loads issued during a tile's last two slabs
+// fetch the next tile's first two, so no tile after the first waits for its
+// first slab, and the epilogue's stores drain while the next tile computes
+// (one block per tile paid about 10 us per tile for its first slab, its
+// epilogue and the block's launch).  Every tile runs at least two slabs (rows
+// past its K range read zeros), so the loads never run more than one tile
+// ahead.  All four waves compute every tile; rows past M and columns past N
+// read clamped operands and are not stored.  A tile sums the same products
+// in the same order as xgemm_q_kernel, so the outputs are bitwise the same.
+//
+// The slab keeps one fragment register set per K step (xgemm_q_kernel
+// rotates three), so every slab starts in the same sets and the loop has one
+// slab body beside the tile's first.
+
+struct XQTileW {
+  int grp, row0, rows, n0, kbeg, kend;
+};
+
+// Tile of virtual block vb; false when vb has none.  Scalar values only.
+__device__ __forceinline__ bool xq_wgrad_tile(const XGemm& g, int64_t vb, XQTileW& t) {
+  int grp, row0, rows, n_tile, kbeg, kend, split;
+  if (!xtile_at<XQ_BM, XQ_BN>(g, vb, grp, row0, rows, n_tile, kbeg, kend, split)) return false;
+  t.grp = __builtin_amdgcn_readfirstlane(grp);
+  t.row0 = __builtin_amdgcn_readfirstlane(row0);
+  t.rows = __builtin_amdgcn_readfirstlane(rows);
+  t.n0 = __builtin_amdgcn_readfirstlane(n_tile) * XQ_BN;
+  t.kbeg = __builtin_amdgcn_readfirstlane(kbeg);
+  t.kend = __builtin_amdgcn_readfirstlane(kend);
+  return true;
+}
+
+// Slabs of a tile in the persistent loop: at least two.
+__device__ __forceinline__ int xq_wgrad_nk(const XQTileW& t) {
+  return max(2, t.kend > t.kbeg ? (int)cdiv(t.kend - t.kbeg, XQ_BK) : 0);
+}
+
+// Loader of tile t whose slab 0 sits at ring index g0.
+__device__ __forceinline__ void xq_wgrad_loader(const XGemm& g, const XQTileW& t, int g0, int wave, int lane,
+                                                XQLoad& L) {
+  L.kbeg = t.kbeg;
+  L.kend = t.kend;
+  L.nk = xq_wgrad_nk(t);
+  L.g0 = g0;
+  L.lds_off = wave * XQ_LD * 1024;
+  L.krow0 = wave * 16;
+  L.a = static_cast<const bf16_t*>(g.A) + (int64_t)t.grp * g.a_col;
+  L.a_ld = g.lda;
+  L.b0 = L.b1 = static_cast<const bf16_t*>(g.Bact) + (int64_t)t.grp * g.b_col;
+  L.kseg = 0x7fffffff;
+  L.b_ld = g.ldb;
+#pragma unroll
+  for (int par = 0; par < 2; ++par) {
+    const int kr = wave * 16 + (lane >> 5);
+    const int c = (lane & 31) ^ (((kr + 2 * par) & 3) << 2);
+    L.kma[par] = (uint32_t)((int64_t)kr * g.lda + min(t.row0 + 8 * c, g.M - 8));
+    L.kmb[par] = (uint32_t)((int64_t)kr * g.ldb + min(t.n0 + 8 * c, g.N - 8));
+  }
+}
+
+// Direct load i of A (KM) or B (activation KM rows) of ring slab kb for the
+// persistent loop.  The row address is formed unconditionally (an opaque
+// copy keeps the compiler from sinking it into a branch) and only the choice
+// between it and the zero block depends on the row: a branch per load would
+// cut the MFMA stream into blocks.
+__device__ __forceinline__ void xqw_issue_a_one(const XQLoad& L, int ka, int lane, int i) {
+  extern __shared__ __attribute__((aligned(16))) char xq_smem[];
+  const uint32_t da = lds_addr(xq_smem) + L.lds_off + (ka & 1) * XQ_REG;
+  const int k0 = L.kbeg + min(ka - L.g0, L.nk - 1) * XQ_BK;
+  const int kr = k0 + L.krow0 + 2 * i + (lane >> 5);
+  int64_t src = reinterpret_cast<int64_t>(L.a + (int64_t)k0 * L.a_ld +
+                                          (L.kma[i & 1] + (uint32_t)(2 * i) * (uint32_t)L.a_ld));
+  asm volatile("" : "+v"(src));
+  dma16(reinterpret_cast<const void*>(kr < L.kend ? src : reinterpret_cast<int64_t>(g_xq_zero)), da + i * 1024);
+}
+
+__device__ __forceinline__ void xqw_issue_b_one(const XQLoad& L, int kb, int lane, int i) {
+  extern __shared__ __attribute__((aligned(16))) char xq_smem[];
+  const uint32_t db = lds_addr(xq_smem) + L.lds_off + XQ_BOFF + (kb % XQ_BSLOTS) * XQ_REG;
+  const int k0 = L.kbeg + min(kb - L.g0, L.nk - 1) * XQ_BK;
+  const int kr = k0 + L.krow0 + 2 * i + (lane >> 5);
+  int64_t src = reinterpret_cast<int64_t>(L.b0 + (int64_t)k0 * L.b_ld +
+                                          (L.kmb[i & 1] + (uint32_t)(2 * i) * (uint32_t)L.b_ld));
+  asm volatile("" : "+v"(src));
+  dma16(reinterpret_cast<const void*>(kr < L.kend ? src : reinterpret_cast<int64_t>(g_xq_zero)), db + i * 1024);
+}
+
+// MFMAs T0 .. T1-1 of one K step (t = j * 4 + ni); the NL direct loads
+// LI0 .. LI0 + NL - 1 of A (LK 0) or B (LK 1) of ring slab kl spread evenly
+// over them.  ZC: the step starts the accumulators (zero accumulator input).
+template <int T0, int T1, int NL, int LK, int LI0, bool ZC>
+__device__ __forceinline__ void xqw_mma(const bf16x8_t (&fa)[4], const bf16x8_t (&fb)[4], f32x16_t (&acc)[4][4],
+                                        const XQLoad& L, int kl, int lane) {
+  const f32x16_t zero = {};
+#pragma unroll
+  for (int t = T0; t < T1; ++t) {
+    acc[t / 4][t % 4] =
+        __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[t % 4], fa[t / 4], ZC ? zero : acc[t / 4][t % 4], 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      if (T0 + i * (T1 - T0) / (NL > 0 ? NL : 1) == t) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (LK == 0)
+          xqw_issue_a_one(L, kl, lane, LI0 + i);
+        else
+          xqw_issue_b_one(L, kl, lane, LI0 + i);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+}
+
+struct XQPipe4 {
+  bf16x8_t fa[4][4];
+  bf16x8_t fb[4][4];
+};
+
+// One slab of the persistent loop: xq_slab's schedule (fragment reads two K
+// steps ahead, the barrier after step 1, B(kb + 2) during steps 0 and 1,
+// A(kb + 2) during steps 2 and 3) with one register set per K step, so every
+// slab starts with its steps 0 and 1 in sets 0 and 1.  FIRST: slab kb starts
+// the tile.
+template <bool FIRST>
+__device__ __forceinline__ void xqw_slab(XQPipe4& P, const XQLoad& L, int kb, int wm, int wn, int lane,
+                                         f32x16_t (&acc)[4][4]) {
+  constexpr int NL = XQ_LD / 2;
+  __builtin_amdgcn_sched_barrier(0);
+  xq_read<XA_KMAJOR, 4>(kb, 2, wm, wn, lane, P.fa[2], P.fb[2]);
+  __builtin_amdgcn_sched_barrier(0);
+  xqw_mma<0, 16, NL, 1, 0, FIRST>(P.fa[0], P.fb[0], acc, L, kb + 2, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  xq_read<XA_KMAJOR, 4>(kb, 3, wm, wn, lane, P.fa[3], P.fb[3]);
+  __builtin_amdgcn_sched_barrier(0);
+  xqw_mma<0, 16, NL, 1, NL, false>(P.fa[1], P.fb[1], acc, L, kb + 2, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  // every read of slab kb has returned, and this wave's loads of slab kb + 1
+  // (only the B(kb + 2) loads are younger; a tile's first slab has none left:
+  // the wave waited for all its loads before the previous tile's stores, so
+  // that this wait need not wait for those stores too)
+  wait_lgkm0();
+  if (!FIRST) wait_vm<XQ_LD>();
+  xq_sync();
+  xqw_mma<0, 4, 1, 0, 0, false>(P.fa[2], P.fb[2], acc, L, kb + 2, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  xq_read<XA_KMAJOR, 4>(kb + 1, 0, wm, wn, lane, P.fa[0], P.fb[0]);
+  __builtin_amdgcn_sched_barrier(0);
+  xqw_mma<4, 16, NL - 1, 0, 1, false>(P.fa[2], P.fb[2], acc, L, kb + 2, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  xq_read<XA_KMAJOR, 4>(kb + 1, 1, wm, wn, lane, P.fa[1], P.fb[1]);
+  __builtin_amdgcn_sched_barrier(0);
+  xqw_mma<0, 16, NL, 0, NL, false>(P.fa[3], P.fb[3], acc, L, kb + 2, lane);
+}
+
+// bf16 tile store of the persistent loop, wave by wave through the B slot of
+// the tile's last slab (no load fills it before the next tile's first slab,
+// and a wave's loads fill only its own 8 KB of a slot): each wave stages its
+// 32 rows x 128 columns of accumulator row block j in its own 8 KB (8-byte
+// unit u of row r at unit u ^ r), reads them back and stores 256-byte row
+// pieces with global 16-byte stores (a flat store would also count against
+// the LDS counter the slab loop waits on).  No barrier: the waves' epilogues
+// are independent.
+__device__ __forceinline__ void xq_wgrad_store_bf16(const XGemm& g, const XQTileW& t, char* slot, int wave, int wm,
+                                                    int wn, int tid_, const f32x16_t (&acc)[4][4]) {
+  // an opaque copy of the thread index keeps the address arithmetic below
+  // here: hoisted out of the tile loop, its registers would be live through
+  // every slab
+  int tid = tid_;
+  asm volatile("" : "+v"(tid));
+  const int lane = tid & 63;
+  char* const reg = slot + wave * XQ_LD * 1024;
+  const int64_t c0 = reinterpret_cast<int64_t>(g.Ctab0[t.grp]);
+  // rows from msplit on go to Ctab1 from its row 0: its base shifted back by msplit rows
+  const int64_t c1 = reinterpret_cast<int64_t>(g.Ctab1[t.grp]) - 2 * (int64_t)g.msplit * g.ldc;
+  const int cc = lane & 15, n = t.n0 + wn * 128 + cc * 8;
+  const bool col_ok = n < g.N;
+  const int rw = lane & 31;
+  wait_vm<0>();  // this wave's loads have landed before its first store
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int u = ni * 8 + q * 2 + (lane >> 5);
+        u32x2_t w;
+        w.x = pack_bf16x2(acc[j][ni][q * 4], acc[j][ni][q * 4 + 1]);
+        w.y = pack_bf16x2(acc[j][ni][q * 4 + 2], acc[j][ni][q * 4 + 3]);
+        *reinterpret_cast<u32x2_t*>(reg + rw * 256 + ((u ^ rw) << 3)) = w;
+      }
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+      const int rl = 4 * p + (lane >> 4);
+      const int pu = (2 * cc) ^ rl;
+      u32x4_t v = *reinterpret_cast<const u32x4_t*>(reg + rl * 256 + ((pu >> 1) << 4));
+      if (rl & 1) v = u32x4_t{v.z, v.w, v.x, v.y};
+      const int m = (2 * j + wm) * 32 + rl;
+      const int r = t.row0 + m;
+      const int64_t row = (r < g.msplit ? c0 : c1) + 2 * (int64_t)r * g.ldc;
+      if (m < t.rows && col_ok) *reinterpret_cast<xq_gv4u*>(row + 2 * (int64_t)n) = v;
+    }
+  }
+  wait_lgkm0();  // the reads are done before this wave's next loads into the slot
+}
+
+// fp32 tile store (fp32 master weights): straight from the accumulators, the
+// 16 bytes of lanes l and l + 32 adjacent in a row.
+__device__ __forceinline__ void xq_wgrad_store_f32(const XGemm& g, const XQTileW& t, int wm, int wn, int lane,
+                                                   const f32x16_t (&acc)[4][4]) {
+  const int64_t c0 = reinterpret_cast<int64_t>(g.Ctab0[t.grp]);
+  const int64_t c1 = reinterpret_cast<int64_t>(g.Ctab1[t.grp]) - 4 * (int64_t)g.msplit * g.ldc;
+  wait_vm<0>();  // this wave's loads have landed before its first store
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int m = (2 * j + wm) * 32 + (lane & 31);
+    const int r = t.row0 + m;
+    const int64_t row = (r < g.msplit ? c0 : c1) + 4 * (int64_t)r * g.ldc;
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = t.n0 + wn * 128 + ni * 32 + q * 8 + (lane >> 5) * 4;
+        if (m < t.rows && n < g.N)
+          *reinterpret_cast<xq_gv4u*>(row + 4 * (int64_t)n) =
+              u32x4_t{__float_as_uint(acc[j][ni][q * 4]), __float_as_uint(acc[j][ni][q * 4 + 1]),
+                      __float_as_uint(acc[j][ni][q * 4 + 2]), __float_as_uint(acc[j][ni][q * 4 + 3])};
+      }
+  }
+}
+
+template <bool F32>
+__global__ __launch_bounds__(256) void xgemm_wgrad_p_kernel(const XGemm g) {
+  extern __shared__ __attribute__((aligned(16))) char xq_smem[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t G = gridDim.x;
+  int64_t vb = blockIdx.x;
+  XQTileW cur, nxt, nn;
+  if (!xq_wgrad_tile(g, vb, cur)) return;
+  bool more = xq_wgrad_tile(g, vb + G, nxt);
+  // L loads the slabs two ahead of the MFMAs: the current tile's loader until
+  // the loads cross into the next tile, then that tile's
+  XQLoad L;
+  xq_wgrad_loader(g, cur, 0, wave, lane, L);
+  f32x16_t acc[4][4];  // started by each tile's first slab
+
+  // first tile: A(0), B(0) and A(1), B(1) in flight together; both landed
+  xq_issue_a<XA_KMAJOR, 0, XQ_LD>(L, 0, lane);
+  xq_issue_b<XB_ACT_KMAJOR, 0, XQ_LD>(L, 0, lane);
+  xq_issue_a<XA_KMAJOR, 0, XQ_LD>(L, 1, lane);
+  xq_issue_b<XB_ACT_KMAJOR, 0, XQ_LD>(L, 1, lane);
+  wait_vm<0>();  // slabs 0 and 1: the tile's first slab does not wait for loads
+  xq_sync();
+  XQPipe4 P;
+  xq_read<XA_KMAJOR, 4>(0, 0, wm, wn, lane, P.fa[0], P.fb[0]);
+  xq_read<XA_KMAJOR, 4>(0, 1, wm, wn, lane, P.fa[1], P.fb[1]);
+  wait_lgkm0();
+  int gs = 0;  // ring index of the current tile's first slab
+  int kb = 0;
+  for (;;) {
+    const int nk = xq_wgrad_nk(cur);
+    // before slab nk - 2 of the tile issues the loads of ring slab gs + nk,
+    // L becomes the next tile's loader
+    if (more && nk == 2) xq_wgrad_loader(g, nxt, gs + nk, wave, lane, L);
+    xqw_slab<true>(P, L, kb, wm, wn, lane, acc);
+    for (++kb; kb - gs < nk; ++kb) {
+      if (more && kb - gs == nk - 2) xq_wgrad_loader(g, nxt, gs + nk, wave, lane, L);
+      xqw_slab<false>(P, L, kb, wm, wn, lane, acc);
+    }
+    // the tile after next: its scalar loads run during the epilogue
+    const bool more2 = more && xq_wgrad_tile(g, vb + 2 * G, nn);
+    __builtin_amdgcn_sched_barrier(0);
+    if (F32)
+      xq_wgrad_store_f32(g, cur, wm, wn, lane, acc);
+    else
+      xq_wgrad_store_bf16(g, cur, xq_smem + XQ_BOFF + ((kb - 1) % XQ_BSLOTS) * XQ_REG, wave, wm, wn, tid, acc);
+    __builtin_amdgcn_sched_barrier(0);
+    if (!more) break;
+    gs = kb;
+    cur = nxt;
+    nxt = nn;
+    more = more2;
+    vb += G;
+    wait_lgkm0();  // no scalar load in flight at the loop head
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  wait_vm<0>();
+}
+
 // ---------------------------------------------------------------- host side
 static bool xq_al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
@@ -622,6 +919,31 @@ static int launch_xq_t(const XGemm& g, int64_t grid, hipStream_t st) {
   return check_launch("xgemm_q");
 }
 
+// Workgroups of the persistent weight-gradient loop: one per CU (the kernel
+// takes a whole CU's LDS), rounded up to a multiple of 8.
+static int64_t xq_persist_grid() {
+  static std::atomic<int> ncu{0};
+  int n = ncu.load(std::memory_order_relaxed);
+  if (n == 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    ncu.store(n, std::memory_order_relaxed);
+  }
+  return 8 * cdiv(n, 8);
+}
+
+template <bool F32>
+static int launch_xq_wgrad_p(const XGemm& g, int64_t grid, hipStream_t st) {
+  auto kern = xgemm_wgrad_p_kernel<F32>;
+  static const hipError_t attr =
+      hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)XQ_LDS);
+  if (attr != hipSuccess) return fail(DSMOE_ERR_HIP, "xgemm_wgrad_p: cannot raise LDS limit");
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(256), XQ_LDS, st, g);
+  return check_launch("xgemm_wgrad_p");
+}
+
 int launch_xgemm_q(const XGemm& g, int epi, hipStream_t st) {
   int64_t m_bound;
   if (g.sched_mode == XS_ROUTED)
@@ -635,6 +957,10 @@ int launch_xgemm_q(const XGemm& g, int epi, hipStream_t st) {
   if (grid > 0x7fffffff) return fail(DSMOE_ERR_UNSUPPORTED, "xgemm_q: grid too large");
   if (epi == XE_SWIGLU_BWD) return launch_xq_t<XE_SWIGLU_BWD, XA_ROWS>(g, grid, st);
   if (epi == XE_STORE) return launch_xq_t<XE_STORE, XA_ROWS>(g, grid, st);
+  if (g.ksplit <= 1) {
+    const int64_t grid_p = std::min(grid, xq_persist_grid());
+    return g.c_f32 ? launch_xq_wgrad_p<true>(g, grid_p, st) : launch_xq_wgrad_p<false>(g, grid_p, st);
+  }
   const int rc = launch_xq_t<XE_WGRAD, XA_KMAJOR>(g, grid, st);
   if (rc || g.ksplit <= 1) return rc;
   return launch_wgrad_reduce(g, st);  // add the split-K partials in ascending part order
