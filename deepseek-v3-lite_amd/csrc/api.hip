@@ -178,6 +178,7 @@ class StageTimer {
     g_timing.recs.push_back({a_, b, stage_});
     stage_ = -1;
   }
+  bool on() const { return on_; }
   void call_done(int kind) {
     if (!on_) return;
     std::lock_guard<std::mutex> lk(g_timing.mu);
@@ -190,6 +191,32 @@ class StageTimer {
   int stage_ = -1;
   hipEvent_t a_{};
 };
+
+// A second stream per calling thread and device, with its fork and join
+// events, for backward work that does not depend on the routed chain.
+struct SideStream {
+  hipStream_t s = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+static SideStream* side_stream() {
+  constexpr int kDev = 16;
+  thread_local SideStream ss[kDev];
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kDev) return nullptr;
+  SideStream& x = ss[dev];
+  if (!x.s) {
+    hipStream_t s = nullptr;
+    hipEvent_t a = nullptr, b = nullptr;
+    if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return nullptr;
+    if (hipEventCreateWithFlags(&a, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&b, hipEventDisableTiming) != hipSuccess)
+      return nullptr;
+    x.s = s;
+    x.fork = a;
+    x.join = b;
+  }
+  return &x;
+}
 
 static GemmDesc desc_zero() {
   GemmDesc g;
@@ -692,39 +719,20 @@ int dsmoe_moe_bwd_ex(const void* x, const float* gate_w, const void* const* w1, 
   if (rc) return rc;
   const int32_t mbound = (int32_t)sched_bound(N, d.E, BWD_BM);
 
-  // routed dh = w * (dy W2), SwiGLU backward -> [dg | du]
-  XGemm h = xdesc_zero();
-  h.sched_mode = XS_ROUTED; h.sched = B.sched; h.sched_count = B.sched_count; h.m_tiles_bound = mbound;
-  h.bm = BWD_BM; h.N = d.I; h.K = d.D;
-  h.a_mode = XA_ROWS; h.A = dy; h.lda = d.D; h.a_map = F.sorted_token;
-  h.b_mode = XB_W_NN; h.Btab = B.w2; h.ldb = d.I; h.kseg = d.D;
-  h.C = B.dgdu; h.ldc = 2 * (int64_t)d.I; h.du_off = d.I;
-  h.Gs = F.g; h.Us = F.u; h.ld_gu = d.I; h.row_w = F.sorted_w;
-  tm.begin(ST_BWD_DH);
-  rc = launch_xgemm(h, XE_SWIGLU_BWD, d.dtype, mf, st);
-  tm.end();
-  if (rc) return rc;
-  // routed dx_slot = [dg | du] [W1; W3], rows back to slot order
-  XGemm xg = xdesc_zero();
-  xg.sched_mode = XS_ROUTED; xg.sched = B.sched; xg.sched_count = B.sched_count; xg.m_tiles_bound = mbound;
-  xg.bm = BWD_BM; xg.N = d.D; xg.K = 2 * d.I;
-  xg.a_mode = XA_ROWS; xg.A = B.dgdu; xg.lda = 2 * (int64_t)d.I;
-  xg.b_mode = XB_W_NN; xg.Btab = B.w13; xg.ldb = d.D; xg.kseg = d.I; xg.nseg = 2;
-  xg.C = B.dx_slots; xg.ldc = d.D; xg.c_map = F.sorted_slot;
-  tm.begin(ST_BWD_DX);
-  rc = launch_xgemm(xg, XE_STORE, d.dtype, mf, st);
-  tm.end();
-  if (rc) return rc;
-  // routed dW1, dW3 = [dg | du]^T X_e ; dW2 = (w dY)^T H_e
-  XGemm w13 = xdesc_zero();
-  w13.sched_mode = XS_WGRAD; w13.groups = d.E; w13.k_off = F.offsets; w13.M = 2 * d.I; w13.N = d.D; w13.K = (int32_t)N;
-  w13.a_mode = XA_KMAJOR; w13.A = B.dgdu; w13.lda = 2 * (int64_t)d.I;
-  w13.b_mode = XB_ACT_KMAJOR; w13.Bact = F.x_sorted; w13.ldb = d.D;
-  w13.Ctab0 = B.dw1; w13.Ctab1 = B.dw3; w13.msplit = d.I; w13.ldc = d.D; w13.c_f32 = dw_f32;
-  tm.begin(ST_BWD_DW13);
-  rc = launch_xgemm(w13, XE_WGRAD, d.dtype, mf, st);
-  tm.end();
-  if (rc) return rc;
+  // The routed dW2, the shared experts' chain and dW_gate depend only on the
+  // preparation above: with stage timing off they go on a second stream while
+  // the routed dh, dx and dW1|dW3 run on the caller's, so the last, partly
+  // filled round of workgroups of each launch can take work from the other
+  // chain.  The caller's stream waits for the second before the dx sum.
+  hipStream_t ss = st;
+  SideStream* side = tm.on() ? nullptr : side_stream();
+  if (side && hipEventRecord(side->fork, st) == hipSuccess && hipStreamWaitEvent(side->s, side->fork, 0) == hipSuccess)
+    ss = side->s;
+  const auto join = [&](int r) {
+    if (ss != st && (hipEventRecord(side->join, ss) != hipSuccess || hipStreamWaitEvent(st, side->join, 0) != hipSuccess))
+      return r ? r : fail(DSMOE_ERR_HIP, "moe_bwd: cannot join the second stream");
+    return r;
+  };
   XGemm w2g = xdesc_zero();
   w2g.sched_mode = XS_WGRAD; w2g.groups = d.E; w2g.k_off = F.offsets; w2g.M = d.D; w2g.N = d.I; w2g.K = (int32_t)N;
   w2g.a_mode = XA_KMAJOR; w2g.lda = d.D;
@@ -736,9 +744,9 @@ int dsmoe_moe_bwd_ex(const void* x, const float* gate_w, const void* const* w1, 
   w2g.b_mode = XB_ACT_KMAJOR; w2g.Bact = F.h; w2g.ldb = d.I;
   w2g.Ctab0 = B.dw2; w2g.Ctab1 = B.dw2; w2g.msplit = d.D; w2g.ldc = d.I; w2g.c_f32 = dw_f32;
   tm.begin(ST_BWD_DW2);
-  rc = launch_xgemm(w2g, XE_WGRAD, d.dtype, mf, st);
+  rc = launch_xgemm(w2g, XE_WGRAD, d.dtype, mf, ss);
   tm.end();
-  if (rc) return rc;
+  if (rc) return join(rc);
 
   if (d.S) {
     const int64_t SIs = (int64_t)d.S * d.I_s;
@@ -749,9 +757,9 @@ int dsmoe_moe_bwd_ex(const void* x, const float* gate_w, const void* const* w1, 
     sh.C = B.dgdu_s; sh.ldc = 2 * SIs; sh.c_group_col = 2 * (int64_t)d.I_s; sh.du_off = d.I_s;
     sh.Gs = F.gs; sh.Us = F.us; sh.ld_gu = SIs; sh.gu_group_col = d.I_s;
     tm.begin(ST_BWD_DH_SHARED);
-    rc = launch_xgemm(sh, XE_SWIGLU_BWD, d.dtype, mf, st);
+    rc = launch_xgemm(sh, XE_SWIGLU_BWD, d.dtype, mf, ss);
     tm.end();
-    if (rc) return rc;
+    if (rc) return join(rc);
     XGemm sx = xdesc_zero();
     sx.sched_mode = XS_DENSE; sx.dense_rows = d.T; sx.groups = 1; sx.N = d.D; sx.K = (int32_t)(2 * SIs);
     sx.a_mode = XA_ROWS; sx.A = B.dgdu_s; sx.lda = 2 * SIs;
@@ -763,14 +771,14 @@ int dsmoe_moe_bwd_ex(const void* x, const float* gate_w, const void* const* w1, 
       for (int s = 0; s < d.S && !rc; ++s)
         for (int h = 0; h < 2 && !rc; ++h)
           if (hipMemcpyAsync(static_cast<char*>(B.sw13_stack) + (2 * s + h) * blk, h ? sw3[s] : sw1[s], blk,
-                             hipMemcpyDeviceToDevice, st) != hipSuccess)
+                             hipMemcpyDeviceToDevice, ss) != hipSuccess)
             rc = fail(DSMOE_ERR_HIP, "moe_bwd: shared weight stack copy failed");
       sx.kseg = (int32_t)(2 * SIs);
       sx.nseg = 1;
     }
-    if (!rc) rc = launch_xgemm(sx, XE_STORE, d.dtype, mf, st);
+    if (!rc) rc = launch_xgemm(sx, XE_STORE, d.dtype, mf, ss);
     tm.end();
-    if (rc) return rc;
+    if (rc) return join(rc);
     XGemm s13 = xdesc_zero();
     s13.sched_mode = XS_WGRAD; s13.groups = d.S; s13.M = 2 * d.I_s; s13.N = d.D; s13.K = d.T;
     s13.a_mode = XA_KMAJOR; s13.A = B.dgdu_s; s13.lda = 2 * SIs; s13.a_col = 2 * (int64_t)d.I_s;
@@ -784,14 +792,49 @@ int dsmoe_moe_bwd_ex(const void* x, const float* gate_w, const void* const* w1, 
     s2.Ctab0 = B.dsw2; s2.Ctab1 = B.dsw2; s2.msplit = d.D; s2.ldc = d.I_s;
     s2.ksplit = B.ks2; s2.part = B.part; s2.c_f32 = dw_f32;
     tm.begin(ST_BWD_DW_SHARED);
-    rc = launch_xgemm(s13, XE_WGRAD, d.dtype, mf, st);
-    if (!rc) rc = launch_xgemm(s2, XE_WGRAD, d.dtype, mf, st);
+    rc = launch_xgemm(s13, XE_WGRAD, d.dtype, mf, ss);
+    if (!rc) rc = launch_xgemm(s2, XE_WGRAD, d.dtype, mf, ss);
     tm.end();
-    if (rc) return rc;
+    if (rc) return join(rc);
   }
   tm.begin(ST_BWD_GATE);
-  rc = launch_dwgate(x, B.dlog, F.sorted_slot, F.sorted_token, F.offsets, d.E, d.D, d.dtype, dgate_w, st);
+  rc = launch_dwgate(x, B.dlog, F.sorted_slot, F.sorted_token, F.offsets, d.E, d.D, d.dtype, dgate_w, ss);
   tm.end();
+  if (rc) return join(rc);
+  // routed dh = w * (dy W2), SwiGLU backward -> [dg | du]
+  XGemm h = xdesc_zero();
+  h.sched_mode = XS_ROUTED; h.sched = B.sched; h.sched_count = B.sched_count; h.m_tiles_bound = mbound;
+  h.bm = BWD_BM; h.N = d.I; h.K = d.D;
+  h.a_mode = XA_ROWS; h.A = dy; h.lda = d.D; h.a_map = F.sorted_token;
+  h.b_mode = XB_W_NN; h.Btab = B.w2; h.ldb = d.I; h.kseg = d.D;
+  h.C = B.dgdu; h.ldc = 2 * (int64_t)d.I; h.du_off = d.I;
+  h.Gs = F.g; h.Us = F.u; h.ld_gu = d.I; h.row_w = F.sorted_w;
+  tm.begin(ST_BWD_DH);
+  rc = launch_xgemm(h, XE_SWIGLU_BWD, d.dtype, mf, st);
+  tm.end();
+  if (rc) return join(rc);
+  // routed dx_slot = [dg | du] [W1; W3], rows back to slot order
+  XGemm xg = xdesc_zero();
+  xg.sched_mode = XS_ROUTED; xg.sched = B.sched; xg.sched_count = B.sched_count; xg.m_tiles_bound = mbound;
+  xg.bm = BWD_BM; xg.N = d.D; xg.K = 2 * d.I;
+  xg.a_mode = XA_ROWS; xg.A = B.dgdu; xg.lda = 2 * (int64_t)d.I;
+  xg.b_mode = XB_W_NN; xg.Btab = B.w13; xg.ldb = d.D; xg.kseg = d.I; xg.nseg = 2;
+  xg.C = B.dx_slots; xg.ldc = d.D; xg.c_map = F.sorted_slot;
+  tm.begin(ST_BWD_DX);
+  rc = launch_xgemm(xg, XE_STORE, d.dtype, mf, st);
+  tm.end();
+  if (rc) return join(rc);
+  // routed dW1, dW3 = [dg | du]^T X_e ; dW2 = (w dY)^T H_e
+  XGemm w13 = xdesc_zero();
+  w13.sched_mode = XS_WGRAD; w13.groups = d.E; w13.k_off = F.offsets; w13.M = 2 * d.I; w13.N = d.D; w13.K = (int32_t)N;
+  w13.a_mode = XA_KMAJOR; w13.A = B.dgdu; w13.lda = 2 * (int64_t)d.I;
+  w13.b_mode = XB_ACT_KMAJOR; w13.Bact = F.x_sorted; w13.ldb = d.D;
+  w13.Ctab0 = B.dw1; w13.Ctab1 = B.dw3; w13.msplit = d.I; w13.ldc = d.D; w13.c_f32 = dw_f32;
+  tm.begin(ST_BWD_DW13);
+  rc = launch_xgemm(w13, XE_WGRAD, d.dtype, mf, st);
+  tm.end();
+  if (rc) return join(rc);
+  rc = join(rc);
   if (rc) return rc;
   tm.begin(ST_BWD_REDUCE);
   rc = launch_dx_final(B.dx_slots, B.dx_shared, B.dlog, F.idx, gate_w, d.T, d.D, d.k, d.dtype, dx, st);

@@ -174,7 +174,12 @@ int dsmoe_moe_fwd(const void* x, const float* gate_w, const float* gate_bias, co
 /* Backward of dsmoe_moe_fwd (training != 0).  dy (T,D).  Writes dx (T,D),
  * dgate_w (E,D) fp32, and per-expert weight gradients (device pointers, the
  * weight dtype): dw1[e], dw2[e], dw3[e], dsw1[s], dsw2[s], dsw3[s].  Unrouted
- * experts receive zeros.  fwd_workspace is the forward call's workspace. */
+ * experts receive zeros.  fwd_workspace is the forward call's workspace.
+ * Work ordered on `stream` as for any other call; inside, the routed dW2, the
+ * shared experts' gradients and dgate_w run on a second stream of the
+ * library's (one per calling thread and device, forked from and joined back
+ * into `stream` with events, so graph capture sees a fork and a join), except
+ * while stage timing is enabled. */
 size_t dsmoe_moe_bwd_workspace_size(const dsmoe_dims* dims);
 int dsmoe_moe_bwd(const void* x, const float* gate_w, const void* const* w1, const void* const* w2,
                   const void* const* w3, const void* const* sw1, const void* const* sw2, const void* const* sw3,

@@ -150,6 +150,31 @@ def test_backward_is_deterministic():
         assert all(torch.equal(u, v) for u, v in zip(a[key], b[key])), key
 
 
+def test_backward_second_stream_matches_one_stream():
+    """The layer backward runs the routed dW2, the shared experts' chain and
+    dW_gate on a second stream of its own, joined before the dx sum; with stage
+    timing on it runs everything on the caller's stream.  Both give the same
+    gradients bit for bit (every GEMM owns its tiles and sums in a fixed order),
+    at a shape with routed and shared experts, on a non-default caller stream."""
+    from dsmoe import _lib as L
+    case = CS.C3.with_tokens(1024)
+    x, p, dy = CS.make_inputs(case, with_dy=True)
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        a = _run(x, p.gate_w, p.gate_bias, p.w1, p.w2, p.w3, p.sw1, p.sw2, p.sw3, case.k, 1.0, dy)
+        L.timing_enable(True)
+        try:
+            b = _run(x, p.gate_w, p.gate_bias, p.w1, p.w2, p.w3, p.sw1, p.sw2, p.sw3, case.k, 1.0, dy)
+        finally:
+            L.timing_enable(False)
+            L.timing_read()
+    torch.cuda.synchronize()
+    for key in ("dx", "dgate_w"):
+        assert torch.equal(a[key], b[key]), key
+    for key in ("dw1", "dw2", "dw3", "dsw1", "dsw2", "dsw3"):
+        assert all(torch.equal(u, v) for u, v in zip(a[key], b[key])), key
+
+
 def test_dgate_full_batches_vs_oracle():
     """dW_gate where the kernel's waves sum full batches of rows, not only the
     one-row tail: at T=2048 and C3 width an expert holds about 192 sorted rows,
