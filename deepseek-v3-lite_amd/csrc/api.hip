@@ -198,19 +198,34 @@ struct SideStream {
   hipStream_t s = nullptr;
   hipEvent_t fork = nullptr, join = nullptr;
 };
-static SideStream* side_stream() {
+// The calling thread's second stream on the device of `st`, or null (the
+// caller then keeps all its work on `st`): when `st` belongs to a device other
+// than the current one, or when the stream or its events cannot be made.  A
+// failed query or creation leaves no error behind for the next launch check.
+static SideStream* side_stream(hipStream_t st) {
   constexpr int kDev = 16;
   thread_local SideStream ss[kDev];
+  const auto none = []() -> SideStream* {
+    (void)hipGetLastError();
+    return nullptr;
+  };
   int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kDev) return nullptr;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kDev) return none();
+  if (st) {
+    hipDevice_t sd = -1;
+    if (hipStreamGetDevice(st, &sd) != hipSuccess || sd != dev) return none();
+  }
   SideStream& x = ss[dev];
   if (!x.s) {
     hipStream_t s = nullptr;
     hipEvent_t a = nullptr, b = nullptr;
-    if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return nullptr;
+    if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) return none();
     if (hipEventCreateWithFlags(&a, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&b, hipEventDisableTiming) != hipSuccess)
-      return nullptr;
+        hipEventCreateWithFlags(&b, hipEventDisableTiming) != hipSuccess) {
+      if (a) (void)hipEventDestroy(a);
+      (void)hipStreamDestroy(s);
+      return none();
+    }
     x.s = s;
     x.fork = a;
     x.join = b;
@@ -725,7 +740,7 @@ int dsmoe_moe_bwd_ex(const void* x, const float* gate_w, const void* const* w1, 
   // filled round of workgroups of each launch can take work from the other
   // chain.  The caller's stream waits for the second before the dx sum.
   hipStream_t ss = st;
-  SideStream* side = tm.on() ? nullptr : side_stream();
+  SideStream* side = tm.on() ? nullptr : side_stream(st);
   if (side && hipEventRecord(side->fork, st) == hipSuccess && hipStreamWaitEvent(side->s, side->fork, 0) == hipSuccess)
     ss = side->s;
   const auto join = [&](int r) {

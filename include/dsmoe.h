@@ -179,7 +179,8 @@ int dsmoe_moe_fwd(const void* x, const float* gate_w, const float* gate_bias, co
  * shared experts' gradients and dgate_w run on a second stream of the
  * library's (one per calling thread and device, forked from and joined back
  * into `stream` with events, so graph capture sees a fork and a join), except
- * while stage timing is enabled. */
+ * while stage timing is enabled or when `stream` belongs to a device other
+ * than the current one (then everything runs on `stream`). */
 size_t dsmoe_moe_bwd_workspace_size(const dsmoe_dims* dims);
 int dsmoe_moe_bwd(const void* x, const float* gate_w, const void* const* w1, const void* const* w2,
                   const void* const* w3, const void* const* sw1, const void* const* sw2, const void* const* sw3,
